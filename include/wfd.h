@@ -1,0 +1,137 @@
+/*
+ * wfd.h -- C ABI of the MI355X wavefront-decode library (libwfd.so).
+ *
+ * Every compute entry point is stream-ordered on the caller's hipStream_t,
+ * allocates nothing, never synchronizes and throws nothing: it returns 0 on
+ * success or a negative status (WFD_BAD_ARG, WFD_UNSUPPORTED, WFD_LAUNCH,
+ * WFD_WORKSPACE) and leaves a message for wfd_last_error(). All tensors are
+ * plain device pointers to contiguous row-major storage; `dtype` is
+ * WFD_F32 (0) or WFD_BF16 (1). Lengths, positions and row tables are device
+ * data, so a launch sequence can be captured once in a hipGraph and replayed
+ * as the wave advances. Row tables (x_rows, flat_row, kv_row_base, ...) are
+ * trusted: the caller guarantees they index inside the buffers it passes.
+ *
+ * Each entry point names the reference interface (file:line under the
+ * reference checkout) whose work it replaces.
+ */
+#ifndef WFD_H_
+#define WFD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* wfd_stream_t; /* == hipStream_t */
+
+enum { WFD_F32 = 0, WFD_BF16 = 1 };
+enum { WFD_OK = 0, WFD_BAD_ARG = -1, WFD_UNSUPPORTED = -2, WFD_LAUNCH = -3, WFD_WORKSPACE = -4 };
+enum { WFD_EPI_PLAIN = 0, WFD_EPI_SWIGLU = 1 };
+
+/* Message for the last failing call on this thread. */
+const char* wfd_last_error(void);
+int wfd_abi_version(void);
+
+/*
+ * Wavefront decode attention (per-query slot prefix, read in place).
+ * Replaces: fa4_attention.attn_varlen / _attn_varlen_torch
+ *   (src/decoding/fa4_attention.py:301-317,348-366) as called by
+ *   ParcaeBlocks._core_attn_varlen (src/decoding/parcae_blocks.py:458-470),
+ *   attn_varlen_q1_padded (fa4_attention.py:320-342) as called by
+ *   HuginnBlocksBatch._union_attn (src/decoding/huginn_blocks_batch.py:282-285),
+ *   the graph path _fa_varlen (src/decoding/graph_blocks.py:40-43,186-194),
+ *   and attn_cutoff_multi (fa4_attention.py:240-291) -- a per-query cutoff is
+ *   kv_len = position + 1.
+ * q: (n, H, Dh); k_cache/v_cache: (rows, Hkv, Dh); out: (n, H, Dh).
+ * Query i attends rows kv_row_base[i] .. kv_row_base[i] + kv_len[i] - 1.
+ * kv_len_max >= every kv_len[i] sizes the grid; workspace >=
+ * wfd_attn_workspace_bytes(n, H, Dh, kv_len_max). Dh in {64, 128};
+ * H / Hkv in {1, 2, 4}.
+ */
+size_t wfd_attn_workspace_bytes(int n, int H, int Dh, int kv_len_max);
+int wfd_attn_split_keys(void);
+int wfd_attn_decode(const void* q, const void* k_cache, const void* v_cache, const int64_t* kv_row_base,
+                    const int32_t* kv_len, void* out, int n, int H, int Hkv, int Dh, int dtype, float scale,
+                    int kv_len_max, void* workspace, size_t ws_bytes, wfd_stream_t stream);
+
+/*
+ * Slot-cache append: k_cache[flat_row[i]] = k[i], v_cache[flat_row[i]] = v[i]
+ * (row_elems = Hkv * Dh elements per row).
+ * Replaces: StaticKVCache.write_range / write_scatter
+ *   (src/decoding/kv_cache.py:97-114), BatchStaticKVCache.write_tokens
+ *   (src/decoding/batch_kv_cache.py:61-73), and the graph index_copy_ writes
+ *   (src/decoding/graph_blocks.py:172-176,306-310).
+ */
+int wfd_kv_append(const void* k, const void* v, void* k_cache, void* v_cache, const int64_t* flat_row, int n,
+                  int row_elems, int dtype, wfd_stream_t stream);
+
+/*
+ * Fused QKV epilogue: split qkv rows (n, (H + 2*Hkv) * Dh) into q|k|v, rotate
+ * q and k by RoPE at pos[i] (interleaved pairs (2j, 2j+1), angle
+ * pos * base^(-2j/Dh), tables (rope_rows, Dh/2) fp32), write q to q_out
+ * (n, H, Dh) and append k, v at flat_row[i].
+ * Replaces: HuginnBlocks._qkv + the cache write
+ *   (src/decoding/huginn_blocks.py:77-87,96-97; huginn_blocks_batch.py:147-157,
+ *   308-310; graph_blocks.py:296-310).
+ */
+int wfd_qkv_rope_append(const void* qkv, int64_t ldq, const int32_t* pos, const float* rope_cos,
+                        const float* rope_sin, int rope_rows, const int64_t* flat_row, void* q_out, void* k_cache,
+                        void* v_cache, int n, int H, int Hkv, int Dh, int dtype, wfd_stream_t stream);
+
+/*
+ * Row-invariant linear: y[m, :] = x[x_rows ? x_rows[m] : m, :K] @ W^T, W (N, K)
+ * row-major. Epilogue WFD_EPI_SWIGLU: N = 2*pair_off, y[m, j] =
+ * silu(g_j) * u_j with g_j = row j, u_j = row pair_off + j of the product.
+ * out_dtype may be WFD_F32 for bf16 inputs (logits). K must be a multiple of
+ * wfd_linear_k_multiple(dtype), N of 16.
+ * Replaces: the nn.Linear calls of the block forwards -- Wqkv, proj, the gated
+ *   MLP, adapter, lm_head (src/decoding/huginn_blocks.py:79,100-102,216,291;
+ *   huginn_blocks_batch.py:149,160-161,299,345).
+ */
+int wfd_linear_k_multiple(int dtype);
+int wfd_linear(const void* x, const int32_t* x_rows, int64_t ldx, const void* W, void* y, int64_t ldy, int n, int N,
+               int K, int dtype, int out_dtype, int epilogue, int pair_off, wfd_stream_t stream);
+
+/*
+ * x_out[out_rows ? out_rows[i] : i] = rmsnorm(a[a_rows ? a_rows[i] : i] + res[i]) * w1
+ * and, if w2, h_out[i] = rmsnorm(x_out row) * w2. res may be NULL (plain
+ * RMSNorm). D <= 4096.
+ * Replaces: the SandwichBlock residual norms `norm_2(att + x)`, `norm_3`,
+ *   `norm_4(mlp + x)`, `norm_1` and `ln_f`
+ *   (src/decoding/huginn_blocks.py:95,101-102,268,290;
+ *   huginn_blocks_batch.py:159-161,329,344).
+ */
+int wfd_add_rmsnorm(const void* a, const int32_t* a_rows, int64_t lda, const void* res, int64_t ldr, const void* w1,
+                    const void* w2, void* x_out, const int32_t* out_rows, int64_t ldo, void* h_out, int64_t ldh, int n,
+                    int D, float eps, int dtype, wfd_stream_t stream);
+
+/*
+ * out[i] = table[ids[i]] * scale.
+ * Replaces: wte(ids) * emb_scale (src/decoding/huginn_blocks.py:184-186;
+ *   huginn_blocks_batch.py:215-217).
+ */
+int wfd_embed(const int64_t* ids, const void* table, float scale, void* out, int64_t ldo, int n, int vocab, int D,
+              int dtype, wfd_stream_t stream);
+
+/*
+ * dst[dst_rows ? dst_rows[i] : i, :width] = src[src_rows ? src_rows[i] : i, :width].
+ * Replaces: the per-token torch.stack of hidden/static rows and the s0 table
+ *   lookup (src/decoding/huginn_blocks.py:190,205-209; parcae_blocks.py:137-146).
+ */
+int wfd_copy_rows(const void* src, const int32_t* src_rows, int64_t lds, void* dst, const int32_t* dst_rows,
+                  int64_t ldd, int n, int width, int dtype, wfd_stream_t stream);
+
+/*
+ * out[i] = argmax_j logits[i, j] (first index on ties), logits fp32.
+ * Replaces: greedy_sample's argmax (src/decoding/acceptance.py:40-44) and
+ *   coda_argmax_union's argmax (src/decoding/huginn_blocks_batch.py:345-346).
+ */
+int wfd_argmax(const float* logits, int64_t ld, int64_t* out, int n, int vocab, wfd_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WFD_H_ */

@@ -1,0 +1,44 @@
+"""The C-ABI library loads on a host without a GPU and exports exactly what include/wfd.h declares (CPU)."""
+from __future__ import annotations
+
+import os
+import re
+import subprocess
+
+from wavefront_decoding_amd import _lib
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared() -> set[str]:
+    text = open(os.path.join(REPO, "include", "wfd.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(wfd_[a-z0-9_]+)\s*\(", text))
+
+
+def test_header_and_binding_agree():
+    assert _declared() == set(_lib.SIGNATURES), _declared() ^ set(_lib.SIGNATURES)
+
+
+def test_library_loads_and_exports_every_symbol():
+    lib = _lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT (wfd_[a-z0-9_]+)$", out, flags=re.M))
+    assert exported == _declared(), exported ^ _declared()
+
+
+def test_host_only_entry_points():
+    lib = _lib.load()
+    assert lib.wfd_abi_version() == 1
+    assert lib.wfd_attn_split_keys() == 256
+    assert lib.wfd_linear_k_multiple(_lib.BF16) == 256 and lib.wfd_linear_k_multiple(_lib.F32) == 128
+    # workspace: n*H*splits*(Dh + 2) floats, each array 256-byte aligned
+    assert lib.wfd_attn_workspace_bytes(8, 16, 64, 1024) == 8 * 16 * 4 * 64 * 4 + 8 * 16 * 4 * 2 * 4
+    # argument validation happens before any device work
+    rc = lib.wfd_attn_decode(None, None, None, None, None, None, 1, 16, 3, 64, 1, 0.1, 10, None, 0, None)
+    assert rc == -1 and b"bad shape" in lib.wfd_last_error()
+    rc = lib.wfd_linear(None, None, 100, None, None, 16, 2, 16, 100, 1, 1, 0, 0, None)
+    assert rc == -1
+    assert lib.wfd_attn_decode(None, None, None, None, None, None, 0, 16, 16, 64, 1, 0.1, 10, None, 0, None) == 0

@@ -1,0 +1,243 @@
+"""Kernel-level parity of libwfd.so against the CPU oracle (GPU).
+
+Tolerances (max|gpu - oracle| / max|oracle|): 2e-2 for bf16, 1e-4 for fp32.
+Integer/index work (slot append rows, argmax ids) must be bit-exact, and every
+kernel must be row-invariant (a row's bits do not depend on the batch).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kernels as ok
+from tests.conftest import rel_err
+from wavefront_decoding_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.bfloat16: 2e-2, torch.float32: 1e-4}
+
+
+def _np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def _attn_case(dev, dtype, n, H, Hkv, Dh, lens, S=None, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    S = S or max(lens) + 3
+    n_slots = n + 1
+    K = torch.randn(n_slots * S, Hkv, Dh, generator=g).to(dtype)
+    V = torch.randn(n_slots * S, Hkv, Dh, generator=g).to(dtype)
+    q = torch.randn(n, H, Dh, generator=g).to(dtype)
+    # query i reads slot (i+1) % n_slots -- a different slot per query
+    rb = torch.tensor([((i + 1) % n_slots) * S for i in range(n)], dtype=torch.int64)
+    kl = torch.tensor(lens, dtype=torch.int32)
+    return q, K, V, rb, kl
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("H,Hkv,Dh,lens", [
+    (16, 16, 64, [1017 + i for i in range(8)]),      # wavefront attention op, W=8, L=1024
+    (16, 16, 128, [512 + i for i in range(8)]),      # 2048-d model decode tick
+    (16, 4, 128, [3000, 2999, 1, 256, 257, 255, 64, 65]),  # GQA 16/4 + split/tile edges
+    (4, 4, 64, [1, 2, 63, 64, 65, 129]),             # tiny model heads
+])
+def test_attn_decode_matches_oracle(gpu, dtype, H, Hkv, Dh, lens):
+    n = len(lens)
+    q, K, V, rb, kl = _attn_case(gpu, dtype, n, H, Hkv, Dh, lens)
+    print(f"[attn] dtype={dtype} n={n} H={H} Hkv={Hkv} Dh={Dh} lens={lens}", flush=True)
+    out = ops.attn_decode(q.to(gpu), K.to(gpu), V.to(gpu), rb.to(gpu), kl.to(gpu), kv_len_max=max(lens))
+    torch.cuda.synchronize()
+    ref = ok.attention_rows(_np(q), _np(K), _np(V), rb.numpy(), kl.numpy())
+    err = rel_err(_np(out), ref)
+    assert err <= TOL[dtype], err
+
+
+@pytest.mark.parametrize("L", [4096, 16384])
+def test_attn_decode_long_prefix(gpu, L):
+    lens = [L - 7 + i for i in range(8)]
+    q, K, V, rb, kl = _attn_case(gpu, torch.bfloat16, 8, 16, 16, 64, lens, seed=L)
+    out = ops.attn_decode(q.to(gpu), K.to(gpu), V.to(gpu), rb.to(gpu), kl.to(gpu), kv_len_max=L)
+    ref = ok.attention_rows(_np(q), _np(K), _np(V), rb.numpy(), kl.numpy())
+    assert rel_err(_np(out), ref) <= 2e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_attn_decode_row_invariant(gpu, dtype):
+    """A query's output bits do not depend on the other queries, the batch
+    size, or kv_len_max (the grid bound)."""
+    lens = [700, 33, 1500, 256, 1, 900, 511, 1024]
+    q, K, V, rb, kl = _attn_case(gpu, dtype, 8, 16, 16, 128, lens, seed=7)
+    q, K, V, rb, kl = (t.to(gpu) for t in (q, K, V, rb, kl))
+    full = ops.attn_decode(q, K, V, rb, kl, kv_len_max=1500)
+    for i in range(8):
+        one = ops.attn_decode(q[i:i + 1].contiguous(), K, V, rb[i:i + 1], kl[i:i + 1], kv_len_max=lens[i] + 300)
+        assert torch.equal(one[0], full[i]), i
+
+
+def test_attn_decode_kv_len_device_data(gpu):
+    """Lengths are read from device memory at launch time: changing them in place changes the result."""
+    q, K, V, rb, kl = _attn_case(gpu, torch.bfloat16, 2, 16, 16, 128, [600, 600], S=2048)
+    q, K, V, rb, kl = (t.to(gpu) for t in (q, K, V, rb, kl))
+    a = ops.attn_decode(q, K, V, rb, kl, kv_len_max=2048).clone()
+    kl.fill_(900)
+    b = ops.attn_decode(q, K, V, rb, kl, kv_len_max=2048)
+    ref = ok.attention_rows(_np(q), _np(K), _np(V), rb.cpu().numpy(), [900, 900])
+    assert rel_err(_np(b), ref) <= 2e-2
+    assert (a.float() - b.float()).abs().max().item() > 1e-3
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("n,N,K", [(1, 2048, 2048), (8, 6144, 2048), (17, 64, 5632), (40, 512, 4096),
+                                   (300, 256, 1024), (3, 32000, 256)])
+def test_linear_matches_oracle(gpu, dtype, n, N, K):
+    if K % ops.linear_k_multiple(dtype):
+        pytest.skip("K not a multiple of the kernel granularity")
+    g = torch.Generator().manual_seed(n * 7 + N)
+    x = torch.randn(n, K, generator=g).to(dtype)
+    W = (0.02 * torch.randn(N, K, generator=g)).to(dtype)
+    print(f"[linear] dtype={dtype} n={n} N={N} K={K}", flush=True)
+    y = ops.linear(x.to(gpu), W.to(gpu))
+    ref = ok.linear(_np(x), _np(W))
+    assert rel_err(_np(y), ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_linear_swiglu_fp32_out_and_row_gather(gpu, dtype):
+    g = torch.Generator().manual_seed(11)
+    n, F_, K = 9, 96, 512
+    pool = torch.randn(20, K + 64, generator=g).to(dtype)
+    rows = torch.tensor([3, 17, 0, 5, 5, 12, 19, 1, 8], dtype=torch.int32)
+    W = (0.05 * torch.randn(2 * F_, K, generator=g)).to(dtype)
+    y = ops.linear(pool.to(gpu), W.to(gpu), x_rows=rows.to(gpu), swiglu=True)
+    xs = _np(pool)[rows.numpy(), :K]
+    gu = ok.linear(xs, _np(W))
+    ref = ok.swiglu(gu[:, :F_], gu[:, F_:])
+    assert rel_err(_np(y), ref) <= TOL[dtype]
+    if dtype == torch.bfloat16:
+        y32 = ops.linear(pool.to(gpu), W.to(gpu), x_rows=rows.to(gpu), out_dtype=torch.float32)
+        assert y32.dtype == torch.float32
+        assert rel_err(_np(y32), gu) <= 1e-4 * 10  # fp32 out of bf16 inputs: only accumulation-order error
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_linear_row_invariant(gpu, dtype):
+    """Row m of y is bit-identical for every batch size and position in the batch."""
+    g = torch.Generator().manual_seed(5)
+    K, N = 2048, 384
+    X = torch.randn(300, K, generator=g).to(dtype).to(gpu)
+    W = (0.02 * torch.randn(N, K, generator=g)).to(dtype).to(gpu)
+    full = ops.linear(X, W)
+    for n in (1, 5, 16, 17, 33, 64, 65, 300):
+        part = ops.linear(X[:n].contiguous(), W)
+        assert torch.equal(part, full[:n]), n
+    rows = torch.tensor([299, 0, 150], dtype=torch.int32, device=gpu)
+    gathered = ops.linear(X, W, x_rows=rows)
+    assert torch.equal(gathered, full[rows.long()])
+    sw = torch.cat([W, W.flip(0)])
+    a = ops.linear(X[:1].contiguous(), sw, swiglu=True)
+    b = ops.linear(X, sw, swiglu=True)
+    assert torch.equal(a[0], b[0])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_add_rmsnorm(gpu, dtype):
+    g = torch.Generator().manual_seed(3)
+    n, D = 6, 2048
+    a = torch.randn(n, D, generator=g).to(dtype)
+    r = torch.randn(n, D, generator=g).to(dtype)
+    w1 = (1 + 0.1 * torch.randn(D, generator=g)).to(dtype)
+    w2 = (1 + 0.1 * torch.randn(D, generator=g)).to(dtype)
+    x, h = ops.add_rmsnorm(a.to(gpu), w1.to(gpu), 1e-6, res=r.to(gpu), w2=w2.to(gpu))
+    xr = ok.rmsnorm(_np(a) + _np(r), _np(w1), 1e-6)
+    assert rel_err(_np(x), xr) <= TOL[dtype]
+    hr = ok.rmsnorm(_np(x), _np(w2), 1e-6)  # second norm reads the stored x
+    assert rel_err(_np(h), hr) <= TOL[dtype]
+    # fused second norm == a separate rmsnorm call on x_out, bit for bit
+    h2 = ops.rmsnorm(x, w2.to(gpu), 1e-6)
+    assert torch.equal(h, h2)
+    # row gather / scatter variants
+    pool = torch.zeros(10, D, dtype=dtype, device=gpu)
+    rows = torch.tensor([7, 2, 9, 0, 4, 5], dtype=torch.int32, device=gpu)
+    ops.add_rmsnorm(a.to(gpu), w1.to(gpu), 1e-6, res=r.to(gpu), x_out=pool, out_rows=rows)
+    assert torch.equal(pool[rows.long()], x)
+    y = ops.rmsnorm(pool, w1.to(gpu), 1e-6, a_rows=rows)
+    assert torch.equal(y, ops.rmsnorm(x, w1.to(gpu), 1e-6))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("H,Hkv,Dh", [(16, 16, 128), (16, 4, 128), (4, 4, 64)])
+def test_qkv_rope_append(gpu, dtype, H, Hkv, Dh):
+    g = torch.Generator().manual_seed(H + Hkv)
+    n, S = 5, 64
+    qkv = torch.randn(n, (H + 2 * Hkv) * Dh, generator=g).to(dtype)
+    pos = torch.tensor([0, 63, 7, 31, 1], dtype=torch.int32)
+    flat = torch.tensor([5, 100, 64, 0, 127], dtype=torch.int64)
+    cos, sin = ok.rope_tables(S, Dh)
+    kc = torch.zeros(128, Hkv, Dh, dtype=dtype, device=gpu)
+    vc = torch.zeros(128, Hkv, Dh, dtype=dtype, device=gpu)
+    q = ops.qkv_rope_append(qkv.to(gpu), pos.to(gpu), torch.from_numpy(cos).to(gpu), torch.from_numpy(sin).to(gpu),
+                            flat.to(gpu), kc, vc, H, Hkv, Dh)
+    x = _np(qkv)
+    for i in range(n):
+        p = int(pos[i])
+        qi = x[i, :H * Dh].reshape(H, Dh)
+        ki = x[i, H * Dh:(H + Hkv) * Dh].reshape(Hkv, Dh)
+        vi = x[i, (H + Hkv) * Dh:].reshape(Hkv, Dh)
+        assert rel_err(_np(q[i]), ok.rope(qi, p, cos, sin)) <= TOL[dtype]
+        assert rel_err(_np(kc[int(flat[i])]), ok.rope(ki, p, cos, sin)) <= TOL[dtype]
+        assert np.array_equal(_np(vc[int(flat[i])]), vi)  # V is copied bit for bit
+    written = set(flat.tolist())
+    untouched = [r for r in range(128) if r not in written]
+    assert kc[untouched].abs().sum().item() == 0 and vc[untouched].abs().sum().item() == 0
+
+
+def test_kv_append_exact_rows(gpu):
+    """Writes land at exactly the requested flat rows, bit for bit (the analogue
+    of experiments/exp5_graph/verify_graph.py gate 1c)."""
+    kc = torch.zeros(2048, 16, 128, dtype=torch.bfloat16, device=gpu)
+    vc = torch.zeros_like(kc)
+    k = torch.randn(3, 16, 128, device=gpu).to(torch.bfloat16)
+    v = torch.randn(3, 16, 128, device=gpu).to(torch.bfloat16)
+    rows = torch.tensor([700, 701, 702], dtype=torch.int64, device=gpu)
+    ops.kv_append(k, v, kc, vc, rows)
+    nz = (kc.float().abs().sum(dim=(1, 2)) > 0).nonzero().flatten().tolist()
+    assert nz == [700, 701, 702]
+    assert torch.equal(kc[700:703], k) and torch.equal(vc[700:703], v)
+
+
+def test_embed_copy_argmax(gpu):
+    g = torch.Generator().manual_seed(9)
+    table = torch.randn(100, 256, generator=g).to(torch.bfloat16).to(gpu)
+    ids = torch.tensor([3, 99, 0, 3], dtype=torch.int64, device=gpu)
+    e = ops.embed(ids, table, 1.0)
+    assert torch.equal(e, table[ids])
+    e2 = ops.embed(ids, table, 2.0)
+    assert torch.equal(e2, (table[ids].float() * 2).to(torch.bfloat16))
+    dst = torch.zeros(8, 300, dtype=torch.bfloat16, device=gpu)
+    ops.copy_rows(table, dst, n=2, width=256, src_rows=torch.tensor([5, 6], dtype=torch.int32, device=gpu),
+                  dst_rows=torch.tensor([7, 1], dtype=torch.int32, device=gpu))
+    assert torch.equal(dst[7, :256], table[5]) and torch.equal(dst[1, :256], table[6])
+    logits = torch.randn(5, 32000, generator=g).to(gpu)
+    logits[2, 17] = 100.0
+    logits[2, 30000] = 100.0  # tie: first index wins, as torch.argmax
+    am = ops.argmax(logits)
+    assert am.tolist() == logits.argmax(dim=-1).tolist()
+    assert am[2].item() == 17
+
+
+def test_bad_arguments_raise(gpu):
+    from wavefront_decoding_amd import _lib
+
+    q = torch.zeros(1, 16, 96, dtype=torch.bfloat16, device=gpu)  # unsupported head_dim
+    kc = torch.zeros(8, 16, 96, dtype=torch.bfloat16, device=gpu)
+    rb = torch.zeros(1, dtype=torch.int64, device=gpu)
+    kl = torch.ones(1, dtype=torch.int32, device=gpu)
+    with pytest.raises(_lib.WfdError, match="unsupported"):
+        ops.attn_decode(q, kc, kc, rb, kl, kv_len_max=8)
+    with pytest.raises(_lib.WfdError):
+        ops.linear(torch.zeros(2, 100, device=gpu), torch.zeros(16, 100, device=gpu))
+    assert math.isfinite(1.0)

@@ -1,0 +1,311 @@
+// Wavefront decode attention over per-depth KV slot caches, read in place.
+//
+// Replaces the reference's per-token R attention: n gathers of every slot
+// prefix + torch.cat into a packed K/V copy + one FA2 varlen call
+// (src/decoding/parcae_blocks.py:458-470 -> fa4_attention.py:301-317,348-366;
+// batch: huginn_blocks_batch.py:265-285 + fa4_attention.py:320-342; graph:
+// graph_blocks.py:40-43,186-194), and the coda per-query cutoff
+// (fa4_attention.py:240-291), which is the same operation with
+// kv_len = query position + 1.
+//
+// For query i and head h (kv head g = h / G):
+//   o[i,h,:] = softmax_t( q[i,h,:] . K[row_base[i] + t, g, :] * scale ) @ V[row_base[i] + t, g, :],
+//   t = 0 .. kv_len[i]-1, fp32 softmax and accumulation.
+//
+// Layout: K/V are flat (rows, Hkv, Dh) buffers; row_base[i] is the flat row of
+// position 0 of query i's slot (for the batched cache (slot*B + b)*S,
+// src/decoding/batch_kv_cache.py:64-65), so key position == buffer row offset.
+//
+// Work split (a function of kv_len only, never of n or of other queries, so
+// results are row-invariant): keys are cut into 256-key splits; a 256-thread
+// workgroup owns one (split, kv head, query) and each of its 4 waves one
+// 64-key tile. QK^T runs on MFMA (q rows = the G query heads of the kv head,
+// padded to 16; K tile as the B operand loaded straight from HBM in 16-byte
+// fragments); P.V runs on the VALU in fp32 with one 16-byte V fragment per
+// lane per key, so K and V are each read exactly once. Waves merge through
+// LDS in fixed order; a second kernel merges splits in fixed split order.
+#include "wfd_common.h"
+
+namespace wfd {
+
+constexpr int kAttnTile = 64;
+constexpr int kAttnWaves = 4;
+constexpr int kAttnSplit = kAttnTile * kAttnWaves;  // 256 keys per workgroup
+
+template <typename T, int DH, int G>
+__global__ __launch_bounds__(256) void attn_split_kernel(const T* __restrict__ q, const T* __restrict__ kc,
+                                                         const T* __restrict__ vc,
+                                                         const int64_t* __restrict__ row_base,
+                                                         const int32_t* __restrict__ kv_len,
+                                                         float* __restrict__ part_o, float* __restrict__ part_ml,
+                                                         int H, int Hkv, int max_splits, float scale_log2) {
+  constexpr int V = Elem<T>::kVec;
+  constexpr int KSTEP = 4 * V;
+  constexpr int NDS = DH / KSTEP;  // MFMA k-steps per 16-key block
+  constexpr int LPR = DH / V;      // lanes covering one V row
+  constexpr int RG = 64 / LPR;     // V row groups per wave
+  constexpr int KPL = kAttnTile / RG;
+  static_assert(DH % KSTEP == 0 && 64 % LPR == 0, "unsupported head_dim");
+
+  __shared__ float p_lds[kAttnWaves][G][kAttnTile];
+  __shared__ float o_lds[kAttnWaves][G][DH];
+  __shared__ float m_lds[kAttnWaves][G];
+  __shared__ float l_lds[kAttnWaves][G];
+
+  const int split = blockIdx.x;
+  const int g = blockIdx.y;
+  const int i = blockIdx.z;
+  const int len = kv_len[i];
+  if (split * kAttnSplit >= len) return;  // uniform for the whole workgroup
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const int t0 = split * kAttnSplit + wave * kAttnTile;
+  const int64_t rs = (int64_t)Hkv * DH;
+  const int64_t base = row_base[i];
+  const T* kb = kc + base * rs + (int64_t)g * DH;
+  const T* vb = vc + base * rs + (int64_t)g * DH;
+
+  // Issue every load of the tile first: K (MFMA B fragments), V, Q.
+  u32x4 kf[4][NDS];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int key = min(t0 + 16 * j + col, len - 1);
+    const T* p = kb + (int64_t)key * rs + grp * V;
+#pragma unroll
+    for (int s = 0; s < NDS; ++s) kf[j][s] = ld16(p + s * KSTEP);
+  }
+  const int vg = lane / LPR;
+  const int dseg = lane % LPR;
+  u32x4 vf[KPL];
+#pragma unroll
+  for (int k = 0; k < KPL; ++k) {
+    const int key = min(t0 + RG * k + vg, len - 1);
+    vf[k] = ld16(vb + (int64_t)key * rs + dseg * V);
+  }
+  u32x4 qf[NDS];
+  {
+    const T* qp = q + ((int64_t)i * H + (int64_t)g * G + (col < G ? col : 0)) * DH + grp * V;
+#pragma unroll
+    for (int s = 0; s < NDS; ++s) qf[s] = col < G ? ld16(qp + s * KSTEP) : zero16();
+  }
+
+  // Scores: lane (grp==0, col) holds S[row r][key 16j+col] in acc[j][r].
+  f32x4 acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NDS; ++s) acc[j] = mfma_step<T>(qf[s], kf[j][s], acc[j]);
+  }
+
+  float mx[G], ls[G];
+#pragma unroll
+  for (int r = 0; r < G; ++r) {
+    mx[r] = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool valid = (t0 + 16 * j + col) < len;
+      const float sv = valid ? acc[j][r] * scale_log2 : -INFINITY;
+      acc[j][r] = sv;
+      mx[r] = fmaxf(mx[r], sv);
+    }
+#pragma unroll
+    for (int m = 8; m >= 1; m >>= 1) mx[r] = fmaxf(mx[r], __shfl_xor(mx[r], m, 64));
+    ls[r] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float p = (acc[j][r] == -INFINITY) ? 0.f : exp2f(acc[j][r] - mx[r]);
+      acc[j][r] = p;
+      ls[r] += p;
+    }
+#pragma unroll
+    for (int m = 8; m >= 1; m >>= 1) ls[r] += __shfl_xor(ls[r], m, 64);
+  }
+  if (grp == 0) {
+#pragma unroll
+    for (int r = 0; r < G; ++r)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int kt = 16 * j + col;  // key within the tile
+        p_lds[wave][r][(kt % RG) * KPL + kt / RG] = acc[j][r];
+      }
+  }
+  __syncthreads();
+
+  // P.V on the VALU: lane owns V columns [dseg*V, dseg*V+V) of keys RG*k + vg.
+  float o[G][V];
+#pragma unroll
+  for (int r = 0; r < G; ++r)
+#pragma unroll
+    for (int e = 0; e < V; ++e) o[r][e] = 0.f;
+#pragma unroll
+  for (int k = 0; k < KPL; ++k) {
+    float v[V];
+    Elem<T>::unpack(vf[k], v);
+#pragma unroll
+    for (int r = 0; r < G; ++r) {
+      const float p = p_lds[wave][r][vg * KPL + k];
+#pragma unroll
+      for (int e = 0; e < V; ++e) o[r][e] = fmaf(p, v[e], o[r][e]);
+    }
+  }
+#pragma unroll
+  for (int m = LPR; m < 64; m <<= 1)
+#pragma unroll
+    for (int r = 0; r < G; ++r)
+#pragma unroll
+      for (int e = 0; e < V; ++e) o[r][e] += __shfl_xor(o[r][e], m, 64);
+  if (vg == 0) {
+#pragma unroll
+    for (int r = 0; r < G; ++r)
+#pragma unroll
+      for (int e = 0; e < V; ++e) o_lds[wave][r][dseg * V + e] = o[r][e];
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < G; ++r) {
+      m_lds[wave][r] = mx[r];
+      l_lds[wave][r] = ls[r];
+    }
+  }
+  __syncthreads();
+
+  // Merge the 4 waves in fixed order; emit this split's unnormalised partial.
+  for (int idx = threadIdx.x; idx < G * DH; idx += 256) {
+    const int r = idx / DH;
+    const int d = idx - r * DH;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, m_lds[w][r]);
+    float O = 0.f, L = 0.f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) {
+      const float mw = m_lds[w][r];
+      const float f = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
+      O = fmaf(o_lds[w][r][d], f, O);
+      L = fmaf(l_lds[w][r], f, L);
+    }
+    const int64_t pidx = ((int64_t)i * H + (int64_t)g * G + r) * max_splits + split;
+    part_o[pidx * DH + d] = O;
+    if (d == 0) {
+      part_ml[pidx * 2] = M;
+      part_ml[pidx * 2 + 1] = L;
+    }
+  }
+}
+
+template <typename T, int DH>
+__global__ __launch_bounds__(DH) void attn_combine_kernel(const float* __restrict__ part_o,
+                                                          const float* __restrict__ part_ml,
+                                                          const int32_t* __restrict__ kv_len, T* __restrict__ out,
+                                                          int H, int max_splits) {
+  const int h = blockIdx.x;
+  const int i = blockIdx.y;
+  const int d = threadIdx.x;
+  const int len = kv_len[i];
+  int ns = len > 0 ? (len + kAttnSplit - 1) / kAttnSplit : 0;
+  ns = min(ns, max_splits);
+  const int64_t base = ((int64_t)i * H + h) * max_splits;
+  float M = -INFINITY;
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, part_ml[(base + s) * 2]);
+  float O = 0.f, L = 0.f;
+  for (int s = 0; s < ns; ++s) {
+    const float ms = part_ml[(base + s) * 2];
+    const float f = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
+    L = fmaf(part_ml[(base + s) * 2 + 1], f, L);
+    O = fmaf(part_o[(base + s) * DH + d], f, O);
+  }
+  const float res = L > 0.f ? O / L : 0.f;
+  Elem<T>::store(out + ((int64_t)i * H + h) * DH + d, res);
+}
+
+static int max_splits_for(int kv_len_max) { return kv_len_max <= 0 ? 1 : (kv_len_max + kAttnSplit - 1) / kAttnSplit; }
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+static size_t attn_ws_bytes(int n, int H, int Dh, int kv_len_max) {
+  const size_t ms = (size_t)max_splits_for(kv_len_max);
+  return align256((size_t)n * H * ms * Dh * sizeof(float)) + align256((size_t)n * H * ms * 2 * sizeof(float));
+}
+
+template <typename T, int DH, int G>
+static void launch_attn(const void* q, const void* kc, const void* vc, const int64_t* rb, const int32_t* kl, void* out,
+                        int n, int H, int Hkv, int ms, float scale, float* po, float* pml, hipStream_t st) {
+  const float scale_log2 = scale * 1.4426950408889634f;
+  hipLaunchKernelGGL((attn_split_kernel<T, DH, G>), dim3(ms, Hkv, n), dim3(256), 0, st, (const T*)q, (const T*)kc,
+                     (const T*)vc, rb, kl, po, pml, H, Hkv, ms, scale_log2);
+  hipLaunchKernelGGL((attn_combine_kernel<T, DH>), dim3(H, n), dim3(DH), 0, st, po, pml, kl, (T*)out, H, ms);
+}
+
+template <typename T>
+static int dispatch_attn(int Dh, int G, const void* q, const void* kc, const void* vc, const int64_t* rb,
+                         const int32_t* kl, void* out, int n, int H, int Hkv, int ms, float scale, float* po,
+                         float* pml, hipStream_t st) {
+#define WFD_ATTN_CASE(DHV, GV)                                                        \
+  if (Dh == DHV && G == GV) {                                                         \
+    launch_attn<T, DHV, GV>(q, kc, vc, rb, kl, out, n, H, Hkv, ms, scale, po, pml, st); \
+    return kOk;                                                                       \
+  }
+  WFD_ATTN_CASE(64, 1)
+  WFD_ATTN_CASE(64, 2)
+  WFD_ATTN_CASE(64, 4)
+  WFD_ATTN_CASE(128, 1)
+  WFD_ATTN_CASE(128, 2)
+  WFD_ATTN_CASE(128, 4)
+#undef WFD_ATTN_CASE
+  return kUnsupported;
+}
+
+}  // namespace wfd
+
+extern "C" {
+
+size_t wfd_attn_workspace_bytes(int n, int H, int Dh, int kv_len_max) {
+  if (n < 0 || H <= 0 || Dh <= 0) return 0;
+  return wfd::attn_ws_bytes(n, H, Dh, kv_len_max);
+}
+
+int wfd_attn_split_keys(void) { return wfd::kAttnSplit; }
+
+int wfd_attn_decode(const void* q, const void* k_cache, const void* v_cache, const int64_t* kv_row_base,
+                    const int32_t* kv_len, void* out, int n, int H, int Hkv, int Dh, int dtype, float scale,
+                    int kv_len_max, void* workspace, size_t ws_bytes, hipStream_t stream) {
+  using namespace wfd;
+  if (n < 0 || H <= 0 || Hkv <= 0 || H % Hkv != 0 || kv_len_max < 1) {
+    set_error("wfd_attn_decode: bad shape n=%d H=%d Hkv=%d kv_len_max=%d", n, H, Hkv, kv_len_max);
+    return kBadArg;
+  }
+  if (n == 0) return kOk;
+  if (!q || !k_cache || !v_cache || !kv_row_base || !kv_len || !out || !workspace) {
+    set_error("wfd_attn_decode: null pointer argument");
+    return kBadArg;
+  }
+  const int G = H / Hkv;
+  const int ms = max_splits_for(kv_len_max);
+  const size_t need = attn_ws_bytes(n, H, Dh, kv_len_max);
+  if (ws_bytes < need) {
+    set_error("wfd_attn_decode: workspace %zu bytes < required %zu", ws_bytes, need);
+    return kWorkspace;
+  }
+  float* po = (float*)workspace;
+  float* pml = (float*)((char*)workspace + align256((size_t)n * H * ms * Dh * sizeof(float)));
+  int rc;
+  if (dtype == kBF16)
+    rc = dispatch_attn<bf16_t>(Dh, G, q, k_cache, v_cache, kv_row_base, kv_len, out, n, H, Hkv, ms, scale, po, pml,
+                               stream);
+  else if (dtype == kF32)
+    rc = dispatch_attn<float>(Dh, G, q, k_cache, v_cache, kv_row_base, kv_len, out, n, H, Hkv, ms, scale, po, pml,
+                              stream);
+  else
+    rc = kUnsupported;
+  if (rc != kOk) {
+    set_error("wfd_attn_decode: unsupported dtype=%d Dh=%d G=%d (supported: Dh 64/128, G 1/2/4)", dtype, Dh, G);
+    return rc;
+  }
+  return launch_status("wfd_attn_decode");
+}
+
+}  // extern "C"

@@ -1,0 +1,362 @@
+// Row-wise fused pieces of the recurrent-block forward and the slot-cache
+// append, plus the small gathers the decode tick needs.
+//
+//  * add_rmsnorm: x' = rmsnorm(a + res) * w1, optionally h = rmsnorm(x') * w2.
+//    The sandwich block's `norm_2(att + x)` followed by `norm_3(x)`, and
+//    `norm_4(mlp + x)` followed by the next block's `norm_1`
+//    (src/decoding/huginn_blocks.py:100-102, huginn_blocks_batch.py:159-161),
+//    in one pass; with res == nullptr it is a plain RMSNorm (ln_f, norm_1).
+//  * qkv_rope_append: split the fused QKV row, rotate q and k by the
+//    position's RoPE angles (interleaved pairs), write q out and append k, v
+//    to the slot cache at flat_row[i] (huginn_blocks.py:77-87 + the cache
+//    write of kv_cache.py:97-104 / batch_kv_cache.py:61-73 /
+//    graph_blocks.py:172-176, fused).
+//  * kv_append: the bare slot-cache append (same indexing, no rotation).
+//  * embed, copy_rows, argmax: token embedding gather (x emb_scale), row
+//    gather/scatter (initial loop state, wave-state pool), greedy argmax
+//    (acceptance.py:40-44) on device.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "wfd_common.h"
+
+namespace wfd {
+
+static thread_local char g_err[512] = {0};
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+int launch_status(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return kLaunch;
+  }
+  return kOk;
+}
+
+constexpr int kRowThreads = 256;
+constexpr int kMaxRowElems = 16;  // elements per thread -> D <= 4096
+
+__device__ __forceinline__ float block_sum_256(float v, float* scratch) {
+  v = wave_sum(v);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __syncthreads();
+  if (lane == 0) scratch[wave] = v;
+  __syncthreads();
+  const float s = ((scratch[0] + scratch[1]) + scratch[2]) + scratch[3];
+  return s;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kRowThreads) void add_rmsnorm_kernel(
+    const T* __restrict__ a, const int32_t* __restrict__ a_rows, int64_t lda, const T* __restrict__ res,
+    int64_t ldr, const T* __restrict__ w1, const T* __restrict__ w2, T* __restrict__ x_out,
+    const int32_t* __restrict__ out_rows, int64_t ldo, T* __restrict__ h_out, int64_t ldh, int D, float eps) {
+  __shared__ float scratch[4];
+  const int i = blockIdx.x;
+  const int64_t ar = a_rows ? a_rows[i] : i;
+  const int64_t orow = out_rows ? out_rows[i] : i;
+  float v[kMaxRowElems];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < kMaxRowElems; ++k) {
+    const int e = threadIdx.x + k * kRowThreads;
+    float s = 0.f;
+    if (e < D) {
+      s = Elem<T>::load(a + ar * lda + e);
+      if (res) s += Elem<T>::load(res + (int64_t)i * ldr + e);
+    }
+    v[k] = s;
+    ss = fmaf(s, s, ss);
+  }
+  float tot = block_sum_256(ss, scratch);
+  float inv = 1.0f / sqrtf(tot / (float)D + eps);
+  float ss2 = 0.f;
+#pragma unroll
+  for (int k = 0; k < kMaxRowElems; ++k) {
+    const int e = threadIdx.x + k * kRowThreads;
+    if (e < D) {
+      const float yv = v[k] * inv * Elem<T>::load(w1 + e);
+      T* dst = x_out + orow * ldo + e;
+      Elem<T>::store(dst, yv);
+      // Continue from the stored (rounded) value so the fused second norm
+      // equals a separate rmsnorm() call on x_out.
+      v[k] = Elem<T>::load(dst);
+      ss2 = fmaf(v[k], v[k], ss2);
+    }
+  }
+  if (w2 == nullptr) return;  // uniform
+  tot = block_sum_256(ss2, scratch);
+  inv = 1.0f / sqrtf(tot / (float)D + eps);
+#pragma unroll
+  for (int k = 0; k < kMaxRowElems; ++k) {
+    const int e = threadIdx.x + k * kRowThreads;
+    if (e < D) Elem<T>::store(h_out + (int64_t)i * ldh + e, v[k] * inv * Elem<T>::load(w2 + e));
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
+    const T* __restrict__ qkv, int64_t ldq, const int32_t* __restrict__ pos, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, int tab_rows, const int64_t* __restrict__ flat_row, T* __restrict__ q_out,
+    T* __restrict__ kc, T* __restrict__ vc, int H, int Hkv, int Dh) {
+  const int i = blockIdx.x;
+  const int half = Dh >> 1;
+  int p = pos[i];
+  p = p < 0 ? 0 : (p >= tab_rows ? tab_rows - 1 : p);
+  const int64_t fr = flat_row[i];
+  const T* src = qkv + (int64_t)i * ldq;
+  const int npairs = (H + Hkv) * half;
+  for (int idx = threadIdx.x; idx < npairs; idx += kRowThreads) {
+    const int head = idx / half;
+    const int j = idx - head * half;
+    const float x0 = Elem<T>::load(src + head * Dh + 2 * j);
+    const float x1 = Elem<T>::load(src + head * Dh + 2 * j + 1);
+    const float c = cos_t[(int64_t)p * half + j];
+    const float s = sin_t[(int64_t)p * half + j];
+    const float y0 = x0 * c - x1 * s;
+    const float y1 = x0 * s + x1 * c;
+    T* dst = head < H ? q_out + ((int64_t)i * H + head) * Dh + 2 * j
+                      : kc + fr * (int64_t)Hkv * Dh + (int64_t)(head - H) * Dh + 2 * j;
+    Elem<T>::store(dst, y0);
+    Elem<T>::store(dst + 1, y1);
+  }
+  const int nv = Hkv * Dh;
+  const T* vsrc = src + (int64_t)(H + Hkv) * Dh;
+  T* vdst = vc + fr * (int64_t)nv;
+  for (int e = threadIdx.x; e < nv; e += kRowThreads) vdst[e] = vsrc[e];
+}
+
+template <typename T>
+__global__ __launch_bounds__(kRowThreads) void kv_append_kernel(const T* __restrict__ k, const T* __restrict__ v,
+                                                                T* __restrict__ kc, T* __restrict__ vc,
+                                                                const int64_t* __restrict__ flat_row, int row_elems) {
+  const int i = blockIdx.x;
+  const int64_t fr = flat_row[i];
+  for (int e = threadIdx.x; e < row_elems; e += kRowThreads) {
+    kc[fr * row_elems + e] = k[(int64_t)i * row_elems + e];
+    vc[fr * row_elems + e] = v[(int64_t)i * row_elems + e];
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kRowThreads) void embed_kernel(const int64_t* __restrict__ ids, const T* __restrict__ table,
+                                                            float scale, T* __restrict__ out, int64_t ldo, int Vocab,
+                                                            int D) {
+  const int i = blockIdx.x;
+  int64_t id = ids[i];
+  id = id < 0 ? 0 : (id >= Vocab ? Vocab - 1 : id);
+  for (int e = threadIdx.x; e < D; e += kRowThreads) {
+    float x = Elem<T>::load(table + id * D + e);
+    if (scale != 1.0f) x *= scale;
+    Elem<T>::store(out + (int64_t)i * ldo + e, x);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kRowThreads) void copy_rows_kernel(const T* __restrict__ src,
+                                                                const int32_t* __restrict__ src_rows, int64_t lds,
+                                                                T* __restrict__ dst, const int32_t* __restrict__ dst_rows,
+                                                                int64_t ldd, int width) {
+  const int i = blockIdx.x;
+  const int64_t sr = src_rows ? src_rows[i] : i;
+  const int64_t dr = dst_rows ? dst_rows[i] : i;
+  for (int e = threadIdx.x; e < width; e += kRowThreads) dst[dr * ldd + e] = src[sr * lds + e];
+}
+
+__global__ __launch_bounds__(kRowThreads) void argmax_kernel(const float* __restrict__ logits, int64_t ld,
+                                                             int64_t* __restrict__ out, int Vocab) {
+  __shared__ float sv[kRowThreads];
+  __shared__ int si[kRowThreads];
+  const int i = blockIdx.x;
+  const float* row = logits + (int64_t)i * ld;
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int e = threadIdx.x; e < Vocab; e += kRowThreads) {
+    const float x = row[e];
+    if (x > best || bi == 0x7fffffff) {  // strictly greater: first index wins ties
+      best = x;
+      bi = e;
+    }
+  }
+  sv[threadIdx.x] = best;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int stride = kRowThreads / 2; stride >= 1; stride >>= 1) {
+    if (threadIdx.x < stride) {
+      const float ov = sv[threadIdx.x + stride];
+      const int oi = si[threadIdx.x + stride];
+      const float mv = sv[threadIdx.x];
+      const int mi = si[threadIdx.x];
+      if (ov > mv || (ov == mv && oi < mi)) {
+        sv[threadIdx.x] = ov;
+        si[threadIdx.x] = oi;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[i] = (int64_t)si[0];
+}
+
+}  // namespace wfd
+
+extern "C" {
+
+const char* wfd_last_error(void) { return wfd::g_err; }
+
+int wfd_abi_version(void) { return 1; }
+
+int wfd_add_rmsnorm(const void* a, const int32_t* a_rows, int64_t lda, const void* res, int64_t ldr, const void* w1,
+                    const void* w2, void* x_out, const int32_t* out_rows, int64_t ldo, void* h_out, int64_t ldh, int n,
+                    int D, float eps, int dtype, hipStream_t stream) {
+  using namespace wfd;
+  if (n < 0 || D <= 0 || D > kRowThreads * kMaxRowElems) {
+    set_error("wfd_add_rmsnorm: bad shape n=%d D=%d (D <= %d)", n, D, kRowThreads * kMaxRowElems);
+    return kBadArg;
+  }
+  if (n == 0) return kOk;
+  if (!a || !w1 || !x_out || (w2 && !h_out)) {
+    set_error("wfd_add_rmsnorm: null pointer argument");
+    return kBadArg;
+  }
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(add_rmsnorm_kernel<bf16_t>, dim3(n), dim3(kRowThreads), 0, stream, (const bf16_t*)a, a_rows,
+                       lda, (const bf16_t*)res, ldr, (const bf16_t*)w1, (const bf16_t*)w2, (bf16_t*)x_out, out_rows,
+                       ldo, (bf16_t*)h_out, ldh, D, eps);
+  else if (dtype == kF32)
+    hipLaunchKernelGGL(add_rmsnorm_kernel<float>, dim3(n), dim3(kRowThreads), 0, stream, (const float*)a, a_rows, lda,
+                       (const float*)res, ldr, (const float*)w1, (const float*)w2, (float*)x_out, out_rows, ldo,
+                       (float*)h_out, ldh, D, eps);
+  else {
+    set_error("wfd_add_rmsnorm: unsupported dtype %d", dtype);
+    return kUnsupported;
+  }
+  return launch_status("wfd_add_rmsnorm");
+}
+
+int wfd_qkv_rope_append(const void* qkv, int64_t ldq, const int32_t* pos, const float* rope_cos,
+                        const float* rope_sin, int rope_rows, const int64_t* flat_row, void* q_out, void* k_cache,
+                        void* v_cache, int n, int H, int Hkv, int Dh, int dtype, hipStream_t stream) {
+  using namespace wfd;
+  if (n < 0 || H <= 0 || Hkv <= 0 || Dh <= 0 || (Dh & 1) || rope_rows <= 0 || ldq < (int64_t)(H + 2 * Hkv) * Dh) {
+    set_error("wfd_qkv_rope_append: bad shape n=%d H=%d Hkv=%d Dh=%d rope_rows=%d", n, H, Hkv, Dh, rope_rows);
+    return kBadArg;
+  }
+  if (n == 0) return kOk;
+  if (!qkv || !pos || !rope_cos || !rope_sin || !flat_row || !q_out || !k_cache || !v_cache) {
+    set_error("wfd_qkv_rope_append: null pointer argument");
+    return kBadArg;
+  }
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(qkv_rope_append_kernel<bf16_t>, dim3(n), dim3(kRowThreads), 0, stream, (const bf16_t*)qkv, ldq,
+                       pos, rope_cos, rope_sin, rope_rows, flat_row, (bf16_t*)q_out, (bf16_t*)k_cache,
+                       (bf16_t*)v_cache, H, Hkv, Dh);
+  else if (dtype == kF32)
+    hipLaunchKernelGGL(qkv_rope_append_kernel<float>, dim3(n), dim3(kRowThreads), 0, stream, (const float*)qkv, ldq,
+                       pos, rope_cos, rope_sin, rope_rows, flat_row, (float*)q_out, (float*)k_cache, (float*)v_cache,
+                       H, Hkv, Dh);
+  else {
+    set_error("wfd_qkv_rope_append: unsupported dtype %d", dtype);
+    return kUnsupported;
+  }
+  return launch_status("wfd_qkv_rope_append");
+}
+
+int wfd_kv_append(const void* k, const void* v, void* k_cache, void* v_cache, const int64_t* flat_row, int n,
+                  int row_elems, int dtype, hipStream_t stream) {
+  using namespace wfd;
+  if (n < 0 || row_elems <= 0) {
+    set_error("wfd_kv_append: bad shape n=%d row_elems=%d", n, row_elems);
+    return kBadArg;
+  }
+  if (n == 0) return kOk;
+  if (!k || !v || !k_cache || !v_cache || !flat_row) {
+    set_error("wfd_kv_append: null pointer argument");
+    return kBadArg;
+  }
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(kv_append_kernel<bf16_t>, dim3(n), dim3(kRowThreads), 0, stream, (const bf16_t*)k,
+                       (const bf16_t*)v, (bf16_t*)k_cache, (bf16_t*)v_cache, flat_row, row_elems);
+  else if (dtype == kF32)
+    hipLaunchKernelGGL(kv_append_kernel<float>, dim3(n), dim3(kRowThreads), 0, stream, (const float*)k,
+                       (const float*)v, (float*)k_cache, (float*)v_cache, flat_row, row_elems);
+  else {
+    set_error("wfd_kv_append: unsupported dtype %d", dtype);
+    return kUnsupported;
+  }
+  return launch_status("wfd_kv_append");
+}
+
+int wfd_embed(const int64_t* ids, const void* table, float scale, void* out, int64_t ldo, int n, int vocab, int D,
+              int dtype, hipStream_t stream) {
+  using namespace wfd;
+  if (n < 0 || vocab <= 0 || D <= 0 || ldo < D) {
+    set_error("wfd_embed: bad shape n=%d vocab=%d D=%d", n, vocab, D);
+    return kBadArg;
+  }
+  if (n == 0) return kOk;
+  if (!ids || !table || !out) {
+    set_error("wfd_embed: null pointer argument");
+    return kBadArg;
+  }
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(embed_kernel<bf16_t>, dim3(n), dim3(kRowThreads), 0, stream, ids, (const bf16_t*)table, scale,
+                       (bf16_t*)out, ldo, vocab, D);
+  else if (dtype == kF32)
+    hipLaunchKernelGGL(embed_kernel<float>, dim3(n), dim3(kRowThreads), 0, stream, ids, (const float*)table, scale,
+                       (float*)out, ldo, vocab, D);
+  else {
+    set_error("wfd_embed: unsupported dtype %d", dtype);
+    return kUnsupported;
+  }
+  return launch_status("wfd_embed");
+}
+
+int wfd_copy_rows(const void* src, const int32_t* src_rows, int64_t lds, void* dst, const int32_t* dst_rows,
+                  int64_t ldd, int n, int width, int dtype, hipStream_t stream) {
+  using namespace wfd;
+  if (n < 0 || width <= 0 || lds < width || ldd < width) {
+    set_error("wfd_copy_rows: bad shape n=%d width=%d", n, width);
+    return kBadArg;
+  }
+  if (n == 0) return kOk;
+  if (!src || !dst) {
+    set_error("wfd_copy_rows: null pointer argument");
+    return kBadArg;
+  }
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(copy_rows_kernel<uint16_t>, dim3(n), dim3(kRowThreads), 0, stream, (const uint16_t*)src,
+                       src_rows, lds, (uint16_t*)dst, dst_rows, ldd, width);
+  else if (dtype == kF32)
+    hipLaunchKernelGGL(copy_rows_kernel<float>, dim3(n), dim3(kRowThreads), 0, stream, (const float*)src, src_rows,
+                       lds, (float*)dst, dst_rows, ldd, width);
+  else {
+    set_error("wfd_copy_rows: unsupported dtype %d", dtype);
+    return kUnsupported;
+  }
+  return launch_status("wfd_copy_rows");
+}
+
+int wfd_argmax(const float* logits, int64_t ld, int64_t* out, int n, int vocab, hipStream_t stream) {
+  using namespace wfd;
+  if (n < 0 || vocab <= 0 || ld < vocab) {
+    set_error("wfd_argmax: bad shape n=%d vocab=%d", n, vocab);
+    return kBadArg;
+  }
+  if (n == 0) return kOk;
+  if (!logits || !out) {
+    set_error("wfd_argmax: null pointer argument");
+    return kBadArg;
+  }
+  hipLaunchKernelGGL(argmax_kernel, dim3(n), dim3(kRowThreads), 0, stream, logits, ld, out, vocab);
+  return launch_status("wfd_argmax");
+}
+
+}  // extern "C"

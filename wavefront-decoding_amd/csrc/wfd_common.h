@@ -1,0 +1,123 @@
+// Shared device helpers for the wavefront-decode kernels (gfx950 / CDNA4).
+//
+// Storage types: fp32 tensors are `float`, bf16 tensors are `bf16_t` (raw
+// 16-bit pattern). All arithmetic is fp32; bf16 results are rounded once,
+// round-to-nearest-even, which is the rounding torch uses for bf16 tensors.
+//
+// Every kernel in this library is row-invariant: the value written for a row
+// depends only on that row's inputs (and the weights), never on how many other
+// rows share the launch or where the row sits in it. This is what keeps the
+// wavefront decode (W rows per tick) bit-identical to sequential looped decode
+// (1 row per tick) -- the losslessness argument of
+// src/decoding/parcae_blocks.py:526-597 needs identical per-token arithmetic.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "wfd.h"
+
+namespace wfd {
+
+struct bf16_t {
+  uint16_t bits;
+};
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+enum DType : int { kF32 = 0, kBF16 = 1 };
+
+enum Status : int {
+  kOk = 0,
+  kBadArg = -1,
+  kUnsupported = -2,
+  kLaunch = -3,
+  kWorkspace = -4,
+};
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<float> {
+  static constexpr int kVec = 4;  // elements per 16-byte vector
+  __device__ __forceinline__ static float load(const float* p) { return *p; }
+  __device__ __forceinline__ static void store(float* p, float v) { *p = v; }
+  __device__ __forceinline__ static void unpack(const u32x4& w, float (&o)[4]) {
+    o[0] = __uint_as_float(w[0]);
+    o[1] = __uint_as_float(w[1]);
+    o[2] = __uint_as_float(w[2]);
+    o[3] = __uint_as_float(w[3]);
+  }
+};
+
+template <>
+struct Elem<bf16_t> {
+  static constexpr int kVec = 8;
+  __device__ __forceinline__ static float load(const bf16_t* p) { return bf16_bits_to_f32(p->bits); }
+  __device__ __forceinline__ static void store(bf16_t* p, float v) { p->bits = f32_to_bf16_bits(v); }
+  __device__ __forceinline__ static void unpack(const u32x4& w, float (&o)[8]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o[2 * e] = __uint_as_float(w[e] << 16);
+      o[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+    }
+  }
+};
+
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+__device__ __forceinline__ u32x4 zero16() {
+  u32x4 z = {0u, 0u, 0u, 0u};
+  return z;
+}
+
+// One MFMA "k-step": acc(16x16) += A(16 x KSTEP) * B(KSTEP x 16), where each
+// lane supplies one 16-byte fragment of A (row lane%16) and of B (column
+// lane%16), both covering k-group lane/16. KSTEP = 4 * kVec: 32 for bf16
+// (v_mfma_f32_16x16x32_bf16), 16 for fp32 (four v_mfma_f32_16x16x4_f32, one
+// per element of the fragment). A and B use the same k mapping, so the
+// product is a true dot product whatever the hardware's internal k order.
+// Output layout: lane l holds D[4*(l/16) + r][l%16], r = 0..3.
+template <typename T>
+__device__ __forceinline__ f32x4 mfma_step(const u32x4& a, const u32x4& b, f32x4 acc);
+
+template <>
+__device__ __forceinline__ f32x4 mfma_step<bf16_t>(const u32x4& a, const u32x4& b, f32x4 acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), acc,
+                                                 0, 0, 0);
+}
+
+template <>
+__device__ __forceinline__ f32x4 mfma_step<float>(const u32x4& a, const u32x4& b, f32x4 acc) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[e]), __uint_as_float(b[e]), acc, 0, 0, 0);
+  return acc;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+}  // namespace wfd
+
+// Host-side error reporting shared by every C-ABI entry point.
+namespace wfd {
+void set_error(const char* fmt, ...);
+int launch_status(const char* what);
+}  // namespace wfd

@@ -1,0 +1,236 @@
+"""Torch-tensor front end of the C ABI (include/wfd.h).
+
+Every function validates shapes/dtypes/devices on the host, then launches the
+HIP kernel on torch's current stream through libwfd.so. Nothing here computes
+on the host and nothing falls back to torch math: a missing library raises.
+Outputs may be passed in (`out=`) so a caller can keep every buffer at a fixed
+address for hipGraph capture; otherwise they are allocated with torch.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+
+_DT = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
+
+
+def _dt(t: torch.Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise _lib.WfdError(f"unsupported dtype {t.dtype} (float32 / bfloat16)") from None
+
+
+def _p(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _need_cuda(*ts: torch.Tensor | None) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise _lib.WfdError("wfd ops need GPU tensors (no host fallback)")
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise _lib.WfdError(msg)
+
+
+def _rows(t: torch.Tensor | None, n: int, name: str) -> None:
+    if t is not None:
+        _need(t.dtype == torch.int32 and t.is_contiguous() and t.numel() >= n, f"{name}: int32 contiguous (>= {n})")
+
+
+# ---------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------
+_WS: dict[int, torch.Tensor] = {}
+
+
+def attn_workspace_bytes(n: int, H: int, Dh: int, kv_len_max: int) -> int:
+    return int(_lib.load().wfd_attn_workspace_bytes(n, H, Dh, kv_len_max))
+
+
+def attn_workspace(n: int, H: int, Dh: int, kv_len_max: int, device) -> torch.Tensor:
+    """A reusable uint8 workspace large enough for this launch shape."""
+    need = attn_workspace_bytes(n, H, Dh, kv_len_max)
+    dev = torch.device(device)
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    ws = _WS.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(max(need, 1 << 20), dtype=torch.uint8, device=dev)
+        _WS[key] = ws
+    return ws
+
+
+def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, kv_row_base: torch.Tensor,
+                kv_len: torch.Tensor, *, kv_len_max: int, scale: float | None = None,
+                out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Wavefront decode attention: q (n, H, Dh) over slot rows of the flat
+    (rows, Hkv, Dh) caches; query i reads rows kv_row_base[i] + [0, kv_len[i])."""
+    _need_cuda(q, k_cache, v_cache, kv_row_base, kv_len)
+    _need(q.dim() == 3 and q.is_contiguous(), "q must be contiguous (n, H, Dh)")
+    n, H, Dh = q.shape
+    _need(k_cache.dim() == 3 and k_cache.shape == v_cache.shape, "k/v cache must be (rows, Hkv, Dh)")
+    _need(k_cache.is_contiguous() and v_cache.is_contiguous(), "caches must be contiguous")
+    Hkv = k_cache.shape[1]
+    _need(k_cache.shape[2] == Dh and k_cache.dtype == q.dtype == v_cache.dtype, "q/k/v dtype or head_dim mismatch")
+    _need(kv_row_base.dtype == torch.int64 and kv_row_base.numel() >= n and kv_row_base.is_contiguous(),
+          "kv_row_base: int64 (n,)")
+    _need(kv_len.dtype == torch.int32 and kv_len.numel() >= n and kv_len.is_contiguous(), "kv_len: int32 (n,)")
+    _need(kv_len_max >= 1, "kv_len_max must be >= 1")
+    if out is None:
+        out = torch.empty_like(q)
+    _need(out.shape == q.shape and out.dtype == q.dtype and out.is_contiguous(), "bad out")
+    if workspace is None:
+        workspace = attn_workspace(n, H, Dh, kv_len_max, q.device)
+    sc = 1.0 / math.sqrt(Dh) if scale is None else float(scale)
+    rc = _lib.load().wfd_attn_decode(
+        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), kv_row_base.data_ptr(), kv_len.data_ptr(),
+        out.data_ptr(), n, H, Hkv, Dh, _dt(q), sc, int(kv_len_max), workspace.data_ptr(),
+        workspace.numel() * workspace.element_size(), _stream())
+    _lib.check(rc, "wfd_attn_decode")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# slot-cache append
+# ---------------------------------------------------------------------------
+def kv_append(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+              flat_row: torch.Tensor) -> None:
+    """k_cache[flat_row[i]] = k[i]; v_cache[flat_row[i]] = v[i]."""
+    _need_cuda(k, v, k_cache, v_cache, flat_row)
+    n = k.shape[0]
+    row = k_cache[0].numel()
+    _need(k.is_contiguous() and v.is_contiguous() and k.shape == v.shape and k[0].numel() == row,
+          "k/v rows must match cache rows")
+    _need(k.dtype == v.dtype == k_cache.dtype == v_cache.dtype, "dtype mismatch")
+    _need(flat_row.dtype == torch.int64 and flat_row.numel() >= n and flat_row.is_contiguous(), "flat_row: int64")
+    rc = _lib.load().wfd_kv_append(k.data_ptr(), v.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                                   flat_row.data_ptr(), n, row, _dt(k), _stream())
+    _lib.check(rc, "wfd_kv_append")
+
+
+def qkv_rope_append(qkv: torch.Tensor, pos: torch.Tensor, rope_cos: torch.Tensor, rope_sin: torch.Tensor,
+                    flat_row: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, H: int, Hkv: int, Dh: int,
+                    q_out: torch.Tensor | None = None) -> torch.Tensor:
+    _need_cuda(qkv, pos, rope_cos, rope_sin, flat_row, k_cache, v_cache)
+    n = qkv.shape[0]
+    _need(qkv.dim() == 2 and qkv.stride(1) == 1 and qkv.shape[1] >= (H + 2 * Hkv) * Dh, "qkv (n, (H+2Hkv)Dh)")
+    _need(pos.dtype == torch.int32 and pos.numel() >= n and pos.is_contiguous(), "pos: int32")
+    _need(flat_row.dtype == torch.int64 and flat_row.numel() >= n and flat_row.is_contiguous(), "flat_row: int64")
+    _need(rope_cos.dtype == torch.float32 and rope_cos.shape == rope_sin.shape and rope_cos.shape[1] == Dh // 2,
+          "rope tables: float32 (S, Dh/2)")
+    _need(k_cache.shape[1:] == (Hkv, Dh) and k_cache.dtype == qkv.dtype, "cache shape/dtype mismatch")
+    if q_out is None:
+        q_out = torch.empty(n, H, Dh, dtype=qkv.dtype, device=qkv.device)
+    rc = _lib.load().wfd_qkv_rope_append(qkv.data_ptr(), qkv.stride(0), pos.data_ptr(), rope_cos.data_ptr(),
+                                         rope_sin.data_ptr(), rope_cos.shape[0], flat_row.data_ptr(),
+                                         q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), n, H, Hkv, Dh,
+                                         _dt(qkv), _stream())
+    _lib.check(rc, "wfd_qkv_rope_append")
+    return q_out
+
+
+# ---------------------------------------------------------------------------
+# linear / norms / small gathers
+# ---------------------------------------------------------------------------
+def linear_k_multiple(dtype: torch.dtype) -> int:
+    return int(_lib.load().wfd_linear_k_multiple(_DT[dtype]))
+
+
+def linear(x: torch.Tensor, W: torch.Tensor, *, n: int | None = None, x_rows: torch.Tensor | None = None,
+           out: torch.Tensor | None = None, swiglu: bool = False, out_dtype: torch.dtype | None = None,
+           k: int | None = None) -> torch.Tensor:
+    """y = x[rows, :K] @ W^T (W: (N, K)); swiglu: N = 2F, y (n, F) = silu(g) * u."""
+    _need_cuda(x, W, x_rows, out)
+    _need(x.dim() == 2 and x.stride(1) == 1 and W.dim() == 2 and W.is_contiguous(), "x (rows, K+), W (N, K)")
+    N, K = W.shape
+    if k is not None:
+        _need(k == K, "K mismatch")
+    n = x.shape[0] if (n is None and x_rows is None) else (n if n is not None else x_rows.numel())
+    _rows(x_rows, n, "x_rows")
+    _need(x.shape[1] >= K and x.dtype == W.dtype, f"x width {x.shape[1]} < K={K} or dtype mismatch")
+    od = out_dtype or x.dtype
+    width = N // 2 if swiglu else N
+    if out is None:
+        out = torch.empty(n, width, dtype=od, device=x.device)
+    _need(out.dim() == 2 and out.stride(1) == 1 and out.shape[0] >= n and out.shape[1] >= width and out.dtype == od,
+          "bad out")
+    rc = _lib.load().wfd_linear(x.data_ptr(), _p(x_rows), x.stride(0), W.data_ptr(), out.data_ptr(), out.stride(0),
+                                n, N, K, _dt(x), _DT[od], _lib.EPI_SWIGLU if swiglu else _lib.EPI_PLAIN,
+                                N // 2 if swiglu else 0, _stream())
+    _lib.check(rc, "wfd_linear")
+    return out
+
+
+def add_rmsnorm(a: torch.Tensor, w1: torch.Tensor, eps: float, *, res: torch.Tensor | None = None,
+                w2: torch.Tensor | None = None, n: int | None = None, a_rows: torch.Tensor | None = None,
+                x_out: torch.Tensor | None = None, out_rows: torch.Tensor | None = None,
+                h_out: torch.Tensor | None = None):
+    """x_out = rmsnorm(a + res) * w1; if w2: also h_out = rmsnorm(x_out) * w2.
+    Returns x_out, or (x_out, h_out) when w2 is given."""
+    _need_cuda(a, w1, res, w2, a_rows, x_out, out_rows, h_out)
+    D = w1.numel()
+    n = (a.shape[0] if a_rows is None else a_rows.numel()) if n is None else n
+    _rows(a_rows, n, "a_rows")
+    _rows(out_rows, n, "out_rows")
+    _need(a.dim() == 2 and a.stride(1) == 1 and a.shape[1] >= D, "a (rows, D+)")
+    if res is not None:
+        _need(res.dim() == 2 and res.stride(1) == 1 and res.shape[0] >= n and res.dtype == a.dtype, "bad res")
+    if x_out is None:
+        x_out = torch.empty(n, D, dtype=a.dtype, device=a.device)
+    if w2 is not None and h_out is None:
+        h_out = torch.empty(n, D, dtype=a.dtype, device=a.device)
+    rc = _lib.load().wfd_add_rmsnorm(a.data_ptr(), _p(a_rows), a.stride(0), _p(res),
+                                     res.stride(0) if res is not None else 0, w1.data_ptr(), _p(w2),
+                                     x_out.data_ptr(), _p(out_rows), x_out.stride(0), _p(h_out),
+                                     h_out.stride(0) if h_out is not None else 0, n, D, float(eps), _dt(a), _stream())
+    _lib.check(rc, "wfd_add_rmsnorm")
+    return (x_out, h_out) if w2 is not None else x_out
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, **kw) -> torch.Tensor:
+    return add_rmsnorm(x, w, eps, **kw)
+
+
+def embed(ids: torch.Tensor, table: torch.Tensor, scale: float = 1.0, *, out: torch.Tensor | None = None):
+    _need_cuda(ids, table, out)
+    _need(ids.dtype == torch.int64 and ids.is_contiguous(), "ids: int64")
+    n = ids.numel()
+    Vocab, D = table.shape
+    if out is None:
+        out = torch.empty(n, D, dtype=table.dtype, device=table.device)
+    rc = _lib.load().wfd_embed(ids.data_ptr(), table.data_ptr(), float(scale), out.data_ptr(), out.stride(0), n,
+                               Vocab, D, _dt(table), _stream())
+    _lib.check(rc, "wfd_embed")
+    return out
+
+
+def copy_rows(src: torch.Tensor, dst: torch.Tensor, *, n: int, width: int, src_rows: torch.Tensor | None = None,
+              dst_rows: torch.Tensor | None = None) -> None:
+    _need_cuda(src, dst, src_rows, dst_rows)
+    _need(src.dtype == dst.dtype and src.stride(-1) == 1 and dst.stride(-1) == 1, "copy_rows dtype/layout")
+    _rows(src_rows, n, "src_rows")
+    _rows(dst_rows, n, "dst_rows")
+    rc = _lib.load().wfd_copy_rows(src.data_ptr(), _p(src_rows), src.stride(0), dst.data_ptr(), _p(dst_rows),
+                                   dst.stride(0), n, width, _dt(src), _stream())
+    _lib.check(rc, "wfd_copy_rows")
+
+
+def argmax(logits: torch.Tensor, *, n: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    _need_cuda(logits, out)
+    _need(logits.dtype == torch.float32 and logits.dim() == 2 and logits.stride(1) == 1, "logits: float32 (n, V)")
+    n = logits.shape[0] if n is None else n
+    if out is None:
+        out = torch.empty(n, dtype=torch.int64, device=logits.device)
+    rc = _lib.load().wfd_argmax(logits.data_ptr(), logits.stride(0), out.data_ptr(), n, logits.shape[1], _stream())
+    _lib.check(rc, "wfd_argmax")
+    return out
