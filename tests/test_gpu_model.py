@@ -1,0 +1,185 @@
+"""End-to-end parity of the HIP decode path against the oracle (GPU).
+
+* tiny fp32 looped LM (d=256, 4x64 heads, SwiGLU 1024, 1 + 2x4 + 1 layers,
+  V=4096, N(0,0.02) seed 0, 128-token prompt): prefill logits within 1e-4 of
+  the oracle; WFD (T_draft 1 and 2) and sequential decode commit the oracle's
+  tokens; batch WFD over ragged prompts matches per-sequence decode; the
+  emulated-acceptance batch trace equals the oracle's.
+* bf16: WFD tokens are bit-identical to sequential decode on the GPU
+  (lossless), and one R tick over a mixed-depth union equals each row run
+  alone, bit for bit; one R tick of the 2048-d model matches the oracle
+  within 2e-2.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import scheduler as osched
+from oracle import state_init
+from oracle.looped_lm import OracleBatchBlocks, OracleLM
+from tests.conftest import rel_err
+from wavefront_decoding_amd import model as M
+from wavefront_decoding_amd.blocks import LoopedBlocks, LoopedBlocksBatch
+from wavefront_decoding_amd.emu import EmulatedAcceptance
+from wavefront_decoding_amd.engine import LoopedModel
+from wavefront_decoding_amd.policy import SsdPolicy
+from wavefront_decoding_amd.scheduler import generate_wavefront_dynamic
+from wavefront_decoding_amd.scheduler_batch import ar_generate_batch, generate_wavefront_batch
+
+pytestmark = pytest.mark.gpu
+
+TINY = M.CONFIGS["tiny"]
+# a small bf16 looped LM with the 2048-d model's head shape (Dh = 128) for fast lossless checks
+MINI_BF16 = M.LoopedLMConfig("mini-bf16", 4096, 512, 4, 4, 128, 1536, 1, 2, 1, 8)
+MINI_GQA = M.LoopedLMConfig("mini-gqa", 4096, 512, 4, 1, 128, 1536, 1, 2, 1, 8)
+
+
+def _prompt(L, seed=0, V=4096, B=None):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, V, (L,) if B is None else (B, L), generator=g)
+
+
+def _round(a: np.ndarray, cfg) -> np.ndarray:
+    return torch.from_numpy(a).to(cfg.torch_dtype).float().numpy()
+
+
+def _oracle(cfg, w, S, B=1):
+    """Oracle blocks with the oracle's own s0 recipe, rounded through the run
+    dtype exactly as the GPU table is."""
+    wn = M.weights_numpy(w)
+    s0t = lambda p: _round(state_init.s0_token(cfg.d_model, cfg.state_std, cfg.emb_scale, 0, p), cfg)  # noqa: E731
+    s0p = lambda L: _round(state_init.s0_prefill(cfg.d_model, cfg.state_std, cfg.emb_scale, 0, L), cfg)  # noqa: E731
+    return OracleBatchBlocks(OracleLM(cfg, wn, S, B, s0t, s0p))
+
+
+@pytest.fixture(scope="module")
+def tiny(gpu):
+    w = M.init_weights(TINY, 0)
+    return w, LoopedModel(TINY, w, gpu, max_seq_len=256, max_batch=3)
+
+
+def test_state_tables_match_oracle_recipe():
+    for p in (0, 7, 300):
+        np.testing.assert_array_equal(M.initial_state_tokens(TINY, [p])[0].numpy(),
+                                      state_init.s0_token(256, 0.02, 1.0, 0, p))
+
+
+def test_tiny_prefill_logits_match_oracle(tiny):
+    w, model = tiny
+    ids = _prompt(128)
+    print("[tiny] prefill 128", flush=True)
+    blocks = LoopedBlocks(model)
+    state, logits = blocks.prefill(ids.to(model.device), TINY.T_total, 2)
+    ob = _oracle(TINY, w, 256)
+    _, ref = ob.prefill([ids.tolist()])
+    assert rel_err(logits.cpu().numpy(), ref[0]) <= 1e-4
+
+
+@pytest.mark.parametrize("T_draft", [1, 2])
+def test_tiny_wfd_matches_oracle_and_sequential(tiny, T_draft):
+    w, model = tiny
+    ids = _prompt(128)
+    N = 40
+    blocks = LoopedBlocks(model)
+    print(f"[tiny] wfd T_draft={T_draft} N={N}", flush=True)
+    toks, trace = generate_wavefront_dynamic(blocks, ids.to(model.device), N, SsdPolicy(TINY.T_total, T_draft))
+    ar, _ = blocks.ar_generate(ids.to(model.device), N)
+    assert toks == ar
+    oc = osched.wfd_single(_oracle(TINY, w, 256), ids.tolist(), N, TINY.T_total, T_draft)
+    assert toks == oc.tokens
+    assert trace.counters() == {k: getattr(oc, k) for k in trace.counters()}
+
+
+def test_tiny_batch_ragged_matches_single(tiny):
+    w, model = tiny
+    P = [_prompt(60, 1), _prompt(23, 2), _prompt(100, 3)]
+    N = [14, 9, 11]
+    bb = LoopedBlocksBatch(model, batch_size=3)
+    print("[tiny] batch ragged", flush=True)
+    bt = generate_wavefront_batch(bb, [p.to(model.device) for p in P], N, SsdPolicy(TINY.T_total, 2))
+    ar = ar_generate_batch(bb, [p.to(model.device) for p in P], N)
+    single = LoopedBlocks(model)
+    for b in range(3):
+        solo, _ = single.ar_generate(P[b].to(model.device), N[b])
+        assert bt.per_seq[b].tokens == solo == ar.per_seq[b].tokens
+    assert bt.r_union_max > 3  # several sequences and depths shared unions
+
+
+def test_tiny_emulated_batch_trace_matches_oracle(tiny):
+    w, model = tiny
+    P = [_prompt(30, 4), _prompt(30, 5)]
+    bb = LoopedBlocksBatch(model, batch_size=2)
+    emus = [EmulatedAcceptance(0.5, 1000 + b) for b in range(2)]
+    bt = generate_wavefront_batch(bb, [p.to(model.device) for p in P], 12, SsdPolicy(TINY.T_total, 2), emus)
+    oe = [osched.Emu(0.5, 1000 + b) for b in range(2)]
+    res = osched.wfd_batch(_oracle(TINY, w, 256, B=2), [p.tolist() for p in P], 12, TINY.T_total, 2, oe)
+    for b in range(2):
+        assert bt.per_seq[b].tokens == res.per_seq[b].tokens
+        assert bt.per_seq[b].counters() == {k: getattr(res.per_seq[b], k) for k in bt.per_seq[b].counters()}
+    assert (bt.n_r_calls, bt.r_union_total) == (res.n_r_calls, res.r_union_total)
+
+
+@pytest.mark.parametrize("cfg", [MINI_BF16, MINI_GQA], ids=lambda c: c.name)
+def test_bf16_wfd_is_lossless(gpu, cfg):
+    w = M.init_weights(cfg, 0)
+    model = LoopedModel(cfg, w, gpu, max_seq_len=512, max_batch=1)
+    blocks = LoopedBlocks(model)
+    ids = _prompt(200, 7).to(gpu)
+    print(f"[{cfg.name}] lossless", flush=True)
+    ar, _ = blocks.ar_generate(ids, 48)
+    for T_draft in (1, 2, 4):
+        toks, tr = generate_wavefront_dynamic(blocks, ids, 48, SsdPolicy(cfg.T_total, T_draft))
+        assert toks == ar, T_draft
+
+
+def test_core_tick_row_invariant(gpu):
+    """One R tick over a mixed-depth union equals each row ticked alone, bit for bit."""
+    cfg = MINI_BF16
+    model = LoopedModel(cfg, M.init_weights(cfg, 1), gpu, max_seq_len=256, max_batch=1)
+    cache = model.create_cache(1)
+    g = torch.Generator().manual_seed(3)
+    cache.flat_k.copy_(torch.randn(cache.flat_k.shape, generator=g).to(cache.flat_k.dtype))
+    cache.flat_v.copy_(torch.randn(cache.flat_v.shape, generator=g).to(cache.flat_v.dtype))
+    pos = [100, 99, 98, 97, 96, 95]
+    steps = [5, 4, 3, 2, 1, 0]
+    rows = [model.pool_row(0, p) for p in pos]
+    model.pool.copy_(torch.randn(model.pool.shape, generator=g).to(model.pool.dtype))
+    init = model.pool.clone()
+    model.core_union(cache, [0] * 6, pos, steps)
+    union = model.pool[rows].clone()
+    for i in range(6):
+        model.pool.copy_(init)
+        model.core_union(cache, [0], [pos[i]], [steps[i]])
+        assert torch.equal(model.pool[rows[i]], union[i]), i
+
+
+def test_2048_core_tick_matches_oracle(gpu):
+    """One R tick of the 2048-d bf16 model (8 rows, depths 0..14, slot prefixes
+    of random K/V) against the fp32 oracle fed the same bf16 values: <= 2e-2."""
+    cfg = M.CONFIGS["looped-2048"]
+    w = M.init_weights(cfg, 0)
+    S = 640
+    model = LoopedModel(cfg, w, gpu, max_seq_len=S, max_batch=1)
+    cache = model.create_cache(1)
+    g = torch.Generator().manual_seed(4)
+    kv = torch.randn(2, cache.flat_k.shape[0], cfg.n_kv_heads, cfg.head_dim, generator=g).to(torch.bfloat16)
+    cache.flat_k.copy_(kv[0])
+    cache.flat_v.copy_(kv[1])
+    pos = [600 - i for i in range(8)]
+    steps = [2 * i for i in range(8)]
+    rows = [model.pool_row(0, p) for p in pos]
+    state = torch.randn(8, 2 * cfg.d_model, generator=g).to(torch.bfloat16)
+    model.pool[rows] = state.to(gpu)
+    print("[2048] core tick", flush=True)
+    model.core_union(cache, [0] * 8, pos, steps)
+    got = model.pool[rows, : cfg.d_model].float().cpu().numpy()
+    lm = OracleLM(cfg, M.weights_numpy(w), S, 1, None, None)
+    K = cache.K.float().cpu().numpy()
+    V = cache.V.float().cpu().numpy()
+    lm.Kc[:] = K
+    lm.Vc[:] = V
+    st = state.float().numpy()
+    ref = np.stack([lm.core(0, pos[i], steps[i], st[i, : cfg.d_model], st[i, cfg.d_model:]) for i in range(8)])
+    assert rel_err(got, ref) <= 2e-2

@@ -1,0 +1,304 @@
+"""Fixed-batch schedulers: sequential looped decode (AR) and WFD with
+per-sequence waves (src/decoding/scheduler_batch.py:36-362).
+
+A fixed batch of B sequences: a finished sequence idles (no refill); each
+tick runs P, R and C once over the union of whatever every live sequence
+needs; each sequence settles independently -- accept/reject comes from its
+EmulatedAcceptance stream when given (Bernoulli(alpha)), else from the real
+argmax comparison -- and a reject rolls back only that sequence.
+
+Extensions over the reference (both optional, the reference's behaviour is
+the default): prompts may have different lengths (a list of 1-D id
+sequences; the reference needs equal lengths, huginn_blocks_batch.py:180-185),
+and max_new_tokens may be a per-sequence list (the reference takes one value,
+scheduler_batch.py:348-349).
+"""
+from __future__ import annotations
+
+import copy
+import time
+from dataclasses import dataclass, field
+
+import torch
+
+from .batch_state import SeqState
+from .policy import SsdPolicy
+from .state import ActiveToken
+
+
+@dataclass
+class BatchTrace:
+    walltime_s: float = 0.0
+    prefill_s: float = 0.0
+    n_r_calls: int = 0
+    n_p_calls: int = 0
+    n_c_calls: int = 0
+    r_union_total: int = 0
+    r_union_max: int = 0
+    peak_alloc_gb: float = 0.0
+    peak_reserved_gb: float = 0.0
+    cache_gb: float = 0.0
+    per_seq: list = field(default_factory=list)
+
+    @property
+    def n_tokens(self) -> int:
+        return sum(len(t.tokens) for t in self.per_seq)
+
+    @property
+    def tokens_per_s(self) -> float:
+        return self.n_tokens / self.walltime_s if self.walltime_s > 0 else float("nan")
+
+    @property
+    def walltime_decode_s(self) -> float:
+        return max(self.walltime_s - self.prefill_s, 0.0)
+
+    @property
+    def decode_tokens_per_s(self) -> float:
+        d = self.walltime_decode_s
+        return self.n_tokens / d if d > 0 else float("nan")
+
+    @property
+    def r_union_mean(self) -> float:
+        return self.r_union_total / self.n_r_calls if self.n_r_calls else 0.0
+
+    @property
+    def acceptance_rate(self) -> float:
+        prop = sum(t.n_drafts_proposed for t in self.per_seq)
+        acc = sum(t.n_drafts_accepted for t in self.per_seq)
+        return acc / prop if prop else float("nan")
+
+
+@dataclass
+class SharedPrefill:
+    """One prompt prefill reused by several decode runs: decode only writes
+    positions >= the prompt length, so restoring the logical lengths is enough
+    (src/decoding/scheduler_batch.py:83-120)."""
+
+    cache: object
+    first_tokens: list[int]
+    prefill_s: float
+    prompt_lens: list[int]
+    _seqlen0: list = field(default_factory=list)
+
+    def restore(self) -> None:
+        self.cache.seqlen = [row[:] for row in self._seqlen0]
+
+
+def _prompt_lens(prompt_ids) -> list[int]:
+    if isinstance(prompt_ids, (list, tuple)):
+        return [int(torch.as_tensor(p).numel()) for p in prompt_ids]
+    return [int(prompt_ids.shape[1])] * int(prompt_ids.shape[0])
+
+
+def _device_of(prompt_ids):
+    p = prompt_ids[0] if isinstance(prompt_ids, (list, tuple)) else prompt_ids
+    return torch.as_tensor(p).device
+
+
+@torch.no_grad()
+def prefill_once(blocks, prompt_ids) -> SharedPrefill:
+    t0 = time.perf_counter()
+    cache, last = blocks.prefill(prompt_ids)
+    first = last.argmax(dim=-1).tolist()
+    if _device_of(prompt_ids).type == "cuda":
+        torch.cuda.synchronize()
+    return SharedPrefill(cache=cache, first_tokens=first, prefill_s=time.perf_counter() - t0,
+                         prompt_lens=_prompt_lens(prompt_ids), _seqlen0=[row[:] for row in cache.seqlen])
+
+
+def _start(blocks, prompt_ids, emus, max_new_tokens, bt: BatchTrace, t0: float, prefilled: SharedPrefill | None):
+    """Prefill (or borrow one) and commit every sequence's first token."""
+    if prefilled is not None:
+        prefilled.restore()
+        cache, first = prefilled.cache, prefilled.first_tokens
+        bt.prefill_s = prefilled.prefill_s
+        t0 = time.perf_counter() - prefilled.prefill_s
+        lens = prefilled.prompt_lens
+    else:
+        cache, last = blocks.prefill(prompt_ids)
+        first = last.argmax(dim=-1).tolist()
+        if _device_of(prompt_ids).type == "cuda":
+            torch.cuda.synchronize()
+        bt.prefill_s = time.perf_counter() - t0
+        lens = _prompt_lens(prompt_ids)
+    B = len(lens)
+    limits = list(max_new_tokens) if isinstance(max_new_tokens, (list, tuple)) else [max_new_tokens] * B
+    seqs = []
+    for b in range(B):
+        s = SeqState(idx=b, prefix_len=lens[b], emu=emus[b] if emus is not None else None, max_new_tokens=limits[b])
+        s.commit(first[b])
+        s.done = len(s.committed) >= limits[b]
+        seqs.append(s)
+    return cache, seqs, t0
+
+
+def _finish(bt: BatchTrace, seqs, t0: float, device, cache) -> BatchTrace:
+    if device.type == "cuda":
+        torch.cuda.synchronize()
+    bt.walltime_s = time.perf_counter() - t0
+    for s in seqs:
+        s.trace.walltime_s = bt.walltime_s
+    bt.per_seq = [s.trace for s in seqs]
+    if device.type == "cuda":
+        bt.peak_alloc_gb = torch.cuda.max_memory_allocated() / 1e9
+        bt.peak_reserved_gb = torch.cuda.max_memory_reserved() / 1e9
+    bt.cache_gb = cache.nbytes / 1e9
+    return bt
+
+
+def _record_r(bt: BatchTrace, n: int) -> None:
+    bt.n_r_calls += 1
+    bt.r_union_total += n
+    bt.r_union_max = max(bt.r_union_max, n)
+
+
+@torch.no_grad()
+def ar_generate_batch(blocks, prompt_ids, max_new_tokens, prefilled: SharedPrefill | None = None) -> BatchTrace:
+    """Lockstep sequential looped decode: per token P -> R x T_total -> C."""
+    device = _device_of(prompt_ids)
+    if device.type == "cuda":
+        torch.cuda.reset_peak_memory_stats()
+    bt = BatchTrace()
+    cache, seqs, t0 = _start(blocks, prompt_ids, None, max_new_tokens, bt, time.perf_counter(), prefilled)
+    while True:
+        act = [s for s in seqs if not s.done]
+        if not act:
+            break
+        toks = []
+        for s in act:
+            toks.append(ActiveToken(token_id=s.committed[-1], position=s.prefix_len + len(s.committed) - 1,
+                                    role="verify"))
+            s.trace.n_p_calls += 1
+        ids = [s.idx for s in act]
+        blocks.prelude_union(ids, toks, cache)
+        bt.n_p_calls += 1
+        for _ in range(blocks.T_total):
+            blocks.advance_union(ids, toks, cache)
+            _record_r(bt, len(toks))
+            for s in act:
+                s.trace.n_r_calls += 1
+        out = blocks.coda_argmax_union(ids, toks, cache)
+        bt.n_c_calls += 1
+        for s, nid in zip(act, out):
+            s.trace.n_c_calls += 1
+            s.commit(nid)
+            s.done = len(s.committed) >= s.max_new_tokens
+    return _finish(bt, seqs, t0, device, cache)
+
+
+@torch.no_grad()
+def generate_wavefront_batch(blocks, prompt_ids, max_new_tokens, policy: SsdPolicy, emus=None,
+                             prefilled: SharedPrefill | None = None) -> BatchTrace:
+    """One independent wave per sequence; P, R and C once per tick over the union."""
+    device = _device_of(prompt_ids)
+    if device.type == "cuda":
+        torch.cuda.reset_peak_memory_stats()
+    bt = BatchTrace()
+    cache, seqs, t0 = _start(blocks, prompt_ids, emus, max_new_tokens, bt, time.perf_counter(), prefilled)
+    T_total, T_draft = policy.T_total, policy.T_draft
+    for s in seqs:
+        if not s.done:
+            s.active_p.append(ActiveToken(token_id=s.committed[-1], position=s.prefix_len, role="draft"))
+            s.trace.n_p_calls += 1
+
+    max_new = max(s.max_new_tokens for s in seqs)
+    ticks, guard = 0, max_new * (T_total + 4) + 100
+    while True:
+        live = [s for s in seqs if not s.done]
+        if not live:
+            break
+        ticks += 1
+        if ticks > guard:
+            raise RuntimeError(f"wfd batch exceeded tick guard ({guard}) -- scheduler bug?")
+
+        # P: everything queued by the previous settle
+        p_pairs = [(s, t) for s in live for t in s.active_p]
+        if p_pairs:
+            blocks.prelude_union([s.idx for s, _ in p_pairs], [t for _, t in p_pairs], cache)
+            for s, t in p_pairs:
+                s.active_r.append(t)
+            for s in live:
+                s.active_p = []
+            bt.n_p_calls += 1
+
+        # R: one tick for every live wave
+        r_pairs = [(s, t) for s in live for t in s.active_r if t.is_alive]
+        if r_pairs:
+            blocks.advance_union([s.idx for s, _ in r_pairs], [t for _, t in r_pairs], cache)
+            _record_r(bt, len(r_pairs))
+            for s in live:
+                if any(t.is_alive for t in s.active_r):
+                    s.trace.n_r_calls += 1
+
+        # routing: commit point -> verify (moved); draft point -> draft (copied)
+        for s in live:
+            keep = []
+            for t in s.active_r:
+                if not t.is_alive:
+                    continue
+                if t.step == T_total:
+                    t.role = "verify"
+                    s.active_c.append(t)
+                else:
+                    keep.append(t)
+                    if t.step == T_draft:
+                        d = copy.copy(t)
+                        d.role = "draft"
+                        s.active_c.append(d)
+            s.active_r = keep
+
+        # C: one union over every sequence's verifies + draft
+        plan, c_toks, c_ids = [], [], []
+        for s in live:
+            if s.active_c:
+                vs = sorted((t for t in s.active_c if t.role == "verify"), key=lambda t: t.position)
+                ds = [t for t in s.active_c if t.role == "draft"]
+                plan.append((s, vs, ds))
+                c_toks += vs + ds
+                c_ids += [s.idx] * (len(vs) + len(ds))
+        gold_of: dict[int, int] = {}
+        if c_toks:
+            gold_of = {id(t): g for t, g in zip(c_toks, blocks.coda_argmax_union(c_ids, c_toks, cache))}
+            bt.n_c_calls += 1
+            for s, _, _ in plan:
+                s.trace.n_c_calls += 1
+
+        # settle each sequence, then seed its new leading draft
+        for s, vs, ds in plan:
+            rejected = boundary = False
+            for i, v in enumerate(vs):
+                gold = gold_of[id(v)]
+                v.is_alive = False
+                nxt_pos = v.position + 1
+                nxt = vs[i + 1] if i + 1 < len(vs) else s.find_active(nxt_pos)
+                if nxt is None:
+                    s.commit(gold)
+                    s.active_p.append(ActiveToken(token_id=gold, position=nxt_pos, role="draft"))
+                    s.trace.n_p_calls += 1
+                    boundary = True
+                else:
+                    ok = s.emu.draw() if s.emu is not None else gold == nxt.token_id
+                    s.trace.n_drafts_proposed += 1
+                    if ok:
+                        s.trace.n_drafts_accepted += 1
+                        s.commit(nxt.token_id)
+                    else:
+                        s.trace.n_drafts_rejected += 1
+                        s.trace.n_rollback_events += 1
+                        rejected = True
+                        s.commit(gold)
+                        s.rollback(nxt_pos, cache)
+                        s.active_p.append(ActiveToken(token_id=gold, position=nxt_pos, role="draft"))
+                        s.trace.n_p_calls += 1
+                s.done = len(s.committed) >= s.max_new_tokens
+                if s.done or rejected or boundary:
+                    break
+            if s.done:
+                s.clear_working_state()
+                continue
+            if ds and not rejected:
+                src = ds[0]
+                s.active_p.append(ActiveToken(token_id=gold_of[id(src)], position=src.position + 1, role="draft"))
+                s.trace.n_p_calls += 1
+            s.active_c = []
+    return _finish(bt, seqs, t0, device, cache)
