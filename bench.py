@@ -1,0 +1,376 @@
+"""Benchmark of the MI355X wavefront decode step (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu] [--only LIST]
+
+Prints ONE JSON line. `value` is bs=1 decode tokens/s of lossless-capable WFD
+on the 2048-d bf16 looped LM (2 prelude + 4-layer core looped 16 times +
+2 coda, 16 heads x 128, SwiGLU 5632, V=32000, random init N(0, 0.02) seed 0),
+512-token prompt (uniform ids, seed 0), 256 new tokens, T_total=16,
+T_draft=2 (wavefront width 8), with acceptance emulated at alpha = 0.9
+(per-draft Bernoulli draws, seed 1000; all compute still runs). A step is one
+whole 256-token decode from the prefilled prompt (the prompt cache is reused,
+prefill excluded from the timed region); value = 256 * steps / timed seconds.
+
+Extra fields: the same model decoded with real greedy acceptance (and its
+measured acceptance rate) and sequentially (AR); bs=32 with ragged prompts
+U[128, 2048] and generation lengths U[64, 512] at emulated alpha 0.5 / 0.7 /
+0.9; the wavefront attention op alone (bf16, 16 heads x 64, W=8,
+L in {1k, 4k, 16k}) and at the decode shapes; a long-context GQA decode tick
+(16 q / 4 kv heads, B=4, 32k context, W=16) over random-filled KV; the
+roofline of the dominant kernel; and the CPU oracle's throughput on a
+bounded sample of the bs=1 workload on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256e6
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--quick", action="store_true", help="fewer extras (development)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--only", default="", help="comma list of sections: bs1,bs32,attn,gqa,cpu")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------
+def timed(fn, iters: int, stream=None) -> float:
+    """Average milliseconds per call with HIP events on the launch stream."""
+    import torch
+
+    st = stream or torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for i in range(iters):
+        fn(i)
+    e1.record(st)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def attn_bench(dev, n, H, Hkv, Dh, lens, iters=40):
+    """Wavefront attention alone; rotates KV sets totalling > 512 MB so the
+    256 MB MALL cannot serve repeats. Returns (us/call, algorithmic bytes)."""
+    import torch
+    from wavefront_decoding_amd import ops
+
+    S = max(lens) + 1
+    per_set = n * S * Hkv * Dh * 2 * 2
+    nsets = max(3, math.ceil(2 * MALL_BYTES / per_set) + 1)
+    g = torch.Generator(device=dev).manual_seed(0)
+    sets = [(torch.randn(n * S, Hkv, Dh, device=dev, dtype=torch.bfloat16, generator=g),
+             torch.randn(n * S, Hkv, Dh, device=dev, dtype=torch.bfloat16, generator=g)) for _ in range(nsets)]
+    q = torch.randn(n, H, Dh, device=dev, dtype=torch.bfloat16, generator=g)
+    rb = torch.tensor([i * S for i in range(n)], dtype=torch.int64, device=dev)
+    kl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    ws = ops.attn_workspace(n, H, Dh, max(lens), dev)
+    call = lambda i: ops.attn_decode(q, sets[i % nsets][0], sets[i % nsets][1], rb, kl,  # noqa: E731
+                                     kv_len_max=max(lens), out=out, workspace=ws)
+    timed(call, 3)
+    ms = timed(call, iters)
+    by = sum(lens) * Hkv * Dh * 2 * 2 + 2 * n * H * Dh * 2
+    del sets
+    torch.cuda.empty_cache()
+    return ms * 1e3, by
+
+
+def linear_roofline(dev, model, n: int, iters: int = 30):
+    """The linear (weight-stream) kernel at the decode shapes of one R tick:
+    average launch duration and algorithmic bytes (W + x + y) per launch,
+    timed with HIP events over rotating weight copies (> 512 MB, so HBM, not
+    MALL, serves every launch)."""
+    import torch
+    from wavefront_decoding_amd import ops
+
+    c = model.cfg
+    D = c.d_model
+    shapes = [("adapter", c.d_model, 2 * D, False), ("Wqkv", c.qkv_dim, D, False),
+              ("proj", D, c.n_heads * c.head_dim, False), ("fc", 2 * c.ffn, D, True), ("mlp_proj", D, c.ffn, False)]
+    per_tick = sum(N * K * 2 for _, N, K, _ in shapes)
+    copies = max(2, math.ceil(2 * MALL_BYTES / per_tick) + 1)
+    g = torch.Generator(device=dev).manual_seed(1)
+    Ws = [[(0.02 * torch.randn(N, K, device=dev, generator=g)).to(torch.bfloat16) for _, N, K, _ in shapes]
+          for _ in range(copies)]
+    x = torch.randn(n, 2 * D, device=dev, generator=g).to(torch.bfloat16)
+    xf = torch.randn(n, c.ffn, device=dev, generator=g).to(torch.bfloat16)
+    out = torch.empty(n, 2 * c.ffn, device=dev, dtype=torch.bfloat16)
+    total_ms, total_bytes, launches = 0.0, 0, 0
+    for j, (name, N, K, sw) in enumerate(shapes):
+        src = xf if K == c.ffn else x
+        call = lambda i, j=j, K=K, sw=sw, src=src: ops.linear(src, Ws[i % copies][j], n=n, out=out, swiglu=sw, k=K)  # noqa: E731
+        timed(call, 2)
+        ms = timed(call, iters)
+        width = N // 2 if sw else N
+        total_ms += ms
+        total_bytes += N * K * 2 + n * K * 2 + n * width * 2
+        launches += 1
+    del Ws
+    torch.cuda.empty_cache()
+    avg_ms = total_ms / launches
+    avg_bytes = total_bytes / launches
+    return avg_ms, avg_bytes
+
+
+# ---------------------------------------------------------------------------
+def bs1_section(args, dev, res):
+    import torch
+    from wavefront_decoding_amd import model as M
+    from wavefront_decoding_amd.blocks import LoopedBlocksBatch, LoopedBlocks
+    from wavefront_decoding_amd.emu import EmulatedAcceptance
+    from wavefront_decoding_amd.engine import LoopedModel
+    from wavefront_decoding_amd.policy import SsdPolicy
+    from wavefront_decoding_amd.scheduler import generate_wavefront_dynamic
+    from wavefront_decoding_amd.scheduler_batch import generate_wavefront_batch, prefill_once
+
+    cfg = M.CONFIGS["looped-2048"]
+    L, N, T_draft, alpha = 512, 256, 2, 0.9
+    t0 = time.perf_counter()
+    w = M.init_weights(cfg, 0)
+    model = LoopedModel(cfg, w, dev, max_seq_len=L + N + 16, max_batch=1)
+    log(f"bs1: model ready in {time.perf_counter() - t0:.1f}s")
+    prompt = torch.randint(0, cfg.vocab_size, (1, L), generator=torch.Generator().manual_seed(0))
+    bb = LoopedBlocksBatch(model, batch_size=1)
+    pf = prefill_once(bb, prompt.to(dev))
+    log(f"bs1: prefill {pf.prefill_s * 1e3:.1f} ms")
+    policy = SsdPolicy(cfg.T_total, T_draft)
+
+    def step():
+        emus = [EmulatedAcceptance(alpha, 1000)]
+        return generate_wavefront_batch(bb, prompt.to(dev), N, policy, emus, prefilled=pf)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    traces = [step() for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    toks = sum(t.n_tokens for t in traces)
+    res["value"] = toks / dt
+    res["ms_per_step"] = dt * 1e3 / args.steps
+    res["bs1_alpha"] = traces[-1].acceptance_rate
+    res["bs1_r_ticks_per_step"] = traces[-1].n_r_calls
+    log(f"bs1: WFD alpha={alpha}: {res['value']:.1f} tok/s ({res['ms_per_step']:.1f} ms/step)")
+
+    if not args.quick:
+        # sequential looped decode on the same prompt (the lossless reference)
+        blocks = LoopedBlocks(model)
+        from wavefront_decoding_amd.scheduler_batch import ar_generate_batch
+        nar = 64
+        ar_generate_batch(bb, prompt.to(dev), 8, prefilled=pf)
+        t0 = time.perf_counter()
+        bt = ar_generate_batch(bb, prompt.to(dev), nar, prefilled=pf)
+        torch.cuda.synchronize()
+        res["extra"]["bs1_sequential_tokens_per_s"] = bt.n_tokens / (time.perf_counter() - t0)
+        # real greedy WFD (random-init weights: drafts rarely match full depth)
+        toks, tr = generate_wavefront_dynamic(blocks, prompt[0].to(dev), 64, policy)
+        res["extra"]["bs1_greedy"] = {"tokens_per_s": len(toks) / tr.walltime_s, "alpha": tr.acceptance_rate,
+                                      "note": "includes prefill; real argmax acceptance on random-init weights"}
+        log(f"bs1: sequential {res['extra']['bs1_sequential_tokens_per_s']:.1f} tok/s; greedy alpha "
+            f"{tr.acceptance_rate:.2f}")
+    # dominant kernel of the R tick: the weight-stream linear
+    avg_ms, avg_bytes = linear_roofline(dev, model, 8)
+    ach = avg_bytes / (avg_ms * 1e-3) / 1e9
+    res["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                       "kernel": "wfd::linear_kernel (bf16, n=8 rows; adapter, Wqkv, proj, fc+SwiGLU, mlp_proj)",
+                       "bytes_per_launch": int(avg_bytes), "avg_launch_us": round(avg_ms * 1e3, 2)}
+    log(f"bs1: linear roofline {ach:.0f} GB/s over {avg_ms * 1e3:.1f} us avg launch")
+    del model, bb, pf
+    torch.cuda.empty_cache()
+    return w
+
+
+def bs32_section(args, dev, res, w=None):
+    import torch
+    from wavefront_decoding_amd import model as M
+    from wavefront_decoding_amd.blocks import LoopedBlocksBatch
+    from wavefront_decoding_amd.emu import EmulatedAcceptance
+    from wavefront_decoding_amd.engine import LoopedModel
+    from wavefront_decoding_amd.policy import SsdPolicy
+    from wavefront_decoding_amd.scheduler_batch import generate_wavefront_batch, prefill_once
+
+    cfg = M.CONFIGS["looped-2048"]
+    B = 32
+    g = torch.Generator().manual_seed(0)
+    plen = torch.randint(128, 2049, (B,), generator=g).tolist()
+    glen = torch.randint(64, 513, (B,), generator=g).tolist()
+    if args.quick:
+        plen = [p // 4 for p in plen]
+        glen = [x // 4 for x in glen]
+    prompts = [torch.randint(0, cfg.vocab_size, (p,), generator=g).to(dev) for p in plen]
+    w = w if w is not None else M.init_weights(cfg, 0)
+    model = LoopedModel(cfg, w, dev, max_seq_len=max(plen) + max(glen) + 16, max_batch=B)
+    bb = LoopedBlocksBatch(model, batch_size=B)
+    t0 = time.perf_counter()
+    pf = prefill_once(bb, prompts)
+    log(f"bs32: prefill of {sum(plen)} prompt tokens in {time.perf_counter() - t0:.1f}s")
+    policy = SsdPolicy(cfg.T_total, 2)
+    out = {}
+    generate_wavefront_batch(bb, prompts, [8] * B, policy, [EmulatedAcceptance(0.9, 1000 + b) for b in range(B)],
+                             prefilled=pf)
+    for alpha in (0.5, 0.7, 0.9):
+        emus = [EmulatedAcceptance(alpha, 1000 + b) for b in range(B)]
+        bt = generate_wavefront_batch(bb, prompts, glen, policy, emus, prefilled=pf)
+        out[str(alpha)] = {"decode_tokens_per_s": round(bt.n_tokens / max(bt.walltime_decode_s, 1e-9), 1),
+                           "tokens": bt.n_tokens, "r_ticks": bt.n_r_calls, "r_union_mean": round(bt.r_union_mean, 1),
+                           "acceptance": round(bt.acceptance_rate, 3)}
+        log(f"bs32: alpha={alpha}: {out[str(alpha)]}")
+    res["extra"]["bs32"] = out
+    res["extra"]["bs32_workload"] = ("32 sequences, prompts U[128,2048], generation U[64,512] (seed 0), "
+                                     "T_total=16, T_draft=2, emulated acceptance seeds 1000+b, prefill excluded")
+    del model, bb, pf
+    torch.cuda.empty_cache()
+
+
+def attn_section(args, dev, res):
+    out = {}
+    for L in (1024, 4096, 16384):
+        us, by = attn_bench(dev, 8, 16, 16, 64, [L - 7 + i for i in range(8)])
+        out[f"op_L{L}"] = {"us": round(us, 2), "MB": round(by / 1e6, 2), "GBs": round(by / us / 1e3, 1),
+                           "frac": round(by / us / 1e3 / HBM_PEAK_GBS, 4)}
+    us, by = attn_bench(dev, 8, 16, 16, 128, [512 + 38 * i for i in range(8)])
+    out["decode_2048d_layer_tick"] = {"us": round(us, 2), "MB": round(by / 1e6, 2), "GBs": round(by / us / 1e3, 1),
+                                      "frac": round(by / us / 1e3 / HBM_PEAK_GBS, 4)}
+    res["extra"]["wavefront_attention"] = out
+    log(f"attn: {out}")
+
+
+def gqa_section(args, dev, res):
+    """Long-context GQA decode: one R tick for 4 sequences x W=16 rows over a
+    32k random-filled prompt cache (prefill of 4 x 32k prompts is out of scope)."""
+    import torch
+    from wavefront_decoding_amd import model as M
+    from wavefront_decoding_amd.engine import LoopedModel
+
+    cfg = M.CONFIGS["looped-2048-gqa"]
+    B, ctx, W = 4, 32768, 16
+    us, by = attn_bench(dev, B * W, 16, 4, 128, [ctx + i for i in range(B * W)], iters=10)
+    res["extra"]["gqa_attention"] = {"us": round(us, 1), "GB": round(by / 1e9, 3), "GBs": round(by / us / 1e3, 1),
+                                     "frac": round(by / us / 1e3 / HBM_PEAK_GBS, 4)}
+    log(f"gqa attention: {res['extra']['gqa_attention']}")
+    if args.quick:
+        return
+    model = LoopedModel(cfg, M.init_weights(cfg, 0), dev, max_seq_len=ctx + 128 + 16, max_batch=B)
+    cache = model.create_cache(B)
+    g = torch.Generator(device=dev).manual_seed(2)
+    for t in (cache.flat_k, cache.flat_v):
+        for chunk in torch.split(t, 1 << 20):
+            chunk.normal_(generator=g)
+    seqs = [b for b in range(B) for _ in range(W)]
+    pos = [ctx + W - 1 - j for _ in range(B) for j in range(W)]
+    steps = [2 * j for _ in range(B) for j in range(W)]
+    tick = lambda i: model.core_union(cache, seqs, pos, steps)  # noqa: E731
+    timed(tick, 1)
+    ms = timed(tick, 5)
+    kv = sum(p + 1 for p in pos) * cfg.n_kv_heads * cfg.head_dim * 2 * 2 * cfg.n_core
+    res["extra"]["gqa_decode_tick"] = {"ms": round(ms, 3), "kv_GB": round(kv / 1e9, 2),
+                                       "note": "B=4 x W=16 rows at depths 0,2,..,30; 32k random-filled context"}
+    log(f"gqa tick: {ms:.2f} ms")
+    del model, cache
+    torch.cuda.empty_cache()
+
+
+def cpu_section(args, res, w=None):
+    """The oracle (numpy float32, this host's cores) on a bounded sample of the
+    bs=1 workload: WFD alpha=0.9 decode ticks over a random-filled 512-token
+    prompt cache (the oracle prefill of 512 x 68 layer passes is skipped)."""
+    import numpy as np
+    import torch
+
+    from oracle import scheduler as osched
+    from oracle.looped_lm import OracleBatchBlocks, OracleLM
+    from wavefront_decoding_amd import model as M
+
+    cfg = M.CONFIGS["looped-2048"]
+    w = w if w is not None else M.init_weights(cfg, 0)
+    L, N = 512, 8
+    s0t = lambda p: M.initial_state_tokens(cfg, [p])[0].numpy()  # noqa: E731
+    lm = OracleLM(cfg, M.weights_numpy(w), L + N + 8, 1, s0t, None)
+    rng = np.random.default_rng(0)
+    lm.Kc[:, :, :L] = rng.standard_normal(lm.Kc[:, :, :L].shape, dtype=np.float32)
+    lm.Vc[:, :, :L] = rng.standard_normal(lm.Vc[:, :, :L].shape, dtype=np.float32)
+
+    class Warm(OracleBatchBlocks):
+        def prefill(self, prompts):
+            logits = np.zeros((1, cfg.vocab_size), dtype=np.float32)
+            logits[0, 7] = 1.0
+            return self._Cache(), logits
+
+    t0 = time.perf_counter()
+    r = osched.wfd_batch(Warm(lm), [[0] * L], N, cfg.T_total, 2, [osched.Emu(0.9, 1000)])
+    dt = time.perf_counter() - t0
+    toks = len(r.per_seq[0].tokens) - 1  # the first token comes from the (skipped) prefill
+    res["cpu_baseline"] = {"value": round(toks / dt, 4), "unit": "tokens/s", "cores": os.cpu_count(),
+                           "kind": "port",
+                           "sample": (f"oracle WFD decode of {toks} tokens (alpha=0.9 emulated, T_total=16, T_draft=2, "
+                                      f"{r.n_r_calls} R ticks) on the 2048-d model in float32 over a random-filled "
+                                      f"512-token prompt cache; {dt:.1f} s; numpy threads = host default; "
+                                      f"cpu={platform.processor() or platform.machine()}")}
+    log(f"cpu: {res['cpu_baseline']}")
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is a design note "
+                                   "(no collectives are built)", "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+
+    import __graft_entry__
+
+    __graft_entry__.load_package()
+    from wavefront_decoding_amd import _lib
+
+    _lib.load()
+    dev = torch.device("cuda:0")
+    only = set(filter(None, args.only.split(",")))
+    want = lambda s: not only or s in only  # noqa: E731
+    res = {
+        "metric": "decode tokens/s bs=1 & bs=32 (looped LM); wavefront-attn HBM GB/s vs peak",
+        "value": None, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init weights N(0,0.02) seed 0, uniform random prompts seed 0)",
+        "config": {"workload": "looped-2048 bf16 bs=1 WFD decode: 512-token prompt, 256 new tokens, T_total=16, "
+                               "T_draft=2 (W=8), emulated acceptance 0.9; step = one 256-token decode",
+                   "model": "looped-2048 (d=2048, 16x128 heads, SwiGLU 5632, 2+4x16+2 layers, V=32000)",
+                   "global_batch": 1, "seq_len": 512 + 256, "parallelism": "single GPU"},
+        "roofline": None, "cpu_baseline": None, "extra": {},
+    }
+    w = None
+    if want("bs1"):
+        w = bs1_section(args, dev, res)
+    if want("attn"):
+        attn_section(args, dev, res)
+    if want("bs32") and not args.quick:
+        bs32_section(args, dev, res, w)
+    if want("gqa"):
+        gqa_section(args, dev, res)
+    if want("cpu") and not args.no_cpu:
+        cpu_section(args, res, w)
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()
