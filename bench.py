@@ -49,6 +49,7 @@ def parse():
     ap.add_argument("--quick", action="store_true", help="fewer extras (development)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--only", default="", help="comma list of sections: bs1,bs32,attn,gqa,cpu")
+    ap.add_argument("--eager", action="store_true", help="launch every pass eagerly (no hipGraph capture)")
     return ap.parse_args()
 
 
@@ -146,7 +147,7 @@ def bs1_section(args, dev, res):
     L, N, T_draft, alpha = 512, 256, 2, 0.9
     t0 = time.perf_counter()
     w = M.init_weights(cfg, 0)
-    model = LoopedModel(cfg, w, dev, max_seq_len=L + N + 16, max_batch=1)
+    model = LoopedModel(cfg, w, dev, max_seq_len=L + N + 16, max_batch=1, use_graphs=not args.eager)
     log(f"bs1: model ready in {time.perf_counter() - t0:.1f}s")
     prompt = torch.randint(0, cfg.vocab_size, (1, L), generator=torch.Generator().manual_seed(0))
     bb = LoopedBlocksBatch(model, batch_size=1)
@@ -220,7 +221,7 @@ def bs32_section(args, dev, res, w=None):
         glen = [x // 4 for x in glen]
     prompts = [torch.randint(0, cfg.vocab_size, (p,), generator=g).to(dev) for p in plen]
     w = w if w is not None else M.init_weights(cfg, 0)
-    model = LoopedModel(cfg, w, dev, max_seq_len=max(plen) + max(glen) + 16, max_batch=B)
+    model = LoopedModel(cfg, w, dev, max_seq_len=max(plen) + max(glen) + 16, max_batch=B, use_graphs=not args.eager)
     bb = LoopedBlocksBatch(model, batch_size=B)
     t0 = time.perf_counter()
     pf = prefill_once(bb, prompts)
@@ -304,7 +305,7 @@ def cpu_section(args, res, w=None):
 
     cfg = M.CONFIGS["looped-2048"]
     w = w if w is not None else M.init_weights(cfg, 0)
-    L, N = 512, 8
+    L, N = 512, 100
     s0t = lambda p: M.initial_state_tokens(cfg, [p])[0].numpy()  # noqa: E731
     lm = OracleLM(cfg, M.weights_numpy(w), L + N + 8, 1, s0t, None)
     rng = np.random.default_rng(0)

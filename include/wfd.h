@@ -85,7 +85,9 @@ int wfd_qkv_rope_append(const void* qkv, int64_t ldq, const int32_t* pos, const 
  * row-major. Epilogue WFD_EPI_SWIGLU: N = 2*pair_off, y[m, j] =
  * silu(g_j) * u_j with g_j = row j, u_j = row pair_off + j of the product.
  * out_dtype may be WFD_F32 for bf16 inputs (logits). K must be a multiple of
- * wfd_linear_k_multiple(dtype), N of 16.
+ * wfd_linear_k_multiple(dtype), N of 16. K is summed in fixed 128 (bf16) /
+ * 64 (fp32) element chunks, chunk partials added in chunk order, so y[m] does
+ * not depend on n or on where row m sits.
  * Replaces: the nn.Linear calls of the block forwards -- Wqkv, proj, the gated
  *   MLP, adapter, lm_head (src/decoding/huginn_blocks.py:79,100-102,216,291;
  *   huginn_blocks_batch.py:149,160-161,299,345).
@@ -95,9 +97,26 @@ int wfd_linear(const void* x, const int32_t* x_rows, int64_t ldx, const void* W,
                int K, int dtype, int out_dtype, int epilogue, int pair_off, wfd_stream_t stream);
 
 /*
+ * The fused q|k|v projection with wfd_qkv_rope_append as its epilogue:
+ * qkv = x[x_rows ? x_rows[i] : i] @ Wqkv^T, Wqkv ((H + 2*Hkv) * Dh, K), under
+ * wfd_linear's arithmetic contract; each qkv value is rounded to `dtype`, then
+ * rotated, written and appended exactly as wfd_qkv_rope_append does, so the
+ * result equals wfd_linear followed by wfd_qkv_rope_append bit for bit. The
+ * qkv rows themselves are never stored. Dh % 16 == 0, K as for wfd_linear.
+ * Replaces: the Wqkv projection + HuginnBlocks._qkv + the cache write
+ *   (src/decoding/huginn_blocks.py:77-87,96-97; huginn_blocks_batch.py:147-157,
+ *   308-310; graph_blocks.py:296-310).
+ */
+int wfd_linear_qkv_rope_append(const void* x, const int32_t* x_rows, int64_t ldx, const void* Wqkv, int n, int K,
+                               const int32_t* pos, const float* rope_cos, const float* rope_sin, int rope_rows,
+                               const int64_t* flat_row, void* q_out, void* k_cache, void* v_cache, int H, int Hkv,
+                               int Dh, int dtype, wfd_stream_t stream);
+
+/*
  * x_out[out_rows ? out_rows[i] : i] = rmsnorm(a[a_rows ? a_rows[i] : i] + res[i]) * w1
  * and, if w2, h_out[i] = rmsnorm(x_out row) * w2. res may be NULL (plain
- * RMSNorm). D <= 4096.
+ * RMSNorm). D <= 4096 and a multiple of 512 (bf16) / 256 (fp32); every row
+ * pointer 16-byte aligned. One wave per row: a row's bits never depend on n.
  * Replaces: the SandwichBlock residual norms `norm_2(att + x)`, `norm_3`,
  *   `norm_4(mlp + x)`, `norm_1` and `ln_f`
  *   (src/decoding/huginn_blocks.py:95,101-102,268,290;
@@ -124,7 +143,8 @@ int wfd_copy_rows(const void* src, const int32_t* src_rows, int64_t lds, void* d
                   int64_t ldd, int n, int width, int dtype, wfd_stream_t stream);
 
 /*
- * out[i] = argmax_j logits[i, j] (first index on ties), logits fp32.
+ * out[i] = argmax_j logits[i, j] (first index on ties), logits fp32, 16-byte
+ * aligned.
  * Replaces: greedy_sample's argmax (src/decoding/acceptance.py:40-44) and
  *   coda_argmax_union's argmax (src/decoding/huginn_blocks_batch.py:345-346).
  */

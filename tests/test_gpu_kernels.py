@@ -92,7 +92,7 @@ def test_attn_decode_kv_len_device_data(gpu):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("n,N,K", [(1, 2048, 2048), (8, 6144, 2048), (17, 64, 5632), (40, 512, 4096),
-                                   (300, 256, 1024), (3, 32000, 256)])
+                                   (300, 256, 1024), (3, 32000, 256), (16, 96, 6144), (5, 48, 8192)])
 def test_linear_matches_oracle(gpu, dtype, n, N, K):
     if K % ops.linear_k_multiple(dtype):
         pytest.skip("K not a multiple of the kernel granularity")
@@ -195,6 +195,40 @@ def test_qkv_rope_append(gpu, dtype, H, Hkv, Dh):
     assert kc[untouched].abs().sum().item() == 0 and vc[untouched].abs().sum().item() == 0
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("H,Hkv,Dh,K", [(16, 16, 128, 2048), (16, 4, 128, 2048), (4, 4, 64, 256)])
+@pytest.mark.parametrize("n", [1, 5, 16, 37])
+def test_linear_qkv_rope_append_fused(gpu, dtype, H, Hkv, Dh, K, n):
+    """The fused projection + RoPE + append equals linear() then
+    qkv_rope_append() bit for bit, in both the wide (n <= 16) and tile regimes,
+    with a gathered x, and touches no other cache row."""
+    g = torch.Generator().manual_seed(n * 7 + Dh)
+    S, rows = 96, 4 * 96
+    N = (H + 2 * Hkv) * Dh
+    X = torch.randn(n + 3, K, generator=g).to(dtype).to(gpu)
+    Wq = (torch.randn(N, K, generator=g) * K ** -0.5).to(dtype).to(gpu)
+    xr = torch.randperm(n + 3, generator=g)[:n].to(torch.int32).to(gpu)
+    pos = torch.randint(0, S, (n,), generator=g, dtype=torch.int32).to(gpu)
+    flat = (torch.randperm(rows, generator=g)[:n]).to(torch.int64).to(gpu)
+    cos, sin = (torch.from_numpy(t).to(gpu) for t in ok.rope_tables(S, Dh))
+    kc0 = torch.zeros(rows, Hkv, Dh, dtype=dtype, device=gpu)
+    vc0 = torch.zeros_like(kc0)
+    qkv = ops.linear(X, Wq, x_rows=xr)
+    q0 = ops.qkv_rope_append(qkv, pos, cos, sin, flat, kc0, vc0, H, Hkv, Dh)
+    kc1 = torch.zeros_like(kc0)
+    vc1 = torch.zeros_like(kc0)
+    q1 = ops.linear_qkv_rope_append(X, Wq, pos, cos, sin, flat, kc1, vc1, H, Hkv, Dh, x_rows=xr)
+    assert torch.equal(q0, q1)
+    assert torch.equal(kc0, kc1) and torch.equal(vc0, vc1)
+    # and against the oracle for one row
+    i = n - 1
+    ref = ok.linear(_np(X)[int(xr[i])][None], _np(Wq))[0]
+    p = int(pos[i])
+    assert rel_err(_np(q1[i]), ok.rope(ref[:H * Dh].reshape(H, Dh), p, cos.cpu().numpy(), sin.cpu().numpy())) \
+        <= TOL[dtype]
+    assert rel_err(_np(vc1[int(flat[i])]), ref[(H + Hkv) * Dh:].reshape(Hkv, Dh)) <= TOL[dtype]
+
+
 def test_kv_append_exact_rows(gpu):
     """Writes land at exactly the requested flat rows, bit for bit (the analogue
     of experiments/exp5_graph/verify_graph.py gate 1c)."""
@@ -241,3 +275,15 @@ def test_bad_arguments_raise(gpu):
     with pytest.raises(_lib.WfdError):
         ops.linear(torch.zeros(2, 100, device=gpu), torch.zeros(16, 100, device=gpu))
     assert math.isfinite(1.0)
+
+
+def test_linear_consecutive_shapes(gpu):
+    """Back-to-back launches of different widths, depths and row counts (both
+    kernel variants) each match the oracle."""
+    g = torch.Generator().manual_seed(21)
+    for N, K, n in [(2048, 2048, 1), (6144, 2048, 8), (512, 4096, 20), (32000, 256, 2), (2048, 5632, 3),
+                    (11264, 2048, 100)]:
+        x = torch.randn(n, K, generator=g).to(torch.bfloat16)
+        W = (0.02 * torch.randn(N, K, generator=g)).to(torch.bfloat16)
+        y = ops.linear(x.to(gpu), W.to(gpu))
+        assert rel_err(_np(y), ok.linear(_np(x), _np(W))) <= 2e-2, (N, K, n)

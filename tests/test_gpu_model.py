@@ -183,3 +183,35 @@ def test_2048_core_tick_matches_oracle(gpu):
     st = state.float().numpy()
     ref = np.stack([lm.core(0, pos[i], steps[i], st[i, : cfg.d_model], st[i, cfg.d_model:]) for i in range(8)])
     assert rel_err(got, ref) <= 2e-2
+
+
+@pytest.mark.parametrize("cfg", [TINY, MINI_BF16], ids=lambda c: c.name)
+def test_graph_mode_matches_eager(gpu, cfg):
+    """Captured decode passes (fixed tables refreshed per replay, padded rows
+    aimed at trash rows) commit exactly the eager tokens and counters; the
+    graphs replay many times with eager work and host syncs in between."""
+    w = M.init_weights(cfg, 2)
+    ids = _prompt(90, 11, V=cfg.vocab_size).to(gpu)
+    eager = LoopedBlocks(LoopedModel(cfg, w, gpu, max_seq_len=200, max_batch=1))
+    graph = LoopedBlocks(LoopedModel(cfg, w, gpu, max_seq_len=200, max_batch=1, use_graphs=True))
+    for T_draft in (1, 2):
+        a, ta = generate_wavefront_dynamic(eager, ids, 30, SsdPolicy(cfg.T_total, T_draft))
+        b, tb = generate_wavefront_dynamic(graph, ids, 30, SsdPolicy(cfg.T_total, T_draft))
+        assert a == b and ta.counters() == tb.counters(), T_draft
+    assert len(graph.model._graphs) >= 3
+    ar_e, _ = eager.ar_generate(ids, 12)
+    ar_g, _ = graph.ar_generate(ids, 12)
+    assert ar_e == ar_g
+
+
+def test_graph_mode_batch_emulated(gpu):
+    cfg = TINY
+    w = M.init_weights(cfg, 0)
+    P = [_prompt(40, 4), _prompt(25, 5), _prompt(33, 6)]
+    res = []
+    for graphs in (False, True):
+        bb = LoopedBlocksBatch(LoopedModel(cfg, w, gpu, max_seq_len=128, max_batch=3, use_graphs=graphs))
+        emus = [EmulatedAcceptance(0.7, 1000 + b) for b in range(3)]
+        bt = generate_wavefront_batch(bb, [p.to(gpu) for p in P], [10, 14, 7], SsdPolicy(cfg.T_total, 2), emus)
+        res.append([(s.tokens, s.counters()) for s in bt.per_seq])
+    assert res[0] == res[1]

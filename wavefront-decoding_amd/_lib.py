@@ -40,6 +40,8 @@ SIGNATURES: dict[str, tuple] = {
                                    _i32, _vp]),
     "wfd_linear_k_multiple": (_i32, [_i32]),
     "wfd_linear": (_i32, [_vp, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
+    "wfd_linear_qkv_rope_append": (_i32, [_vp, _vp, _i64, _vp, _i32, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp,
+                                          _i32, _i32, _i32, _i32, _vp]),
     "wfd_add_rmsnorm": (_i32, [_vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i32, _i32, _f32,
                                _i32, _vp]),
     "wfd_embed": (_i32, [_vp, _vp, _f32, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),

@@ -85,10 +85,16 @@ class LoopedBlocks(RecursiveBlocks):
 
     @torch.no_grad()
     def prefill(self, input_ids: torch.Tensor, T_total: int, T_draft: int):
+        """Prompt prefill into this blocks object's cache. The cache is allocated
+        once and reused by every generation (its lengths are reset here), so
+        captured decode graphs stay valid; one generation at a time."""
         if T_total != self.T_total:
             raise AssertionError("Prefill T_total must match the blocks' T_total")
         ids = input_ids.reshape(-1).tolist()
-        cache = self.create_cache()
+        if getattr(self, "_cache", None) is None:
+            self._cache = self.create_cache()
+        cache = self._cache
+        cache.reset_lengths()
         logits = self.model.prefill_seq(cache, 0, ids)
         L = len(ids)
         cache._seen_tokens = L
@@ -239,7 +245,11 @@ class LoopedBlocksBatch:
         seqs = [row for row in input_ids] if not isinstance(input_ids, (list, tuple)) else list(input_ids)
         if len(seqs) != self.B:
             raise AssertionError(f"prefill expects B={self.B} prompts, got {len(seqs)}")
-        cache = self.create_cache()
+        # one cache per blocks object, reused across generations (keeps captured graphs valid)
+        if getattr(self, "_cache", None) is None:
+            self._cache = self.create_cache()
+        cache = self._cache
+        cache.reset_lengths()
         last = torch.stack([self.model.prefill_seq(cache, b, torch.as_tensor(s).reshape(-1).tolist())
                             for b, s in enumerate(seqs)])
         return cache, last

@@ -42,63 +42,72 @@ int launch_status(const char* what) {
 }
 
 constexpr int kRowThreads = 256;
-constexpr int kMaxRowElems = 16;  // elements per thread -> D <= 4096
+constexpr int kNormMaxD = 4096;
 
-__device__ __forceinline__ float block_sum_256(float v, float* scratch) {
-  v = wave_sum(v);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  __syncthreads();
-  if (lane == 0) scratch[wave] = v;
-  __syncthreads();
-  const float s = ((scratch[0] + scratch[1]) + scratch[2]) + scratch[3];
-  return s;
-}
-
+// One wave per row, 16-byte vector loads; each lane owns D/64 consecutive-vector
+// elements. Sum of squares: lane-sequential, then a fixed xor butterfly, so a
+// row's result does not depend on the other rows of the launch.
 template <typename T>
-__global__ __launch_bounds__(kRowThreads) void add_rmsnorm_kernel(
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(
     const T* __restrict__ a, const int32_t* __restrict__ a_rows, int64_t lda, const T* __restrict__ res,
     int64_t ldr, const T* __restrict__ w1, const T* __restrict__ w2, T* __restrict__ x_out,
-    const int32_t* __restrict__ out_rows, int64_t ldo, T* __restrict__ h_out, int64_t ldh, int D, float eps) {
-  __shared__ float scratch[4];
-  const int i = blockIdx.x;
+    const int32_t* __restrict__ out_rows, int64_t ldo, T* __restrict__ h_out, int64_t ldh, int n, int D, float eps) {
+  constexpr int V = Elem<T>::kVec;
+  constexpr int MAXJ = kNormMaxD / (64 * V);
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (i >= n) return;  // no barriers below
+  const int nj = D / (64 * V);
   const int64_t ar = a_rows ? a_rows[i] : i;
   const int64_t orow = out_rows ? out_rows[i] : i;
-  float v[kMaxRowElems];
+  float v[MAXJ][V];
   float ss = 0.f;
 #pragma unroll
-  for (int k = 0; k < kMaxRowElems; ++k) {
-    const int e = threadIdx.x + k * kRowThreads;
-    float s = 0.f;
-    if (e < D) {
-      s = Elem<T>::load(a + ar * lda + e);
-      if (res) s += Elem<T>::load(res + (int64_t)i * ldr + e);
+  for (int j = 0; j < MAXJ; ++j) {
+    if (j < nj) {
+      const int e = (j * 64 + lane) * V;
+      Elem<T>::unpack(ld16(a + ar * lda + e), v[j]);
+      if (res) {
+        float r[V];
+        Elem<T>::unpack(ld16(res + (int64_t)i * ldr + e), r);
+#pragma unroll
+        for (int k = 0; k < V; ++k) v[j][k] += r[k];
+      }
+#pragma unroll
+      for (int k = 0; k < V; ++k) ss = fmaf(v[j][k], v[j][k], ss);
     }
-    v[k] = s;
-    ss = fmaf(s, s, ss);
   }
-  float tot = block_sum_256(ss, scratch);
-  float inv = 1.0f / sqrtf(tot / (float)D + eps);
+  float inv = 1.0f / sqrtf(wave_sum(ss) / (float)D + eps);
   float ss2 = 0.f;
 #pragma unroll
-  for (int k = 0; k < kMaxRowElems; ++k) {
-    const int e = threadIdx.x + k * kRowThreads;
-    if (e < D) {
-      const float yv = v[k] * inv * Elem<T>::load(w1 + e);
+  for (int j = 0; j < MAXJ; ++j) {
+    if (j < nj) {
+      const int e = (j * 64 + lane) * V;
+      float w[V];
+      Elem<T>::unpack(ld16(w1 + e), w);
       T* dst = x_out + orow * ldo + e;
-      Elem<T>::store(dst, yv);
-      // Continue from the stored (rounded) value so the fused second norm
-      // equals a separate rmsnorm() call on x_out.
-      v[k] = Elem<T>::load(dst);
-      ss2 = fmaf(v[k], v[k], ss2);
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        Elem<T>::store(dst + k, v[j][k] * inv * w[k]);
+        // continue from the stored (rounded) value: the fused second norm then
+        // equals a separate rmsnorm() of x_out
+        v[j][k] = Elem<T>::round(v[j][k] * inv * w[k]);
+        ss2 = fmaf(v[j][k], v[j][k], ss2);
+      }
     }
   }
-  if (w2 == nullptr) return;  // uniform
-  tot = block_sum_256(ss2, scratch);
-  inv = 1.0f / sqrtf(tot / (float)D + eps);
+  if (w2 == nullptr) return;
+  inv = 1.0f / sqrtf(wave_sum(ss2) / (float)D + eps);
 #pragma unroll
-  for (int k = 0; k < kMaxRowElems; ++k) {
-    const int e = threadIdx.x + k * kRowThreads;
-    if (e < D) Elem<T>::store(h_out + (int64_t)i * ldh + e, v[k] * inv * Elem<T>::load(w2 + e));
+  for (int j = 0; j < MAXJ; ++j) {
+    if (j < nj) {
+      const int e = (j * 64 + lane) * V;
+      float w[V];
+      Elem<T>::unpack(ld16(w2 + e), w);
+      T* dst = h_out + (int64_t)i * ldh + e;
+#pragma unroll
+      for (int k = 0; k < V; ++k) Elem<T>::store(dst + k, v[j][k] * inv * w[k]);
+    }
   }
 }
 
@@ -121,8 +130,8 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
     const float x1 = Elem<T>::load(src + head * Dh + 2 * j + 1);
     const float c = cos_t[(int64_t)p * half + j];
     const float s = sin_t[(int64_t)p * half + j];
-    const float y0 = x0 * c - x1 * s;
-    const float y1 = x0 * s + x1 * c;
+    const float y0 = fmaf(x0, c, -(x1 * s));
+    const float y1 = fmaf(x0, s, x1 * c);
     T* dst = head < H ? q_out + ((int64_t)i * H + head) * Dh + 2 * j
                       : kc + fr * (int64_t)Hkv * Dh + (int64_t)(head - H) * Dh + 2 * j;
     Elem<T>::store(dst, y0);
@@ -171,38 +180,49 @@ __global__ __launch_bounds__(kRowThreads) void copy_rows_kernel(const T* __restr
   for (int e = threadIdx.x; e < width; e += kRowThreads) dst[dr * ldd + e] = src[sr * lds + e];
 }
 
-__global__ __launch_bounds__(kRowThreads) void argmax_kernel(const float* __restrict__ logits, int64_t ld,
-                                                             int64_t* __restrict__ out, int Vocab) {
-  __shared__ float sv[kRowThreads];
-  __shared__ int si[kRowThreads];
+constexpr int kArgThreads = 1024;
+
+__device__ __forceinline__ void argmax_merge(float& bv, int& bi, float ov, int oi) {
+  if (ov > bv || (ov == bv && oi < bi)) {
+    bv = ov;
+    bi = oi;
+  }
+}
+
+// One 1024-thread workgroup per row; first index wins ties (as torch.argmax).
+__global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float* __restrict__ logits, int64_t ld,
+                                                            int64_t* __restrict__ out, int Vocab) {
+  __shared__ float sv[kArgThreads / 64];
+  __shared__ int si[kArgThreads / 64];
   const int i = blockIdx.x;
   const float* row = logits + (int64_t)i * ld;
   float best = -INFINITY;
   int bi = 0x7fffffff;
-  for (int e = threadIdx.x; e < Vocab; e += kRowThreads) {
-    const float x = row[e];
-    if (x > best || bi == 0x7fffffff) {  // strictly greater: first index wins ties
-      best = x;
-      bi = e;
-    }
+  const int nv = ((ld & 3) == 0) ? Vocab / 4 : 0;  // 16-byte loads when rows stay aligned
+  for (int q = threadIdx.x; q < nv; q += kArgThreads) {
+    const u32x4 w = ld16(row + 4 * q);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) argmax_merge(best, bi, __uint_as_float(w[k]), 4 * q + k);
   }
-  sv[threadIdx.x] = best;
-  si[threadIdx.x] = bi;
+  for (int e = 4 * nv + threadIdx.x; e < Vocab; e += kArgThreads) argmax_merge(best, bi, row[e], e);
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ov = __shfl_xor(best, m, 64);
+    const int oi = __shfl_xor(bi, m, 64);
+    argmax_merge(best, bi, ov, oi);
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    sv[wave] = best;
+    si[wave] = bi;
+  }
   __syncthreads();
-  for (int stride = kRowThreads / 2; stride >= 1; stride >>= 1) {
-    if (threadIdx.x < stride) {
-      const float ov = sv[threadIdx.x + stride];
-      const int oi = si[threadIdx.x + stride];
-      const float mv = sv[threadIdx.x];
-      const int mi = si[threadIdx.x];
-      if (ov > mv || (ov == mv && oi < mi)) {
-        sv[threadIdx.x] = ov;
-        si[threadIdx.x] = oi;
-      }
-    }
-    __syncthreads();
+  if (threadIdx.x == 0) {
+    float b = sv[0];
+    int ix = si[0];
+    for (int w = 1; w < kArgThreads / 64; ++w) argmax_merge(b, ix, sv[w], si[w]);
+    out[i] = (int64_t)ix;
   }
-  if (threadIdx.x == 0) out[i] = (int64_t)si[0];
 }
 
 }  // namespace wfd
@@ -217,8 +237,15 @@ int wfd_add_rmsnorm(const void* a, const int32_t* a_rows, int64_t lda, const voi
                     const void* w2, void* x_out, const int32_t* out_rows, int64_t ldo, void* h_out, int64_t ldh, int n,
                     int D, float eps, int dtype, hipStream_t stream) {
   using namespace wfd;
-  if (n < 0 || D <= 0 || D > kRowThreads * kMaxRowElems) {
-    set_error("wfd_add_rmsnorm: bad shape n=%d D=%d (D <= %d)", n, D, kRowThreads * kMaxRowElems);
+  const int vec = dtype == kBF16 ? Elem<bf16_t>::kVec : Elem<float>::kVec;
+  if (n < 0 || D <= 0 || D > kNormMaxD || D % (64 * vec) != 0) {
+    set_error("wfd_add_rmsnorm: bad shape n=%d D=%d (D <= %d, multiple of %d)", n, D, kNormMaxD, 64 * vec);
+    return kBadArg;
+  }
+  const int esz = dtype == kBF16 ? 2 : 4;
+  if ((((uintptr_t)a | (uintptr_t)res | (uintptr_t)w1 | (uintptr_t)w2 | (uintptr_t)x_out | (uintptr_t)h_out) & 15) ||
+      ((lda * esz) & 15) || (res && ((ldr * esz) & 15)) || ((ldo * esz) & 15) || (h_out && ((ldh * esz) & 15))) {
+    set_error("wfd_add_rmsnorm: rows must be 16-byte aligned");
     return kBadArg;
   }
   if (n == 0) return kOk;
@@ -227,13 +254,13 @@ int wfd_add_rmsnorm(const void* a, const int32_t* a_rows, int64_t lda, const voi
     return kBadArg;
   }
   if (dtype == kBF16)
-    hipLaunchKernelGGL(add_rmsnorm_kernel<bf16_t>, dim3(n), dim3(kRowThreads), 0, stream, (const bf16_t*)a, a_rows,
+    hipLaunchKernelGGL(add_rmsnorm_kernel<bf16_t>, dim3((n + 3) / 4), dim3(256), 0, stream, (const bf16_t*)a, a_rows,
                        lda, (const bf16_t*)res, ldr, (const bf16_t*)w1, (const bf16_t*)w2, (bf16_t*)x_out, out_rows,
-                       ldo, (bf16_t*)h_out, ldh, D, eps);
+                       ldo, (bf16_t*)h_out, ldh, n, D, eps);
   else if (dtype == kF32)
-    hipLaunchKernelGGL(add_rmsnorm_kernel<float>, dim3(n), dim3(kRowThreads), 0, stream, (const float*)a, a_rows, lda,
-                       (const float*)res, ldr, (const float*)w1, (const float*)w2, (float*)x_out, out_rows, ldo,
-                       (float*)h_out, ldh, D, eps);
+    hipLaunchKernelGGL(add_rmsnorm_kernel<float>, dim3((n + 3) / 4), dim3(256), 0, stream, (const float*)a, a_rows,
+                       lda, (const float*)res, ldr, (const float*)w1, (const float*)w2, (float*)x_out, out_rows, ldo,
+                       (float*)h_out, ldh, n, D, eps);
   else {
     set_error("wfd_add_rmsnorm: unsupported dtype %d", dtype);
     return kUnsupported;
@@ -355,7 +382,11 @@ int wfd_argmax(const float* logits, int64_t ld, int64_t* out, int n, int vocab, 
     set_error("wfd_argmax: null pointer argument");
     return kBadArg;
   }
-  hipLaunchKernelGGL(argmax_kernel, dim3(n), dim3(kRowThreads), 0, stream, logits, ld, out, vocab);
+  if (((uintptr_t)logits) & 15) {
+    set_error("wfd_argmax: logits must be 16-byte aligned");
+    return kBadArg;
+  }
+  hipLaunchKernelGGL(argmax_kernel, dim3(n), dim3(kArgThreads), 0, stream, logits, ld, out, vocab);
   return launch_status("wfd_argmax");
 }
 

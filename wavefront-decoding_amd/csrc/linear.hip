@@ -6,161 +6,312 @@
 // rows while W is 4-128 MB, so the layer is a weight stream: each weight byte
 // is read from HBM once per launch.
 //
-// Work split: a workgroup owns NT tiles of 16 output features and all rows;
-// its 8 waves split K into 8 fixed contiguous ranges. A wave keeps a chunk of
-// its weight fragment in registers and sweeps every 16-row M-tile of x over
-// it (x comes from L2), accumulating one MFMA per k-step in k order. The 8
-// wave partials are summed through LDS in wave order. The k partition and the
-// summation order depend only on K, so y[m] is bit-identical whatever n is and
-// wherever row m sits -- the property sequential and wavefront decode need to
-// agree token for token.
+// Arithmetic contract (depends on K and the dtype only, never on n or on how
+// the work is split): K is cut into P = K / KC chunks of 4 MFMA k-steps
+// (KC = 128 bf16 / 64 fp32 elements); a chunk partial is the MFMA chain over
+// its 4 steps starting from zero; y = epilogue(((0 + c_0) + c_1) + ... + c_{P-1})
+// in fp32. Two kernels honour it bit for bit:
 //
-// Epilogues: plain store (bf16 or fp32 out) and SwiGLU, where tile 0 is the
+//  * wide (n <= 16): one 1024-thread workgroup per 16-column tile; its 16
+//    waves take the chunks round-robin (all loads of a wave issued together),
+//    park the chunk partials in LDS, and threads sum them in chunk order.
+//    No cross-workgroup synchronization: the column tile's whole K is reduced
+//    inside one workgroup.
+//  * tile (n > 16): a workgroup owns 64 rows x 32 columns; each of its 4 waves
+//    walks the chunks in order for one 16-row tile and two column tiles, with
+//    a two-stage register pipeline (chunk p+1 in flight while chunk p runs on
+//    MFMA). The waves of a workgroup read the same weight fragments, so the
+//    weights stream from HBM once per 64 rows.
+//
+// So y[m] is bit-identical whatever n is and wherever row m sits -- the
+// property that keeps wavefront decode token-identical to sequential decode.
+//
+// Epilogues: plain store (bf16 or fp32 out); SwiGLU, where tile 0 is the
 // gate feature block and tile 1 the matching up block `pair_off` rows below
-// it: out = silu(gate) * up.
+// it: out = silu(gate) * up; and QKV-RoPE-append, for the fused q|k|v
+// projection: the output row is rounded to the element type, q and k heads are
+// rotated by the row's position (interleaved pairs: columns 2j and 2j+1 sit in
+// one 16-column tile, so the partner value is one lane shuffle away), q goes to
+// q_out and k, v are written straight into the slot cache row flat_row[m]
+// (src/decoding/huginn_blocks.py:77-87 + kv_cache.py:97-104 fused into the
+// projection; the separate qkv_rope_append pass and its qkv round trip vanish).
 #include "wfd_common.h"
 
 namespace wfd {
 
-constexpr int kLinWaves = 8;
-enum Epilogue : int { kEpiPlain = 0, kEpiSwiGLU = 1 };
+constexpr int kChunkSteps = 4;
+constexpr int kWideWaves = 16;
+constexpr int kWideMaxChunksPerWave = 3;
+constexpr int kWideMaxRows = 16;
+enum Epilogue : int { kEpiPlain = 0, kEpiSwiGLU = 1, kEpiRope = 2 };
 
-template <typename T, typename TO, int NT, int EPI, int MT, int CH>
-__global__ __launch_bounds__(64 * kLinWaves) void linear_kernel(const T* __restrict__ x,
-                                                                const int32_t* __restrict__ x_rows, int64_t ldx,
-                                                                const T* __restrict__ W, TO* __restrict__ y,
-                                                                int64_t ldy, int n, int K, int pair_off) {
-  constexpr int V = Elem<T>::kVec;
-  constexpr int KSTEP = 4 * V;
-  __shared__ float red[kLinWaves][NT][64][4];
+// Operands of the QKV-RoPE-append epilogue (unused by the others).
+struct RopeArgs {
+  const int32_t* pos;       // [n] positions (clamped into the table)
+  const float* cos_t;       // [rows, Dh/2]
+  const float* sin_t;       // [rows, Dh/2]
+  int tab_rows;
+  const int64_t* flat_row;  // [n] slot-cache row of each token
+  void* q_out;              // [n, H, Dh]
+  void* k_cache;            // [rows, Hkv, Dh]
+  void* v_cache;
+  int H, Hkv, Dh;
+};
 
+template <typename T>
+struct LinTraits {
+  static constexpr int V = Elem<T>::kVec;
+  static constexpr int KSTEP = 4 * V;             // k elements per MFMA step
+  static constexpr int KC = KSTEP * kChunkSteps;  // k elements per chunk
+};
+
+// Column start of tile t (0..NT-1) of column group g.
+template <int NT, int EPI>
+__device__ __forceinline__ int tile_col(int g, int t, int pair_off) {
+  if (EPI == kEpiSwiGLU) return (t == 0 ? 0 : pair_off) + g * 16;
+  return (g * NT + t) * 16;
+}
+
+template <typename TO, int EPI>
+__device__ __forceinline__ void store_elem(TO* __restrict__ y, int64_t ldy, int row, int col, float v0, float v1) {
+  if (EPI == kEpiSwiGLU)
+    Elem<TO>::store(y + (int64_t)row * ldy + col, (v0 / (1.0f + expf(-v0))) * v1);
+  else
+    Elem<TO>::store(y + (int64_t)row * ldy + col, v0);
+}
+
+// Value v0 of output (row, col) and its RoPE partner v1 = value of column col ^ 1.
+template <typename TO>
+__device__ __forceinline__ void store_rope(const RopeArgs& ra, int row, int col, float v0, float v1) {
+  const int head = col / ra.Dh;
+  const int d = col - head * ra.Dh;
+  TO* dst;
+  float out;
+  if (head >= ra.H + ra.Hkv) {
+    dst = (TO*)ra.v_cache + ra.flat_row[row] * (int64_t)(ra.Hkv * ra.Dh) + (head - ra.H - ra.Hkv) * ra.Dh + d;
+    out = v0;
+  } else {
+    int p = ra.pos[row];
+    p = p < 0 ? 0 : (p >= ra.tab_rows ? ra.tab_rows - 1 : p);
+    const int half = ra.Dh >> 1;
+    const float c = ra.cos_t[(int64_t)p * half + (d >> 1)];
+    const float s = ra.sin_t[(int64_t)p * half + (d >> 1)];
+    const float xm = Elem<TO>::round(v0);
+    const float xp = Elem<TO>::round(v1);
+    out = (d & 1) ? fmaf(xp, s, xm * c) : fmaf(xm, c, -(xp * s));
+    dst = head < ra.H ? (TO*)ra.q_out + ((int64_t)row * ra.H + head) * ra.Dh + d
+                      : (TO*)ra.k_cache + ra.flat_row[row] * (int64_t)(ra.Hkv * ra.Dh) + (head - ra.H) * ra.Dh + d;
+  }
+  Elem<TO>::store(dst, out);
+}
+
+template <typename T, int NT>
+__device__ __forceinline__ void load_w(u32x4 (&wf)[NT][kChunkSteps], const T* const (&wrow)[NT], int p) {
+  constexpr int KSTEP = LinTraits<T>::KSTEP;
+#pragma unroll
+  for (int s = 0; s < kChunkSteps; ++s)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) wf[t][s] = ld16(wrow[t] + (int64_t)(p * kChunkSteps + s) * KSTEP);
+}
+
+template <typename T>
+__device__ __forceinline__ void load_x(u32x4 (&xf)[kChunkSteps], const T* xp, bool valid, int p) {
+  constexpr int KSTEP = LinTraits<T>::KSTEP;
+#pragma unroll
+  for (int s = 0; s < kChunkSteps; ++s) xf[s] = valid ? ld16(xp + (int64_t)(p * kChunkSteps + s) * KSTEP) : zero16();
+}
+
+template <typename T, int NT>
+__device__ __forceinline__ void chunk_mma(f32x4 (&acc)[NT], const u32x4 (&xf)[kChunkSteps],
+                                          const u32x4 (&wf)[NT][kChunkSteps]) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < kChunkSteps; ++s)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = mfma_step<T>(xf[s], wf[t][s], acc[t]);
+}
+
+// ---------------------------------------------------------------------------
+// wide: grid (groups), 1024 threads; NT = 2 only for SwiGLU (gate + up tiles).
+template <typename T, typename TO, int NT, int EPI, int MC>
+__global__ __launch_bounds__(64 * kWideWaves) void linear_wide_kernel(
+    const T* __restrict__ x, const int32_t* __restrict__ x_rows, int64_t ldx, const T* __restrict__ W,
+    TO* __restrict__ y, int64_t ldy, int n, int K, int pair_off, const RopeArgs ra) {
+  extern __shared__ f32x4 red[];  // [P][NT][64 lanes]
+  constexpr int V = LinTraits<T>::V;
+  const int P = K / LinTraits<T>::KC;
+  const int g = blockIdx.x;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int col = lane & 15;
   const int grp = lane >> 4;
-  const int spw = K / (KSTEP * kLinWaves);  // k-steps per wave
-  const int s0 = wave * spw;
 
-  int c0[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    if (EPI == kEpiSwiGLU)
-      c0[t] = (t == 0 ? 0 : pair_off) + blockIdx.x * 16;
-    else
-      c0[t] = (blockIdx.x * NT + t) * 16;
-  }
+  const int xr = col < n ? (x_rows ? x_rows[col] : col) : -1;  // first: never waits behind the weights
   const T* wrow[NT];
 #pragma unroll
-  for (int t = 0; t < NT; ++t) wrow[t] = W + (int64_t)(c0[t] + col) * K + grp * V;
+  for (int t = 0; t < NT; ++t) wrow[t] = W + (int64_t)(tile_col<NT, EPI>(g, t, pair_off) + col) * K + grp * V;
+  const T* xp = x + (int64_t)(xr < 0 ? 0 : xr) * ldx + grp * V;
 
-  for (int rb = 0; rb < n; rb += MT * 16) {
-    f32x4 acc[MT][NT];
+  u32x4 wf[MC][NT][kChunkSteps];
+  u32x4 xf[MC][kChunkSteps];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int t = 0; t < NT; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    int xr[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int row = rb + mt * 16 + col;
-      xr[mt] = row < n ? (x_rows ? x_rows[row] : row) : -1;
+  for (int j = 0; j < MC; ++j) {
+    const int p = wave + kWideWaves * j;
+    if (p < P) {
+      load_w<T, NT>(wf[j], wrow, p);
+      load_x<T>(xf[j], xp, xr >= 0, p);
     }
-
-    for (int ch = 0; ch < spw; ch += CH) {
-      u32x4 wf[NT][CH];
+  }
 #pragma unroll
-      for (int s = 0; s < CH; ++s)
+  for (int j = 0; j < MC; ++j) {
+    const int p = wave + kWideWaves * j;
+    if (p < P) {
+      f32x4 acc[NT];
+      chunk_mma<T, NT>(acc, xf[j], wf[j]);
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
-          wf[t][s] = (ch + s < spw) ? ld16(wrow[t] + (int64_t)(s0 + ch + s) * KSTEP) : zero16();
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        if (rb + mt * 16 >= n) break;  // uniform across the workgroup
-        u32x4 xf[CH];
-        const T* xp = x + (int64_t)(xr[mt] < 0 ? 0 : xr[mt]) * ldx + grp * V;
-#pragma unroll
-        for (int s = 0; s < CH; ++s)
-          xf[s] = (xr[mt] >= 0 && ch + s < spw) ? ld16(xp + (int64_t)(s0 + ch + s) * KSTEP) : zero16();
-#pragma unroll
-        for (int s = 0; s < CH; ++s) {
-          if (ch + s < spw) {
-#pragma unroll
-            for (int t = 0; t < NT; ++t) acc[mt][t] = mfma_step<T>(xf[s], wf[t][s], acc[mt][t]);
-          }
-        }
-      }
+      for (int t = 0; t < NT; ++t) red[(p * NT + t) * 64 + lane] = acc[t];
     }
+  }
+  __syncthreads();
 
-    // Reduce the 8 wave partials of each M-tile in wave order, then store.
+  // threads 0..255: one (lane', r) output each; sum chunk partials in chunk order
+  if (threadIdx.x < 256) {
+    const int ln = threadIdx.x >> 2;
+    const int r = threadIdx.x & 3;
+    const int row = 4 * (ln >> 4) + r;
+    const float* rf = reinterpret_cast<const float*>(red);
+    float v[NT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      if (rb + mt * 16 >= n) break;
-      __syncthreads();
+    for (int t = 0; t < NT; ++t) v[t] = 0.f;
+    for (int p = 0; p < P; ++p)
 #pragma unroll
-      for (int t = 0; t < NT; ++t)
+      for (int t = 0; t < NT; ++t) v[t] += rf[((p * NT + t) * 64 + ln) * 4 + r];
+    // column ln ^ 1 lives in thread threadIdx.x ^ 4 (all 256 threads take part)
+    const float partner = EPI == kEpiRope ? __shfl_xor(v[0], 4, 64) : 0.f;
+    if (row < n) {
+      if (EPI == kEpiSwiGLU)
+        store_elem<TO, EPI>(y, ldy, row, g * 16 + (ln & 15), v[0], v[NT - 1]);
+      else if (EPI == kEpiRope)
+        store_rope<TO>(ra, row, g * 16 + (ln & 15), v[0], partner);
+      else
+        store_elem<TO, EPI>(y, ldy, row, g * 16 + (ln & 15), v[0], 0.f);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// tile: grid (ceil(n/64), ceil(groups/NB)), 256 threads; wave = 16-row tile,
+// NB column groups per workgroup.
+template <typename T, typename TO, int NT, int EPI, int NB>
+__global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ x, const int32_t* __restrict__ x_rows,
+                                                          int64_t ldx, const T* __restrict__ W, TO* __restrict__ y,
+                                                          int64_t ldy, int n, int K, int pair_off, int groups,
+                                                          const RopeArgs ra) {
+  constexpr int V = LinTraits<T>::V;
+  constexpr int NC = NB * NT;  // weight tiles per wave
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const int row0 = (blockIdx.x * 4 + wave) * 16;
+  if (row0 >= n) return;  // no barriers in this kernel
+  const int P = K / LinTraits<T>::KC;
+  const int row = row0 + col;
+  const bool valid = row < n;
+  const int xr = valid ? (x_rows ? x_rows[row] : row) : 0;
+
+  const T* wrow[NC];
+  bool gok[NB];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[wave][t][lane][r] = acc[mt][t][r];
-      __syncthreads();
-      const int tid = threadIdx.x;
-      const int nthreads_out = (EPI == kEpiSwiGLU) ? 256 : 256 * NT;
-      if (tid < nthreads_out) {
-        const int t = (EPI == kEpiSwiGLU) ? 0 : tid >> 8;
-        const int ln = (tid & 255) >> 2;
-        const int r = tid & 3;
-        const int m = 4 * (ln >> 4) + r;
-        const int cc = ln & 15;
-        const int row = rb + mt * 16 + m;
-        if (row < n) {
-          float v0 = 0.f;
+  for (int b = 0; b < NB; ++b) {
+    const int g = blockIdx.y * NB + b;
+    gok[b] = g < groups;
+    const int gg = gok[b] ? g : 0;
 #pragma unroll
-          for (int w = 0; w < kLinWaves; ++w) v0 += red[w][t][ln][r];
-          float res;
-          if (EPI == kEpiSwiGLU) {
-            float v1 = 0.f;
+    for (int t = 0; t < NT; ++t) wrow[b * NT + t] = W + (int64_t)(tile_col<NT, EPI>(gg, t, pair_off) + col) * K + grp * V;
+  }
+  const T* xp = x + (int64_t)xr * ldx + grp * V;
+
+  f32x4 tot[NC];
 #pragma unroll
-            for (int w = 0; w < kLinWaves; ++w) v1 += red[w][NT - 1][ln][r];
-            res = (v0 / (1.0f + expf(-v0))) * v1;
-          } else {
-            res = v0;
-          }
-          const int outc = (EPI == kEpiSwiGLU) ? (blockIdx.x * 16 + cc) : (c0[t] + cc);
-          Elem<TO>::store(y + (int64_t)row * ldy + outc, res);
-        }
-      }
+  for (int c = 0; c < NC; ++c) tot[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  u32x4 wa[NC][kChunkSteps], wb[NC][kChunkSteps], xa[kChunkSteps], xb[kChunkSteps];
+  load_w<T, NC>(wa, wrow, 0);
+  load_x<T>(xa, xp, valid, 0);
+  for (int p = 0; p < P; p += 2) {
+    if (p + 1 < P) {
+      load_w<T, NC>(wb, wrow, p + 1);
+      load_x<T>(xb, xp, valid, p + 1);
+    }
+    f32x4 acc[NC];
+    chunk_mma<T, NC>(acc, xa, wa);
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) tot[c][r] += acc[c][r];
+    if (p + 1 >= P) break;
+    if (p + 2 < P) {
+      load_w<T, NC>(wa, wrow, p + 2);
+      load_x<T>(xa, xp, valid, p + 2);
+    }
+    chunk_mma<T, NC>(acc, xb, wb);
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) tot[c][r] += acc[c][r];
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    if (!gok[b]) continue;
+    const int g = blockIdx.y * NB + b;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int orow = row0 + 4 * grp + r;
+      // column col ^ 1 lives in lane ^ 1 (the whole wave takes part)
+      const float partner = EPI == kEpiRope ? __shfl_xor(tot[b * NT][r], 1, 64) : 0.f;
+      if (orow >= n) continue;
+      if (EPI == kEpiRope)
+        store_rope<TO>(ra, orow, g * 16 + col, tot[b * NT][r], partner);
+      else if (EPI == kEpiSwiGLU)
+        store_elem<TO, EPI>(y, ldy, orow, g * 16 + col, tot[b * NT][r], tot[b * NT + NT - 1][r]);
+      else
+        store_elem<TO, EPI>(y, ldy, orow, tile_col<NT, EPI>(g, 0, pair_off) + col, tot[b * NT][r], 0.f);
     }
   }
 }
 
 template <typename T, typename TO, int NT, int EPI>
-static void launch_linear_mt(const void* x, const int32_t* xr, int64_t ldx, const void* W, void* y, int64_t ldy,
-                             int n, int N, int K, int pair_off, hipStream_t st) {
-  const int groups = (EPI == kEpiSwiGLU) ? pair_off / 16 : N / (16 * NT);
-  const dim3 grid(groups), block(64 * kLinWaves);
-  // MT only changes how many M-tiles share one weight chunk; per-row
-  // arithmetic (k order, wave order) is identical in every variant.
-  if (n <= 16)
-    hipLaunchKernelGGL((linear_kernel<T, TO, NT, EPI, 1, 8>), grid, block, 0, st, (const T*)x, xr, ldx, (const T*)W,
-                       (TO*)y, ldy, n, K, pair_off);
-  else if (n <= 32)
-    hipLaunchKernelGGL((linear_kernel<T, TO, NT, EPI, 2, 8>), grid, block, 0, st, (const T*)x, xr, ldx, (const T*)W,
-                       (TO*)y, ldy, n, K, pair_off);
-  else if (n <= 64)
-    hipLaunchKernelGGL((linear_kernel<T, TO, NT, EPI, 4, 8>), grid, block, 0, st, (const T*)x, xr, ldx, (const T*)W,
-                       (TO*)y, ldy, n, K, pair_off);
-  else
-    hipLaunchKernelGGL((linear_kernel<T, TO, NT, EPI, 8, 8>), grid, block, 0, st, (const T*)x, xr, ldx, (const T*)W,
-                       (TO*)y, ldy, n, K, pair_off);
+static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const void* W, void* y, int64_t ldy, int n,
+                          int N, int K, int pair_off, const RopeArgs& ra, hipStream_t st) {
+  const int groups = (EPI == kEpiSwiGLU) ? pair_off / 16 : N / 16;
+  const int P = K / LinTraits<T>::KC;
+  const size_t lds = (size_t)P * NT * 64 * sizeof(f32x4);
+  const int mc = (P + kWideWaves - 1) / kWideWaves;  // chunks per wave
+  const bool wide = n <= kWideMaxRows && mc <= kWideMaxChunksPerWave && lds <= 65536 && (NT == 1 || mc == 1);
+  if (wide && mc == 1) {
+    hipLaunchKernelGGL((linear_wide_kernel<T, TO, NT, EPI, 1>), dim3(groups), dim3(64 * kWideWaves), lds, st,
+                       (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra);
+  } else if (wide && mc == 2) {
+    hipLaunchKernelGGL((linear_wide_kernel<T, TO, 1, EPI, 2>), dim3(groups), dim3(64 * kWideWaves), lds, st,
+                       (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra);
+  } else if (wide) {
+    hipLaunchKernelGGL((linear_wide_kernel<T, TO, 1, EPI, 3>), dim3(groups), dim3(64 * kWideWaves), lds, st,
+                       (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra);
+  } else {
+    constexpr int NB = (NT == 1) ? 2 : 1;
+    hipLaunchKernelGGL((linear_tile_kernel<T, TO, NT, EPI, NB>), dim3((n + 63) / 64, (groups + NB - 1) / NB),
+                       dim3(256), 0, st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, groups, ra);
+  }
 }
 
 }  // namespace wfd
 
 extern "C" {
 
-// Minimum K granularity: K must be a multiple of this for the given dtype.
 int wfd_linear_k_multiple(int dtype) {
   using namespace wfd;
-  return (dtype == kBF16 ? 32 : 16) * kLinWaves;
+  return dtype == kBF16 ? LinTraits<bf16_t>::KC : LinTraits<float>::KC;
 }
 
 int wfd_linear(const void* x, const int32_t* x_rows, int64_t ldx, const void* W, void* y, int64_t ldy, int n, int N,
@@ -194,31 +345,58 @@ int wfd_linear(const void* x, const int32_t* x_rows, int64_t ldx, const void* W,
     set_error("wfd_linear: unknown epilogue %d", epilogue);
     return kUnsupported;
   }
-  const bool nt2 = (epilogue == kEpiPlain) && (N % 32 == 0);
+  const RopeArgs ra{};
   if (dtype == kBF16 && out_dtype == kBF16) {
     if (epilogue == kEpiSwiGLU)
-      launch_linear_mt<bf16_t, bf16_t, 2, kEpiSwiGLU>(x, x_rows, ldx, W, y, ldy, n, N, K, pair_off, stream);
-    else if (nt2)
-      launch_linear_mt<bf16_t, bf16_t, 2, kEpiPlain>(x, x_rows, ldx, W, y, ldy, n, N, K, 0, stream);
+      launch_linear<bf16_t, bf16_t, 2, kEpiSwiGLU>(x, x_rows, ldx, W, y, ldy, n, N, K, pair_off, ra, stream);
     else
-      launch_linear_mt<bf16_t, bf16_t, 1, kEpiPlain>(x, x_rows, ldx, W, y, ldy, n, N, K, 0, stream);
+      launch_linear<bf16_t, bf16_t, 1, kEpiPlain>(x, x_rows, ldx, W, y, ldy, n, N, K, 0, ra, stream);
   } else if (dtype == kBF16 && out_dtype == kF32 && epilogue == kEpiPlain) {
-    if (nt2)
-      launch_linear_mt<bf16_t, float, 2, kEpiPlain>(x, x_rows, ldx, W, y, ldy, n, N, K, 0, stream);
-    else
-      launch_linear_mt<bf16_t, float, 1, kEpiPlain>(x, x_rows, ldx, W, y, ldy, n, N, K, 0, stream);
+    launch_linear<bf16_t, float, 1, kEpiPlain>(x, x_rows, ldx, W, y, ldy, n, N, K, 0, ra, stream);
   } else if (dtype == kF32 && out_dtype == kF32) {
     if (epilogue == kEpiSwiGLU)
-      launch_linear_mt<float, float, 2, kEpiSwiGLU>(x, x_rows, ldx, W, y, ldy, n, N, K, pair_off, stream);
-    else if (nt2)
-      launch_linear_mt<float, float, 2, kEpiPlain>(x, x_rows, ldx, W, y, ldy, n, N, K, 0, stream);
+      launch_linear<float, float, 2, kEpiSwiGLU>(x, x_rows, ldx, W, y, ldy, n, N, K, pair_off, ra, stream);
     else
-      launch_linear_mt<float, float, 1, kEpiPlain>(x, x_rows, ldx, W, y, ldy, n, N, K, 0, stream);
+      launch_linear<float, float, 1, kEpiPlain>(x, x_rows, ldx, W, y, ldy, n, N, K, 0, ra, stream);
   } else {
     set_error("wfd_linear: unsupported dtype=%d out_dtype=%d epilogue=%d", dtype, out_dtype, epilogue);
     return kUnsupported;
   }
   return launch_status("wfd_linear");
+}
+
+int wfd_linear_qkv_rope_append(const void* x, const int32_t* x_rows, int64_t ldx, const void* Wqkv, int n, int K,
+                               const int32_t* pos, const float* rope_cos, const float* rope_sin, int rope_rows,
+                               const int64_t* flat_row, void* q_out, void* k_cache, void* v_cache, int H, int Hkv,
+                               int Dh, int dtype, hipStream_t stream) {
+  using namespace wfd;
+  if (n < 0 || K <= 0 || ldx < K || H <= 0 || Hkv <= 0 || H % Hkv != 0 || Dh <= 0 || Dh % 16 != 0 ||
+      rope_rows <= 0) {
+    set_error("wfd_linear_qkv_rope_append: bad shape n=%d K=%d H=%d Hkv=%d Dh=%d rope_rows=%d", n, K, H, Hkv, Dh,
+              rope_rows);
+    return kBadArg;
+  }
+  if (n == 0) return kOk;
+  if (!x || !Wqkv || !pos || !rope_cos || !rope_sin || !flat_row || !q_out || !k_cache || !v_cache) {
+    set_error("wfd_linear_qkv_rope_append: null pointer argument");
+    return kBadArg;
+  }
+  const int kmul = wfd_linear_k_multiple(dtype);
+  if (K % kmul != 0) {
+    set_error("wfd_linear_qkv_rope_append: K=%d must be a multiple of %d", K, kmul);
+    return kUnsupported;
+  }
+  const int N = (H + 2 * Hkv) * Dh;
+  const RopeArgs ra{pos, rope_cos, rope_sin, rope_rows, flat_row, q_out, k_cache, v_cache, H, Hkv, Dh};
+  if (dtype == kBF16)
+    launch_linear<bf16_t, bf16_t, 1, kEpiRope>(x, x_rows, ldx, Wqkv, nullptr, 0, n, N, K, 0, ra, stream);
+  else if (dtype == kF32)
+    launch_linear<float, float, 1, kEpiRope>(x, x_rows, ldx, Wqkv, nullptr, 0, n, N, K, 0, ra, stream);
+  else {
+    set_error("wfd_linear_qkv_rope_append: unsupported dtype=%d", dtype);
+    return kUnsupported;
+  }
+  return launch_status("wfd_linear_qkv_rope_append");
 }
 
 }  // extern "C"

@@ -55,6 +55,7 @@ struct Elem<float> {
   static constexpr int kVec = 4;  // elements per 16-byte vector
   __device__ __forceinline__ static float load(const float* p) { return *p; }
   __device__ __forceinline__ static void store(float* p, float v) { *p = v; }
+  __device__ __forceinline__ static float round(float v) { return v; }
   __device__ __forceinline__ static void unpack(const u32x4& w, float (&o)[4]) {
     o[0] = __uint_as_float(w[0]);
     o[1] = __uint_as_float(w[1]);
@@ -68,6 +69,8 @@ struct Elem<bf16_t> {
   static constexpr int kVec = 8;
   __device__ __forceinline__ static float load(const bf16_t* p) { return bf16_bits_to_f32(p->bits); }
   __device__ __forceinline__ static void store(bf16_t* p, float v) { p->bits = f32_to_bf16_bits(v); }
+  // the value a store then a load would give back
+  __device__ __forceinline__ static float round(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
   __device__ __forceinline__ static void unpack(const u32x4& w, float (&o)[8]) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {

@@ -9,16 +9,23 @@ of rows -- any mix of sequences, positions and loop depths -- through:
   coda_union     ln_f(pool[row][:D]) -> coda blocks -> ln_f -> lm_head -> argmax
   prefill_seq    the same blocks over a whole prompt, every slot filled
 
-and every block is: linear(Wqkv) -> qkv_rope_append -> attn_decode ->
+and every block is: linear(Wqkv) with RoPE + cache append fused -> attn_decode ->
 linear(proj) -> add_rmsnorm(norm_2, norm_3) -> linear(fc, swiglu) ->
 linear(mlp_proj) -> add_rmsnorm(norm_4, next norm_1).
 
 Row tables (positions, slot row bases, append rows, pool rows) are built on
-the host per call and uploaded with one copy through a ring of pinned
-buffers; the kernels read them as device data. Each row's arithmetic is
-independent of the other rows in the union (every kernel is row-invariant),
-so a token computed in a wavefront union is bit-identical to the same token
-computed alone -- which is what makes wavefront decoding lossless here.
+the host per call and read by the kernels as device data. Each row's
+arithmetic is independent of the other rows in the union (every kernel is
+row-invariant), so a token computed in a wavefront union is bit-identical to
+the same token computed alone -- which is what makes wavefront decoding
+lossless here.
+
+hipGraph mode (use_graphs=True): each (pass, row bucket, cache) gets one
+captured launch sequence over fixed scratch and fixed table buffers; a call
+pads its rows to the bucket (power of two) with rows that point at the
+cache's trash row and the pool's trash row, refreshes the tables with one
+host->device copy, and replays. The grid bound for attention is the cache
+length, so one graph serves every position, depth mix and rollback.
 
 Wave-state pool: row of (seq b, position p) = b*R + p % R with
 R = T_total + 2. At most T_total + 1 consecutive positions of one sequence
@@ -73,11 +80,45 @@ class _Staging:
         return out
 
 
+class _Captured:
+    """One captured pass: fixed device tables + pinned host copies + the graph."""
+
+    def __init__(self, kind: str, nb: int, cache, n32: int, n64: int, device):
+        self.kind, self.nb, self.cache = kind, nb, cache
+        # one buffer [int64 tables | int32 tables] so a replay needs one host->device copy
+        words = n64 + (n32 + 1) // 2
+        self.host = torch.empty(words, dtype=torch.int64).pin_memory()
+        self.dev = torch.empty(words, dtype=torch.int64, device=device)
+        self.n32, self.n64 = n32, n64
+        self.d64 = self.dev[:n64]
+        self.d32 = self.dev[n64:].view(torch.int32)[:n32]
+        self.event: torch.cuda.Event | None = None
+        self.graph: torch.cuda.CUDAGraph | None = None
+
+    def load(self, i32: np.ndarray, i64: np.ndarray) -> None:
+        if self.event is not None:
+            self.event.synchronize()          # the previous copy out of the pinned buffer is done
+        h = self.host.numpy()
+        h[: self.n64] = i64
+        h[self.n64:].view(np.int32)[: self.n32] = i32
+        self.dev.copy_(self.host, non_blocking=True)
+        self.event = torch.cuda.Event()
+        self.event.record()
+
+
+def _bucket(n: int) -> int:
+    b = 1
+    while b < n:
+        b *= 2
+    return b
+
+
 class LoopedModel:
     """Device-resident looped LM running unions of rows through libwfd."""
 
     def __init__(self, cfg: LoopedLMConfig, weights: dict[str, torch.Tensor], device="cuda", *, max_seq_len: int,
-                 max_batch: int = 1, state_init: str = "random", state_seed: int = 0):
+                 max_batch: int = 1, state_init: str = "random", state_seed: int = 0, use_graphs: bool = False,
+                 max_rows: int | None = None):
         self.cfg = cfg
         self.device = torch.device(device)
         self.dtype = cfg.torch_dtype
@@ -85,6 +126,7 @@ class LoopedModel:
         self.max_batch = max_batch
         self.state_init = state_init
         self.state_seed = state_seed
+        self.use_graphs = use_graphs
         self.W = {k: v.to(device=self.device, dtype=self.dtype).contiguous() for k, v in weights.items()}
         cos, sin = rope_tables(max_seq_len, cfg.head_dim, cfg.rope_base)
         self.rope_cos = cos.to(self.device)
@@ -93,17 +135,23 @@ class LoopedModel:
             device=self.device, dtype=self.dtype)
         self.R = cfg.T_total + 2
         D = cfg.d_model
-        self.pool = torch.zeros(max_batch * self.R, 2 * D, dtype=self.dtype, device=self.device)
-        self._scratch: dict[str, torch.Tensor] = {}
-        self._cap = 0
-        self._logit_bufs: dict[str, torch.Tensor] = {}
-        self._logit_cap = 0
-        self.staging = _Staging(self.device)
+        # pool rows: R per sequence + one trash row for padding rows
+        self.pool = torch.zeros(max_batch * self.R + 1, 2 * D, dtype=self.dtype, device=self.device)
+        self.trash_pool_row = max_batch * self.R
         self.coda_base = cfg.n_prelude + cfg.T_total * cfg.n_core
         k_mult = ops.linear_k_multiple(self.dtype)
         for K in (D, 2 * D, cfg.n_heads * cfg.head_dim, cfg.ffn):
             if K % k_mult:
                 raise ValueError(f"{cfg.name}: K={K} is not a multiple of {k_mult} (linear kernel granularity)")
+        # decode scratch: fixed capacity (captured graphs keep these addresses)
+        self.max_rows = _bucket(max_rows or max_batch * self.R)
+        self.sc = self._scratch(self.max_rows)
+        self.sc["logits"] = torch.empty(self.max_rows, cfg.vocab_size, dtype=torch.float32, device=self.device)
+        self.sc["ids"] = torch.empty(self.max_rows, dtype=torch.int64, device=self.device)
+        self.attn_ws = torch.empty(ops.attn_workspace_bytes(self.max_rows, cfg.n_heads, cfg.head_dim, max_seq_len),
+                                   dtype=torch.uint8, device=self.device)
+        self.staging = _Staging(self.device)
+        self._graphs: dict[tuple, _Captured] = {}
 
     # -- slots / rows ----------------------------------------------------------
     def slot_prelude(self, i: int) -> int:
@@ -123,44 +171,28 @@ class LoopedModel:
         return BatchStaticKVCache(c.n_slots, batch_size or self.max_batch, c.n_kv_heads, c.head_dim,
                                   self.max_seq_len, self.dtype, self.device)
 
-    # -- scratch -----------------------------------------------------------------
-    def _ensure(self, n: int) -> dict[str, torch.Tensor]:
-        if n <= self._cap:
-            return self._scratch
-        c = self.cfg
-        cap = max(n, 16)
-        mk = lambda w, dt=self.dtype: torch.empty(cap, w, dtype=dt, device=self.device)  # noqa: E731
-        self._scratch = dict(
-            x=mk(c.d_model), h=mk(c.d_model), qkv=mk(c.qkv_dim),
-            q=torch.empty(cap, c.n_heads, c.head_dim, dtype=self.dtype, device=self.device),
-            o=torch.empty(cap, c.n_heads, c.head_dim, dtype=self.dtype, device=self.device),
-            a=mk(c.d_model), u=mk(c.ffn), m=mk(c.d_model),
-        )
-        self._scratch.update(self._logit_bufs)
-        self._cap = cap
-        return self._scratch
+    def clear_graphs(self) -> None:
+        self._graphs.clear()
 
-    def _ensure_logits(self, n: int) -> None:
-        """(n, V) float32 logits + (n,) ids, sized separately from the row scratch
-        (a prompt prefill needs one logits row, not L)."""
-        if n > self._logit_cap:
-            cap = max(n, 16)
-            self._logit_bufs = dict(
-                logits=torch.empty(cap, self.cfg.vocab_size, dtype=torch.float32, device=self.device),
-                ids=torch.empty(cap, dtype=torch.int64, device=self.device))
-            self._logit_cap = cap
-            self._scratch.update(self._logit_bufs)
+    # -- scratch -----------------------------------------------------------------
+    def _scratch(self, cap: int) -> dict[str, torch.Tensor]:
+        c = self.cfg
+        mk = lambda w: torch.empty(cap, w, dtype=self.dtype, device=self.device)  # noqa: E731
+        return dict(x=mk(c.d_model), h=mk(c.d_model),
+                    q=torch.empty(cap, c.n_heads, c.head_dim, dtype=self.dtype, device=self.device),
+                    o=torch.empty(cap, c.n_heads, c.head_dim, dtype=self.dtype, device=self.device),
+                    a=mk(c.d_model), u=mk(c.ffn), m=mk(c.d_model))
 
     # -- one SandwichBlock over n rows --------------------------------------------
-    def _block(self, prefix: str, n: int, sc, pos_d, kvlen_d, rb_d, fr_d, kv_len_max: int,
+    def _block(self, prefix: str, n: int, sc, pos_d, kvlen_d, rb_d, fr_d, kv_len_max: int, ws,
                cache: BatchStaticKVCache, next_norm: torch.Tensor | None, final_out=None, final_rows=None):
         c, W = self.cfg, self.W
         x, h = sc["x"], sc["h"]
-        qkv = ops.linear(h, W[prefix + "Wqkv"], n=n, out=sc["qkv"])
-        q = ops.qkv_rope_append(qkv[:n], pos_d, self.rope_cos, self.rope_sin, fr_d, cache.flat_k, cache.flat_v,
-                                c.n_heads, c.n_kv_heads, c.head_dim, q_out=sc["q"][:n])
+        q = ops.linear_qkv_rope_append(h, W[prefix + "Wqkv"], pos_d, self.rope_cos, self.rope_sin, fr_d,
+                                       cache.flat_k, cache.flat_v, c.n_heads, c.n_kv_heads, c.head_dim, n=n,
+                                       q_out=sc["q"][:n])
         o = ops.attn_decode(q, cache.flat_k, cache.flat_v, rb_d, kvlen_d, kv_len_max=kv_len_max, out=sc["o"][:n],
-                            workspace=self._attn_ws(n, kv_len_max))
+                            workspace=ws)
         a = ops.linear(o.view(n, -1), W[prefix + "proj"], n=n, out=sc["a"])
         ops.add_rmsnorm(a, W[prefix + "norm_2"], c.norm_eps, res=x, w2=W[prefix + "norm_3"], n=n, x_out=x,
                         h_out=h)
@@ -171,127 +203,167 @@ class LoopedModel:
         else:
             ops.add_rmsnorm(m, W[prefix + "norm_4"], c.norm_eps, res=x, n=n, x_out=final_out, out_rows=final_rows)
 
-    def _attn_ws(self, n: int, kv_len_max: int) -> torch.Tensor:
-        return ops.attn_workspace(n, self.cfg.n_heads, self.cfg.head_dim, kv_len_max, self.device)
+    # -- row tables ------------------------------------------------------------------
+    def _layers(self, kind: str) -> int:
+        c = self.cfg
+        return {"P": c.n_prelude, "R": c.n_core, "C": c.n_coda}[kind]
 
-    def _tables(self, cache, seqs: np.ndarray, pos: np.ndarray, slots: np.ndarray):
-        """slots: (layers, n) -> row_base, flat_row: (layers, n) int64."""
-        rb = (slots * cache.B + seqs[None, :]) * cache.S
-        return rb.astype(np.int64), (rb + pos[None, :]).astype(np.int64)
+    def _tables(self, kind: str, cache, seqs, pos, steps, ids, nb: int):
+        """int32 [pos | kv_len | pool_row] and int64 [ids? | row_base x L | flat_row x L],
+        each block nb wide; rows n..nb-1 are padding aimed at the trash rows."""
+        c = self.cfg
+        n = len(pos)
+        L = self._layers(kind)
+        if kind == "P":
+            slots = np.repeat(np.arange(L, dtype=np.int64)[:, None], n, axis=1)
+        elif kind == "R":
+            slots = c.n_prelude + steps[None, :] * c.n_core + np.arange(L, dtype=np.int64)[:, None]
+        else:
+            slots = self.coda_base + np.repeat(np.arange(L, dtype=np.int64)[:, None], n, axis=1)
+        rb = np.full((L, nb), cache.trash_row, dtype=np.int64)
+        rb[:, :n] = (slots * cache.B + seqs[None, :]) * cache.S
+        fr = rb.copy()
+        fr[:, :n] += pos[None, :]
+        i32 = np.zeros(3 * nb, dtype=np.int32)
+        i32[:n] = pos
+        i32[nb: nb + n] = pos + 1
+        i32[nb + n: 2 * nb] = 1
+        i32[2 * nb: 2 * nb + n] = seqs * self.R + pos % self.R
+        i32[2 * nb + n:] = self.trash_pool_row
+        parts = [rb.reshape(-1), fr.reshape(-1)]
+        if kind == "P":
+            idp = np.zeros(nb, dtype=np.int64)
+            idp[:n] = ids
+            parts.insert(0, idp)
+        return i32, np.concatenate(parts)
+
+    def _launch(self, kind: str, cache, nb: int, t32: torch.Tensor, t64: torch.Tensor, kv_max: int) -> None:
+        """The launch sequence of one pass over nb rows (eager or under capture)."""
+        c, W, sc, ws = self.cfg, self.W, self.sc, self.attn_ws
+        pos_d, kvlen_d, rows_d = t32[:nb], t32[nb: 2 * nb], t32[2 * nb: 3 * nb]
+        L = self._layers(kind)
+        off = nb if kind == "P" else 0
+        rb = lambda l: t64[off + l * nb: off + (l + 1) * nb]  # noqa: E731
+        fr = lambda l: t64[off + (L + l) * nb: off + (L + l + 1) * nb]  # noqa: E731
+        if kind == "P":
+            ops.embed(t64[:nb], W["wte"], c.emb_scale, out=sc["x"])
+            ops.rmsnorm(sc["x"], W["prelude.0.norm_1"], c.norm_eps, n=nb, x_out=sc["h"])
+            static_half = self.pool[:, c.d_model:]
+            for i in range(L):
+                nxt = W[f"prelude.{i + 1}.norm_1"] if i + 1 < L else None
+                self._block(f"prelude.{i}.", nb, sc, pos_d, kvlen_d, rb(i), fr(i), kv_max, ws, cache, nxt,
+                            final_out=static_half, final_rows=rows_d)
+            ops.copy_rows(self.s0, self.pool, n=nb, width=c.d_model, src_rows=pos_d, dst_rows=rows_d)
+        elif kind == "R":
+            ops.linear(self.pool, W["adapter"], n=nb, x_rows=rows_d, out=sc["x"])
+            ops.rmsnorm(sc["x"], W["core.0.norm_1"], c.norm_eps, n=nb, x_out=sc["h"])
+            for l in range(L):
+                nxt = W[f"core.{l + 1}.norm_1"] if l + 1 < L else None
+                self._block(f"core.{l}.", nb, sc, pos_d, kvlen_d, rb(l), fr(l), kv_max, ws, cache, nxt,
+                            final_out=self.pool, final_rows=rows_d)
+        else:
+            ops.rmsnorm(self.pool, W["ln_f"], c.norm_eps, n=nb, a_rows=rows_d, x_out=sc["x"])
+            ops.rmsnorm(sc["x"], W["coda.0.norm_1"], c.norm_eps, n=nb, x_out=sc["h"])
+            for i in range(L):
+                nxt = W[f"coda.{i + 1}.norm_1"] if i + 1 < L else W["ln_f"]
+                self._block(f"coda.{i}.", nb, sc, pos_d, kvlen_d, rb(i), fr(i), kv_max, ws, cache, nxt)
+            ops.linear(sc["h"], W["lm_head"], n=nb, out=sc["logits"], out_dtype=torch.float32)
+            ops.argmax(sc["logits"], n=nb, out=sc["ids"])
+
+    def _captured(self, kind: str, nb: int, cache) -> _Captured:
+        key = (kind, nb, id(cache))
+        g = self._graphs.get(key)
+        if g is not None and g.cache is cache:
+            return g
+        L = self._layers(kind)
+        g = _Captured(kind, nb, cache, 3 * nb, (2 * L + (1 if kind == "P" else 0)) * nb, self.device)
+        empty = np.zeros(0, dtype=np.int64)
+        i32, i64 = self._tables(kind, cache, empty, empty, empty, empty, nb)   # all padding rows
+        g.load(i32, i64)
+        torch.cuda.synchronize()
+        self._launch(kind, cache, nb, g.d32, g.d64, cache.S)                   # warm-up, then capture
+        torch.cuda.synchronize()
+        g.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g.graph):
+            self._launch(kind, cache, nb, g.d32, g.d64, cache.S)
+        torch.cuda.synchronize()
+        self._graphs[key] = g
+        return g
+
+    def _run(self, kind: str, cache, seqs, pos, steps=None, ids=None) -> None:
+        n = len(pos)
+        if self.use_graphs:
+            nb = _bucket(n)
+            if nb > self.max_rows:
+                raise ValueError(f"union of {n} rows exceeds max_rows={self.max_rows}")
+            g = self._captured(kind, nb, cache)
+            i32, i64 = self._tables(kind, cache, seqs, pos, steps, ids, nb)
+            g.load(i32, i64)
+            g.graph.replay()
+        else:
+            if n > self.max_rows:
+                raise ValueError(f"union of {n} rows exceeds max_rows={self.max_rows}")
+            i32, i64 = self._tables(kind, cache, seqs, pos, steps, ids, n)
+            t32, t64 = self.staging.upload([i32, i64])
+            self._launch(kind, cache, n, t32, t64, int(pos.max()) + 1)
 
     def _check(self, cache, seqs, pos):
         if len(pos) and (pos.min() < 0 or pos.max() >= cache.S):
             raise IndexError(f"position out of range [0, {cache.S})")
         if len(seqs) and (seqs.min() < 0 or seqs.max() >= cache.B or seqs.max() >= self.max_batch):
             raise IndexError("sequence index out of range")
+        if cache.S > self.max_seq_len:
+            raise ValueError("cache longer than the engine's tables (max_seq_len)")
 
-    # -- P ---------------------------------------------------------------------------
+    # -- P / R / C ---------------------------------------------------------------------
     def prelude_union(self, cache, seqs, positions, token_ids) -> np.ndarray:
         """Embed + prelude blocks for n new tokens; fills pool[row] = [s0(pos) | e].
         Returns the pool rows."""
-        c = self.cfg
         seqs = np.asarray(seqs, dtype=np.int64)
         pos = np.asarray(positions, dtype=np.int64)
-        n = len(pos)
-        if n == 0:
+        if len(pos) == 0:
             return np.zeros(0, dtype=np.int64)
         self._check(cache, seqs, pos)
-        rows = seqs * self.R + pos % self.R
-        slots = np.repeat(np.arange(c.n_prelude, dtype=np.int64)[:, None], n, axis=1)
-        rb, fr = self._tables(cache, seqs, pos, slots)
-        i32 = np.concatenate([pos, pos + 1, rows]).astype(np.int32)
-        i64 = np.concatenate([np.asarray(token_ids, dtype=np.int64), rb.reshape(-1), fr.reshape(-1)])
-        t32, t64 = self.staging.upload([i32, i64])
-        pos_d, kvlen_d, rows_d = t32[:n], t32[n: 2 * n], t32[2 * n:]
-        ids_d = t64[:n]
-        sc = self._ensure(n)
-        kv_max = int(pos.max()) + 1
-        ops.embed(ids_d, self.W["wte"], c.emb_scale, out=sc["x"])
-        ops.rmsnorm(sc["x"], self.W["prelude.0.norm_1"], c.norm_eps, n=n, x_out=sc["h"])
-        static_half = self.pool[:, c.d_model:]
-        for i in range(c.n_prelude):
-            last = i == c.n_prelude - 1
-            self._block(f"prelude.{i}.", n, sc, pos_d, kvlen_d, t64[n + i * n: n + (i + 1) * n],
-                        t64[n + (c.n_prelude + i) * n: n + (c.n_prelude + i + 1) * n], kv_max, cache,
-                        None if last else self.W[f"prelude.{i + 1}.norm_1"], final_out=static_half,
-                        final_rows=rows_d)
-        ops.copy_rows(self.s0, self.pool, n=n, width=c.d_model, src_rows=pos_d, dst_rows=rows_d)
+        self._run("P", cache, seqs, pos, ids=np.asarray(token_ids, dtype=np.int64))
         for b, p in zip(seqs.tolist(), pos.tolist()):
-            for i in range(c.n_prelude):
+            for i in range(self.cfg.n_prelude):
                 cache.note_write(self.slot_prelude(i), b, p)
-        return rows
+        return seqs * self.R + pos % self.R
 
-    # -- R ---------------------------------------------------------------------------
     def core_union(self, cache, seqs, positions, steps) -> None:
         """One recurrence for n rows at their own depths: pool[row][:D] advances one step."""
         c = self.cfg
         seqs = np.asarray(seqs, dtype=np.int64)
         pos = np.asarray(positions, dtype=np.int64)
         st = np.asarray(steps, dtype=np.int64)
-        n = len(pos)
-        if n == 0:
+        if len(pos) == 0:
             return
         self._check(cache, seqs, pos)
         if st.min() < 0 or st.max() >= c.T_total:
             raise ValueError(f"core step out of range [0, {c.T_total})")
-        rows = seqs * self.R + pos % self.R
-        slots = c.n_prelude + st[None, :] * c.n_core + np.arange(c.n_core, dtype=np.int64)[:, None]
-        rb, fr = self._tables(cache, seqs, pos, slots)
-        i32 = np.concatenate([pos, pos + 1, rows]).astype(np.int32)
-        i64 = np.concatenate([rb.reshape(-1), fr.reshape(-1)])
-        t32, t64 = self.staging.upload([i32, i64])
-        pos_d, kvlen_d, rows_d = t32[:n], t32[n: 2 * n], t32[2 * n:]
-        sc = self._ensure(n)
-        kv_max = int(pos.max()) + 1
-        ops.linear(self.pool, self.W["adapter"], n=n, x_rows=rows_d, out=sc["x"])
-        ops.rmsnorm(sc["x"], self.W["core.0.norm_1"], c.norm_eps, n=n, x_out=sc["h"])
-        L = c.n_core
-        for l in range(L):
-            last = l == L - 1
-            self._block(f"core.{l}.", n, sc, pos_d, kvlen_d, t64[l * n: (l + 1) * n],
-                        t64[(L + l) * n: (L + l + 1) * n], kv_max, cache,
-                        None if last else self.W[f"core.{l + 1}.norm_1"], final_out=self.pool, final_rows=rows_d)
+        self._run("R", cache, seqs, pos, steps=st)
         for b, p, s in zip(seqs.tolist(), pos.tolist(), st.tolist()):
-            for l in range(L):
+            for l in range(c.n_core):
                 cache.note_write(self.slot_core(s, l), b, p)
 
-    # -- C ---------------------------------------------------------------------------
     def coda_union(self, cache, seqs, positions) -> tuple[torch.Tensor, torch.Tensor]:
         """ln_f -> coda blocks -> ln_f -> lm_head for n rows. Returns
         (logits (n, V) float32, argmax ids (n,) int64), both device views."""
-        c = self.cfg
         seqs = np.asarray(seqs, dtype=np.int64)
         pos = np.asarray(positions, dtype=np.int64)
         n = len(pos)
         self._check(cache, seqs, pos)
-        rows = seqs * self.R + pos % self.R
-        slots = self.coda_base + np.repeat(np.arange(c.n_coda, dtype=np.int64)[:, None], n, axis=1)
-        rb, fr = self._tables(cache, seqs, pos, slots)
-        i32 = np.concatenate([pos, pos + 1, rows]).astype(np.int32)
-        i64 = np.concatenate([rb.reshape(-1), fr.reshape(-1)])
-        t32, t64 = self.staging.upload([i32, i64])
-        pos_d, kvlen_d, rows_d = t32[:n], t32[n: 2 * n], t32[2 * n:]
-        self._ensure_logits(n)
-        sc = self._ensure(n)
-        kv_max = int(pos.max()) + 1
-        ops.rmsnorm(self.pool, self.W["ln_f"], c.norm_eps, n=n, a_rows=rows_d, x_out=sc["x"])
-        ops.rmsnorm(sc["x"], self.W["coda.0.norm_1"], c.norm_eps, n=n, x_out=sc["h"])
-        L = c.n_coda
-        for i in range(L):
-            nxt = self.W[f"coda.{i + 1}.norm_1"] if i + 1 < L else self.W["ln_f"]
-            self._block(f"coda.{i}.", n, sc, pos_d, kvlen_d, t64[i * n: (i + 1) * n],
-                        t64[(L + i) * n: (L + i + 1) * n], kv_max, cache, nxt)
-        logits = ops.linear(sc["h"], self.W["lm_head"], n=n, out=sc["logits"], out_dtype=torch.float32)
-        ids = ops.argmax(logits, n=n, out=sc["ids"])
+        self._run("C", cache, seqs, pos)
         for b, p in zip(seqs.tolist(), pos.tolist()):
-            for i in range(L):
+            for i in range(self.cfg.n_coda):
                 cache.note_write(self.slot_coda(i), b, p)
-        return logits[:n], ids[:n]
+        return self.sc["logits"][:n], self.sc["ids"][:n]
 
     # -- prefill -----------------------------------------------------------------------
     def prefill_seq(self, cache, b: int, token_ids) -> torch.Tensor:
         """Whole prompt of sequence b at positions [0, L): fills every slot's
-        [0, L) and returns the last position's logits (V,) float32."""
+        [0, L) and returns the last position's logits (V,) float32. Runs eagerly
+        with its own L-row scratch."""
         c, W = self.cfg, self.W
         ids = np.asarray(token_ids, dtype=np.int64).reshape(-1)
         L = len(ids)
@@ -301,24 +373,25 @@ class LoopedModel:
             raise IndexError("sequence index out of range")
         D = c.d_model
         pos = np.arange(L, dtype=np.int64)
-        seqs = np.full(L, b, dtype=np.int64)
         n_layers = c.n_prelude + c.T_total * c.n_core + c.n_coda
-        slots = np.repeat(np.arange(n_layers, dtype=np.int64)[:, None], L, axis=1)
-        rb, fr = self._tables(cache, seqs, pos, slots)
+        rb = np.repeat(((np.arange(n_layers, dtype=np.int64) * cache.B + b) * cache.S)[:, None], L, axis=1)
+        fr = rb + pos[None, :]
         t32, t64, ids_d = self.staging.upload([np.concatenate([pos, pos + 1]).astype(np.int32),
                                                np.concatenate([rb.reshape(-1), fr.reshape(-1)]), ids])
         pos_d, kvlen_d = t32[:L], t32[L:]
         rb_l = lambda s: t64[s * L: (s + 1) * L]  # noqa: E731
         fr_l = lambda s: t64[(n_layers + s) * L: (n_layers + s + 1) * L]  # noqa: E731
-        self._ensure_logits(1)
-        sc = self._ensure(L)
+        sc = self._scratch(L)
+        ws = torch.empty(ops.attn_workspace_bytes(L, c.n_heads, c.head_dim, L), dtype=torch.uint8,
+                         device=self.device)
+        logits = torch.empty(1, c.vocab_size, dtype=torch.float32, device=self.device)
         state = torch.empty(L, 2 * D, dtype=self.dtype, device=self.device)  # [s | e] per prompt row
         ops.embed(ids_d, W["wte"], c.emb_scale, out=sc["x"])
         ops.rmsnorm(sc["x"], W["prelude.0.norm_1"], c.norm_eps, n=L, x_out=sc["h"])
         for i in range(c.n_prelude):
-            last = i == c.n_prelude - 1
-            self._block(f"prelude.{i}.", L, sc, pos_d, kvlen_d, rb_l(i), fr_l(i), L, cache,
-                        None if last else W[f"prelude.{i + 1}.norm_1"], final_out=state[:, D:])
+            nxt = W[f"prelude.{i + 1}.norm_1"] if i + 1 < c.n_prelude else None
+            self._block(f"prelude.{i}.", L, sc, pos_d, kvlen_d, rb_l(i), fr_l(i), L, ws, cache, nxt,
+                        final_out=state[:, D:])
         s0 = initial_state_prefill(c, L, self.state_seed, self.state_init)
         state[:, :D].copy_(s0.to(device=self.device, dtype=self.dtype))
         for r in range(c.T_total):
@@ -326,16 +399,16 @@ class LoopedModel:
             ops.rmsnorm(sc["x"], W["core.0.norm_1"], c.norm_eps, n=L, x_out=sc["h"])
             for l in range(c.n_core):
                 s = self.slot_core(r, l)
-                last = l == c.n_core - 1
-                self._block(f"core.{l}.", L, sc, pos_d, kvlen_d, rb_l(s), fr_l(s), L, cache,
-                            None if last else W[f"core.{l + 1}.norm_1"], final_out=state[:, :D])
+                nxt = W[f"core.{l + 1}.norm_1"] if l + 1 < c.n_core else None
+                self._block(f"core.{l}.", L, sc, pos_d, kvlen_d, rb_l(s), fr_l(s), L, ws, cache, nxt,
+                            final_out=state[:, :D])
         ops.rmsnorm(state, W["ln_f"], c.norm_eps, n=L, x_out=sc["x"])
         ops.rmsnorm(sc["x"], W["coda.0.norm_1"], c.norm_eps, n=L, x_out=sc["h"])
         for i in range(c.n_coda):
             s = self.slot_coda(i)
             nxt = W[f"coda.{i + 1}.norm_1"] if i + 1 < c.n_coda else W["ln_f"]
-            self._block(f"coda.{i}.", L, sc, pos_d, kvlen_d, rb_l(s), fr_l(s), L, cache, nxt)
-        logits = ops.linear(sc["h"][L - 1: L], W["lm_head"], n=1, out=sc["logits"], out_dtype=torch.float32)
+            self._block(f"coda.{i}.", L, sc, pos_d, kvlen_d, rb_l(s), fr_l(s), L, ws, cache, nxt)
+        ops.linear(sc["h"][L - 1: L], W["lm_head"], n=1, out=logits, out_dtype=torch.float32)
         for s in range(n_layers):
             cache.seqlen[s][b] = max(cache.seqlen[s][b], L)
-        return logits[0].clone()
+        return logits[0]

@@ -38,11 +38,14 @@ class BatchStaticKVCache:
         self.dtype = dtype
         self.device = torch.device(device)
         rows = n_slots * batch_size * max_seq_len
-        # zero-filled like the reference, so a clamped read never sees NaN garbage
-        self.flat_k = torch.zeros(rows, n_kv_head, head_dim, dtype=dtype, device=self.device)
-        self.flat_v = torch.zeros(rows, n_kv_head, head_dim, dtype=dtype, device=self.device)
-        self.K = self.flat_k.view(n_slots, batch_size, max_seq_len, n_kv_head, head_dim)
-        self.V = self.flat_v.view(n_slots, batch_size, max_seq_len, n_kv_head, head_dim)
+        # zero-filled like the reference, so a clamped read never sees NaN garbage;
+        # one extra trailing "trash" row absorbs the appends of padding rows of a
+        # captured (fixed-width) launch and is never part of any slot.
+        self.flat_k = torch.zeros(rows + 1, n_kv_head, head_dim, dtype=dtype, device=self.device)
+        self.flat_v = torch.zeros(rows + 1, n_kv_head, head_dim, dtype=dtype, device=self.device)
+        self.trash_row = rows
+        self.K = self.flat_k[:rows].view(n_slots, batch_size, max_seq_len, n_kv_head, head_dim)
+        self.V = self.flat_v[:rows].view(n_slots, batch_size, max_seq_len, n_kv_head, head_dim)
         # logical per-(slot, seq) lengths: bookkeeping and bounds checks only
         self.seqlen = [[0] * batch_size for _ in range(n_slots)]
 
@@ -55,7 +58,7 @@ class BatchStaticKVCache:
 
     @property
     def nbytes(self) -> int:
-        return 2 * self.flat_k.numel() * self.flat_k.element_size()
+        return 2 * self.K.numel() * self.K.element_size()
 
     def check_position(self, pos: int) -> None:
         if pos < 0 or pos >= self.S:
@@ -108,6 +111,11 @@ class BatchStaticKVCache:
             if self.seqlen[sl][b] > position:
                 self.seqlen[sl][b] = position
 
+    def reset_lengths(self) -> None:
+        """Forget every sequence (buffers are reused as they are; reads are
+        bounded by the reading query's position, so stale rows are never read)."""
+        self.seqlen = [[0] * self.B for _ in range(self.n_slots)]
+
 
 class StaticKVCache(BatchStaticKVCache):
     """Single-sequence (B = 1) view with the reference's StaticKVCache methods
@@ -153,3 +161,6 @@ class StaticKVCache(BatchStaticKVCache):
     def reset(self) -> None:
         self.seqlen = [[0] for _ in range(self.n_slots)]
         self._seen_tokens = 0
+
+    def reset_lengths(self) -> None:
+        self.reset()

@@ -139,6 +139,35 @@ def qkv_rope_append(qkv: torch.Tensor, pos: torch.Tensor, rope_cos: torch.Tensor
     return q_out
 
 
+def linear_qkv_rope_append(x: torch.Tensor, Wqkv: torch.Tensor, pos: torch.Tensor, rope_cos: torch.Tensor,
+                           rope_sin: torch.Tensor, flat_row: torch.Tensor, k_cache: torch.Tensor,
+                           v_cache: torch.Tensor, H: int, Hkv: int, Dh: int, *, n: int | None = None,
+                           x_rows: torch.Tensor | None = None, q_out: torch.Tensor | None = None) -> torch.Tensor:
+    """q_out, plus k/v appended at flat_row: the Wqkv projection with RoPE and
+    the cache append as its epilogue (== linear() then qkv_rope_append())."""
+    _need_cuda(x, Wqkv, pos, rope_cos, rope_sin, flat_row, k_cache, v_cache, x_rows, q_out)
+    n = (x.shape[0] if x_rows is None else x_rows.numel()) if n is None else n
+    _rows(x_rows, n, "x_rows")
+    K = Wqkv.shape[1]
+    _need(x.dim() == 2 and x.stride(1) == 1 and x.shape[1] >= K and x.dtype == Wqkv.dtype, "x (rows, K+)")
+    _need(Wqkv.is_contiguous() and Wqkv.shape[0] == (H + 2 * Hkv) * Dh, "Wqkv ((H+2Hkv)Dh, K) contiguous")
+    _need(pos.dtype == torch.int32 and pos.numel() >= n and pos.is_contiguous(), "pos: int32")
+    _need(flat_row.dtype == torch.int64 and flat_row.numel() >= n and flat_row.is_contiguous(), "flat_row: int64")
+    _need(rope_cos.dtype == torch.float32 and rope_cos.shape == rope_sin.shape and rope_cos.shape[1] == Dh // 2
+          and rope_cos.is_contiguous() and rope_sin.is_contiguous(), "rope tables: float32 (S, Dh/2)")
+    _need(k_cache.shape[1:] == (Hkv, Dh) and k_cache.dtype == x.dtype and v_cache.shape == k_cache.shape
+          and k_cache.is_contiguous() and v_cache.is_contiguous(), "cache shape/dtype mismatch")
+    if q_out is None:
+        q_out = torch.empty(n, H, Dh, dtype=x.dtype, device=x.device)
+    _need(q_out.is_contiguous() and q_out.numel() >= n * H * Dh and q_out.dtype == x.dtype, "q_out (n, H, Dh)")
+    rc = _lib.load().wfd_linear_qkv_rope_append(x.data_ptr(), _p(x_rows), x.stride(0), Wqkv.data_ptr(), n, K,
+                                                pos.data_ptr(), rope_cos.data_ptr(), rope_sin.data_ptr(),
+                                                rope_cos.shape[0], flat_row.data_ptr(), q_out.data_ptr(),
+                                                k_cache.data_ptr(), v_cache.data_ptr(), H, Hkv, Dh, _dt(x), _stream())
+    _lib.check(rc, "wfd_linear_qkv_rope_append")
+    return q_out
+
+
 # ---------------------------------------------------------------------------
 # linear / norms / small gathers
 # ---------------------------------------------------------------------------
@@ -164,9 +193,9 @@ def linear(x: torch.Tensor, W: torch.Tensor, *, n: int | None = None, x_rows: to
         out = torch.empty(n, width, dtype=od, device=x.device)
     _need(out.dim() == 2 and out.stride(1) == 1 and out.shape[0] >= n and out.shape[1] >= width and out.dtype == od,
           "bad out")
+    epi = _lib.EPI_SWIGLU if swiglu else _lib.EPI_PLAIN
     rc = _lib.load().wfd_linear(x.data_ptr(), _p(x_rows), x.stride(0), W.data_ptr(), out.data_ptr(), out.stride(0),
-                                n, N, K, _dt(x), _DT[od], _lib.EPI_SWIGLU if swiglu else _lib.EPI_PLAIN,
-                                N // 2 if swiglu else 0, _stream())
+                                n, N, K, _dt(x), _DT[od], epi, N // 2 if swiglu else 0, _stream())
     _lib.check(rc, "wfd_linear")
     return out
 
