@@ -48,7 +48,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--quick", action="store_true", help="fewer extras (development)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--only", default="", help="comma list of sections: bs1,bs32,attn,gqa,cpu")
+    ap.add_argument("--only", default="", help="comma list of sections: bs1,roofline,attn,bs32,gqa,cpu")
     ap.add_argument("--eager", action="store_true", help="launch every pass eagerly (no hipGraph capture)")
     return ap.parse_args()
 
@@ -95,18 +95,20 @@ def attn_bench(dev, n, H, Hkv, Dh, lens, iters=40):
     return ms * 1e3, by
 
 
-def linear_roofline(dev, model, n: int, iters: int = 30):
-    """The linear (weight-stream) kernel at the decode shapes of one R tick:
-    average launch duration and algorithmic bytes (W + x + y) per launch,
-    timed with HIP events over rotating weight copies (> 512 MB, so HBM, not
-    MALL, serves every launch)."""
+def linear_roofline(dev, cfg, n: int, iters: int = 30):
+    """The weight-stream linear kernel at the decode shapes of one R tick
+    (n rows): per shape, average launch duration (HIP events on the launch
+    stream) and algorithmic bytes (W + x + y) per launch, over rotating weight
+    copies (> 512 MB, so HBM, not the MALL, serves every launch). Returns
+    {name: (us, bytes)}."""
     import torch
     from wavefront_decoding_amd import ops
 
-    c = model.cfg
+    c = cfg
     D = c.d_model
-    shapes = [("adapter", c.d_model, 2 * D, False), ("Wqkv", c.qkv_dim, D, False),
-              ("proj", D, c.n_heads * c.head_dim, False), ("fc", 2 * c.ffn, D, True), ("mlp_proj", D, c.ffn, False)]
+    shapes = [("fc_swiglu", 2 * c.ffn, D, True), ("Wqkv", c.qkv_dim, D, False),
+              ("proj", D, c.n_heads * c.head_dim, False), ("mlp_proj", D, c.ffn, False),
+              ("adapter", D, 2 * D, False)]
     per_tick = sum(N * K * 2 for _, N, K, _ in shapes)
     copies = max(2, math.ceil(2 * MALL_BYTES / per_tick) + 1)
     g = torch.Generator(device=dev).manual_seed(1)
@@ -115,21 +117,17 @@ def linear_roofline(dev, model, n: int, iters: int = 30):
     x = torch.randn(n, 2 * D, device=dev, generator=g).to(torch.bfloat16)
     xf = torch.randn(n, c.ffn, device=dev, generator=g).to(torch.bfloat16)
     out = torch.empty(n, 2 * c.ffn, device=dev, dtype=torch.bfloat16)
-    total_ms, total_bytes, launches = 0.0, 0, 0
+    res = {}
     for j, (name, N, K, sw) in enumerate(shapes):
         src = xf if K == c.ffn else x
         call = lambda i, j=j, K=K, sw=sw, src=src: ops.linear(src, Ws[i % copies][j], n=n, out=out, swiglu=sw, k=K)  # noqa: E731
         timed(call, 2)
         ms = timed(call, iters)
         width = N // 2 if sw else N
-        total_ms += ms
-        total_bytes += N * K * 2 + n * K * 2 + n * width * 2
-        launches += 1
+        res[name] = (ms * 1e3, N * K * 2 + n * K * 2 + n * width * 2)
     del Ws
     torch.cuda.empty_cache()
-    avg_ms = total_ms / launches
-    avg_bytes = total_bytes / launches
-    return avg_ms, avg_bytes
+    return res
 
 
 # ---------------------------------------------------------------------------
@@ -189,14 +187,6 @@ def bs1_section(args, dev, res):
                                       "note": "includes prefill; real argmax acceptance on random-init weights"}
         log(f"bs1: sequential {res['extra']['bs1_sequential_tokens_per_s']:.1f} tok/s; greedy alpha "
             f"{tr.acceptance_rate:.2f}")
-    # dominant kernel of the R tick: the weight-stream linear
-    avg_ms, avg_bytes = linear_roofline(dev, model, 8)
-    ach = avg_bytes / (avg_ms * 1e-3) / 1e9
-    res["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                       "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-                       "kernel": "wfd::linear_kernel (bf16, n=8 rows; adapter, Wqkv, proj, fc+SwiGLU, mlp_proj)",
-                       "bytes_per_launch": int(avg_bytes), "avg_launch_us": round(avg_ms * 1e3, 2)}
-    log(f"bs1: linear roofline {ach:.0f} GB/s over {avg_ms * 1e3:.1f} us avg launch")
     del model, bb, pf
     torch.cuda.empty_cache()
     return w
@@ -292,6 +282,56 @@ def gqa_section(args, dev, res):
     torch.cuda.empty_cache()
 
 
+def roofline_section(args, dev, res):
+    """Dominant kernel of the decode tick: the weight-stream linear. The
+    headline figure is its largest stream, the gate|up projection with the
+    SwiGLU epilogue, at the bs=1 wavefront width (8 rows)."""
+    from wavefront_decoding_amd import model as M
+
+    lin = linear_roofline(dev, M.CONFIGS["looped-2048"], 8)
+    us, by = lin["fc_swiglu"]
+    ach = by / (us * 1e-6) / 1e9
+    res["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                       "kernel": "wfd::linear_wide_kernel<bf16_t, bf16_t, 2, 1, 1> (gate|up 11264x2048 + SwiGLU, "
+                                 "n=8 rows)",
+                       "bytes_per_launch": int(by), "avg_launch_us": round(us, 2)}
+    # HBM bytes per launch of this kernel at this shape, from the committed
+    # rocprofv3 FETCH_SIZE / WRITE_SIZE passes (a counter run cannot time itself)
+    tpath = os.path.join(REPO, "profiles", "linear_swiglu_n8_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            t = json.load(f)
+        if t.get("kernel", "") in res["roofline"]["kernel"]:
+            res["roofline"]["traffic"] = t["traffic_bytes"]
+            res["roofline"]["traffic_source"] = t["source"]
+    res["extra"]["linear_shapes_n8"] = {k: {"us": round(u, 2), "MB": round(b / 1e6, 2),
+                                            "GBs": round(b / (u * 1e-6) / 1e9, 1)} for k, (u, b) in lin.items()}
+    log(f"roofline: fc+SwiGLU linear {ach:.0f} GB/s over {us:.2f} us avg launch; shapes "
+        f"{res['extra']['linear_shapes_n8']}")
+    # a plain device copy of known size (256 MiB read + 256 MiB written): the
+    # scale for HBM byte counters (FETCH_SIZE / WRITE_SIZE) read in the same run
+    import torch
+
+    a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    del a, b
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def cpu_section(args, res, w=None):
     """The oracle (numpy float32, this host's cores) on a bounded sample of the
     bs=1 workload: WFD alpha=0.9 decode ticks over a random-filled 512-token
@@ -305,7 +345,7 @@ def cpu_section(args, res, w=None):
 
     cfg = M.CONFIGS["looped-2048"]
     w = w if w is not None else M.init_weights(cfg, 0)
-    L, N = 512, 100
+    L, N = 512, 150
     s0t = lambda p: M.initial_state_tokens(cfg, [p])[0].numpy()  # noqa: E731
     lm = OracleLM(cfg, M.weights_numpy(w), L + N + 8, 1, s0t, None)
     rng = np.random.default_rng(0)
@@ -322,12 +362,16 @@ def cpu_section(args, res, w=None):
     r = osched.wfd_batch(Warm(lm), [[0] * L], N, cfg.T_total, 2, [osched.Emu(0.9, 1000)])
     dt = time.perf_counter() - t0
     toks = len(r.per_seq[0].tokens) - 1  # the first token comes from the (skipped) prefill
-    res["cpu_baseline"] = {"value": round(toks / dt, 4), "unit": "tokens/s", "cores": os.cpu_count(),
-                           "kind": "port",
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max(i["num_threads"] for i in threadpool_info())
+    except Exception:  # threadpoolctl missing: numpy's BLAS defaults to one thread per core
+        threads = os.cpu_count()
+    res["cpu_baseline"] = {"value": round(toks / dt, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
                            "sample": (f"oracle WFD decode of {toks} tokens (alpha=0.9 emulated, T_total=16, T_draft=2, "
                                       f"{r.n_r_calls} R ticks) on the 2048-d model in float32 over a random-filled "
-                                      f"512-token prompt cache; {dt:.1f} s; numpy threads = host default; "
-                                      f"cpu={platform.processor() or platform.machine()}")}
+                                      f"512-token prompt cache; {dt:.1f} s; BLAS threads {threads} of "
+                                      f"{os.cpu_count()} cpus; cpu={_cpu_model()}")}
     log(f"cpu: {res['cpu_baseline']}")
 
 
@@ -353,15 +397,18 @@ def main():
         "value": None, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (random-init weights N(0,0.02) seed 0, uniform random prompts seed 0)",
-        "config": {"workload": "looped-2048 bf16 bs=1 WFD decode: 512-token prompt, 256 new tokens, T_total=16, "
-                               "T_draft=2 (W=8), emulated acceptance 0.9; step = one 256-token decode",
-                   "model": "looped-2048 (d=2048, 16x128 heads, SwiGLU 5632, 2+4x16+2 layers, V=32000)",
-                   "global_batch": 1, "seq_len": 512 + 256, "parallelism": "single GPU"},
+        "config": {"workload": "looped-2048 bf16 bs=1 WFD decode (d=2048, 16x128 heads, SwiGLU 5632, "
+                               "2 prelude + 4-layer core x 16 loops + 2 coda, V=32000): 512-token prompt, "
+                               "256 new tokens, T_total=16, T_draft=2 (W=8), emulated acceptance 0.9; "
+                               "step = one 256-token decode",
+                   "batch": 1, "prompt_len": 512, "new_tokens": 256, "T_total": 16, "T_draft": 2},
         "roofline": None, "cpu_baseline": None, "extra": {},
     }
     w = None
     if want("bs1"):
         w = bs1_section(args, dev, res)
+    if want("roofline"):
+        roofline_section(args, dev, res)
     if want("attn"):
         attn_section(args, dev, res)
     if want("bs32") and not args.quick:
