@@ -115,8 +115,10 @@ int wfd_linear_qkv_rope_append(const void* x, const int32_t* x_rows, int64_t ldx
 /*
  * x_out[out_rows ? out_rows[i] : i] = rmsnorm(a[a_rows ? a_rows[i] : i] + res[i]) * w1
  * and, if w2, h_out[i] = rmsnorm(x_out row) * w2. res may be NULL (plain
- * RMSNorm). D <= 4096 and a multiple of 512 (bf16) / 256 (fp32); every row
- * pointer 16-byte aligned. One wave per row: a row's bits never depend on n.
+ * RMSNorm). With w2, x_out may be NULL (not kept). D <= 4096 and a multiple of
+ * 128 (bf16) / 64 (fp32); every row 16-byte aligned. One wave per row; the
+ * sum of squares is reduced in wfd_linear's chunk order (chunks of 128 / 64
+ * elements), so a row's bits never depend on n.
  * Replaces: the SandwichBlock residual norms `norm_2(att + x)`, `norm_3`,
  *   `norm_4(mlp + x)`, `norm_1` and `ln_f`
  *   (src/decoding/huginn_blocks.py:95,101-102,268,290;

@@ -168,6 +168,25 @@ def test_add_rmsnorm(gpu, dtype):
     assert torch.equal(y, ops.rmsnorm(x, w1.to(gpu), 1e-6))
 
 
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 512), (torch.bfloat16, 4096), (torch.float32, 256),
+                                     (torch.float32, 1984)])
+def test_add_rmsnorm_widths(gpu, dtype, D):
+    """Widths with fewer than 16 chunks, several rounds of 16 chunks, and a
+    ragged last round: against the oracle, and the fused second norm equals a
+    separate call on the stored first result."""
+    g = torch.Generator().manual_seed(D)
+    n = 7
+    a = torch.randn(n, D, generator=g).to(dtype).to(gpu)
+    r = torch.randn(n, D, generator=g).to(dtype).to(gpu)
+    w1 = (1 + 0.1 * torch.randn(D, generator=g)).to(dtype).to(gpu)
+    w2 = (1 + 0.1 * torch.randn(D, generator=g)).to(dtype).to(gpu)
+    x, h = ops.add_rmsnorm(a, w1, 1e-6, res=r, w2=w2)
+    assert rel_err(_np(x), ok.rmsnorm(_np(a) + _np(r), _np(w1), 1e-6)) <= TOL[dtype]
+    assert torch.equal(h, ops.rmsnorm(x, w2, 1e-6))
+    # rows of different launches agree bit for bit
+    assert torch.equal(ops.add_rmsnorm(a[3:4], w1, 1e-6, res=r[3:4]), x[3:4])
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("H,Hkv,Dh", [(16, 16, 128), (16, 4, 128), (4, 4, 64)])
 def test_qkv_rope_append(gpu, dtype, H, Hkv, Dh):

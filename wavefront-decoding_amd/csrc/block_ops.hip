@@ -44,71 +44,129 @@ int launch_status(const char* what) {
 constexpr int kRowThreads = 256;
 constexpr int kNormMaxD = 4096;
 
-// One wave per row, 16-byte vector loads; each lane owns D/64 consecutive-vector
-// elements. Sum of squares: lane-sequential, then a fixed xor butterfly, so a
-// row's result does not depend on the other rows of the launch.
-template <typename T>
+// One wave per row, 16-byte vector loads. The row is cut into the linear
+// layer's K chunks (KC elements); lane (j = lane / 16, c = lane % 16) holds,
+// per round r, chunk p = 16 r + c exactly as an MFMA A-operand lane holds it
+// (4 steps x V elements of lane group j), and the sum of squares is reduced in
+// the library's one order (chunk_sumsq, then chunks in order). Every load is
+// unconditional, and the residual / second-norm variants are compile-time, so
+// no load sits behind a data-dependent branch (whose join would wait for it).
+template <typename T, bool RES, bool TWO>
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
     const T* __restrict__ a, const int32_t* __restrict__ a_rows, int64_t lda, const T* __restrict__ res,
     int64_t ldr, const T* __restrict__ w1, const T* __restrict__ w2, T* __restrict__ x_out,
     const int32_t* __restrict__ out_rows, int64_t ldo, T* __restrict__ h_out, int64_t ldh, int n, int D, float eps) {
-  constexpr int V = Elem<T>::kVec;
-  constexpr int MAXJ = kNormMaxD / (64 * V);
-  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+  constexpr int V = Chunk<T>::V;
+  constexpr int KSTEP = Chunk<T>::KSTEP;
+  constexpr int KC = Chunk<T>::KC;
+  constexpr int MAXR = kNormMaxD / (16 * KC);
+  const int i = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
+  const int c = lane & 15;
+  const int j = lane >> 4;
   if (i >= n) return;  // no barriers below
-  const int nj = D / (64 * V);
+  const int P = D / KC;
   const int64_t ar = a_rows ? a_rows[i] : i;
-  const int64_t orow = out_rows ? out_rows[i] : i;
-  float v[MAXJ][V];
+  // every load is unconditional: a lane past the last chunk re-reads chunk
+  // P-1 (its sum is never used, nothing is stored for it)
+  float v[MAXR][kChunkSteps][V];
+  u32x4 wa[MAXR][kChunkSteps], wb[MAXR][kChunkSteps];
+#pragma unroll
+  for (int r = 0; r < MAXR; ++r) {
+    const int p = r * 16 + c < P ? r * 16 + c : P - 1;
+#pragma unroll
+    for (int s = 0; s < kChunkSteps; ++s) {
+      const int64_t off = (int64_t)p * KC + s * KSTEP + j * V;
+      Elem<T>::unpack(ld16(a + ar * lda + off), v[r][s]);
+      wa[r][s] = ld16(w1 + off);
+      if constexpr (TWO) wb[r][s] = ld16(w2 + off);
+      if constexpr (RES) {
+        float q[V];
+        Elem<T>::unpack(ld16(res + (int64_t)i * ldr + off), q);
+#pragma unroll
+        for (int e = 0; e < V; ++e) v[r][s][e] += q[e];
+      }
+    }
+  }
+  // first norm
+  float cp[MAXR];
+#pragma unroll
+  for (int r = 0; r < MAXR; ++r) cp[r] = chunk_sumsq<V>(v[r]);
   float ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < MAXJ; ++j) {
-    if (j < nj) {
-      const int e = (j * 64 + lane) * V;
-      Elem<T>::unpack(ld16(a + ar * lda + e), v[j]);
-      if (res) {
-        float r[V];
-        Elem<T>::unpack(ld16(res + (int64_t)i * ldr + e), r);
+  for (int r = 0; r < MAXR; ++r)
+    for (int q = 0; q < 16 && r * 16 + q < P; ++q) ss += __shfl(cp[r], q, 64);
+  float inv = rms_inv(ss, D, eps);
+  const int64_t orow = out_rows ? out_rows[i] : i;
 #pragma unroll
-        for (int k = 0; k < V; ++k) v[j][k] += r[k];
-      }
+  for (int r = 0; r < MAXR; ++r) {
+    const int p = r * 16 + c;
 #pragma unroll
-      for (int k = 0; k < V; ++k) ss = fmaf(v[j][k], v[j][k], ss);
-    }
-  }
-  float inv = 1.0f / sqrtf(wave_sum(ss) / (float)D + eps);
-  float ss2 = 0.f;
-#pragma unroll
-  for (int j = 0; j < MAXJ; ++j) {
-    if (j < nj) {
-      const int e = (j * 64 + lane) * V;
+    for (int s = 0; s < kChunkSteps; ++s) {
       float w[V];
-      Elem<T>::unpack(ld16(w1 + e), w);
-      T* dst = x_out + orow * ldo + e;
+      Elem<T>::unpack(wa[r][s], w);
 #pragma unroll
-      for (int k = 0; k < V; ++k) {
-        Elem<T>::store(dst + k, v[j][k] * inv * w[k]);
-        // continue from the stored (rounded) value: the fused second norm then
-        // equals a separate rmsnorm() of x_out
-        v[j][k] = Elem<T>::round(v[j][k] * inv * w[k]);
-        ss2 = fmaf(v[j][k], v[j][k], ss2);
+      for (int e = 0; e < V; ++e) v[r][s][e] = v[r][s][e] * inv * w[e];
+      const u32x4 pk = Elem<T>::pack(v[r][s]);
+      Elem<T>::unpack(pk, v[r][s]);  // continue from the rounded values
+      if (x_out && p < P) *reinterpret_cast<u32x4*>(x_out + orow * ldo + (int64_t)p * KC + s * KSTEP + j * V) = pk;
+    }
+  }
+  if constexpr (TWO) {
+    // second norm, from the rounded first result (== a separate rmsnorm of x_out)
+#pragma unroll
+    for (int r = 0; r < MAXR; ++r) cp[r] = chunk_sumsq<V>(v[r]);
+    ss = 0.f;
+#pragma unroll
+    for (int r = 0; r < MAXR; ++r)
+      for (int q = 0; q < 16 && r * 16 + q < P; ++q) ss += __shfl(cp[r], q, 64);
+    inv = rms_inv(ss, D, eps);
+#pragma unroll
+    for (int r = 0; r < MAXR; ++r) {
+      const int p = r * 16 + c;
+#pragma unroll
+      for (int s = 0; s < kChunkSteps; ++s) {
+        float w[V];
+        Elem<T>::unpack(wb[r][s], w);
+        float h[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) h[e] = v[r][s][e] * inv * w[e];
+        if (p < P)
+          *reinterpret_cast<u32x4*>(h_out + (int64_t)i * ldh + (int64_t)p * KC + s * KSTEP + j * V) =
+              Elem<T>::pack(h);
       }
     }
   }
-  if (w2 == nullptr) return;
-  inv = 1.0f / sqrtf(wave_sum(ss2) / (float)D + eps);
-#pragma unroll
-  for (int j = 0; j < MAXJ; ++j) {
-    if (j < nj) {
-      const int e = (j * 64 + lane) * V;
-      float w[V];
-      Elem<T>::unpack(ld16(w2 + e), w);
-      T* dst = h_out + (int64_t)i * ldh + e;
-#pragma unroll
-      for (int k = 0; k < V; ++k) Elem<T>::store(dst + k, v[j][k] * inv * w[k]);
-    }
-  }
+}
+
+template <typename T>
+static void launch_norm_t(const void* a, const int32_t* a_rows, int64_t lda, const void* res, int64_t ldr,
+                          const void* w1, const void* w2, void* x_out, const int32_t* out_rows, int64_t ldo,
+                          void* h_out, int64_t ldh, int n, int D, float eps, hipStream_t stream) {
+  const dim3 grid((n + 3) / 4), block(256);
+  const T *at = (const T*)a, *rt = (const T*)res, *w1t = (const T*)w1, *w2t = (const T*)w2;
+  T *xo = (T*)x_out, *ho = (T*)h_out;
+  if (res && w2)
+    hipLaunchKernelGGL((add_rmsnorm_kernel<T, true, true>), grid, block, 0, stream, at, a_rows, lda, rt, ldr, w1t, w2t,
+                       xo, out_rows, ldo, ho, ldh, n, D, eps);
+  else if (res)
+    hipLaunchKernelGGL((add_rmsnorm_kernel<T, true, false>), grid, block, 0, stream, at, a_rows, lda, rt, ldr, w1t,
+                       w2t, xo, out_rows, ldo, ho, ldh, n, D, eps);
+  else if (w2)
+    hipLaunchKernelGGL((add_rmsnorm_kernel<T, false, true>), grid, block, 0, stream, at, a_rows, lda, rt, ldr, w1t,
+                       w2t, xo, out_rows, ldo, ho, ldh, n, D, eps);
+  else
+    hipLaunchKernelGGL((add_rmsnorm_kernel<T, false, false>), grid, block, 0, stream, at, a_rows, lda, rt, ldr, w1t,
+                       w2t, xo, out_rows, ldo, ho, ldh, n, D, eps);
+}
+
+static void launch_add_rmsnorm(int dtype, const void* a, const int32_t* a_rows, int64_t lda, const void* res, int64_t ldr,
+                        const void* w1, const void* w2, void* x_out, const int32_t* out_rows, int64_t ldo,
+                        void* h_out, int64_t ldh, int n, int D, float eps, hipStream_t stream) {
+  if (dtype == kBF16)
+    launch_norm_t<bf16_t>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, stream);
+  else
+    launch_norm_t<float>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, stream);
 }
 
 template <typename T>
@@ -237,34 +295,28 @@ int wfd_add_rmsnorm(const void* a, const int32_t* a_rows, int64_t lda, const voi
                     const void* w2, void* x_out, const int32_t* out_rows, int64_t ldo, void* h_out, int64_t ldh, int n,
                     int D, float eps, int dtype, hipStream_t stream) {
   using namespace wfd;
-  const int vec = dtype == kBF16 ? Elem<bf16_t>::kVec : Elem<float>::kVec;
-  if (n < 0 || D <= 0 || D > kNormMaxD || D % (64 * vec) != 0) {
-    set_error("wfd_add_rmsnorm: bad shape n=%d D=%d (D <= %d, multiple of %d)", n, D, kNormMaxD, 64 * vec);
+  if (dtype != kBF16 && dtype != kF32) {
+    set_error("wfd_add_rmsnorm: unsupported dtype %d", dtype);
+    return kUnsupported;
+  }
+  const int kc = dtype == kBF16 ? Chunk<bf16_t>::KC : Chunk<float>::KC;
+  if (n < 0 || D <= 0 || D > kNormMaxD || D % kc != 0) {
+    set_error("wfd_add_rmsnorm: bad shape n=%d D=%d (D <= %d, multiple of %d)", n, D, kNormMaxD, kc);
     return kBadArg;
   }
   const int esz = dtype == kBF16 ? 2 : 4;
   if ((((uintptr_t)a | (uintptr_t)res | (uintptr_t)w1 | (uintptr_t)w2 | (uintptr_t)x_out | (uintptr_t)h_out) & 15) ||
-      ((lda * esz) & 15) || (res && ((ldr * esz) & 15)) || ((ldo * esz) & 15) || (h_out && ((ldh * esz) & 15))) {
+      ((lda * esz) & 15) || (res && ((ldr * esz) & 15)) || (x_out && ((ldo * esz) & 15)) ||
+      (h_out && ((ldh * esz) & 15))) {
     set_error("wfd_add_rmsnorm: rows must be 16-byte aligned");
     return kBadArg;
   }
   if (n == 0) return kOk;
-  if (!a || !w1 || !x_out || (w2 && !h_out)) {
+  if (!a || !w1 || (w2 && !h_out) || (!w2 && !x_out)) {
     set_error("wfd_add_rmsnorm: null pointer argument");
     return kBadArg;
   }
-  if (dtype == kBF16)
-    hipLaunchKernelGGL(add_rmsnorm_kernel<bf16_t>, dim3((n + 3) / 4), dim3(256), 0, stream, (const bf16_t*)a, a_rows,
-                       lda, (const bf16_t*)res, ldr, (const bf16_t*)w1, (const bf16_t*)w2, (bf16_t*)x_out, out_rows,
-                       ldo, (bf16_t*)h_out, ldh, n, D, eps);
-  else if (dtype == kF32)
-    hipLaunchKernelGGL(add_rmsnorm_kernel<float>, dim3((n + 3) / 4), dim3(256), 0, stream, (const float*)a, a_rows,
-                       lda, (const float*)res, ldr, (const float*)w1, (const float*)w2, (float*)x_out, out_rows, ldo,
-                       (float*)h_out, ldh, n, D, eps);
-  else {
-    set_error("wfd_add_rmsnorm: unsupported dtype %d", dtype);
-    return kUnsupported;
-  }
+  launch_add_rmsnorm(dtype, a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, stream);
   return launch_status("wfd_add_rmsnorm");
 }
 

@@ -39,11 +39,11 @@
 
 namespace wfd {
 
-constexpr int kChunkSteps = 4;
 constexpr int kWideWaves = 16;
 constexpr int kWideMaxChunksPerWave = 3;
 constexpr int kWideMaxRows = 16;
 enum Epilogue : int { kEpiPlain = 0, kEpiSwiGLU = 1, kEpiRope = 2 };
+
 
 // Operands of the QKV-RoPE-append epilogue (unused by the others).
 struct RopeArgs {
@@ -59,11 +59,8 @@ struct RopeArgs {
 };
 
 template <typename T>
-struct LinTraits {
-  static constexpr int V = Elem<T>::kVec;
-  static constexpr int KSTEP = 4 * V;             // k elements per MFMA step
-  static constexpr int KC = KSTEP * kChunkSteps;  // k elements per chunk
-};
+using LinTraits = Chunk<T>;
+
 
 // Column start of tile t (0..NT-1) of column group g.
 template <int NT, int EPI>
@@ -115,10 +112,28 @@ __device__ __forceinline__ void load_w(u32x4 (&wf)[NT][kChunkSteps], const T* co
 }
 
 template <typename T>
-__device__ __forceinline__ void load_x(u32x4 (&xf)[kChunkSteps], const T* xp, bool valid, int p) {
+__device__ __forceinline__ void load_x(u32x4 (&xf)[kChunkSteps], const T* xp, int p) {
   constexpr int KSTEP = LinTraits<T>::KSTEP;
 #pragma unroll
-  for (int s = 0; s < kChunkSteps; ++s) xf[s] = valid ? ld16(xp + (int64_t)(p * kChunkSteps + s) * KSTEP) : zero16();
+  for (int s = 0; s < kChunkSteps; ++s) xf[s] = ld16(xp + (int64_t)(p * kChunkSteps + s) * KSTEP);
+}
+
+// Operand row of lane `col` in the 16-row tile starting at `base` (uniform
+// over the wave): x_rows[base + col], read with uniform scalar loads, so the
+// vector-memory counter tracks operand data only and no weight load waits for
+// an index. Lanes at or past n take the tile's first row: every load stays in
+// range and straight-line (a divergent guarded load costs a wait at the join),
+// and their results are never stored -- MFMA rows never mix.
+__device__ __forceinline__ int tile_row(const int32_t* __restrict__ x_rows, int base, int col, int n) {
+  const int m = n - base < 16 ? n - base : 16;
+  if (!x_rows) return base + (col < m ? col : 0);
+  int r = 0;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int v = x_rows[base + (j < m ? j : 0)];
+    r = col == j ? v : r;
+  }
+  return r;
 }
 
 template <typename T, int NT>
@@ -147,21 +162,22 @@ __global__ __launch_bounds__(64 * kWideWaves) void linear_wide_kernel(
   const int col = lane & 15;
   const int grp = lane >> 4;
 
-  const int xr = col < n ? (x_rows ? x_rows[col] : col) : -1;  // first: never waits behind the weights
+  const int xr = tile_row(x_rows, 0, col, n);
   const T* wrow[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) wrow[t] = W + (int64_t)(tile_col<NT, EPI>(g, t, pair_off) + col) * K + grp * V;
-  const T* xp = x + (int64_t)(xr < 0 ? 0 : xr) * ldx + grp * V;
+  const T* xp = x + (int64_t)xr * ldx + grp * V;
 
+  // Every load below is unconditional; a wave past the last chunk re-reads
+  // chunk P-1 and discards it.
   u32x4 wf[MC][NT][kChunkSteps];
   u32x4 xf[MC][kChunkSteps];
 #pragma unroll
   for (int j = 0; j < MC; ++j) {
     const int p = wave + kWideWaves * j;
-    if (p < P) {
-      load_w<T, NT>(wf[j], wrow, p);
-      load_x<T>(xf[j], xp, xr >= 0, p);
-    }
+    const int pc = p < P ? p : P - 1;
+    load_w<T, NT>(wf[j], wrow, pc);
+    load_x<T>(xf[j], xp, pc);
   }
 #pragma unroll
   for (int j = 0; j < MC; ++j) {
@@ -210,16 +226,14 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ 
                                                           const RopeArgs ra) {
   constexpr int V = LinTraits<T>::V;
   constexpr int NC = NB * NT;  // weight tiles per wave
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int col = lane & 15;
   const int grp = lane >> 4;
   const int row0 = (blockIdx.x * 4 + wave) * 16;
   if (row0 >= n) return;  // no barriers in this kernel
   const int P = K / LinTraits<T>::KC;
-  const int row = row0 + col;
-  const bool valid = row < n;
-  const int xr = valid ? (x_rows ? x_rows[row] : row) : 0;
+  const int xr = tile_row(x_rows, row0, col, n);
 
   const T* wrow[NC];
   bool gok[NB];
@@ -233,17 +247,18 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ 
   }
   const T* xp = x + (int64_t)xr * ldx + grp * V;
 
+  // two-stage register pipeline; every load is unconditional (the stage past
+  // the last chunk re-reads chunk P-1 and is never used)
   f32x4 tot[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) tot[c] = f32x4{0.f, 0.f, 0.f, 0.f};
   u32x4 wa[NC][kChunkSteps], wb[NC][kChunkSteps], xa[kChunkSteps], xb[kChunkSteps];
   load_w<T, NC>(wa, wrow, 0);
-  load_x<T>(xa, xp, valid, 0);
+  load_x<T>(xa, xp, 0);
   for (int p = 0; p < P; p += 2) {
-    if (p + 1 < P) {
-      load_w<T, NC>(wb, wrow, p + 1);
-      load_x<T>(xb, xp, valid, p + 1);
-    }
+    const int p1 = p + 1 < P ? p + 1 : P - 1;
+    load_w<T, NC>(wb, wrow, p1);
+    load_x<T>(xb, xp, p1);
     f32x4 acc[NC];
     chunk_mma<T, NC>(acc, xa, wa);
 #pragma unroll
@@ -251,10 +266,9 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ 
 #pragma unroll
       for (int r = 0; r < 4; ++r) tot[c][r] += acc[c][r];
     if (p + 1 >= P) break;
-    if (p + 2 < P) {
-      load_w<T, NC>(wa, wrow, p + 2);
-      load_x<T>(xa, xp, valid, p + 2);
-    }
+    const int p2 = p + 2 < P ? p + 2 : P - 1;
+    load_w<T, NC>(wa, wrow, p2);
+    load_x<T>(xa, xp, p2);
     chunk_mma<T, NC>(acc, xb, wb);
 #pragma unroll
     for (int c = 0; c < NC; ++c)

@@ -40,12 +40,19 @@ enum Status : int {
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
-__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// fp32 -> bf16, round to nearest even, NaN kept quiet: one v_cvt_pk_bf16_f32
+// per pair on gfx950 (checked on the device against the bit-level RNE
+// formula over 2^26 patterns, ties, denormals and specials included: no
+// difference).
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float lo, float hi) {
+  const f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
+
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) { return (uint16_t)f32x2_to_bf16x2_bits(f, 0.f); }
 
 template <typename T>
 struct Elem;
@@ -62,6 +69,10 @@ struct Elem<float> {
     o[2] = __uint_as_float(w[2]);
     o[3] = __uint_as_float(w[3]);
   }
+  __device__ __forceinline__ static u32x4 pack(const float (&o)[4]) {
+    u32x4 w = {__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]), __float_as_uint(o[3])};
+    return w;
+  }
 };
 
 template <>
@@ -77,6 +88,12 @@ struct Elem<bf16_t> {
       o[2 * e] = __uint_as_float(w[e] << 16);
       o[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
     }
+  }
+  __device__ __forceinline__ static u32x4 pack(const float (&o)[8]) {
+    u32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w[e] = f32x2_to_bf16x2_bits(o[2 * e], o[2 * e + 1]);
+    return w;
   }
 };
 
@@ -109,6 +126,40 @@ __device__ __forceinline__ f32x4 mfma_step<float>(const u32x4& a, const u32x4& b
   for (int e = 0; e < 4; ++e)
     acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[e]), __uint_as_float(b[e]), acc, 0, 0, 0);
   return acc;
+}
+
+// K is consumed in chunks of kChunkSteps MFMA k-steps: KC = 128 bf16 / 64
+// fp32 elements. Lane group j (= lane / 16) of a wave holds, for step s of a
+// chunk, the V elements at chunk*KC + s*KSTEP + j*V.
+constexpr int kChunkSteps = 4;
+
+template <typename T>
+struct Chunk {
+  static constexpr int V = Elem<T>::kVec;
+  static constexpr int KSTEP = 4 * V;             // k elements per MFMA step
+  static constexpr int KC = KSTEP * kChunkSteps;  // k elements per chunk
+};
+
+// Sum of squares of one chunk of a row, held as above by the four lanes
+// l, l^16, l^32, l^48: g_j = sequential fma over (s, e) of lane group j, then
+// (g0 + g1) + (g2 + g3). A row's sum of squares is ((0 + cp_0) + cp_1) + ...
+// over its chunks in order: the RMSNorm kernel reduces in exactly this order,
+// the order of the linear layer's K chunks, so a norm fused into a linear
+// operand load can reproduce it bit for bit.
+template <int V>
+__device__ __forceinline__ float chunk_sumsq(const float (&v)[kChunkSteps][V]) {
+  float g = 0.f;
+#pragma unroll
+  for (int s = 0; s < kChunkSteps; ++s)
+#pragma unroll
+    for (int e = 0; e < V; ++e) g = fmaf(v[s][e], v[s][e], g);
+  g += __shfl_xor(g, 16, 64);
+  g += __shfl_xor(g, 32, 64);
+  return g;
+}
+
+__device__ __forceinline__ float rms_inv(float sumsq, int D, float eps) {
+  return 1.0f / sqrtf(sumsq / (float)D + eps);
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
