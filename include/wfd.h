@@ -87,7 +87,8 @@ int wfd_qkv_rope_append(const void* qkv, int64_t ldq, const int32_t* pos, const 
  * out_dtype may be WFD_F32 for bf16 inputs (logits). K must be a multiple of
  * wfd_linear_k_multiple(dtype), N of 16. K is summed in fixed 128 (bf16) /
  * 64 (fp32) element chunks, chunk partials added in chunk order, so y[m] does
- * not depend on n or on where row m sits.
+ * not depend on n or on where row m sits. Every x row read (x_rows[m] * ldx)
+ * must lie within the first 2 GiB of x.
  * Replaces: the nn.Linear calls of the block forwards -- Wqkv, proj, the gated
  *   MLP, adapter, lm_head (src/decoding/huginn_blocks.py:79,100-102,216,291;
  *   huginn_blocks_batch.py:149,160-161,299,345).
@@ -129,12 +130,15 @@ int wfd_add_rmsnorm(const void* a, const int32_t* a_rows, int64_t lda, const voi
                     int D, float eps, int dtype, wfd_stream_t stream);
 
 /*
- * out[i] = table[ids[i]] * scale.
+ * out[i] = table[id_i] * scale, id_i = ids[i]; a negative ids[i] with a ring
+ * is a token handle: id_i = ring[-ids[i] - 1] (the device token ring that
+ * wfd_argmax fills), so a sampled token feeds the next prelude without a
+ * host round trip. Ids are clamped into [0, vocab).
  * Replaces: wte(ids) * emb_scale (src/decoding/huginn_blocks.py:184-186;
  *   huginn_blocks_batch.py:215-217).
  */
-int wfd_embed(const int64_t* ids, const void* table, float scale, void* out, int64_t ldo, int n, int vocab, int D,
-              int dtype, wfd_stream_t stream);
+int wfd_embed(const int64_t* ids, const int64_t* ring, int64_t ring_len, const void* table, float scale, void* out,
+              int64_t ldo, int n, int vocab, int D, int dtype, wfd_stream_t stream);
 
 /*
  * dst[dst_rows ? dst_rows[i] : i, :width] = src[src_rows ? src_rows[i] : i, :width].
@@ -146,11 +150,14 @@ int wfd_copy_rows(const void* src, const int32_t* src_rows, int64_t lds, void* d
 
 /*
  * out[i] = argmax_j logits[i, j] (first index on ties), logits fp32, 16-byte
- * aligned.
- * Replaces: greedy_sample's argmax (src/decoding/acceptance.py:40-44) and
- *   coda_argmax_union's argmax (src/decoding/huginn_blocks_batch.py:345-346).
+ * aligned; with a ring, also ring[ring_rows[i]] = out[i] (rows outside
+ * [0, ring_len) are skipped).
+ * Replaces: greedy_sample's argmax and its .item() (src/decoding/acceptance.py:40-44)
+ *   and coda_argmax_union's argmax + .tolist() (src/decoding/huginn_blocks_batch.py:345-346):
+ *   with the ring, ids stay on the device until the caller reads them.
  */
-int wfd_argmax(const float* logits, int64_t ld, int64_t* out, int n, int vocab, wfd_stream_t stream);
+int wfd_argmax(const float* logits, int64_t ld, int64_t* out, int64_t* ring, const int32_t* ring_rows,
+               int64_t ring_len, int n, int vocab, wfd_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -282,6 +282,25 @@ def test_embed_copy_argmax(gpu):
     assert am[2].item() == 17
 
 
+def test_token_ring_round_trip(gpu):
+    """argmax drops ids into ring slots (padding rows aimed at a trash slot);
+    embed takes a handle -(slot + 1) from the ring, and plain ids as before."""
+    g = torch.Generator().manual_seed(10)
+    logits = torch.randn(4, 500, generator=g).to(gpu)
+    ring = torch.full((9,), -7, dtype=torch.int64, device=gpu)
+    rows = torch.tensor([5, 0, 8, 2], dtype=torch.int32, device=gpu)  # 8 = trash slot
+    out = ops.argmax(logits, ring=ring, ring_rows=rows)
+    ref = logits.argmax(dim=-1)
+    assert torch.equal(out, ref)
+    assert ring[5].item() == ref[0].item() and ring[0].item() == ref[1].item() and ring[2].item() == ref[3].item()
+    assert ring[1].item() == -7  # untouched
+    table = torch.randn(500, 256, generator=g).to(torch.bfloat16).to(gpu)
+    ids = torch.tensor([-6, 3, -1, -3], dtype=torch.int64, device=gpu)  # handles of slots 5, 0, 2
+    e = ops.embed(ids, table, 1.0, ring=ring)
+    want = torch.stack([ref[0], torch.tensor(3, device=gpu), ref[1], ref[3]])
+    assert torch.equal(e, table[want])
+
+
 def test_bad_arguments_raise(gpu):
     from wavefront_decoding_amd import _lib
 

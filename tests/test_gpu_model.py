@@ -215,3 +215,36 @@ def test_graph_mode_batch_emulated(gpu):
         bt = generate_wavefront_batch(bb, [p.to(gpu) for p in P], [10, 14, 7], SsdPolicy(cfg.T_total, 2), emus)
         res.append([(s.tokens, s.counters()) for s in bt.per_seq])
     assert res[0] == res[1]
+
+
+class _NoHandles:
+    """The same blocks without token handles: the schedulers then read every
+    argmax back as it is produced (the reference's behaviour)."""
+
+    def __init__(self, inner):
+        self._inner = inner
+
+    def __getattr__(self, name):
+        if name in ("resolve_tokens", "reset_token_ring"):
+            raise AttributeError(name)
+        return getattr(self._inner, name)
+
+
+@pytest.mark.parametrize("graphs", [False, True])
+def test_token_handles_match_eager_ids(gpu, graphs):
+    """Keeping sampled ids on the device (token ring + handles, no host read
+    per commit) gives the same tokens and counters as reading every id back,
+    for emulated WFD and for sequential batch decode."""
+    cfg = TINY
+    w = M.init_weights(cfg, 0)
+    P = [_prompt(40, 4), _prompt(25, 5), _prompt(33, 6)]
+    res = []
+    for handles in (True, False):
+        bb = LoopedBlocksBatch(LoopedModel(cfg, w, gpu, max_seq_len=128, max_batch=3, use_graphs=graphs))
+        blk = bb if handles else _NoHandles(bb)
+        emus = [EmulatedAcceptance(0.6, 2000 + b) for b in range(3)]
+        bt = generate_wavefront_batch(blk, [p.to(gpu) for p in P], [12, 9, 15], SsdPolicy(cfg.T_total, 2), emus)
+        ar = ar_generate_batch(blk, [p.to(gpu) for p in P], [6, 8, 5])
+        res.append(([(t.tokens, t.counters()) for t in bt.per_seq], [t.tokens for t in ar.per_seq]))
+        assert all(v >= 0 for t in bt.per_seq for v in t.tokens)
+    assert res[0] == res[1]

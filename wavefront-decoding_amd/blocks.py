@@ -272,11 +272,23 @@ class LoopedBlocksBatch:
             t.step += 1
 
     @torch.no_grad()
-    def coda_argmax_union(self, seq_ids, toks, cache) -> list[int]:
+    def coda_argmax_union(self, seq_ids, toks, cache, lazy: bool = False) -> list[int]:
+        """Greedy next-token ids of the union (src/decoding/huginn_blocks_batch.py:323-346).
+        lazy=True returns token handles (negative ints naming device token-ring
+        slots) without waiting for the GPU; `resolve_tokens` turns them into ids,
+        and prelude_union accepts them as token ids directly."""
         if not toks:
             return []
         _, ids = self.model.coda_union(cache, seq_ids, [t.position for t in toks])
+        if lazy and self.model.last_c_handles is not None:
+            return list(self.model.last_c_handles)
         return ids.tolist()
+
+    def reset_token_ring(self) -> None:
+        self.model.reset_token_ring()
+
+    def resolve_tokens(self, values) -> list[int]:
+        return self.model.resolve_tokens(values)
 
 
 def seq_positions(toks) -> np.ndarray:

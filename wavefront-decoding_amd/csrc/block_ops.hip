@@ -14,7 +14,9 @@
 //  * kv_append: the bare slot-cache append (same indexing, no rotation).
 //  * embed, copy_rows, argmax: token embedding gather (x emb_scale), row
 //    gather/scatter (initial loop state, wave-state pool), greedy argmax
-//    (acceptance.py:40-44) on device.
+//    (acceptance.py:40-44) on device. argmax can also drop each id into a
+//    device token ring and embed can take its ids from there, so a decode
+//    loop feeds sampled tokens back without a host round trip.
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -214,11 +216,16 @@ __global__ __launch_bounds__(kRowThreads) void kv_append_kernel(const T* __restr
 }
 
 template <typename T>
-__global__ __launch_bounds__(kRowThreads) void embed_kernel(const int64_t* __restrict__ ids, const T* __restrict__ table,
-                                                            float scale, T* __restrict__ out, int64_t ldo, int Vocab,
-                                                            int D) {
+__global__ __launch_bounds__(kRowThreads) void embed_kernel(const int64_t* __restrict__ ids,
+                                                            const int64_t* __restrict__ ring, int64_t ring_len,
+                                                            const T* __restrict__ table, float scale,
+                                                            T* __restrict__ out, int64_t ldo, int Vocab, int D) {
   const int i = blockIdx.x;
   int64_t id = ids[i];
+  if (id < 0 && ring) {  // a token handle: the id sits in the device token ring
+    const int64_t slot = -id - 1;
+    id = slot < ring_len ? ring[slot] : 0;
+  }
   id = id < 0 ? 0 : (id >= Vocab ? Vocab - 1 : id);
   for (int e = threadIdx.x; e < D; e += kRowThreads) {
     float x = Elem<T>::load(table + id * D + e);
@@ -249,7 +256,9 @@ __device__ __forceinline__ void argmax_merge(float& bv, int& bi, float ov, int o
 
 // One 1024-thread workgroup per row; first index wins ties (as torch.argmax).
 __global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float* __restrict__ logits, int64_t ld,
-                                                            int64_t* __restrict__ out, int Vocab) {
+                                                            int64_t* __restrict__ out, int64_t* __restrict__ ring,
+                                                            const int32_t* __restrict__ ring_rows, int64_t ring_len,
+                                                            int Vocab) {
   __shared__ float sv[kArgThreads / 64];
   __shared__ int si[kArgThreads / 64];
   const int i = blockIdx.x;
@@ -280,6 +289,10 @@ __global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float* __rest
     int ix = si[0];
     for (int w = 1; w < kArgThreads / 64; ++w) argmax_merge(b, ix, sv[w], si[w]);
     out[i] = (int64_t)ix;
+    if (ring) {
+      const int32_t r = ring_rows[i];
+      if (r >= 0 && r < ring_len) ring[r] = (int64_t)ix;
+    }
   }
 }
 
@@ -373,24 +386,24 @@ int wfd_kv_append(const void* k, const void* v, void* k_cache, void* v_cache, co
   return launch_status("wfd_kv_append");
 }
 
-int wfd_embed(const int64_t* ids, const void* table, float scale, void* out, int64_t ldo, int n, int vocab, int D,
-              int dtype, hipStream_t stream) {
+int wfd_embed(const int64_t* ids, const int64_t* ring, int64_t ring_len, const void* table, float scale, void* out,
+              int64_t ldo, int n, int vocab, int D, int dtype, hipStream_t stream) {
   using namespace wfd;
   if (n < 0 || vocab <= 0 || D <= 0 || ldo < D) {
     set_error("wfd_embed: bad shape n=%d vocab=%d D=%d", n, vocab, D);
     return kBadArg;
   }
   if (n == 0) return kOk;
-  if (!ids || !table || !out) {
-    set_error("wfd_embed: null pointer argument");
+  if (!ids || !table || !out || (ring && ring_len <= 0)) {
+    set_error("wfd_embed: null pointer argument (or empty ring)");
     return kBadArg;
   }
   if (dtype == kBF16)
-    hipLaunchKernelGGL(embed_kernel<bf16_t>, dim3(n), dim3(kRowThreads), 0, stream, ids, (const bf16_t*)table, scale,
-                       (bf16_t*)out, ldo, vocab, D);
+    hipLaunchKernelGGL(embed_kernel<bf16_t>, dim3(n), dim3(kRowThreads), 0, stream, ids, ring, ring_len,
+                       (const bf16_t*)table, scale, (bf16_t*)out, ldo, vocab, D);
   else if (dtype == kF32)
-    hipLaunchKernelGGL(embed_kernel<float>, dim3(n), dim3(kRowThreads), 0, stream, ids, (const float*)table, scale,
-                       (float*)out, ldo, vocab, D);
+    hipLaunchKernelGGL(embed_kernel<float>, dim3(n), dim3(kRowThreads), 0, stream, ids, ring, ring_len,
+                       (const float*)table, scale, (float*)out, ldo, vocab, D);
   else {
     set_error("wfd_embed: unsupported dtype %d", dtype);
     return kUnsupported;
@@ -423,22 +436,24 @@ int wfd_copy_rows(const void* src, const int32_t* src_rows, int64_t lds, void* d
   return launch_status("wfd_copy_rows");
 }
 
-int wfd_argmax(const float* logits, int64_t ld, int64_t* out, int n, int vocab, hipStream_t stream) {
+int wfd_argmax(const float* logits, int64_t ld, int64_t* out, int64_t* ring, const int32_t* ring_rows,
+               int64_t ring_len, int n, int vocab, hipStream_t stream) {
   using namespace wfd;
   if (n < 0 || vocab <= 0 || ld < vocab) {
     set_error("wfd_argmax: bad shape n=%d vocab=%d", n, vocab);
     return kBadArg;
   }
   if (n == 0) return kOk;
-  if (!logits || !out) {
-    set_error("wfd_argmax: null pointer argument");
+  if (!logits || !out || (ring && (!ring_rows || ring_len <= 0))) {
+    set_error("wfd_argmax: null pointer argument (ring needs ring_rows and a length)");
     return kBadArg;
   }
   if (((uintptr_t)logits) & 15) {
     set_error("wfd_argmax: logits must be 16-byte aligned");
     return kBadArg;
   }
-  hipLaunchKernelGGL(argmax_kernel, dim3(n), dim3(kArgThreads), 0, stream, logits, ld, out, vocab);
+  hipLaunchKernelGGL(argmax_kernel, dim3(n), dim3(kArgThreads), 0, stream, logits, ld, out, ring, ring_rows,
+                     ring_len, vocab);
   return launch_status("wfd_argmax");
 }
 

@@ -99,6 +99,19 @@ struct Elem<bf16_t> {
 
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 
+// Raw buffer view of a small operand (< 2 GiB): a load at an offset at or past
+// kBufInvalid reads zeros and sends no request to memory, so lanes that carry
+// padding rows cost no bandwidth and need no branch.
+constexpr uint32_t kBufInvalid = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+
+__device__ __forceinline__ u32x4 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+
 __device__ __forceinline__ u32x4 zero16() {
   u32x4 z = {0u, 0u, 0u, 0u};
   return z;

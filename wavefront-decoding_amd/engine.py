@@ -81,29 +81,40 @@ class _Staging:
 
 
 class _Captured:
-    """One captured pass: fixed device tables + pinned host copies + the graph."""
+    """One captured pass: fixed device tables, a ring of pinned host copies, the graph.
+
+    The device table buffer is baked into the graph; each replay is preceded by
+    one host->device copy into it (stream-ordered behind the previous replay).
+    The pinned source buffers rotate through a ring, so the host can enqueue
+    several replays ahead of the GPU and only waits when it laps the ring."""
+
+    DEPTH = 8
 
     def __init__(self, kind: str, nb: int, cache, n32: int, n64: int, device):
         self.kind, self.nb, self.cache = kind, nb, cache
         # one buffer [int64 tables | int32 tables] so a replay needs one host->device copy
         words = n64 + (n32 + 1) // 2
-        self.host = torch.empty(words, dtype=torch.int64).pin_memory()
+        self.host = [torch.empty(words, dtype=torch.int64).pin_memory() for _ in range(self.DEPTH)]
+        self.events: list[torch.cuda.Event | None] = [None] * self.DEPTH
+        self.i = 0
         self.dev = torch.empty(words, dtype=torch.int64, device=device)
         self.n32, self.n64 = n32, n64
         self.d64 = self.dev[:n64]
         self.d32 = self.dev[n64:].view(torch.int32)[:n32]
-        self.event: torch.cuda.Event | None = None
         self.graph: torch.cuda.CUDAGraph | None = None
 
     def load(self, i32: np.ndarray, i64: np.ndarray) -> None:
-        if self.event is not None:
-            self.event.synchronize()          # the previous copy out of the pinned buffer is done
-        h = self.host.numpy()
+        j = self.i
+        self.i = (j + 1) % self.DEPTH
+        if self.events[j] is not None:
+            self.events[j].synchronize()      # the copy out of this pinned buffer DEPTH loads ago is done
+        h = self.host[j].numpy()
         h[: self.n64] = i64
         h[self.n64:].view(np.int32)[: self.n32] = i32
-        self.dev.copy_(self.host, non_blocking=True)
-        self.event = torch.cuda.Event()
-        self.event.record()
+        self.dev.copy_(self.host[j], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self.events[j] = ev
 
 
 def _bucket(n: int) -> int:
@@ -118,7 +129,7 @@ class LoopedModel:
 
     def __init__(self, cfg: LoopedLMConfig, weights: dict[str, torch.Tensor], device="cuda", *, max_seq_len: int,
                  max_batch: int = 1, state_init: str = "random", state_seed: int = 0, use_graphs: bool = False,
-                 max_rows: int | None = None):
+                 max_rows: int | None = None, ring_len: int = 1 << 20):
         self.cfg = cfg
         self.device = torch.device(device)
         self.dtype = cfg.torch_dtype
@@ -152,6 +163,14 @@ class LoopedModel:
                                    dtype=torch.uint8, device=self.device)
         self.staging = _Staging(self.device)
         self._graphs: dict[tuple, _Captured] = {}
+        # device token ring: every C pass drops its argmax ids at host-allocated
+        # slots; a token is then a handle -(slot + 1) until read back, and the P
+        # pass embeds handles straight from the ring (no host round trip per
+        # commit). The extra last slot absorbs padding rows.
+        self.ring_len = ring_len
+        self.tok_ring = torch.zeros(ring_len + 1, dtype=torch.int64, device=self.device)
+        self._ring_next = 0
+        self.last_c_handles: list[int] | None = None
 
     # -- slots / rows ----------------------------------------------------------
     def slot_prelude(self, i: int) -> int:
@@ -208,9 +227,10 @@ class LoopedModel:
         c = self.cfg
         return {"P": c.n_prelude, "R": c.n_core, "C": c.n_coda}[kind]
 
-    def _tables(self, kind: str, cache, seqs, pos, steps, ids, nb: int):
-        """int32 [pos | kv_len | pool_row] and int64 [ids? | row_base x L | flat_row x L],
-        each block nb wide; rows n..nb-1 are padding aimed at the trash rows."""
+    def _tables(self, kind: str, cache, seqs, pos, steps, ids, nb: int, ring_base: int | None = None):
+        """int32 [pos | kv_len | pool_row | ring_slot (C only)] and int64
+        [ids (P only) | row_base x L | flat_row x L], each block nb wide; rows
+        n..nb-1 are padding aimed at the trash rows / trash ring slot."""
         c = self.cfg
         n = len(pos)
         L = self._layers(kind)
@@ -224,12 +244,16 @@ class LoopedModel:
         rb[:, :n] = (slots * cache.B + seqs[None, :]) * cache.S
         fr = rb.copy()
         fr[:, :n] += pos[None, :]
-        i32 = np.zeros(3 * nb, dtype=np.int32)
+        i32 = np.zeros((4 if kind == "C" else 3) * nb, dtype=np.int32)
         i32[:n] = pos
         i32[nb: nb + n] = pos + 1
         i32[nb + n: 2 * nb] = 1
         i32[2 * nb: 2 * nb + n] = seqs * self.R + pos % self.R
-        i32[2 * nb + n:] = self.trash_pool_row
+        i32[2 * nb + n: 3 * nb] = self.trash_pool_row
+        if kind == "C":
+            i32[3 * nb:] = self.ring_len
+            if ring_base is not None:
+                i32[3 * nb: 3 * nb + n] = np.arange(ring_base, ring_base + n, dtype=np.int32)
         parts = [rb.reshape(-1), fr.reshape(-1)]
         if kind == "P":
             idp = np.zeros(nb, dtype=np.int64)
@@ -246,7 +270,7 @@ class LoopedModel:
         rb = lambda l: t64[off + l * nb: off + (l + 1) * nb]  # noqa: E731
         fr = lambda l: t64[off + (L + l) * nb: off + (L + l + 1) * nb]  # noqa: E731
         if kind == "P":
-            ops.embed(t64[:nb], W["wte"], c.emb_scale, out=sc["x"])
+            ops.embed(t64[:nb], W["wte"], c.emb_scale, out=sc["x"], ring=self.tok_ring)
             ops.rmsnorm(sc["x"], W["prelude.0.norm_1"], c.norm_eps, n=nb, x_out=sc["h"])
             static_half = self.pool[:, c.d_model:]
             for i in range(L):
@@ -268,7 +292,7 @@ class LoopedModel:
                 nxt = W[f"coda.{i + 1}.norm_1"] if i + 1 < L else W["ln_f"]
                 self._block(f"coda.{i}.", nb, sc, pos_d, kvlen_d, rb(i), fr(i), kv_max, ws, cache, nxt)
             ops.linear(sc["h"], W["lm_head"], n=nb, out=sc["logits"], out_dtype=torch.float32)
-            ops.argmax(sc["logits"], n=nb, out=sc["ids"])
+            ops.argmax(sc["logits"], n=nb, out=sc["ids"], ring=self.tok_ring, ring_rows=t32[3 * nb: 4 * nb])
 
     def _captured(self, kind: str, nb: int, cache) -> _Captured:
         key = (kind, nb, id(cache))
@@ -276,7 +300,8 @@ class LoopedModel:
         if g is not None and g.cache is cache:
             return g
         L = self._layers(kind)
-        g = _Captured(kind, nb, cache, 3 * nb, (2 * L + (1 if kind == "P" else 0)) * nb, self.device)
+        g = _Captured(kind, nb, cache, (4 if kind == "C" else 3) * nb, (2 * L + (1 if kind == "P" else 0)) * nb,
+                      self.device)
         empty = np.zeros(0, dtype=np.int64)
         i32, i64 = self._tables(kind, cache, empty, empty, empty, empty, nb)   # all padding rows
         g.load(i32, i64)
@@ -290,20 +315,20 @@ class LoopedModel:
         self._graphs[key] = g
         return g
 
-    def _run(self, kind: str, cache, seqs, pos, steps=None, ids=None) -> None:
+    def _run(self, kind: str, cache, seqs, pos, steps=None, ids=None, ring_base=None) -> None:
         n = len(pos)
         if self.use_graphs:
             nb = _bucket(n)
             if nb > self.max_rows:
                 raise ValueError(f"union of {n} rows exceeds max_rows={self.max_rows}")
             g = self._captured(kind, nb, cache)
-            i32, i64 = self._tables(kind, cache, seqs, pos, steps, ids, nb)
+            i32, i64 = self._tables(kind, cache, seqs, pos, steps, ids, nb, ring_base)
             g.load(i32, i64)
             g.graph.replay()
         else:
             if n > self.max_rows:
                 raise ValueError(f"union of {n} rows exceeds max_rows={self.max_rows}")
-            i32, i64 = self._tables(kind, cache, seqs, pos, steps, ids, n)
+            i32, i64 = self._tables(kind, cache, seqs, pos, steps, ids, n, ring_base)
             t32, t64 = self.staging.upload([i32, i64])
             self._launch(kind, cache, n, t32, t64, int(pos.max()) + 1)
 
@@ -347,17 +372,39 @@ class LoopedModel:
                 cache.note_write(self.slot_core(s, l), b, p)
 
     def coda_union(self, cache, seqs, positions) -> tuple[torch.Tensor, torch.Tensor]:
-        """ln_f -> coda blocks -> ln_f -> lm_head for n rows. Returns
-        (logits (n, V) float32, argmax ids (n,) int64), both device views."""
+        """ln_f -> coda blocks -> ln_f -> lm_head -> argmax for n rows. Returns
+        (logits (n, V) float32, argmax ids (n,) int64), both device views that
+        the next call overwrites. The ids also land in the token ring:
+        `last_c_handles` lists their handles (None when the ring is full)."""
         seqs = np.asarray(seqs, dtype=np.int64)
         pos = np.asarray(positions, dtype=np.int64)
         n = len(pos)
         self._check(cache, seqs, pos)
-        self._run("C", cache, seqs, pos)
+        base = None
+        if self._ring_next + n <= self.ring_len:
+            base = self._ring_next
+            self._ring_next += n
+        self._run("C", cache, seqs, pos, ring_base=base)
+        self.last_c_handles = None if base is None else [-(base + i) - 1 for i in range(n)]
         for b, p in zip(seqs.tolist(), pos.tolist()):
             for i in range(self.cfg.n_coda):
                 cache.note_write(self.slot_coda(i), b, p)
         return self.sc["logits"][:n], self.sc["ids"][:n]
+
+    # -- token ring --------------------------------------------------------------------
+    def reset_token_ring(self) -> None:
+        """Start handing out ring slots from 0 (handles of earlier calls become invalid)."""
+        self._ring_next = 0
+
+    def resolve_tokens(self, values) -> list[int]:
+        """Token ids for a mix of plain ids (>= 0) and ring handles (< 0); one
+        device->host read of the used part of the ring."""
+        values = list(values)
+        slots = [-v - 1 for v in values if v < 0]
+        if not slots:
+            return values
+        host = self.tok_ring[: max(slots) + 1].cpu().numpy()
+        return [int(host[-v - 1]) if v < 0 else v for v in values]
 
     # -- prefill -----------------------------------------------------------------------
     def prefill_seq(self, cache, b: int, token_ids) -> torch.Tensor:

@@ -230,15 +230,20 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, **kw) -> torch.Tensor:
     return add_rmsnorm(x, w, eps, **kw)
 
 
-def embed(ids: torch.Tensor, table: torch.Tensor, scale: float = 1.0, *, out: torch.Tensor | None = None):
-    _need_cuda(ids, table, out)
+def embed(ids: torch.Tensor, table: torch.Tensor, scale: float = 1.0, *, out: torch.Tensor | None = None,
+          ring: torch.Tensor | None = None):
+    """out[i] = table[id_i] * scale; with `ring`, a negative ids[i] = -(slot + 1)
+    takes its id from ring[slot] on the device."""
+    _need_cuda(ids, table, out, ring)
     _need(ids.dtype == torch.int64 and ids.is_contiguous(), "ids: int64")
+    if ring is not None:
+        _need(ring.dtype == torch.int64 and ring.is_contiguous(), "ring: int64 contiguous")
     n = ids.numel()
     Vocab, D = table.shape
     if out is None:
         out = torch.empty(n, D, dtype=table.dtype, device=table.device)
-    rc = _lib.load().wfd_embed(ids.data_ptr(), table.data_ptr(), float(scale), out.data_ptr(), out.stride(0), n,
-                               Vocab, D, _dt(table), _stream())
+    rc = _lib.load().wfd_embed(ids.data_ptr(), _p(ring), ring.numel() if ring is not None else 0, table.data_ptr(),
+                               float(scale), out.data_ptr(), out.stride(0), n, Vocab, D, _dt(table), _stream())
     _lib.check(rc, "wfd_embed")
     return out
 
@@ -254,12 +259,20 @@ def copy_rows(src: torch.Tensor, dst: torch.Tensor, *, n: int, width: int, src_r
     _lib.check(rc, "wfd_copy_rows")
 
 
-def argmax(logits: torch.Tensor, *, n: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
-    _need_cuda(logits, out)
+def argmax(logits: torch.Tensor, *, n: int | None = None, out: torch.Tensor | None = None,
+           ring: torch.Tensor | None = None, ring_rows: torch.Tensor | None = None) -> torch.Tensor:
+    """out[i] = argmax logits[i] (first index on ties); with `ring`, also
+    ring[ring_rows[i]] = out[i]."""
+    _need_cuda(logits, out, ring, ring_rows)
     _need(logits.dtype == torch.float32 and logits.dim() == 2 and logits.stride(1) == 1, "logits: float32 (n, V)")
     n = logits.shape[0] if n is None else n
+    if ring is not None:
+        _need(ring.dtype == torch.int64 and ring.is_contiguous(), "ring: int64 contiguous")
+        _rows(ring_rows, n, "ring_rows")
+        _need(ring_rows is not None, "ring needs ring_rows")
     if out is None:
         out = torch.empty(n, dtype=torch.int64, device=logits.device)
-    rc = _lib.load().wfd_argmax(logits.data_ptr(), logits.stride(0), out.data_ptr(), n, logits.shape[1], _stream())
+    rc = _lib.load().wfd_argmax(logits.data_ptr(), logits.stride(0), out.data_ptr(), _p(ring), _p(ring_rows),
+                                ring.numel() if ring is not None else 0, n, logits.shape[1], _stream())
     _lib.check(rc, "wfd_argmax")
     return out

@@ -132,7 +132,19 @@ def _start(blocks, prompt_ids, emus, max_new_tokens, bt: BatchTrace, t0: float, 
     return cache, seqs, t0
 
 
-def _finish(bt: BatchTrace, seqs, t0: float, device, cache) -> BatchTrace:
+def _lazy_tokens(blocks) -> bool:
+    """Blocks that can hand out device token handles (no host sync per commit)."""
+    ok = hasattr(blocks, "resolve_tokens") and hasattr(blocks, "reset_token_ring")
+    if ok:
+        blocks.reset_token_ring()
+    return ok
+
+
+def _finish(bt: BatchTrace, seqs, t0: float, device, cache, blocks=None, lazy: bool = False) -> BatchTrace:
+    if lazy:  # one read of the token ring for the whole generation
+        for s in seqs:
+            s.committed[:] = blocks.resolve_tokens(s.committed)
+            s.trace.tokens[:] = blocks.resolve_tokens(s.trace.tokens)
     if device.type == "cuda":
         torch.cuda.synchronize()
     bt.walltime_s = time.perf_counter() - t0
@@ -160,6 +172,7 @@ def ar_generate_batch(blocks, prompt_ids, max_new_tokens, prefilled: SharedPrefi
         torch.cuda.reset_peak_memory_stats()
     bt = BatchTrace()
     cache, seqs, t0 = _start(blocks, prompt_ids, None, max_new_tokens, bt, time.perf_counter(), prefilled)
+    lazy = _lazy_tokens(blocks)  # sequential decode never compares ids: keep them on the device
     while True:
         act = [s for s in seqs if not s.done]
         if not act:
@@ -177,13 +190,14 @@ def ar_generate_batch(blocks, prompt_ids, max_new_tokens, prefilled: SharedPrefi
             _record_r(bt, len(toks))
             for s in act:
                 s.trace.n_r_calls += 1
-        out = blocks.coda_argmax_union(ids, toks, cache)
+        out = blocks.coda_argmax_union(ids, toks, cache, lazy=True) if lazy else blocks.coda_argmax_union(
+            ids, toks, cache)
         bt.n_c_calls += 1
         for s, nid in zip(act, out):
             s.trace.n_c_calls += 1
             s.commit(nid)
             s.done = len(s.committed) >= s.max_new_tokens
-    return _finish(bt, seqs, t0, device, cache)
+    return _finish(bt, seqs, t0, device, cache, blocks, lazy)
 
 
 @torch.no_grad()
@@ -196,6 +210,8 @@ def generate_wavefront_batch(blocks, prompt_ids, max_new_tokens, policy: SsdPoli
     bt = BatchTrace()
     cache, seqs, t0 = _start(blocks, prompt_ids, emus, max_new_tokens, bt, time.perf_counter(), prefilled)
     T_total, T_draft = policy.T_total, policy.T_draft
+    # emulated acceptance never compares ids, so they can stay on the device
+    lazy = emus is not None and all(e is not None for e in emus) and _lazy_tokens(blocks)
     for s in seqs:
         if not s.done:
             s.active_p.append(ActiveToken(token_id=s.committed[-1], position=s.prefix_len, role="draft"))
@@ -258,7 +274,9 @@ def generate_wavefront_batch(blocks, prompt_ids, max_new_tokens, policy: SsdPoli
                 c_ids += [s.idx] * (len(vs) + len(ds))
         gold_of: dict[int, int] = {}
         if c_toks:
-            gold_of = {id(t): g for t, g in zip(c_toks, blocks.coda_argmax_union(c_ids, c_toks, cache))}
+            golds = (blocks.coda_argmax_union(c_ids, c_toks, cache, lazy=True) if lazy
+                     else blocks.coda_argmax_union(c_ids, c_toks, cache))
+            gold_of = {id(t): g for t, g in zip(c_toks, golds)}
             bt.n_c_calls += 1
             for s, _, _ in plan:
                 s.trace.n_c_calls += 1
@@ -301,4 +319,4 @@ def generate_wavefront_batch(blocks, prompt_ids, max_new_tokens, policy: SsdPoli
                 s.active_p.append(ActiveToken(token_id=gold_of[id(src)], position=src.position + 1, role="draft"))
                 s.trace.n_p_calls += 1
             s.active_c = []
-    return _finish(bt, seqs, t0, device, cache)
+    return _finish(bt, seqs, t0, device, cache, blocks, lazy)
