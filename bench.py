@@ -95,11 +95,12 @@ def attn_bench(dev, n, H, Hkv, Dh, lens, iters=40):
     return ms * 1e3, by
 
 
-def linear_roofline(dev, cfg, n: int, iters: int = 30):
+def linear_roofline(dev, cfg, n: int, iters: int = 24):
     """The weight-stream linear kernel at the decode shapes of one R tick
     (n rows): per shape, average launch duration (HIP events on the launch
-    stream) and algorithmic bytes (W + x + y) per launch, over rotating weight
-    copies (> 512 MB, so HBM, not the MALL, serves every launch). Returns
+    stream around graph replays of `iters` back-to-back launches) and
+    algorithmic bytes (W + x + y) per launch, over rotating weight copies
+    (> 512 MB, so HBM, not the MALL, serves every launch). Returns
     {name: (us, bytes)}."""
     import torch
     from wavefront_decoding_amd import ops
@@ -112,19 +113,30 @@ def linear_roofline(dev, cfg, n: int, iters: int = 30):
     per_tick = sum(N * K * 2 for _, N, K, _ in shapes)
     copies = max(2, math.ceil(2 * MALL_BYTES / per_tick) + 1)
     g = torch.Generator(device=dev).manual_seed(1)
-    Ws = [[(0.02 * torch.randn(N, K, device=dev, generator=g)).to(torch.bfloat16) for _, N, K, _ in shapes]
-          for _ in range(copies)]
+    Ws = [[ops.pack_linear((0.02 * torch.randn(N, K, device=dev, generator=g)).to(torch.bfloat16), swiglu=sw)
+           for _, N, K, sw in shapes] for _ in range(copies)]
     x = torch.randn(n, 2 * D, device=dev, generator=g).to(torch.bfloat16)
     xf = torch.randn(n, c.ffn, device=dev, generator=g).to(torch.bfloat16)
     out = torch.empty(n, 2 * c.ffn, device=dev, dtype=torch.bfloat16)
     res = {}
     for j, (name, N, K, sw) in enumerate(shapes):
         src = xf if K == c.ffn else x
-        call = lambda i, j=j, K=K, sw=sw, src=src: ops.linear(src, Ws[i % copies][j], n=n, out=out, swiglu=sw, k=K)  # noqa: E731
-        timed(call, 2)
-        ms = timed(call, iters)
+
+        def loop(j=j, K=K, sw=sw, src=src):
+            for i in range(iters):
+                ops.linear(src, Ws[i % copies][j], n=n, out=out, swiglu=sw, k=K)
+
+        # captured once, so the launches are back to back (no host gaps between them)
+        loop()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            loop()
+        graph.replay()
+        ms = timed(lambda i: graph.replay(), 3) / iters
         width = N // 2 if sw else N
         res[name] = (ms * 1e3, N * K * 2 + n * K * 2 + n * width * 2)
+        del graph
     del Ws
     torch.cuda.empty_cache()
     return res

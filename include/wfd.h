@@ -80,11 +80,28 @@ int wfd_qkv_rope_append(const void* qkv, int64_t ldq, const int32_t* pos, const 
                         const float* rope_sin, int rope_rows, const int64_t* flat_row, void* q_out, void* k_cache,
                         void* v_cache, int n, int H, int Hkv, int Dh, int dtype, wfd_stream_t stream);
 
+/* Granularity of K for wfd_linear: 128 (bf16) / 64 (fp32) elements. */
+int wfd_linear_k_multiple(int dtype);
+
 /*
- * Row-invariant linear: y[m, :] = x[x_rows ? x_rows[m] : m, :K] @ W^T, W (N, K)
- * row-major. Epilogue WFD_EPI_SWIGLU: N = 2*pair_off, y[m, j] =
- * silu(g_j) * u_j with g_j = row j, u_j = row pair_off + j of the product.
- * out_dtype may be WFD_F32 for bf16 inputs (logits). K must be a multiple of
+ * Packs a row-major weight W (N, K) -- nn.Linear layout, for SwiGLU the gate
+ * rows [0, pair_off) then the up rows [pair_off, N) -- into the layout
+ * wfd_linear and wfd_linear_qkv_rope_append read: MFMA fragment order, tile
+ * by tile (16 output columns; a SwiGLU tile pairs 8 gate rows with their 8 up
+ * rows), so each weight load of the kernels reads 1 KB of contiguous memory.
+ * Same size as W; W_packed must not overlap W. Pack once, at load time.
+ * Replaces: nothing in the reference (its weights are read in place by
+ *   cuBLAS); the packed copy is the device-resident weight of this library.
+ */
+int wfd_linear_pack(const void* W, void* W_packed, int N, int K, int dtype, int epilogue, int pair_off,
+                    wfd_stream_t stream);
+
+/*
+ * Row-invariant linear: y[m, :] = x[x_rows ? x_rows[m] : m, :K] @ W^T with W
+ * (N, K) given packed by wfd_linear_pack (same epilogue and pair_off).
+ * Epilogue WFD_EPI_SWIGLU: N = 2*pair_off, y[m, j] = silu(g_j) * u_j with
+ * g_j = row j, u_j = row pair_off + j of the product. out_dtype may be
+ * WFD_F32 for bf16 inputs (logits). K must be a multiple of
  * wfd_linear_k_multiple(dtype), N of 16. K is summed in fixed 128 (bf16) /
  * 64 (fp32) element chunks, chunk partials added in chunk order, so y[m] does
  * not depend on n or on where row m sits. Every x row read (x_rows[m] * ldx)
@@ -93,14 +110,14 @@ int wfd_qkv_rope_append(const void* qkv, int64_t ldq, const int32_t* pos, const 
  *   MLP, adapter, lm_head (src/decoding/huginn_blocks.py:79,100-102,216,291;
  *   huginn_blocks_batch.py:149,160-161,299,345).
  */
-int wfd_linear_k_multiple(int dtype);
 int wfd_linear(const void* x, const int32_t* x_rows, int64_t ldx, const void* W, void* y, int64_t ldy, int n, int N,
                int K, int dtype, int out_dtype, int epilogue, int pair_off, wfd_stream_t stream);
 
 /*
  * The fused q|k|v projection with wfd_qkv_rope_append as its epilogue:
- * qkv = x[x_rows ? x_rows[i] : i] @ Wqkv^T, Wqkv ((H + 2*Hkv) * Dh, K), under
- * wfd_linear's arithmetic contract; each qkv value is rounded to `dtype`, then
+ * qkv = x[x_rows ? x_rows[i] : i] @ Wqkv^T, Wqkv ((H + 2*Hkv) * Dh, K) packed
+ * by wfd_linear_pack (plain epilogue), under wfd_linear's arithmetic
+ * contract; each qkv value is rounded to `dtype`, then
  * rotated, written and appended exactly as wfd_qkv_rope_append does, so the
  * result equals wfd_linear followed by wfd_qkv_rope_append bit for bit. The
  * qkv rows themselves are never stored. Dh % 16 == 0, K as for wfd_linear.

@@ -42,3 +42,7 @@ def test_host_only_entry_points():
     rc = lib.wfd_linear(None, None, 100, None, None, 16, 2, 16, 100, 1, 1, 0, 0, None)
     assert rc == -1
     assert lib.wfd_attn_decode(None, None, None, None, None, None, 0, 16, 16, 64, 1, 0.1, 10, None, 0, None) == 0
+    # packing: shape and aliasing are checked on the host
+    assert lib.wfd_linear_pack(8, 16, 24, 128, 1, 0, 0, None) == -1      # N not a multiple of 16
+    assert lib.wfd_linear_pack(8, 8, 32, 128, 1, 0, 0, None) == -1       # W_packed aliases W
+    assert lib.wfd_linear_pack(8, 16, 32, 128, 1, 1, 12, None) == -1     # swiglu pair_off mismatch

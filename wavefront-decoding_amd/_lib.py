@@ -39,6 +39,7 @@ SIGNATURES: dict[str, tuple] = {
     "wfd_qkv_rope_append": (_i32, [_vp, _i64, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
                                    _i32, _vp]),
     "wfd_linear_k_multiple": (_i32, [_i32]),
+    "wfd_linear_pack": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
     "wfd_linear": (_i32, [_vp, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
     "wfd_linear_qkv_rope_append": (_i32, [_vp, _vp, _i64, _vp, _i32, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp,
                                           _i32, _i32, _i32, _i32, _vp]),

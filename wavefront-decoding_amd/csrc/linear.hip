@@ -32,6 +32,13 @@
 // So y[m] is bit-identical whatever n is and wherever row m sits -- the
 // property that keeps wavefront decode token-identical to sequential decode.
 //
+// Weight layout ("packed", made once by wfd_linear_pack): W is stored in MFMA
+// fragment order, tile by tile -- for tile g, chunk p, step s the 64 lanes'
+// 16-byte B fragments sit back to back, so every weight load instruction of a
+// wave reads 1 KB of contiguous memory (row-major W would make each
+// instruction touch 16 rows x 64 B). SwiGLU gate/up rows are paired into
+// tiles by the packing.
+//
 // Epilogues: plain store (bf16 or fp32 out); SwiGLU, out = silu(gate) * up
 // from columns c and c + 8 of a tile (one lane shuffle apart); and
 // QKV-RoPE-append, for the fused q|k|v projection: the output row is rounded
@@ -114,13 +121,39 @@ __device__ __forceinline__ void store_out(TO* __restrict__ y, int64_t ldy, const
   }
 }
 
+// Packed weights: element offset of lane `lane`'s fragment of (tile g, chunk
+// p, step 0); step s adds s * 64 * V.
+template <typename T>
+__device__ __forceinline__ int64_t packed_off(int g, int p, int P, int lane) {
+  return (((int64_t)g * P + p) * kChunkSteps * 64 + lane) * Chunk<T>::V;
+}
+
 template <typename T, int NT>
-__device__ __forceinline__ void load_w(u32x4 (&wf)[NT][kChunkSteps], const T* const (&wrow)[NT], int p) {
-  constexpr int KSTEP = LinTraits<T>::KSTEP;
+__device__ __forceinline__ void load_w(u32x4 (&wf)[NT][kChunkSteps], const T* const (&wtile)[NT], int P, int p,
+                                       int lane) {
 #pragma unroll
   for (int s = 0; s < kChunkSteps; ++s)
 #pragma unroll
-    for (int t = 0; t < NT; ++t) wf[t][s] = ld16(wrow[t] + (int64_t)(p * kChunkSteps + s) * KSTEP);
+    for (int t = 0; t < NT; ++t)
+      wf[t][s] = ld16(wtile[t] + packed_off<T>(0, p, P, lane) + (int64_t)s * 64 * Chunk<T>::V);
+}
+
+// Packing: one thread per 16-byte fragment, in packed order.
+template <typename T, int EPI>
+__global__ __launch_bounds__(256) void linear_pack_kernel(const T* __restrict__ W, T* __restrict__ Wp, int K,
+                                                          int pair_off, int64_t nfrag) {
+  constexpr int V = Chunk<T>::V;
+  const int64_t f = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (f >= nfrag) return;
+  const int P = K / Chunk<T>::KC;
+  const int lane = (int)(f % 64);
+  const int s = (int)((f / 64) % kChunkSteps);
+  const int64_t gp = f / (64 * kChunkSteps);
+  const int p = (int)(gp % P);
+  const int g = (int)(gp / P);
+  const int row = weight_row<EPI>(g, lane & 15, pair_off);
+  const int64_t k = (int64_t)p * Chunk<T>::KC + s * Chunk<T>::KSTEP + (lane >> 4) * V;
+  *reinterpret_cast<u32x4*>(Wp + f * V) = ld16(W + (int64_t)row * K + k);
 }
 
 // x fragments of chunk p for the lane whose row starts at byte offset xoff in
@@ -182,7 +215,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void linear_wide_kernel(
 
   const uint32_t xoff = x_offset<T>(x_rows, ldx, 0, col, grp, n);
   const __amdgpu_buffer_rsrc_t xrs = buf_rsrc(x);
-  const T* const wrow[1] = {W + (int64_t)weight_row<EPI>(g, col, pair_off) * K + grp * V};
+  const T* const wtile[1] = {W + packed_off<T>(g, 0, P, 0)};
 
   // Every load is unconditional; a wave past the last chunk re-reads chunk
   // P-1 and discards it.
@@ -192,7 +225,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void linear_wide_kernel(
   for (int j = 0; j < MC; ++j) {
     const int p = wave + kWideWaves * j;
     const int pc = p < P ? p : P - 1;
-    load_w<T, 1>(wf[j], wrow, pc);
+    load_w<T, 1>(wf[j], wtile, P, pc, lane);
     load_x<T>(xf[j], xrs, xoff, pc);
   }
 #pragma unroll
@@ -241,13 +274,13 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ 
   const uint32_t xoff = x_offset<T>(x_rows, ldx, row0, col, grp, n);
   const __amdgpu_buffer_rsrc_t xrs = buf_rsrc(x);
 
-  const T* wrow[NB];
+  const T* wtile[NB];
   bool gok[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
     const int g = blockIdx.y * NB + b;
     gok[b] = g < tiles;
-    wrow[b] = W + (int64_t)weight_row<EPI>(gok[b] ? g : 0, col, pair_off) * K + grp * V;
+    wtile[b] = W + packed_off<T>(gok[b] ? g : 0, 0, P, 0);
   }
 
   // two-stage register pipeline; every load is unconditional (the stage past
@@ -256,11 +289,11 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ 
 #pragma unroll
   for (int c = 0; c < NB; ++c) tot[c] = f32x4{0.f, 0.f, 0.f, 0.f};
   u32x4 wa[NB][kChunkSteps], wb[NB][kChunkSteps], xa[kChunkSteps], xb[kChunkSteps];
-  load_w<T, NB>(wa, wrow, 0);
+  load_w<T, NB>(wa, wtile, P, 0, lane);
   load_x<T>(xa, xrs, xoff, 0);
   for (int p = 0; p < P; p += 2) {
     const int p1 = p + 1 < P ? p + 1 : P - 1;
-    load_w<T, NB>(wb, wrow, p1);
+    load_w<T, NB>(wb, wtile, P, p1, lane);
     load_x<T>(xb, xrs, xoff, p1);
     f32x4 acc[NB];
     chunk_mma<T, NB>(acc, xa, wa);
@@ -270,7 +303,7 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ 
       for (int r = 0; r < 4; ++r) tot[c][r] += acc[c][r];
     if (p + 1 >= P) break;
     const int p2 = p + 2 < P ? p + 2 : P - 1;
-    load_w<T, NB>(wa, wrow, p2);
+    load_w<T, NB>(wa, wtile, P, p2, lane);
     load_x<T>(xa, xrs, xoff, p2);
     chunk_mma<T, NB>(acc, xb, wb);
 #pragma unroll
@@ -325,6 +358,48 @@ extern "C" {
 int wfd_linear_k_multiple(int dtype) {
   using namespace wfd;
   return dtype == kBF16 ? LinTraits<bf16_t>::KC : LinTraits<float>::KC;
+}
+
+int wfd_linear_pack(const void* W, void* W_packed, int N, int K, int dtype, int epilogue, int pair_off,
+                    hipStream_t stream) {
+  using namespace wfd;
+  const int kmul = wfd_linear_k_multiple(dtype);
+  if (N <= 0 || K <= 0 || N % 16 != 0 || K % kmul != 0) {
+    set_error("wfd_linear_pack: N=%d must be a multiple of 16 and K=%d of %d", N, K, kmul);
+    return kBadArg;
+  }
+  if (!W || !W_packed || W == W_packed) {
+    set_error("wfd_linear_pack: null or aliased pointer argument");
+    return kBadArg;
+  }
+  if (epilogue == kEpiSwiGLU && (pair_off <= 0 || pair_off % 8 != 0 || N != 2 * pair_off)) {
+    set_error("wfd_linear_pack: swiglu needs N == 2*pair_off, pair_off %% 8 == 0 (N=%d pair_off=%d)", N, pair_off);
+    return kBadArg;
+  }
+  if (epilogue != kEpiPlain && epilogue != kEpiSwiGLU) {
+    set_error("wfd_linear_pack: unknown epilogue %d", epilogue);
+    return kUnsupported;
+  }
+  const int V = dtype == kBF16 ? Chunk<bf16_t>::V : Chunk<float>::V;
+  const int64_t nfrag = (int64_t)N * K / V;
+  const dim3 grid((unsigned)((nfrag + 255) / 256)), block(256);
+  if (dtype == kBF16 && epilogue == kEpiSwiGLU)
+    hipLaunchKernelGGL((linear_pack_kernel<bf16_t, kEpiSwiGLU>), grid, block, 0, stream, (const bf16_t*)W,
+                       (bf16_t*)W_packed, K, pair_off, nfrag);
+  else if (dtype == kBF16)
+    hipLaunchKernelGGL((linear_pack_kernel<bf16_t, kEpiPlain>), grid, block, 0, stream, (const bf16_t*)W,
+                       (bf16_t*)W_packed, K, pair_off, nfrag);
+  else if (dtype == kF32 && epilogue == kEpiSwiGLU)
+    hipLaunchKernelGGL((linear_pack_kernel<float, kEpiSwiGLU>), grid, block, 0, stream, (const float*)W,
+                       (float*)W_packed, K, pair_off, nfrag);
+  else if (dtype == kF32)
+    hipLaunchKernelGGL((linear_pack_kernel<float, kEpiPlain>), grid, block, 0, stream, (const float*)W,
+                       (float*)W_packed, K, pair_off, nfrag);
+  else {
+    set_error("wfd_linear_pack: unsupported dtype %d", dtype);
+    return kUnsupported;
+  }
+  return launch_status("wfd_linear_pack");
 }
 
 int wfd_linear(const void* x, const int32_t* x_rows, int64_t ldx, const void* W, void* y, int64_t ldy, int n, int N,

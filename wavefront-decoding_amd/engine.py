@@ -117,6 +117,10 @@ class _Captured:
         self.events[j] = ev
 
 
+# weights read by the linear kernels (the rest -- embedding, norms -- stay plain)
+_LINEAR_WEIGHTS = frozenset({"Wqkv", "proj", "fc", "mlp_proj", "adapter", "lm_head"})
+
+
 def _bucket(n: int) -> int:
     b = 1
     while b < n:
@@ -138,7 +142,13 @@ class LoopedModel:
         self.state_init = state_init
         self.state_seed = state_seed
         self.use_graphs = use_graphs
-        self.W = {k: v.to(device=self.device, dtype=self.dtype).contiguous() for k, v in weights.items()}
+        self.W = {}
+        for k, v in weights.items():
+            w = v.to(device=self.device, dtype=self.dtype).contiguous()
+            leaf = k.rsplit(".", 1)[-1]
+            if leaf in _LINEAR_WEIGHTS:  # stored once, in the kernels' packed layout
+                w = ops.pack_linear(w, swiglu=leaf == "fc")
+            self.W[k] = w
         cos, sin = rope_tables(max_seq_len, cfg.head_dim, cfg.rope_base)
         self.rope_cos = cos.to(self.device)
         self.rope_sin = sin.to(self.device)

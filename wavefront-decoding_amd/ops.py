@@ -145,12 +145,13 @@ def linear_qkv_rope_append(x: torch.Tensor, Wqkv: torch.Tensor, pos: torch.Tenso
                            x_rows: torch.Tensor | None = None, q_out: torch.Tensor | None = None) -> torch.Tensor:
     """q_out, plus k/v appended at flat_row: the Wqkv projection with RoPE and
     the cache append as its epilogue (== linear() then qkv_rope_append())."""
-    _need_cuda(x, Wqkv, pos, rope_cos, rope_sin, flat_row, k_cache, v_cache, x_rows, q_out)
+    _need_cuda(x, pos, rope_cos, rope_sin, flat_row, k_cache, v_cache, x_rows, q_out)
+    Wp = _packed(Wqkv, False)
     n = (x.shape[0] if x_rows is None else x_rows.numel()) if n is None else n
     _rows(x_rows, n, "x_rows")
-    K = Wqkv.shape[1]
-    _need(x.dim() == 2 and x.stride(1) == 1 and x.shape[1] >= K and x.dtype == Wqkv.dtype, "x (rows, K+)")
-    _need(Wqkv.is_contiguous() and Wqkv.shape[0] == (H + 2 * Hkv) * Dh, "Wqkv ((H+2Hkv)Dh, K) contiguous")
+    K = Wp.K
+    _need(x.dim() == 2 and x.stride(1) == 1 and x.shape[1] >= K and x.dtype == Wp.dtype, "x (rows, K+)")
+    _need(Wp.N == (H + 2 * Hkv) * Dh, "Wqkv ((H+2Hkv)Dh, K)")
     _need(pos.dtype == torch.int32 and pos.numel() >= n and pos.is_contiguous(), "pos: int32")
     _need(flat_row.dtype == torch.int64 and flat_row.numel() >= n and flat_row.is_contiguous(), "flat_row: int64")
     _need(rope_cos.dtype == torch.float32 and rope_cos.shape == rope_sin.shape and rope_cos.shape[1] == Dh // 2
@@ -160,7 +161,7 @@ def linear_qkv_rope_append(x: torch.Tensor, Wqkv: torch.Tensor, pos: torch.Tenso
     if q_out is None:
         q_out = torch.empty(n, H, Dh, dtype=x.dtype, device=x.device)
     _need(q_out.is_contiguous() and q_out.numel() >= n * H * Dh and q_out.dtype == x.dtype, "q_out (n, H, Dh)")
-    rc = _lib.load().wfd_linear_qkv_rope_append(x.data_ptr(), _p(x_rows), x.stride(0), Wqkv.data_ptr(), n, K,
+    rc = _lib.load().wfd_linear_qkv_rope_append(x.data_ptr(), _p(x_rows), x.stride(0), Wp.data.data_ptr(), n, K,
                                                 pos.data_ptr(), rope_cos.data_ptr(), rope_sin.data_ptr(),
                                                 rope_cos.shape[0], flat_row.data_ptr(), q_out.data_ptr(),
                                                 k_cache.data_ptr(), v_cache.data_ptr(), H, Hkv, Dh, _dt(x), _stream())
@@ -175,18 +176,64 @@ def linear_k_multiple(dtype: torch.dtype) -> int:
     return int(_lib.load().wfd_linear_k_multiple(_DT[dtype]))
 
 
-def linear(x: torch.Tensor, W: torch.Tensor, *, n: int | None = None, x_rows: torch.Tensor | None = None,
+class PackedWeight:
+    """A linear weight in the kernels' packed layout (wfd_linear_pack): same
+    bytes as the (N, K) nn.Linear weight, in MFMA fragment order. `swiglu`
+    records the gate|up pairing the packing baked in."""
+
+    __slots__ = ("data", "N", "K", "swiglu")
+
+    def __init__(self, data: torch.Tensor, N: int, K: int, swiglu: bool):
+        self.data, self.N, self.K, self.swiglu = data, N, K, swiglu
+
+    @property
+    def dtype(self) -> torch.dtype:
+        return self.data.dtype
+
+    @property
+    def device(self) -> torch.device:
+        return self.data.device
+
+    @property
+    def shape(self) -> tuple[int, int]:
+        return (self.N, self.K)
+
+
+def pack_linear(W: torch.Tensor, *, swiglu: bool = False) -> PackedWeight:
+    """Pack a (N, K) weight (for swiglu: gate rows then up rows) once."""
+    _need_cuda(W)
+    _need(W.dim() == 2 and W.is_contiguous(), "W: contiguous (N, K)")
+    N, K = W.shape
+    out = torch.empty_like(W)
+    epi = _lib.EPI_SWIGLU if swiglu else _lib.EPI_PLAIN
+    rc = _lib.load().wfd_linear_pack(W.data_ptr(), out.data_ptr(), N, K, _dt(W), epi, N // 2 if swiglu else 0,
+                                     _stream())
+    _lib.check(rc, "wfd_linear_pack")
+    return PackedWeight(out, N, K, swiglu)
+
+
+def _packed(W, swiglu: bool) -> PackedWeight:
+    if isinstance(W, PackedWeight):
+        _need(W.swiglu == swiglu, "weight packed for a different epilogue")
+        return W
+    return pack_linear(W, swiglu=swiglu)  # a plain (N, K) tensor: pack a copy for this call
+
+
+def linear(x: torch.Tensor, W, *, n: int | None = None, x_rows: torch.Tensor | None = None,
            out: torch.Tensor | None = None, swiglu: bool = False, out_dtype: torch.dtype | None = None,
            k: int | None = None) -> torch.Tensor:
-    """y = x[rows, :K] @ W^T (W: (N, K)); swiglu: N = 2F, y (n, F) = silu(g) * u."""
-    _need_cuda(x, W, x_rows, out)
-    _need(x.dim() == 2 and x.stride(1) == 1 and W.dim() == 2 and W.is_contiguous(), "x (rows, K+), W (N, K)")
-    N, K = W.shape
+    """y = x[rows, :K] @ W^T (W: PackedWeight or plain (N, K)); swiglu: N = 2F,
+    y (n, F) = silu(g) * u."""
+    _need_cuda(x, x_rows, out)
+    Wp = _packed(W, swiglu)
+    _need_cuda(Wp.data)
+    _need(x.dim() == 2 and x.stride(1) == 1, "x (rows, K+)")
+    N, K = Wp.N, Wp.K
     if k is not None:
         _need(k == K, "K mismatch")
     n = x.shape[0] if (n is None and x_rows is None) else (n if n is not None else x_rows.numel())
     _rows(x_rows, n, "x_rows")
-    _need(x.shape[1] >= K and x.dtype == W.dtype, f"x width {x.shape[1]} < K={K} or dtype mismatch")
+    _need(x.shape[1] >= K and x.dtype == Wp.dtype, f"x width {x.shape[1]} < K={K} or dtype mismatch")
     od = out_dtype or x.dtype
     width = N // 2 if swiglu else N
     if out is None:
@@ -194,8 +241,8 @@ def linear(x: torch.Tensor, W: torch.Tensor, *, n: int | None = None, x_rows: to
     _need(out.dim() == 2 and out.stride(1) == 1 and out.shape[0] >= n and out.shape[1] >= width and out.dtype == od,
           "bad out")
     epi = _lib.EPI_SWIGLU if swiglu else _lib.EPI_PLAIN
-    rc = _lib.load().wfd_linear(x.data_ptr(), _p(x_rows), x.stride(0), W.data_ptr(), out.data_ptr(), out.stride(0),
-                                n, N, K, _dt(x), _DT[od], epi, N // 2 if swiglu else 0, _stream())
+    rc = _lib.load().wfd_linear(x.data_ptr(), _p(x_rows), x.stride(0), Wp.data.data_ptr(), out.data_ptr(),
+                                out.stride(0), n, N, K, _dt(x), _DT[od], epi, N // 2 if swiglu else 0, _stream())
     _lib.check(rc, "wfd_linear")
     return out
 
