@@ -53,7 +53,7 @@ constexpr int kNormMaxD = 4096;
 // the library's one order (chunk_sumsq, then chunks in order). Every load is
 // unconditional, and the residual / second-norm variants are compile-time, so
 // no load sits behind a data-dependent branch (whose join would wait for it).
-template <typename T, bool RES, bool TWO>
+template <typename T, bool RES, bool TWO, int MAXR>
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
     const T* __restrict__ a, const int32_t* __restrict__ a_rows, int64_t lda, const T* __restrict__ res,
     int64_t ldr, const T* __restrict__ w1, const T* __restrict__ w2, T* __restrict__ x_out,
@@ -61,7 +61,6 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
   constexpr int V = Chunk<T>::V;
   constexpr int KSTEP = Chunk<T>::KSTEP;
   constexpr int KC = Chunk<T>::KC;
-  constexpr int MAXR = kNormMaxD / (16 * KC);
   const int i = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int c = lane & 15;
@@ -141,25 +140,38 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
   }
 }
 
-template <typename T>
-static void launch_norm_t(const void* a, const int32_t* a_rows, int64_t lda, const void* res, int64_t ldr,
+template <typename T, int MAXR>
+static void launch_norm_r(const void* a, const int32_t* a_rows, int64_t lda, const void* res, int64_t ldr,
                           const void* w1, const void* w2, void* x_out, const int32_t* out_rows, int64_t ldo,
                           void* h_out, int64_t ldh, int n, int D, float eps, hipStream_t stream) {
   const dim3 grid((n + 3) / 4), block(256);
   const T *at = (const T*)a, *rt = (const T*)res, *w1t = (const T*)w1, *w2t = (const T*)w2;
   T *xo = (T*)x_out, *ho = (T*)h_out;
   if (res && w2)
-    hipLaunchKernelGGL((add_rmsnorm_kernel<T, true, true>), grid, block, 0, stream, at, a_rows, lda, rt, ldr, w1t, w2t,
-                       xo, out_rows, ldo, ho, ldh, n, D, eps);
+    hipLaunchKernelGGL((add_rmsnorm_kernel<T, true, true, MAXR>), grid, block, 0, stream, at, a_rows, lda, rt, ldr,
+                       w1t, w2t, xo, out_rows, ldo, ho, ldh, n, D, eps);
   else if (res)
-    hipLaunchKernelGGL((add_rmsnorm_kernel<T, true, false>), grid, block, 0, stream, at, a_rows, lda, rt, ldr, w1t,
-                       w2t, xo, out_rows, ldo, ho, ldh, n, D, eps);
+    hipLaunchKernelGGL((add_rmsnorm_kernel<T, true, false, MAXR>), grid, block, 0, stream, at, a_rows, lda, rt, ldr,
+                       w1t, w2t, xo, out_rows, ldo, ho, ldh, n, D, eps);
   else if (w2)
-    hipLaunchKernelGGL((add_rmsnorm_kernel<T, false, true>), grid, block, 0, stream, at, a_rows, lda, rt, ldr, w1t,
-                       w2t, xo, out_rows, ldo, ho, ldh, n, D, eps);
+    hipLaunchKernelGGL((add_rmsnorm_kernel<T, false, true, MAXR>), grid, block, 0, stream, at, a_rows, lda, rt, ldr,
+                       w1t, w2t, xo, out_rows, ldo, ho, ldh, n, D, eps);
   else
-    hipLaunchKernelGGL((add_rmsnorm_kernel<T, false, false>), grid, block, 0, stream, at, a_rows, lda, rt, ldr, w1t,
-                       w2t, xo, out_rows, ldo, ho, ldh, n, D, eps);
+    hipLaunchKernelGGL((add_rmsnorm_kernel<T, false, false, MAXR>), grid, block, 0, stream, at, a_rows, lda, rt, ldr,
+                       w1t, w2t, xo, out_rows, ldo, ho, ldh, n, D, eps);
+}
+
+// Rounds of 16 chunks per lane: a row of up to 16 chunks needs one (the usual
+// d_model), wider rows up to kNormMaxD take the general form.
+template <typename T>
+static void launch_norm_t(const void* a, const int32_t* a_rows, int64_t lda, const void* res, int64_t ldr,
+                          const void* w1, const void* w2, void* x_out, const int32_t* out_rows, int64_t ldo,
+                          void* h_out, int64_t ldh, int n, int D, float eps, hipStream_t stream) {
+  if (D <= 16 * Chunk<T>::KC)
+    launch_norm_r<T, 1>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, stream);
+  else
+    launch_norm_r<T, kNormMaxD / (16 * Chunk<T>::KC)>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out,
+                                                       ldh, n, D, eps, stream);
 }
 
 static void launch_add_rmsnorm(int dtype, const void* a, const int32_t* a_rows, int64_t lda, const void* res, int64_t ldr,

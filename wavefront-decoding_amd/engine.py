@@ -169,7 +169,7 @@ class LoopedModel:
         self.sc = self._scratch(self.max_rows)
         self.sc["logits"] = torch.empty(self.max_rows, cfg.vocab_size, dtype=torch.float32, device=self.device)
         self.sc["ids"] = torch.empty(self.max_rows, dtype=torch.int64, device=self.device)
-        self.attn_ws = torch.empty(ops.attn_workspace_bytes(self.max_rows, cfg.n_heads, cfg.head_dim, max_seq_len),
+        self.attn_ws = torch.zeros(ops.attn_workspace_bytes(self.max_rows, cfg.n_heads, cfg.head_dim, max_seq_len),
                                    dtype=torch.uint8, device=self.device)
         self.staging = _Staging(self.device)
         self._graphs: dict[tuple, _Captured] = {}
@@ -296,8 +296,8 @@ class LoopedModel:
                 self._block(f"core.{l}.", nb, sc, pos_d, kvlen_d, rb(l), fr(l), kv_max, ws, cache, nxt,
                             final_out=self.pool, final_rows=rows_d)
         else:
-            ops.rmsnorm(self.pool, W["ln_f"], c.norm_eps, n=nb, a_rows=rows_d, x_out=sc["x"])
-            ops.rmsnorm(sc["x"], W["coda.0.norm_1"], c.norm_eps, n=nb, x_out=sc["h"])
+            ops.add_rmsnorm(self.pool, W["ln_f"], c.norm_eps, w2=W["coda.0.norm_1"], n=nb, a_rows=rows_d,
+                            x_out=sc["x"], h_out=sc["h"])
             for i in range(L):
                 nxt = W[f"coda.{i + 1}.norm_1"] if i + 1 < L else W["ln_f"]
                 self._block(f"coda.{i}.", nb, sc, pos_d, kvlen_d, rb(i), fr(i), kv_max, ws, cache, nxt)
@@ -439,7 +439,7 @@ class LoopedModel:
         rb_l = lambda s: t64[s * L: (s + 1) * L]  # noqa: E731
         fr_l = lambda s: t64[(n_layers + s) * L: (n_layers + s + 1) * L]  # noqa: E731
         sc = self._scratch(L)
-        ws = torch.empty(ops.attn_workspace_bytes(L, c.n_heads, c.head_dim, L), dtype=torch.uint8,
+        ws = torch.zeros(ops.attn_workspace_bytes(L, c.n_heads, c.head_dim, L), dtype=torch.uint8,
                          device=self.device)
         logits = torch.empty(1, c.vocab_size, dtype=torch.float32, device=self.device)
         state = torch.empty(L, 2 * D, dtype=self.dtype, device=self.device)  # [s | e] per prompt row
@@ -459,8 +459,7 @@ class LoopedModel:
                 nxt = W[f"core.{l + 1}.norm_1"] if l + 1 < c.n_core else None
                 self._block(f"core.{l}.", L, sc, pos_d, kvlen_d, rb_l(s), fr_l(s), L, ws, cache, nxt,
                             final_out=state[:, :D])
-        ops.rmsnorm(state, W["ln_f"], c.norm_eps, n=L, x_out=sc["x"])
-        ops.rmsnorm(sc["x"], W["coda.0.norm_1"], c.norm_eps, n=L, x_out=sc["h"])
+        ops.add_rmsnorm(state, W["ln_f"], c.norm_eps, w2=W["coda.0.norm_1"], n=L, x_out=sc["x"], h_out=sc["h"])
         for i in range(c.n_coda):
             s = self.slot_coda(i)
             nxt = W[f"coda.{i + 1}.norm_1"] if i + 1 < c.n_coda else W["ln_f"]

@@ -65,7 +65,7 @@ def attn_workspace(n: int, H: int, Dh: int, kv_len_max: int, device) -> torch.Te
     key = dev.index if dev.index is not None else torch.cuda.current_device()
     ws = _WS.get(key)
     if ws is None or ws.numel() < need:
-        ws = torch.empty(max(need, 1 << 20), dtype=torch.uint8, device=dev)
+        ws = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=dev)
         _WS[key] = ws
     return ws
 
