@@ -68,7 +68,7 @@ def timed(fn, iters: int, stream=None) -> float:
     return e0.elapsed_time(e1) / iters
 
 
-def attn_bench(dev, n, H, Hkv, Dh, lens, iters=40):
+def attn_bench(dev, n, H, Hkv, Dh, lens, iters=24):
     """Wavefront attention alone; rotates KV sets totalling > 512 MB so the
     256 MB MALL cannot serve repeats. Returns (us/call, algorithmic bytes)."""
     import torch
@@ -85,10 +85,20 @@ def attn_bench(dev, n, H, Hkv, Dh, lens, iters=40):
     kl = torch.tensor(lens, dtype=torch.int32, device=dev)
     out = torch.empty_like(q)
     ws = ops.attn_workspace(n, H, Dh, max(lens), dev)
-    call = lambda i: ops.attn_decode(q, sets[i % nsets][0], sets[i % nsets][1], rb, kl,  # noqa: E731
-                                     kv_len_max=max(lens), out=out, workspace=ws)
-    timed(call, 3)
-    ms = timed(call, iters)
+    def loop():
+        for i in range(iters):
+            ops.attn_decode(q, sets[i % nsets][0], sets[i % nsets][1], rb, kl, kv_len_max=max(lens), out=out,
+                            workspace=ws)
+
+    # captured once, so the launches run back to back (no host gaps between them)
+    loop()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        loop()
+    graph.replay()
+    ms = timed(lambda i: graph.replay(), 3) / iters
+    del graph
     by = sum(lens) * Hkv * Dh * 2 * 2 + 2 * n * H * Dh * 2
     del sets
     torch.cuda.empty_cache()

@@ -32,10 +32,10 @@ def test_library_loads_and_exports_every_symbol():
 def test_host_only_entry_points():
     lib = _lib.load()
     assert lib.wfd_abi_version() == 1
-    assert lib.wfd_attn_split_keys() == 256
+    assert lib.wfd_attn_split_keys() == 2048
     assert lib.wfd_linear_k_multiple(_lib.BF16) == 128 and lib.wfd_linear_k_multiple(_lib.F32) == 64
     # workspace: n*H*splits*(Dh + 2) floats, each array 256-byte aligned
-    assert lib.wfd_attn_workspace_bytes(8, 16, 64, 1024) == 8 * 16 * 4 * 64 * 4 + 8 * 16 * 4 * 2 * 4
+    assert lib.wfd_attn_workspace_bytes(8, 16, 64, 1024) == 8 * 16 * 1 * 64 * 4 + 8 * 16 * 1 * 2 * 4
     # argument validation happens before any device work
     rc = lib.wfd_attn_decode(None, None, None, None, None, None, 1, 16, 3, 64, 1, 0.1, 10, None, 0, None)
     assert rc == -1 and b"bad shape" in lib.wfd_last_error()

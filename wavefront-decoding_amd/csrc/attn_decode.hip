@@ -17,74 +17,66 @@
 // src/decoding/batch_kv_cache.py:64-65), so key position == buffer row offset.
 //
 // Work split (a function of kv_len only, never of n or of other queries, so
-// results are row-invariant): keys are cut into 256-key splits; a 256-thread
-// workgroup owns one (split, kv head, query) and each of its 4 waves one
-// 64-key tile. QK^T runs on MFMA (q rows = the G query heads of the kv head,
-// padded to 16; K tile as the B operand loaded straight from HBM in 16-byte
-// fragments); P.V runs on the VALU in fp32 with one 16-byte V fragment per
-// lane per key, so K and V are each read exactly once. Waves merge through
-// LDS in fixed order; a second kernel merges splits in fixed split order.
+// results are row-invariant): keys are cut into 2048-key splits; a workgroup
+// of NW waves owns one (split, kv head, query), and its waves take the
+// split's key tiles round-robin (TK keys per tile: 64 for Dh 64, 32 for Dh 128
+// -- what fits the registers of a 1024-thread workgroup), each keeping an
+// online softmax. QK^T runs on MFMA (q rows = the G query heads of the kv
+// head, padded to 16; K tile as the B operand loaded straight from HBM in
+// 16-byte fragments); P.V runs on the VALU in fp32 with one 16-byte V
+// fragment per lane per key, so K and V are each read exactly once. The waves
+// merge through LDS in fixed order. A query whose keys fit one split (every
+// decode query up to 2048 keys) is finished in its workgroup; longer ones
+// leave per-split partials that a second kernel merges in fixed split order.
 #include "wfd_common.h"
 
 namespace wfd {
 
-constexpr int kAttnTile = 64;
-constexpr int kAttnWaves = 4;
-constexpr int kAttnSplit = kAttnTile * kAttnWaves;  // 256 keys per workgroup
+constexpr int kAttnSplit = 2048;  // keys per workgroup
 
-template <typename T, int DH, int G>
-__global__ __launch_bounds__(256) void attn_split_kernel(const T* __restrict__ q, const T* __restrict__ kc,
-                                                         const T* __restrict__ vc,
-                                                         const int64_t* __restrict__ row_base,
-                                                         const int32_t* __restrict__ kv_len,
-                                                         float* __restrict__ part_o, float* __restrict__ part_ml,
-                                                         int H, int Hkv, int max_splits, float scale_log2) {
+__device__ __forceinline__ float attn_finish(float O, float L) { return L > 0.f ? O / L : 0.f; }
+
+template <typename T, int DH, int G, int NW, int TK>
+__global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict__ q, const T* __restrict__ kc,
+                                                             const T* __restrict__ vc,
+                                                             const int64_t* __restrict__ row_base,
+                                                             const int32_t* __restrict__ kv_len,
+                                                             float* __restrict__ part_o, float* __restrict__ part_ml,
+                                                             T* __restrict__ out, int H, int Hkv, int max_splits,
+                                                             float scale_log2) {
   constexpr int V = Elem<T>::kVec;
   constexpr int KSTEP = 4 * V;
   constexpr int NDS = DH / KSTEP;  // MFMA k-steps per 16-key block
+  constexpr int NJ = TK / 16;      // 16-key blocks per tile
   constexpr int LPR = DH / V;      // lanes covering one V row
   constexpr int RG = 64 / LPR;     // V row groups per wave
-  constexpr int KPL = kAttnTile / RG;
-  static_assert(DH % KSTEP == 0 && 64 % LPR == 0, "unsupported head_dim");
+  constexpr int KPL = TK / RG;     // V rows per lane per tile
+  static_assert(DH % KSTEP == 0 && 64 % LPR == 0 && TK % 16 == 0 && TK % RG == 0, "unsupported tile");
 
-  __shared__ float p_lds[kAttnWaves][G][kAttnTile];
-  __shared__ float o_lds[kAttnWaves][G][DH];
-  __shared__ float m_lds[kAttnWaves][G];
-  __shared__ float l_lds[kAttnWaves][G];
+  __shared__ float p_lds[NW][G][TK];
+  __shared__ float o_lds[NW][G][DH];
+  __shared__ float m_lds[NW][G];
+  __shared__ float l_lds[NW][G];
 
   const int split = blockIdx.x;
   const int g = blockIdx.y;
   const int i = blockIdx.z;
   const int len = kv_len[i];
   if (split * kAttnSplit >= len) return;  // uniform for the whole workgroup
+  const int kend = min(len, (split + 1) * kAttnSplit);
+  const int ntiles = (kend - split * kAttnSplit + TK - 1) / TK;
 
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int col = lane & 15;
   const int grp = lane >> 4;
-  const int t0 = split * kAttnSplit + wave * kAttnTile;
+  const int vg = lane / LPR;
+  const int dseg = lane % LPR;
   const int64_t rs = (int64_t)Hkv * DH;
   const int64_t base = row_base[i];
   const T* kb = kc + base * rs + (int64_t)g * DH;
   const T* vb = vc + base * rs + (int64_t)g * DH;
 
-  // Issue every load of the tile first: K (MFMA B fragments), V, Q.
-  u32x4 kf[4][NDS];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int key = min(t0 + 16 * j + col, len - 1);
-    const T* p = kb + (int64_t)key * rs + grp * V;
-#pragma unroll
-    for (int s = 0; s < NDS; ++s) kf[j][s] = ld16(p + s * KSTEP);
-  }
-  const int vg = lane / LPR;
-  const int dseg = lane % LPR;
-  u32x4 vf[KPL];
-#pragma unroll
-  for (int k = 0; k < KPL; ++k) {
-    const int key = min(t0 + RG * k + vg, len - 1);
-    vf[k] = ld16(vb + (int64_t)key * rs + dseg * V);
-  }
   u32x4 qf[NDS];
   {
     const T* qp = q + ((int64_t)i * H + (int64_t)g * G + (col < G ? col : 0)) * DH + grp * V;
@@ -92,65 +84,106 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const T* __restrict__ q
     for (int s = 0; s < NDS; ++s) qf[s] = col < G ? ld16(qp + s * KSTEP) : zero16();
   }
 
-  // Scores: lane (grp==0, col) holds S[row r][key 16j+col] in acc[j][r].
-  f32x4 acc[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < NDS; ++s) acc[j] = mfma_step<T>(qf[s], kf[j][s], acc[j]);
-  }
-
-  float mx[G], ls[G];
+  // running softmax state of this wave: max (log2 domain), sum, output
+  float mrun[G], lrun[G], o[G][V];
 #pragma unroll
   for (int r = 0; r < G; ++r) {
-    mx[r] = -INFINITY;
+    mrun[r] = -INFINITY;
+    lrun[r] = 0.f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const bool valid = (t0 + 16 * j + col) < len;
-      const float sv = valid ? acc[j][r] * scale_log2 : -INFINITY;
-      acc[j][r] = sv;
-      mx[r] = fmaxf(mx[r], sv);
-    }
-#pragma unroll
-    for (int m = 8; m >= 1; m >>= 1) mx[r] = fmaxf(mx[r], __shfl_xor(mx[r], m, 64));
-    ls[r] = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float p = (acc[j][r] == -INFINITY) ? 0.f : exp2f(acc[j][r] - mx[r]);
-      acc[j][r] = p;
-      ls[r] += p;
-    }
-#pragma unroll
-    for (int m = 8; m >= 1; m >>= 1) ls[r] += __shfl_xor(ls[r], m, 64);
+    for (int e = 0; e < V; ++e) o[r][e] = 0.f;
   }
-  if (grp == 0) {
+
+  for (int t = wave; t < ntiles; t += NW) {  // uniform over the wave
+    const int t0 = split * kAttnSplit + t * TK;
+    // every load of the tile first: K (MFMA B fragments), V
+    u32x4 kf[NJ][NDS];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int key = min(t0 + 16 * j + col, len - 1);
+      const T* p = kb + (int64_t)key * rs + grp * V;
+#pragma unroll
+      for (int s = 0; s < NDS; ++s) kf[j][s] = ld16(p + s * KSTEP);
+    }
+    u32x4 vf[KPL];
+#pragma unroll
+    for (int k = 0; k < KPL; ++k) {
+      const int key = min(t0 + RG * k + vg, len - 1);
+      vf[k] = ld16(vb + (int64_t)key * rs + dseg * V);
+    }
+
+    // scores: lane (grp == 0, col) holds S[row r][key 16j + col] in acc[j][r]
+    f32x4 acc[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < NDS; ++s) acc[j] = mfma_step<T>(qf[s], kf[j][s], acc[j]);
+    }
+    float corr[G];
+#pragma unroll
+    for (int r = 0; r < G; ++r) {
+      float mt = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const bool valid = (t0 + 16 * j + col) < kend;
+        const float sv = valid ? acc[j][r] * scale_log2 : -INFINITY;
+        acc[j][r] = sv;
+        mt = fmaxf(mt, sv);
+      }
+#pragma unroll
+      for (int m = 8; m >= 1; m >>= 1) mt = fmaxf(mt, __shfl_xor(mt, m, 64));
+      // lanes 0-15 hold the real query rows: their statistics are the wave's
+      // (every lane rescales its slice of o with them)
+      mt = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(mt)));
+      const float mnew = fmaxf(mrun[r], mt);
+      corr[r] = (mrun[r] == -INFINITY) ? 0.f : exp2f(mrun[r] - mnew);
+      float lt = 0.f;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const float p = (acc[j][r] == -INFINITY) ? 0.f : exp2f(acc[j][r] - mnew);
+        acc[j][r] = p;
+        lt += p;
+      }
+#pragma unroll
+      for (int m = 8; m >= 1; m >>= 1) lt += __shfl_xor(lt, m, 64);
+      lt = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(lt)));
+      lrun[r] = fmaf(lrun[r], corr[r], lt);
+      mrun[r] = mnew;
+    }
+    // P to this wave's LDS rows, in the V lanes' key order
+    if (grp == 0) {
+#pragma unroll
+      for (int r = 0; r < G; ++r)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const int kt = 16 * j + col;  // key within the tile
+          p_lds[wave][r][(kt % RG) * KPL + kt / RG] = acc[j][r];
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // P.V on the VALU: lane owns V columns [dseg*V, dseg*V+V) of keys RG*k + vg
 #pragma unroll
     for (int r = 0; r < G; ++r)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int kt = 16 * j + col;  // key within the tile
-        p_lds[wave][r][(kt % RG) * KPL + kt / RG] = acc[j][r];
+      for (int e = 0; e < V; ++e) o[r][e] *= corr[r];
+#pragma unroll
+    for (int k = 0; k < KPL; ++k) {
+      float v[V];
+      Elem<T>::unpack(vf[k], v);
+#pragma unroll
+      for (int r = 0; r < G; ++r) {
+        const float p = p_lds[wave][r][vg * KPL + k];
+#pragma unroll
+        for (int e = 0; e < V; ++e) o[r][e] = fmaf(p, v[e], o[r][e]);
       }
-  }
-  __syncthreads();
-
-  // P.V on the VALU: lane owns V columns [dseg*V, dseg*V+V) of keys RG*k + vg.
-  float o[G][V];
-#pragma unroll
-  for (int r = 0; r < G; ++r)
-#pragma unroll
-    for (int e = 0; e < V; ++e) o[r][e] = 0.f;
-#pragma unroll
-  for (int k = 0; k < KPL; ++k) {
-    float v[V];
-    Elem<T>::unpack(vf[k], v);
-#pragma unroll
-    for (int r = 0; r < G; ++r) {
-      const float p = p_lds[wave][r][vg * KPL + k];
-#pragma unroll
-      for (int e = 0; e < V; ++e) o[r][e] = fmaf(p, v[e], o[r][e]);
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();  // P rows are rewritten by the next tile
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 #pragma unroll
   for (int m = LPR; m < 64; m <<= 1)
@@ -167,32 +200,42 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const T* __restrict__ q
   if (lane == 0) {
 #pragma unroll
     for (int r = 0; r < G; ++r) {
-      m_lds[wave][r] = mx[r];
-      l_lds[wave][r] = ls[r];
+      m_lds[wave][r] = mrun[r];
+      l_lds[wave][r] = lrun[r];
     }
   }
   __syncthreads();
 
-  // Merge the 4 waves in fixed order; emit this split's unnormalised partial.
-  for (int idx = threadIdx.x; idx < G * DH; idx += 256) {
+  // Merge the NW waves in fixed order. One split: finish here (the split merge
+  // over one split, exactly as attn_combine_kernel computes it); otherwise
+  // emit this split's unnormalised partial.
+  int ns = (len + kAttnSplit - 1) / kAttnSplit;
+  ns = ns < max_splits ? ns : max_splits;
+  for (int idx = threadIdx.x; idx < G * DH; idx += 64 * NW) {
     const int r = idx / DH;
     const int d = idx - r * DH;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, m_lds[w][r]);
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, m_lds[w][r]);
     float O = 0.f, L = 0.f;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) {
+    for (int w = 0; w < NW; ++w) {
       const float mw = m_lds[w][r];
       const float f = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
       O = fmaf(o_lds[w][r][d], f, O);
       L = fmaf(l_lds[w][r], f, L);
     }
-    const int64_t pidx = ((int64_t)i * H + (int64_t)g * G + r) * max_splits + split;
-    part_o[pidx * DH + d] = O;
-    if (d == 0) {
-      part_ml[pidx * 2] = M;
-      part_ml[pidx * 2 + 1] = L;
+    const int h = g * G + r;
+    if (ns == 1) {
+      const float f = (M == -INFINITY) ? 0.f : exp2f(M - M);
+      Elem<T>::store(out + ((int64_t)i * H + h) * DH + d, attn_finish(fmaf(O, f, 0.f), fmaf(L, f, 0.f)));
+    } else {
+      const int64_t pidx = ((int64_t)i * H + h) * max_splits + split;
+      part_o[pidx * DH + d] = O;
+      if (d == 0) {
+        part_ml[pidx * 2] = M;
+        part_ml[pidx * 2 + 1] = L;
+      }
     }
   }
 }
@@ -208,6 +251,7 @@ __global__ __launch_bounds__(DH) void attn_combine_kernel(const float* __restric
   const int len = kv_len[i];
   int ns = len > 0 ? (len + kAttnSplit - 1) / kAttnSplit : 0;
   ns = min(ns, max_splits);
+  if (ns <= 1) return;  // finished by its split workgroup
   const int64_t base = ((int64_t)i * H + h) * max_splits;
   float M = -INFINITY;
   for (int s = 0; s < ns; ++s) M = fmaxf(M, part_ml[(base + s) * 2]);
@@ -218,8 +262,7 @@ __global__ __launch_bounds__(DH) void attn_combine_kernel(const float* __restric
     L = fmaf(part_ml[(base + s) * 2 + 1], f, L);
     O = fmaf(part_o[(base + s) * DH + d], f, O);
   }
-  const float res = L > 0.f ? O / L : 0.f;
-  Elem<T>::store(out + ((int64_t)i * H + h) * DH + d, res);
+  Elem<T>::store(out + ((int64_t)i * H + h) * DH + d, attn_finish(O, L));
 }
 
 static int max_splits_for(int kv_len_max) { return kv_len_max <= 0 ? 1 : (kv_len_max + kAttnSplit - 1) / kAttnSplit; }
@@ -235,9 +278,12 @@ template <typename T, int DH, int G>
 static void launch_attn(const void* q, const void* kc, const void* vc, const int64_t* rb, const int32_t* kl, void* out,
                         int n, int H, int Hkv, int ms, float scale, float* po, float* pml, hipStream_t st) {
   const float scale_log2 = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL((attn_split_kernel<T, DH, G>), dim3(ms, Hkv, n), dim3(256), 0, st, (const T*)q, (const T*)kc,
-                     (const T*)vc, rb, kl, po, pml, H, Hkv, ms, scale_log2);
-  hipLaunchKernelGGL((attn_combine_kernel<T, DH>), dim3(H, n), dim3(DH), 0, st, po, pml, kl, (T*)out, H, ms);
+  constexpr int TK = DH == 64 ? 64 : 32;  // key tile that fits the registers
+  constexpr int NW = (G >= 4 || sizeof(T) == 4) ? 8 : 16;  // waves per workgroup (register budget)
+  hipLaunchKernelGGL((attn_split_kernel<T, DH, G, NW, TK>), dim3(ms, Hkv, n), dim3(64 * NW), 0, st, (const T*)q,
+                     (const T*)kc, (const T*)vc, rb, kl, po, pml, (T*)out, H, Hkv, ms, scale_log2);
+  if (ms > 1)  // some query may span several splits
+    hipLaunchKernelGGL((attn_combine_kernel<T, DH>), dim3(H, n), dim3(DH), 0, st, po, pml, kl, (T*)out, H, ms);
 }
 
 template <typename T>
