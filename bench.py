@@ -69,8 +69,9 @@ def timed(fn, iters: int, stream=None) -> float:
 
 
 def attn_bench(dev, n, H, Hkv, Dh, lens, iters=24):
-    """Wavefront attention alone; rotates KV sets totalling > 512 MB so the
-    256 MB MALL cannot serve repeats. Returns (us/call, algorithmic bytes)."""
+    """Wavefront attention alone over the engine's cache layout (head-major
+    blocks of S rows, one per query's slot); rotates KV sets totalling > 512 MB
+    so the 256 MB MALL cannot serve repeats. Returns (us/call, algorithmic bytes)."""
     import torch
     from wavefront_decoding_amd import ops
 
@@ -78,8 +79,8 @@ def attn_bench(dev, n, H, Hkv, Dh, lens, iters=24):
     per_set = n * S * Hkv * Dh * 2 * 2
     nsets = max(3, math.ceil(2 * MALL_BYTES / per_set) + 1)
     g = torch.Generator(device=dev).manual_seed(0)
-    sets = [(torch.randn(n * S, Hkv, Dh, device=dev, dtype=torch.bfloat16, generator=g),
-             torch.randn(n * S, Hkv, Dh, device=dev, dtype=torch.bfloat16, generator=g)) for _ in range(nsets)]
+    sets = [(torch.randn(n, Hkv, S, Dh, device=dev, dtype=torch.bfloat16, generator=g),
+             torch.randn(n, Hkv, S, Dh, device=dev, dtype=torch.bfloat16, generator=g)) for _ in range(nsets)]
     q = torch.randn(n, H, Dh, device=dev, dtype=torch.bfloat16, generator=g)
     rb = torch.tensor([i * S for i in range(n)], dtype=torch.int64, device=dev)
     kl = torch.tensor(lens, dtype=torch.int32, device=dev)
@@ -288,7 +289,7 @@ def gqa_section(args, dev, res):
     cache = model.create_cache(B)
     g = torch.Generator(device=dev).manual_seed(2)
     for t in (cache.flat_k, cache.flat_v):
-        for chunk in torch.split(t, 1 << 20):
+        for chunk in torch.split(t.view(-1), 1 << 28):
             chunk.normal_(generator=g)
     seqs = [b for b in range(B) for _ in range(W)]
     pos = [ctx + W - 1 - j for _ in range(B) for j in range(W)]

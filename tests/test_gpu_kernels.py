@@ -38,6 +38,16 @@ def _attn_case(dev, dtype, n, H, Hkv, Dh, lens, S=None, seed=0):
     return q, K, V, rb, kl
 
 
+def _blocks(t: torch.Tensor, S: int) -> torch.Tensor:
+    """Token-major cache (nblk*S, Hkv, Dh) -> head-major blocks (nblk, Hkv, S, Dh)."""
+    return t.view(-1, S, t.shape[1], t.shape[2]).permute(0, 2, 1, 3).contiguous()
+
+
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    """Head-major blocks (nblk, Hkv, S, Dh) -> token-major rows (nblk*S, Hkv, Dh)."""
+    return t.permute(0, 2, 1, 3).reshape(-1, t.shape[1], t.shape[3])
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("H,Hkv,Dh,lens", [
     (16, 16, 64, [1017 + i for i in range(8)]),      # wavefront attention op, W=8, L=1024
@@ -46,21 +56,29 @@ def _attn_case(dev, dtype, n, H, Hkv, Dh, lens, S=None, seed=0):
     (4, 4, 64, [1, 2, 63, 64, 65, 129]),             # tiny model heads
 ])
 def test_attn_decode_matches_oracle(gpu, dtype, H, Hkv, Dh, lens):
+    """Both cache layouts, against the oracle; the head-major block layout
+    gives the token-major result bit for bit (only addresses differ)."""
     n = len(lens)
-    q, K, V, rb, kl = _attn_case(gpu, dtype, n, H, Hkv, Dh, lens)
+    S = max(lens) + 3
+    q, K, V, rb, kl = _attn_case(gpu, dtype, n, H, Hkv, Dh, lens, S=S)
     print(f"[attn] dtype={dtype} n={n} H={H} Hkv={Hkv} Dh={Dh} lens={lens}", flush=True)
     out = ops.attn_decode(q.to(gpu), K.to(gpu), V.to(gpu), rb.to(gpu), kl.to(gpu), kv_len_max=max(lens))
+    outb = ops.attn_decode(q.to(gpu), _blocks(K, S).to(gpu), _blocks(V, S).to(gpu), rb.to(gpu), kl.to(gpu),
+                           kv_len_max=max(lens))
     torch.cuda.synchronize()
     ref = ok.attention_rows(_np(q), _np(K), _np(V), rb.numpy(), kl.numpy())
     err = rel_err(_np(out), ref)
     assert err <= TOL[dtype], err
+    assert torch.equal(out, outb)
 
 
 @pytest.mark.parametrize("L", [4096, 16384])
 def test_attn_decode_long_prefix(gpu, L):
     lens = [L - 7 + i for i in range(8)]
-    q, K, V, rb, kl = _attn_case(gpu, torch.bfloat16, 8, 16, 16, 64, lens, seed=L)
-    out = ops.attn_decode(q.to(gpu), K.to(gpu), V.to(gpu), rb.to(gpu), kl.to(gpu), kv_len_max=L)
+    S = L + 3
+    q, K, V, rb, kl = _attn_case(gpu, torch.bfloat16, 8, 16, 16, 64, lens, S=S, seed=L)
+    out = ops.attn_decode(q.to(gpu), _blocks(K, S).to(gpu), _blocks(V, S).to(gpu), rb.to(gpu), kl.to(gpu),
+                          kv_len_max=L)
     ref = ok.attention_rows(_np(q), _np(K), _np(V), rb.numpy(), kl.numpy())
     assert rel_err(_np(out), ref) <= 2e-2
 
@@ -70,7 +88,8 @@ def test_attn_decode_row_invariant(gpu, dtype):
     """A query's output bits do not depend on the other queries, the batch
     size, or kv_len_max (the grid bound)."""
     lens = [700, 33, 1500, 256, 1, 900, 511, 1024]
-    q, K, V, rb, kl = _attn_case(gpu, dtype, 8, 16, 16, 128, lens, seed=7)
+    q, K, V, rb, kl = _attn_case(gpu, dtype, 8, 16, 16, 128, lens, S=1803, seed=7)
+    K, V = _blocks(K, 1803), _blocks(V, 1803)
     q, K, V, rb, kl = (t.to(gpu) for t in (q, K, V, rb, kl))
     full = ops.attn_decode(q, K, V, rb, kl, kv_len_max=1500)
     for i in range(8):
@@ -187,19 +206,23 @@ def test_add_rmsnorm_widths(gpu, dtype, D):
     assert torch.equal(ops.add_rmsnorm(a[3:4], w1, 1e-6, res=r[3:4]), x[3:4])
 
 
+@pytest.mark.parametrize("blocks", [False, True])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("H,Hkv,Dh", [(16, 16, 128), (16, 4, 128), (4, 4, 64)])
-def test_qkv_rope_append(gpu, dtype, H, Hkv, Dh):
+def test_qkv_rope_append(gpu, dtype, H, Hkv, Dh, blocks):
     g = torch.Generator().manual_seed(H + Hkv)
     n, S = 5, 64
     qkv = torch.randn(n, (H + 2 * Hkv) * Dh, generator=g).to(dtype)
     pos = torch.tensor([0, 63, 7, 31, 1], dtype=torch.int32)
     flat = torch.tensor([5, 100, 64, 0, 127], dtype=torch.int64)
     cos, sin = ok.rope_tables(S, Dh)
-    kc = torch.zeros(128, Hkv, Dh, dtype=dtype, device=gpu)
-    vc = torch.zeros(128, Hkv, Dh, dtype=dtype, device=gpu)
+    shape = (2, Hkv, 64, Dh) if blocks else (128, Hkv, Dh)  # 128 cache rows either way
+    kc = torch.zeros(shape, dtype=dtype, device=gpu)
+    vc = torch.zeros(shape, dtype=dtype, device=gpu)
     q = ops.qkv_rope_append(qkv.to(gpu), pos.to(gpu), torch.from_numpy(cos).to(gpu), torch.from_numpy(sin).to(gpu),
                             flat.to(gpu), kc, vc, H, Hkv, Dh)
+    if blocks:
+        kc, vc = _rows(kc), _rows(vc)
     x = _np(qkv)
     for i in range(n):
         p = int(pos[i])
@@ -214,10 +237,11 @@ def test_qkv_rope_append(gpu, dtype, H, Hkv, Dh):
     assert kc[untouched].abs().sum().item() == 0 and vc[untouched].abs().sum().item() == 0
 
 
+@pytest.mark.parametrize("blocks", [False, True])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("H,Hkv,Dh,K", [(16, 16, 128, 2048), (16, 4, 128, 2048), (4, 4, 64, 256)])
 @pytest.mark.parametrize("n", [1, 5, 16, 37])
-def test_linear_qkv_rope_append_fused(gpu, dtype, H, Hkv, Dh, K, n):
+def test_linear_qkv_rope_append_fused(gpu, dtype, H, Hkv, Dh, K, n, blocks):
     """The fused projection + RoPE + append equals linear() then
     qkv_rope_append() bit for bit, in both the wide (n <= 16) and tile regimes,
     with a gathered x, and touches no other cache row."""
@@ -230,7 +254,7 @@ def test_linear_qkv_rope_append_fused(gpu, dtype, H, Hkv, Dh, K, n):
     pos = torch.randint(0, S, (n,), generator=g, dtype=torch.int32).to(gpu)
     flat = (torch.randperm(rows, generator=g)[:n]).to(torch.int64).to(gpu)
     cos, sin = (torch.from_numpy(t).to(gpu) for t in ok.rope_tables(S, Dh))
-    kc0 = torch.zeros(rows, Hkv, Dh, dtype=dtype, device=gpu)
+    kc0 = torch.zeros((4, Hkv, S, Dh) if blocks else (rows, Hkv, Dh), dtype=dtype, device=gpu)
     vc0 = torch.zeros_like(kc0)
     qkv = ops.linear(X, Wq, x_rows=xr)
     q0 = ops.qkv_rope_append(qkv, pos, cos, sin, flat, kc0, vc0, H, Hkv, Dh)
@@ -239,6 +263,8 @@ def test_linear_qkv_rope_append_fused(gpu, dtype, H, Hkv, Dh, K, n):
     q1 = ops.linear_qkv_rope_append(X, Wq, pos, cos, sin, flat, kc1, vc1, H, Hkv, Dh, x_rows=xr)
     assert torch.equal(q0, q1)
     assert torch.equal(kc0, kc1) and torch.equal(vc0, vc1)
+    if blocks:
+        vc1 = _rows(vc1)
     # and against the oracle for one row
     i = n - 1
     ref = ok.linear(_np(X)[int(xr[i])][None], _np(Wq))[0]
@@ -260,6 +286,21 @@ def test_kv_append_exact_rows(gpu):
     nz = (kc.float().abs().sum(dim=(1, 2)) > 0).nonzero().flatten().tolist()
     assert nz == [700, 701, 702]
     assert torch.equal(kc[700:703], k) and torch.equal(vc[700:703], v)
+
+
+def test_kv_append_blocks_match_rows(gpu):
+    """The head-major block layout receives exactly the token-major rows:
+    rows 700-702 of 512-row blocks land in block 1 at positions 188-190, every
+    head, and nothing else changes."""
+    kc = torch.zeros(4, 16, 512, 128, dtype=torch.bfloat16, device=gpu)
+    vc = torch.zeros_like(kc)
+    k = torch.randn(3, 16, 128, device=gpu).to(torch.bfloat16)
+    v = torch.randn(3, 16, 128, device=gpu).to(torch.bfloat16)
+    rows = torch.tensor([700, 701, 702], dtype=torch.int64, device=gpu)
+    ops.kv_append(k, v, kc, vc, rows)
+    assert torch.equal(kc[1, :, 188:191].transpose(0, 1), k) and torch.equal(vc[1, :, 188:191].transpose(0, 1), v)
+    nz = (_rows(kc).float().abs().sum(dim=(1, 2)) > 0).nonzero().flatten().tolist()
+    assert nz == [700, 701, 702]
 
 
 def test_embed_copy_argmax(gpu):

@@ -164,7 +164,7 @@ def test_2048_core_tick_matches_oracle(gpu):
     model = LoopedModel(cfg, w, gpu, max_seq_len=S, max_batch=1)
     cache = model.create_cache(1)
     g = torch.Generator().manual_seed(4)
-    kv = torch.randn(2, cache.flat_k.shape[0], cfg.n_kv_heads, cfg.head_dim, generator=g).to(torch.bfloat16)
+    kv = torch.randn(2, *cache.flat_k.shape, generator=g).to(torch.bfloat16)
     cache.flat_k.copy_(kv[0])
     cache.flat_v.copy_(kv[1])
     pos = [600 - i for i in range(8)]

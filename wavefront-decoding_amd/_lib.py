@@ -33,16 +33,16 @@ SIGNATURES: dict[str, tuple] = {
     "wfd_abi_version": (_i32, []),
     "wfd_attn_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
     "wfd_attn_split_keys": (_i32, []),
-    "wfd_attn_decode": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp, _sz,
-                               _vp]),
-    "wfd_kv_append": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp]),
-    "wfd_qkv_rope_append": (_i32, [_vp, _i64, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
-                                   _i32, _vp]),
+    "wfd_attn_decode": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp,
+                               _sz, _vp]),
+    "wfd_kv_append": (_i32, [_vp, _vp, _vp, _vp, _i64, _vp, _i32, _i32, _i32, _i32, _vp]),
+    "wfd_qkv_rope_append": (_i32, [_vp, _i64, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32,
+                                   _i32, _i32, _vp]),
     "wfd_linear_k_multiple": (_i32, [_i32]),
     "wfd_linear_pack": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
     "wfd_linear": (_i32, [_vp, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
     "wfd_linear_qkv_rope_append": (_i32, [_vp, _vp, _i64, _vp, _i32, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp,
-                                          _i32, _i32, _i32, _i32, _vp]),
+                                          _i64, _i32, _i32, _i32, _i32, _vp]),
     "wfd_add_rmsnorm": (_i32, [_vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i32, _i32, _f32,
                                _i32, _vp]),
     "wfd_embed": (_i32, [_vp, _vp, _i64, _vp, _f32, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),

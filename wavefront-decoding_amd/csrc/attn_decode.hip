@@ -12,16 +12,19 @@
 //   o[i,h,:] = softmax_t( q[i,h,:] . K[row_base[i] + t, g, :] * scale ) @ V[row_base[i] + t, g, :],
 //   t = 0 .. kv_len[i]-1, fp32 softmax and accumulation.
 //
-// Layout: K/V are flat (rows, Hkv, Dh) buffers; row_base[i] is the flat row of
-// position 0 of query i's slot (for the batched cache (slot*B + b)*S,
-// src/decoding/batch_kv_cache.py:64-65), so key position == buffer row offset.
+// Layout: row_base[i] is the cache row of position 0 of query i's slot (for
+// the batched cache (slot*B + b)*S, src/decoding/batch_kv_cache.py:64-65), so
+// key position == row offset. The cache is token-major (rows, Hkv, Dh) or
+// head-major blocks (rows / block_rows, Hkv, block_rows, Dh) (kv_offset); with
+// blocks, a query's rows lie in one block, so each workgroup streams one
+// contiguous run of Dh-element rows per tensor -- on MI355X ~20% more HBM
+// bandwidth than the 2 KB-strided rows of the token-major layout.
 //
 // Work split (a function of kv_len only, never of n or of other queries, so
 // results are row-invariant): keys are cut into 2048-key splits; a workgroup
-// of NW waves owns one (split, kv head, query), and its waves take the
-// split's key tiles round-robin (TK keys per tile: 64 for Dh 64, 32 for Dh 128
-// -- what fits the registers of a 1024-thread workgroup), each keeping an
-// online softmax. QK^T runs on MFMA (q rows = the G query heads of the kv
+// of 8 waves owns one (split, kv head, query), and its waves take the split's
+// key tiles round-robin (TK keys per tile: 64 for Dh 64, 32 for Dh 128, 64
+// VGPRs of K and V fragments per lane), each keeping an online softmax. QK^T runs on MFMA (q rows = the G query heads of the kv
 // head, padded to 16; K tile as the B operand loaded straight from HBM in
 // 16-byte fragments); P.V runs on the VALU in fp32 with one 16-byte V
 // fragment per lane per key, so K and V are each read exactly once. The waves
@@ -43,7 +46,7 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict
                                                              const int32_t* __restrict__ kv_len,
                                                              float* __restrict__ part_o, float* __restrict__ part_ml,
                                                              T* __restrict__ out, int H, int Hkv, int max_splits,
-                                                             float scale_log2) {
+                                                             float scale_log2, int64_t block_rows) {
   constexpr int V = Elem<T>::kVec;
   constexpr int KSTEP = 4 * V;
   constexpr int NDS = DH / KSTEP;  // MFMA k-steps per 16-key block
@@ -72,10 +75,10 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict
   const int grp = lane >> 4;
   const int vg = lane / LPR;
   const int dseg = lane % LPR;
-  const int64_t rs = (int64_t)Hkv * DH;
-  const int64_t base = row_base[i];
-  const T* kb = kc + base * rs + (int64_t)g * DH;
-  const T* vb = vc + base * rs + (int64_t)g * DH;
+  const int64_t hb = kv_offset(row_base[i], g, Hkv, DH, block_rows);  // position 0, kv head g
+  const int64_t rs = block_rows > 1 ? (int64_t)DH : (int64_t)Hkv * DH;   // key stride
+  const T* kb = kc + hb;
+  const T* vb = vc + hb;
 
   u32x4 qf[NDS];
   {
@@ -276,23 +279,24 @@ static size_t attn_ws_bytes(int n, int H, int Dh, int kv_len_max) {
 
 template <typename T, int DH, int G>
 static void launch_attn(const void* q, const void* kc, const void* vc, const int64_t* rb, const int32_t* kl, void* out,
-                        int n, int H, int Hkv, int ms, float scale, float* po, float* pml, hipStream_t st) {
+                        int n, int H, int Hkv, int ms, float scale, int64_t br, float* po, float* pml,
+                        hipStream_t st) {
   const float scale_log2 = scale * 1.4426950408889634f;
   constexpr int TK = DH == 64 ? 64 : 32;  // key tile that fits the registers
-  constexpr int NW = (G >= 4 || sizeof(T) == 4) ? 8 : 16;  // waves per workgroup (register budget)
+  constexpr int NW = 8;  // waves per workgroup: 8 beat 4 and 16 on every measured shape
   hipLaunchKernelGGL((attn_split_kernel<T, DH, G, NW, TK>), dim3(ms, Hkv, n), dim3(64 * NW), 0, st, (const T*)q,
-                     (const T*)kc, (const T*)vc, rb, kl, po, pml, (T*)out, H, Hkv, ms, scale_log2);
+                     (const T*)kc, (const T*)vc, rb, kl, po, pml, (T*)out, H, Hkv, ms, scale_log2, br);
   if (ms > 1)  // some query may span several splits
     hipLaunchKernelGGL((attn_combine_kernel<T, DH>), dim3(H, n), dim3(DH), 0, st, po, pml, kl, (T*)out, H, ms);
 }
 
 template <typename T>
 static int dispatch_attn(int Dh, int G, const void* q, const void* kc, const void* vc, const int64_t* rb,
-                         const int32_t* kl, void* out, int n, int H, int Hkv, int ms, float scale, float* po,
-                         float* pml, hipStream_t st) {
+                         const int32_t* kl, void* out, int n, int H, int Hkv, int ms, float scale, int64_t br,
+                         float* po, float* pml, hipStream_t st) {
 #define WFD_ATTN_CASE(DHV, GV)                                                        \
   if (Dh == DHV && G == GV) {                                                         \
-    launch_attn<T, DHV, GV>(q, kc, vc, rb, kl, out, n, H, Hkv, ms, scale, po, pml, st); \
+    launch_attn<T, DHV, GV>(q, kc, vc, rb, kl, out, n, H, Hkv, ms, scale, br, po, pml, st); \
     return kOk;                                                                       \
   }
   WFD_ATTN_CASE(64, 1)
@@ -316,12 +320,14 @@ size_t wfd_attn_workspace_bytes(int n, int H, int Dh, int kv_len_max) {
 
 int wfd_attn_split_keys(void) { return wfd::kAttnSplit; }
 
-int wfd_attn_decode(const void* q, const void* k_cache, const void* v_cache, const int64_t* kv_row_base,
-                    const int32_t* kv_len, void* out, int n, int H, int Hkv, int Dh, int dtype, float scale,
-                    int kv_len_max, void* workspace, size_t ws_bytes, hipStream_t stream) {
+int wfd_attn_decode(const void* q, const void* k_cache, const void* v_cache, int64_t kv_block_rows,
+                    const int64_t* kv_row_base, const int32_t* kv_len, void* out, int n, int H, int Hkv, int Dh,
+                    int dtype, float scale, int kv_len_max, void* workspace, size_t ws_bytes, hipStream_t stream) {
   using namespace wfd;
-  if (n < 0 || H <= 0 || Hkv <= 0 || H % Hkv != 0 || kv_len_max < 1) {
-    set_error("wfd_attn_decode: bad shape n=%d H=%d Hkv=%d kv_len_max=%d", n, H, Hkv, kv_len_max);
+  if (n < 0 || H <= 0 || Hkv <= 0 || H % Hkv != 0 || kv_len_max < 1 || kv_block_rows < 0 ||
+      (kv_block_rows > 1 && kv_len_max > kv_block_rows)) {
+    set_error("wfd_attn_decode: bad shape n=%d H=%d Hkv=%d kv_len_max=%d kv_block_rows=%lld", n, H, Hkv, kv_len_max,
+              (long long)kv_block_rows);
     return kBadArg;
   }
   if (n == 0) return kOk;
@@ -340,11 +346,11 @@ int wfd_attn_decode(const void* q, const void* k_cache, const void* v_cache, con
   float* pml = (float*)((char*)workspace + align256((size_t)n * H * ms * Dh * sizeof(float)));
   int rc;
   if (dtype == kBF16)
-    rc = dispatch_attn<bf16_t>(Dh, G, q, k_cache, v_cache, kv_row_base, kv_len, out, n, H, Hkv, ms, scale, po, pml,
-                               stream);
+    rc = dispatch_attn<bf16_t>(Dh, G, q, k_cache, v_cache, kv_row_base, kv_len, out, n, H, Hkv, ms, scale,
+                               kv_block_rows, po, pml, stream);
   else if (dtype == kF32)
-    rc = dispatch_attn<float>(Dh, G, q, k_cache, v_cache, kv_row_base, kv_len, out, n, H, Hkv, ms, scale, po, pml,
-                              stream);
+    rc = dispatch_attn<float>(Dh, G, q, k_cache, v_cache, kv_row_base, kv_len, out, n, H, Hkv, ms, scale,
+                              kv_block_rows, po, pml, stream);
   else
     rc = kUnsupported;
   if (rc != kOk) {

@@ -187,7 +187,7 @@ template <typename T>
 __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
     const T* __restrict__ qkv, int64_t ldq, const int32_t* __restrict__ pos, const float* __restrict__ cos_t,
     const float* __restrict__ sin_t, int tab_rows, const int64_t* __restrict__ flat_row, T* __restrict__ q_out,
-    T* __restrict__ kc, T* __restrict__ vc, int H, int Hkv, int Dh) {
+    T* __restrict__ kc, T* __restrict__ vc, int64_t block_rows, int H, int Hkv, int Dh) {
   const int i = blockIdx.x;
   const int half = Dh >> 1;
   int p = pos[i];
@@ -205,25 +205,31 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
     const float y0 = fmaf(x0, c, -(x1 * s));
     const float y1 = fmaf(x0, s, x1 * c);
     T* dst = head < H ? q_out + ((int64_t)i * H + head) * Dh + 2 * j
-                      : kc + fr * (int64_t)Hkv * Dh + (int64_t)(head - H) * Dh + 2 * j;
+                      : kc + kv_offset(fr, head - H, Hkv, Dh, block_rows) + 2 * j;
     Elem<T>::store(dst, y0);
     Elem<T>::store(dst + 1, y1);
   }
-  const int nv = Hkv * Dh;
   const T* vsrc = src + (int64_t)(H + Hkv) * Dh;
-  T* vdst = vc + fr * (int64_t)nv;
-  for (int e = threadIdx.x; e < nv; e += kRowThreads) vdst[e] = vsrc[e];
+  for (int e = threadIdx.x; e < Hkv * Dh; e += kRowThreads) {
+    const int h = e / Dh;
+    vc[kv_offset(fr, h, Hkv, Dh, block_rows) + (e - h * Dh)] = vsrc[e];
+  }
 }
 
 template <typename T>
 __global__ __launch_bounds__(kRowThreads) void kv_append_kernel(const T* __restrict__ k, const T* __restrict__ v,
                                                                 T* __restrict__ kc, T* __restrict__ vc,
-                                                                const int64_t* __restrict__ flat_row, int row_elems) {
+                                                                int64_t block_rows,
+                                                                const int64_t* __restrict__ flat_row, int Hkv,
+                                                                int Dh) {
   const int i = blockIdx.x;
   const int64_t fr = flat_row[i];
+  const int row_elems = Hkv * Dh;
   for (int e = threadIdx.x; e < row_elems; e += kRowThreads) {
-    kc[fr * row_elems + e] = k[(int64_t)i * row_elems + e];
-    vc[fr * row_elems + e] = v[(int64_t)i * row_elems + e];
+    const int h = e / Dh;
+    const int64_t dst = kv_offset(fr, h, Hkv, Dh, block_rows) + (e - h * Dh);
+    kc[dst] = k[(int64_t)i * row_elems + e];
+    vc[dst] = v[(int64_t)i * row_elems + e];
   }
 }
 
@@ -314,7 +320,7 @@ extern "C" {
 
 const char* wfd_last_error(void) { return wfd::g_err; }
 
-int wfd_abi_version(void) { return 1; }
+int wfd_abi_version(void) { return 2; }
 
 int wfd_add_rmsnorm(const void* a, const int32_t* a_rows, int64_t lda, const void* res, int64_t ldr, const void* w1,
                     const void* w2, void* x_out, const int32_t* out_rows, int64_t ldo, void* h_out, int64_t ldh, int n,
@@ -347,9 +353,11 @@ int wfd_add_rmsnorm(const void* a, const int32_t* a_rows, int64_t lda, const voi
 
 int wfd_qkv_rope_append(const void* qkv, int64_t ldq, const int32_t* pos, const float* rope_cos,
                         const float* rope_sin, int rope_rows, const int64_t* flat_row, void* q_out, void* k_cache,
-                        void* v_cache, int n, int H, int Hkv, int Dh, int dtype, hipStream_t stream) {
+                        void* v_cache, int64_t kv_block_rows, int n, int H, int Hkv, int Dh, int dtype,
+                        hipStream_t stream) {
   using namespace wfd;
-  if (n < 0 || H <= 0 || Hkv <= 0 || Dh <= 0 || (Dh & 1) || rope_rows <= 0 || ldq < (int64_t)(H + 2 * Hkv) * Dh) {
+  if (n < 0 || H <= 0 || Hkv <= 0 || Dh <= 0 || (Dh & 1) || rope_rows <= 0 || ldq < (int64_t)(H + 2 * Hkv) * Dh ||
+      kv_block_rows < 0) {
     set_error("wfd_qkv_rope_append: bad shape n=%d H=%d Hkv=%d Dh=%d rope_rows=%d", n, H, Hkv, Dh, rope_rows);
     return kBadArg;
   }
@@ -361,11 +369,11 @@ int wfd_qkv_rope_append(const void* qkv, int64_t ldq, const int32_t* pos, const 
   if (dtype == kBF16)
     hipLaunchKernelGGL(qkv_rope_append_kernel<bf16_t>, dim3(n), dim3(kRowThreads), 0, stream, (const bf16_t*)qkv, ldq,
                        pos, rope_cos, rope_sin, rope_rows, flat_row, (bf16_t*)q_out, (bf16_t*)k_cache,
-                       (bf16_t*)v_cache, H, Hkv, Dh);
+                       (bf16_t*)v_cache, kv_block_rows, H, Hkv, Dh);
   else if (dtype == kF32)
     hipLaunchKernelGGL(qkv_rope_append_kernel<float>, dim3(n), dim3(kRowThreads), 0, stream, (const float*)qkv, ldq,
                        pos, rope_cos, rope_sin, rope_rows, flat_row, (float*)q_out, (float*)k_cache, (float*)v_cache,
-                       H, Hkv, Dh);
+                       kv_block_rows, H, Hkv, Dh);
   else {
     set_error("wfd_qkv_rope_append: unsupported dtype %d", dtype);
     return kUnsupported;
@@ -373,11 +381,11 @@ int wfd_qkv_rope_append(const void* qkv, int64_t ldq, const int32_t* pos, const 
   return launch_status("wfd_qkv_rope_append");
 }
 
-int wfd_kv_append(const void* k, const void* v, void* k_cache, void* v_cache, const int64_t* flat_row, int n,
-                  int row_elems, int dtype, hipStream_t stream) {
+int wfd_kv_append(const void* k, const void* v, void* k_cache, void* v_cache, int64_t kv_block_rows,
+                  const int64_t* flat_row, int n, int Hkv, int Dh, int dtype, hipStream_t stream) {
   using namespace wfd;
-  if (n < 0 || row_elems <= 0) {
-    set_error("wfd_kv_append: bad shape n=%d row_elems=%d", n, row_elems);
+  if (n < 0 || Hkv <= 0 || Dh <= 0 || kv_block_rows < 0) {
+    set_error("wfd_kv_append: bad shape n=%d Hkv=%d Dh=%d kv_block_rows=%lld", n, Hkv, Dh, (long long)kv_block_rows);
     return kBadArg;
   }
   if (n == 0) return kOk;
@@ -387,10 +395,10 @@ int wfd_kv_append(const void* k, const void* v, void* k_cache, void* v_cache, co
   }
   if (dtype == kBF16)
     hipLaunchKernelGGL(kv_append_kernel<bf16_t>, dim3(n), dim3(kRowThreads), 0, stream, (const bf16_t*)k,
-                       (const bf16_t*)v, (bf16_t*)k_cache, (bf16_t*)v_cache, flat_row, row_elems);
+                       (const bf16_t*)v, (bf16_t*)k_cache, (bf16_t*)v_cache, kv_block_rows, flat_row, Hkv, Dh);
   else if (dtype == kF32)
     hipLaunchKernelGGL(kv_append_kernel<float>, dim3(n), dim3(kRowThreads), 0, stream, (const float*)k,
-                       (const float*)v, (float*)k_cache, (float*)v_cache, flat_row, row_elems);
+                       (const float*)v, (float*)k_cache, (float*)v_cache, kv_block_rows, flat_row, Hkv, Dh);
   else {
     set_error("wfd_kv_append: unsupported dtype %d", dtype);
     return kUnsupported;

@@ -65,8 +65,9 @@ struct RopeArgs {
   int tab_rows;
   const int64_t* flat_row;  // [n] slot-cache row of each token
   void* q_out;              // [n, H, Dh]
-  void* k_cache;            // [rows, Hkv, Dh]
+  void* k_cache;            // slot cache, laid out as kv_offset() describes
   void* v_cache;
+  int64_t block_rows;       // cache layout (kv_offset)
   int H, Hkv, Dh;
 };
 
@@ -89,7 +90,7 @@ __device__ __forceinline__ void store_rope(const RopeArgs& ra, int row, int col,
   TO* dst;
   float out;
   if (head >= ra.H + ra.Hkv) {
-    dst = (TO*)ra.v_cache + ra.flat_row[row] * (int64_t)(ra.Hkv * ra.Dh) + (head - ra.H - ra.Hkv) * ra.Dh + d;
+    dst = (TO*)ra.v_cache + kv_offset(ra.flat_row[row], head - ra.H - ra.Hkv, ra.Hkv, ra.Dh, ra.block_rows) + d;
     out = v0;
   } else {
     int p = ra.pos[row];
@@ -101,7 +102,7 @@ __device__ __forceinline__ void store_rope(const RopeArgs& ra, int row, int col,
     const float xp = Elem<TO>::round(v1);
     out = (d & 1) ? fmaf(xp, s, xm * c) : fmaf(xm, c, -(xp * s));
     dst = head < ra.H ? (TO*)ra.q_out + ((int64_t)row * ra.H + head) * ra.Dh + d
-                      : (TO*)ra.k_cache + ra.flat_row[row] * (int64_t)(ra.Hkv * ra.Dh) + (head - ra.H) * ra.Dh + d;
+                      : (TO*)ra.k_cache + kv_offset(ra.flat_row[row], head - ra.H, ra.Hkv, ra.Dh, ra.block_rows) + d;
   }
   Elem<TO>::store(dst, out);
 }
@@ -460,11 +461,11 @@ int wfd_linear(const void* x, const int32_t* x_rows, int64_t ldx, const void* W,
 
 int wfd_linear_qkv_rope_append(const void* x, const int32_t* x_rows, int64_t ldx, const void* Wqkv, int n, int K,
                                const int32_t* pos, const float* rope_cos, const float* rope_sin, int rope_rows,
-                               const int64_t* flat_row, void* q_out, void* k_cache, void* v_cache, int H, int Hkv,
-                               int Dh, int dtype, hipStream_t stream) {
+                               const int64_t* flat_row, void* q_out, void* k_cache, void* v_cache,
+                               int64_t kv_block_rows, int H, int Hkv, int Dh, int dtype, hipStream_t stream) {
   using namespace wfd;
   if (n < 0 || K <= 0 || ldx < K || H <= 0 || Hkv <= 0 || H % Hkv != 0 || Dh <= 0 || Dh % 16 != 0 ||
-      rope_rows <= 0) {
+      rope_rows <= 0 || kv_block_rows < 0) {
     set_error("wfd_linear_qkv_rope_append: bad shape n=%d K=%d H=%d Hkv=%d Dh=%d rope_rows=%d", n, K, H, Hkv, Dh,
               rope_rows);
     return kBadArg;
@@ -484,7 +485,7 @@ int wfd_linear_qkv_rope_append(const void* x, const int32_t* x_rows, int64_t ldx
     return kUnsupported;
   }
   const int N = (H + 2 * Hkv) * Dh;
-  const RopeArgs ra{pos, rope_cos, rope_sin, rope_rows, flat_row, q_out, k_cache, v_cache, H, Hkv, Dh};
+  const RopeArgs ra{pos, rope_cos, rope_sin, rope_rows, flat_row, q_out, k_cache, v_cache, kv_block_rows, H, Hkv, Dh};
   if (dtype == kBF16)
     launch_linear<bf16_t, bf16_t, kEpiRope>(x, x_rows, ldx, Wqkv, nullptr, 0, n, N, K, 0, ra, stream);
   else if (dtype == kF32)

@@ -117,6 +117,21 @@ __device__ __forceinline__ u32x4 zero16() {
   return z;
 }
 
+// Element offset of (cache row, kv head) in a KV slot cache.
+//   block_rows <= 1: token-major (rows, Hkv, Dh), one row = all heads of a token;
+//   block_rows  > 1: head-major blocks (rows / block_rows, Hkv, block_rows, Dh),
+//                    so one head's rows of a block are contiguous.
+// 32-bit division whenever the operands fit (every realistic cache).
+__device__ __forceinline__ int64_t kv_offset(int64_t row, int head, int Hkv, int Dh, int64_t block_rows) {
+  if (block_rows <= 1) return (row * Hkv + head) * Dh;
+  int64_t blk;
+  if (((uint64_t)row | (uint64_t)block_rows) >> 32 == 0)
+    blk = (uint32_t)row / (uint32_t)block_rows;
+  else
+    blk = row / block_rows;
+  return ((blk * Hkv + head) * block_rows + (row - blk * block_rows)) * Dh;
+}
+
 // One MFMA "k-step": acc(16x16) += A(16 x KSTEP) * B(KSTEP x 16), where each
 // lane supplies one 16-byte fragment of A (row lane%16) and of B (column
 // lane%16), both covering k-group lane/16. KSTEP = 4 * kVec: 32 for bf16

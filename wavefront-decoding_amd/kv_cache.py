@@ -5,13 +5,19 @@ K/V buffer per (slot, sequence) -- and its slot numbering (prelude i -> i;
 core step r layer l -> n_prelude + r*n_core + l; coda i ->
 n_prelude + T_total*n_core + i; src/decoding/kv_cache.py:8-22,
 huginn_blocks_batch.py:90-100). What changes is the storage: all slots of
-all sequences live in one contiguous (n_slots*B*S, Hkv, Dh) buffer per K and
-V, so the decode kernel reads any slot prefix in place from
-(row_base, kv_len) tables instead of gathering and concatenating copies
-(the pack of batch_kv_cache.py:75-96 / parcae_blocks.py:458-466 is gone).
+all sequences live in one contiguous buffer per K and V, so the decode kernel
+reads any slot prefix in place from (row_base, kv_len) tables instead of
+gathering and concatenating copies (the pack of batch_kv_cache.py:75-96 /
+parcae_blocks.py:458-466 is gone).
 
 Flat row of (slot, seq b, pos) = (slot*B + b)*S + pos
-(src/decoding/batch_kv_cache.py:64-65).
+(src/decoding/batch_kv_cache.py:64-65). Layout of the buffers:
+  head_major=True (default): (n_slots*B + 1, Hkv, S, Dh) -- one block of S rows
+      per (slot, sequence), each head's positions contiguous, so attention
+      streams one contiguous run per (query, head);
+  head_major=False: (n_slots*B*S + 1, Hkv, Dh) -- token-major, the reference's
+      per-slot (S, Hkv, Dh) buffers laid end to end.
+`K` / `V` are (n_slots, B, S, Hkv, Dh) views of either layout.
 
 Rollback only truncates the logical lengths (kv_cache.py:158-165,
 batch_kv_cache.py:99-105): every read is bounded by the reading query's own
@@ -29,7 +35,7 @@ class BatchStaticKVCache:
     """Flat per-(slot, sequence) cache; mirrors src/decoding/batch_kv_cache.py:29-105."""
 
     def __init__(self, n_slots: int, batch_size: int, n_kv_head: int, head_dim: int, max_seq_len: int,
-                 dtype: torch.dtype, device):
+                 dtype: torch.dtype, device, *, head_major: bool = True):
         self.n_slots = n_slots
         self.B = batch_size
         self.S = max_seq_len
@@ -37,15 +43,26 @@ class BatchStaticKVCache:
         self.head_dim = head_dim
         self.dtype = dtype
         self.device = torch.device(device)
-        rows = n_slots * batch_size * max_seq_len
+        self.head_major = head_major
+        nblk = n_slots * batch_size
+        rows = nblk * max_seq_len
         # zero-filled like the reference, so a clamped read never sees NaN garbage;
-        # one extra trailing "trash" row absorbs the appends of padding rows of a
-        # captured (fixed-width) launch and is never part of any slot.
-        self.flat_k = torch.zeros(rows + 1, n_kv_head, head_dim, dtype=dtype, device=self.device)
-        self.flat_v = torch.zeros(rows + 1, n_kv_head, head_dim, dtype=dtype, device=self.device)
+        # one extra trailing "trash" row (a whole block when head-major) absorbs
+        # the appends of padding rows of a captured (fixed-width) launch and is
+        # never part of any slot.
+        if head_major:
+            shape = (nblk + 1, n_kv_head, max_seq_len, head_dim)
+            self.flat_k = torch.zeros(shape, dtype=dtype, device=self.device)
+            self.flat_v = torch.zeros(shape, dtype=dtype, device=self.device)
+            view = lambda t: t[:nblk].view(n_slots, batch_size, n_kv_head, max_seq_len,  # noqa: E731
+                                           head_dim).permute(0, 1, 3, 2, 4)
+        else:
+            self.flat_k = torch.zeros(rows + 1, n_kv_head, head_dim, dtype=dtype, device=self.device)
+            self.flat_v = torch.zeros(rows + 1, n_kv_head, head_dim, dtype=dtype, device=self.device)
+            view = lambda t: t[:rows].view(n_slots, batch_size, max_seq_len, n_kv_head, head_dim)  # noqa: E731
         self.trash_row = rows
-        self.K = self.flat_k[:rows].view(n_slots, batch_size, max_seq_len, n_kv_head, head_dim)
-        self.V = self.flat_v[:rows].view(n_slots, batch_size, max_seq_len, n_kv_head, head_dim)
+        self.K = view(self.flat_k)
+        self.V = view(self.flat_v)
         # logical per-(slot, seq) lengths: bookkeeping and bounds checks only
         self.seqlen = [[0] * batch_size for _ in range(n_slots)]
 
@@ -97,13 +114,11 @@ class BatchStaticKVCache:
         copies the n prefixes [0, upto_i] into contiguous K/V + int32 cu_k. The
         decode path never calls it -- the kernel reads the slots in place."""
         lengths = [u + 1 for u in uptos]
-        idx = torch.cat([torch.arange(self.row_base(sl, b), self.row_base(sl, b) + ln, device=self.device)
-                         for sl, b, ln in zip(slots, seq_ids, lengths)])
         cu = [0]
         for ln in lengths:
             cu.append(cu[-1] + ln)
-        return (self.flat_k.index_select(0, idx), self.flat_v.index_select(0, idx),
-                torch.tensor(cu, dtype=torch.int32, device=self.device), max(lengths))
+        pack = lambda t: torch.cat([t[sl, b, :ln] for sl, b, ln in zip(slots, seq_ids, lengths)])  # noqa: E731
+        return (pack(self.K), pack(self.V), torch.tensor(cu, dtype=torch.int32, device=self.device), max(lengths))
 
     def drop_positions_at_and_after(self, b: int, position: int) -> None:
         """Per-sequence rollback: truncate sequence b's logical lengths only."""
@@ -125,8 +140,8 @@ class StaticKVCache(BatchStaticKVCache):
     (src/decoding/huginn_blocks.py:274,279) address the last two slots."""
 
     def __init__(self, n_kv_head: int, head_dim: int, max_seq_len: int, dtype: torch.dtype, device, *,
-                 n_slots: int):
-        super().__init__(n_slots, 1, n_kv_head, head_dim, max_seq_len, dtype, device)
+                 n_slots: int, head_major: bool = True):
+        super().__init__(n_slots, 1, n_kv_head, head_dim, max_seq_len, dtype, device, head_major=head_major)
         self._seen_tokens = 0
 
     def _slot(self, step_idx: int) -> int:

@@ -70,18 +70,31 @@ def attn_workspace(n: int, H: int, Dh: int, kv_len_max: int, device) -> torch.Te
     return ws
 
 
+def kv_layout(k_cache: torch.Tensor, v_cache: torch.Tensor) -> tuple[int, int, int]:
+    """(Hkv, Dh, block_rows) of a pair of KV caches, read from their shape:
+    3-D (rows, Hkv, Dh) is token-major (block_rows 1); 4-D
+    (blocks, Hkv, block_rows, Dh) is head-major blocks, cache row r of kv head
+    h at [r // block_rows, h, r % block_rows]."""
+    _need(k_cache.shape == v_cache.shape and k_cache.dtype == v_cache.dtype, "k/v caches differ in shape or dtype")
+    _need(k_cache.is_contiguous() and v_cache.is_contiguous(), "caches must be contiguous")
+    if k_cache.dim() == 3:
+        return k_cache.shape[1], k_cache.shape[2], 1
+    _need(k_cache.dim() == 4, "a KV cache is (rows, Hkv, Dh) or (blocks, Hkv, block_rows, Dh)")
+    return k_cache.shape[1], k_cache.shape[3], k_cache.shape[2]
+
+
 def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, kv_row_base: torch.Tensor,
                 kv_len: torch.Tensor, *, kv_len_max: int, scale: float | None = None,
                 out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """Wavefront decode attention: q (n, H, Dh) over slot rows of the flat
-    (rows, Hkv, Dh) caches; query i reads rows kv_row_base[i] + [0, kv_len[i])."""
+    """Wavefront decode attention: q (n, H, Dh) over slot rows of the KV
+    caches (layout: kv_layout); query i reads cache rows
+    kv_row_base[i] + [0, kv_len[i])."""
     _need_cuda(q, k_cache, v_cache, kv_row_base, kv_len)
     _need(q.dim() == 3 and q.is_contiguous(), "q must be contiguous (n, H, Dh)")
     n, H, Dh = q.shape
-    _need(k_cache.dim() == 3 and k_cache.shape == v_cache.shape, "k/v cache must be (rows, Hkv, Dh)")
-    _need(k_cache.is_contiguous() and v_cache.is_contiguous(), "caches must be contiguous")
-    Hkv = k_cache.shape[1]
-    _need(k_cache.shape[2] == Dh and k_cache.dtype == q.dtype == v_cache.dtype, "q/k/v dtype or head_dim mismatch")
+    Hkv, cDh, br = kv_layout(k_cache, v_cache)
+    _need(cDh == Dh and k_cache.dtype == q.dtype, "q/k/v dtype or head_dim mismatch")
+    _need(br == 1 or kv_len_max <= br, f"kv_len_max {kv_len_max} exceeds the cache block ({br} rows)")
     _need(kv_row_base.dtype == torch.int64 and kv_row_base.numel() >= n and kv_row_base.is_contiguous(),
           "kv_row_base: int64 (n,)")
     _need(kv_len.dtype == torch.int32 and kv_len.numel() >= n and kv_len.is_contiguous(), "kv_len: int32 (n,)")
@@ -93,7 +106,7 @@ def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, k
         workspace = attn_workspace(n, H, Dh, kv_len_max, q.device)
     sc = 1.0 / math.sqrt(Dh) if scale is None else float(scale)
     rc = _lib.load().wfd_attn_decode(
-        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), kv_row_base.data_ptr(), kv_len.data_ptr(),
+        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), br, kv_row_base.data_ptr(), kv_len.data_ptr(),
         out.data_ptr(), n, H, Hkv, Dh, _dt(q), sc, int(kv_len_max), workspace.data_ptr(),
         workspace.numel() * workspace.element_size(), _stream())
     _lib.check(rc, "wfd_attn_decode")
@@ -105,16 +118,16 @@ def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, k
 # ---------------------------------------------------------------------------
 def kv_append(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
               flat_row: torch.Tensor) -> None:
-    """k_cache[flat_row[i]] = k[i]; v_cache[flat_row[i]] = v[i]."""
+    """Cache row flat_row[i] of k_cache / v_cache = k[i] / v[i] (each (Hkv, Dh))."""
     _need_cuda(k, v, k_cache, v_cache, flat_row)
     n = k.shape[0]
-    row = k_cache[0].numel()
-    _need(k.is_contiguous() and v.is_contiguous() and k.shape == v.shape and k[0].numel() == row,
+    Hkv, Dh, br = kv_layout(k_cache, v_cache)
+    _need(k.is_contiguous() and v.is_contiguous() and k.shape == v.shape and k[0].numel() == Hkv * Dh,
           "k/v rows must match cache rows")
-    _need(k.dtype == v.dtype == k_cache.dtype == v_cache.dtype, "dtype mismatch")
+    _need(k.dtype == v.dtype == k_cache.dtype, "dtype mismatch")
     _need(flat_row.dtype == torch.int64 and flat_row.numel() >= n and flat_row.is_contiguous(), "flat_row: int64")
-    rc = _lib.load().wfd_kv_append(k.data_ptr(), v.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
-                                   flat_row.data_ptr(), n, row, _dt(k), _stream())
+    rc = _lib.load().wfd_kv_append(k.data_ptr(), v.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), br,
+                                   flat_row.data_ptr(), n, Hkv, Dh, _dt(k), _stream())
     _lib.check(rc, "wfd_kv_append")
 
 
@@ -128,13 +141,14 @@ def qkv_rope_append(qkv: torch.Tensor, pos: torch.Tensor, rope_cos: torch.Tensor
     _need(flat_row.dtype == torch.int64 and flat_row.numel() >= n and flat_row.is_contiguous(), "flat_row: int64")
     _need(rope_cos.dtype == torch.float32 and rope_cos.shape == rope_sin.shape and rope_cos.shape[1] == Dh // 2,
           "rope tables: float32 (S, Dh/2)")
-    _need(k_cache.shape[1:] == (Hkv, Dh) and k_cache.dtype == qkv.dtype, "cache shape/dtype mismatch")
+    cHkv, cDh, br = kv_layout(k_cache, v_cache)
+    _need((cHkv, cDh) == (Hkv, Dh) and k_cache.dtype == qkv.dtype, "cache shape/dtype mismatch")
     if q_out is None:
         q_out = torch.empty(n, H, Dh, dtype=qkv.dtype, device=qkv.device)
     rc = _lib.load().wfd_qkv_rope_append(qkv.data_ptr(), qkv.stride(0), pos.data_ptr(), rope_cos.data_ptr(),
                                          rope_sin.data_ptr(), rope_cos.shape[0], flat_row.data_ptr(),
-                                         q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), n, H, Hkv, Dh,
-                                         _dt(qkv), _stream())
+                                         q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), br, n, H, Hkv,
+                                         Dh, _dt(qkv), _stream())
     _lib.check(rc, "wfd_qkv_rope_append")
     return q_out
 
@@ -156,15 +170,16 @@ def linear_qkv_rope_append(x: torch.Tensor, Wqkv: torch.Tensor, pos: torch.Tenso
     _need(flat_row.dtype == torch.int64 and flat_row.numel() >= n and flat_row.is_contiguous(), "flat_row: int64")
     _need(rope_cos.dtype == torch.float32 and rope_cos.shape == rope_sin.shape and rope_cos.shape[1] == Dh // 2
           and rope_cos.is_contiguous() and rope_sin.is_contiguous(), "rope tables: float32 (S, Dh/2)")
-    _need(k_cache.shape[1:] == (Hkv, Dh) and k_cache.dtype == x.dtype and v_cache.shape == k_cache.shape
-          and k_cache.is_contiguous() and v_cache.is_contiguous(), "cache shape/dtype mismatch")
+    cHkv, cDh, br = kv_layout(k_cache, v_cache)
+    _need((cHkv, cDh) == (Hkv, Dh) and k_cache.dtype == x.dtype, "cache shape/dtype mismatch")
     if q_out is None:
         q_out = torch.empty(n, H, Dh, dtype=x.dtype, device=x.device)
     _need(q_out.is_contiguous() and q_out.numel() >= n * H * Dh and q_out.dtype == x.dtype, "q_out (n, H, Dh)")
     rc = _lib.load().wfd_linear_qkv_rope_append(x.data_ptr(), _p(x_rows), x.stride(0), Wp.data.data_ptr(), n, K,
                                                 pos.data_ptr(), rope_cos.data_ptr(), rope_sin.data_ptr(),
                                                 rope_cos.shape[0], flat_row.data_ptr(), q_out.data_ptr(),
-                                                k_cache.data_ptr(), v_cache.data_ptr(), H, Hkv, Dh, _dt(x), _stream())
+                                                k_cache.data_ptr(), v_cache.data_ptr(), br, H, Hkv, Dh, _dt(x),
+                                                _stream())
     _lib.check(rc, "wfd_linear_qkv_rope_append")
     return q_out
 
