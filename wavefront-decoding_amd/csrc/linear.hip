@@ -55,6 +55,7 @@ namespace wfd {
 constexpr int kWideWaves = 16;
 constexpr int kWideMaxChunksPerWave = 3;
 constexpr int kWideMaxRows = 16;
+constexpr int kHalfTileMax = 256;  // wide launches of at most this many tiles use half tiles
 enum Epilogue : int { kEpiPlain = 0, kEpiSwiGLU = 1, kEpiRope = 2 };
 
 // Operands of the QKV-RoPE-append epilogue (unused by the others).
@@ -200,15 +201,21 @@ __device__ __forceinline__ void chunk_mma(f32x4 (&acc)[NT], const u32x4 (&xf)[kC
 }
 
 // ---------------------------------------------------------------------------
-// wide: grid (tiles), 1024 threads; MC chunks per wave.
-template <typename T, typename TO, int EPI, int MC>
+// wide: grid (tiles << HALF), 1024 threads; MC chunks per wave. HALF: two
+// workgroups per tile, each owning 8 of its 16 columns (its other lanes load
+// zero weights through an invalid buffer offset: no memory traffic), so a
+// 2048-column projection spreads over 256 workgroups instead of 128. The MFMA
+// output of a column does not depend on the other columns' operands, so both
+// forms give the same bits.
+template <typename T, typename TO, int EPI, int MC, bool HALF>
 __global__ __launch_bounds__(64 * kWideWaves) void linear_wide_kernel(
     const T* __restrict__ x, const int32_t* __restrict__ x_rows, int64_t ldx, const T* __restrict__ W,
     TO* __restrict__ y, int64_t ldy, int n, int K, int pair_off, const RopeArgs ra) {
   extern __shared__ f32x4 red[];  // [P][64 lanes]
   constexpr int V = LinTraits<T>::V;
   const int P = K / LinTraits<T>::KC;
-  const int g = blockIdx.x;
+  const int g = HALF ? blockIdx.x >> 1 : blockIdx.x;
+  const int half = HALF ? (int)(blockIdx.x & 1) : 0;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int col = lane & 15;
@@ -217,6 +224,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void linear_wide_kernel(
   const uint32_t xoff = x_offset<T>(x_rows, ldx, 0, col, grp, n);
   const __amdgpu_buffer_rsrc_t xrs = buf_rsrc(x);
   const T* const wtile[1] = {W + packed_off<T>(g, 0, P, 0)};
+  const __amdgpu_buffer_rsrc_t wrs = buf_rsrc(wtile[0]);
 
   // Every load is unconditional; a wave past the last chunk re-reads chunk
   // P-1 and discards it.
@@ -226,7 +234,16 @@ __global__ __launch_bounds__(64 * kWideWaves) void linear_wide_kernel(
   for (int j = 0; j < MC; ++j) {
     const int p = wave + kWideWaves * j;
     const int pc = p < P ? p : P - 1;
-    load_w<T, 1>(wf[j], wtile, P, pc, lane);
+    if (HALF) {
+      const bool mine = (col >> 3) == half;
+#pragma unroll
+      for (int s2 = 0; s2 < kChunkSteps; ++s2) {
+        const uint32_t off = (uint32_t)((packed_off<T>(0, pc, P, lane) + (int64_t)s2 * 64 * V) * sizeof(T));
+        wf[j][0][s2] = buf_ld16(wrs, mine ? off : kBufInvalid);
+      }
+    } else {
+      load_w<T, 1>(wf[j], wtile, P, pc, lane);
+    }
     load_x<T>(xf[j], xrs, xoff, pc);
   }
 #pragma unroll
@@ -252,7 +269,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void linear_wide_kernel(
     const float partner = EPI == kEpiRope     ? __shfl_xor(v, 4, 64)
                           : EPI == kEpiSwiGLU ? __shfl_xor(v, 32, 64)
                                               : 0.f;
-    if (row < n) store_out<TO, EPI>(y, ldy, ra, row, g, ln & 15, v, partner);
+    if (row < n && (!HALF || ((ln & 15) >> 3) == half)) store_out<TO, EPI>(y, ldy, ra, row, g, ln & 15, v, partner);
   }
 }
 
@@ -336,16 +353,24 @@ static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const v
   const size_t lds = (size_t)P * 64 * sizeof(f32x4);
   const int mc = (P + kWideWaves - 1) / kWideWaves;  // chunks per wave
   const bool wide = n <= kWideMaxRows && mc <= kWideMaxChunksPerWave && lds <= 65536;
+  // fewer tiles than half the chip's 256 CUs x 2: split tiles into column halves
+  // (not for SwiGLU, whose partner column c ^ 8 lies in the other half)
+  const bool half = EPI != kEpiSwiGLU && tiles <= kHalfTileMax;
+#define WFD_WIDE(MCV)                                                                                            \
+  if (half)                                                                                                      \
+    hipLaunchKernelGGL((linear_wide_kernel<T, TO, EPI, MCV, true>), dim3(2 * tiles), dim3(64 * kWideWaves), lds, \
+                       st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra);                  \
+  else                                                                                                           \
+    hipLaunchKernelGGL((linear_wide_kernel<T, TO, EPI, MCV, false>), dim3(tiles), dim3(64 * kWideWaves), lds, st, \
+                       (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra);
   if (wide && mc == 1) {
-    hipLaunchKernelGGL((linear_wide_kernel<T, TO, EPI, 1>), dim3(tiles), dim3(64 * kWideWaves), lds, st,
-                       (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra);
+    WFD_WIDE(1)
   } else if (wide && mc == 2) {
-    hipLaunchKernelGGL((linear_wide_kernel<T, TO, EPI, 2>), dim3(tiles), dim3(64 * kWideWaves), lds, st,
-                       (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra);
+    WFD_WIDE(2)
   } else if (wide) {
-    hipLaunchKernelGGL((linear_wide_kernel<T, TO, EPI, 3>), dim3(tiles), dim3(64 * kWideWaves), lds, st,
-                       (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra);
+    WFD_WIDE(3)
   } else {
+#undef WFD_WIDE
     constexpr int NB = 2;
     hipLaunchKernelGGL((linear_tile_kernel<T, TO, EPI, NB>), dim3((n + 63) / 64, (tiles + NB - 1) / NB), dim3(256),
                        0, st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra);
