@@ -68,6 +68,23 @@ int wfd_attn_decode(const void* q, const void* k_cache, const void* v_cache, int
                     wfd_stream_t stream);
 
 /*
+ * Causal prefill attention on MFMA (bf16; Dh 64 or 128; any H / Hkv).
+ * Segment s owns query rows [seg_q_start[s], seg_q_start[s+1]) of q (n, H, Dh)
+ * at positions seg_pos0[s], seg_pos0[s] + 1, ... of one slot whose cache rows
+ * start at seg_row_base[s]; query row j attends that slot's keys [0, its
+ * position] (bottom-right causal), which must already be appended. out: (n, H,
+ * Dh). max_seg_len >= every segment length sizes the grid. Tables are device
+ * data.
+ * Replaces: attn_dense(q, k, v, causal=True) (src/decoding/fa4_attention.py:189-215)
+ *   from _block_dense (src/decoding/huginn_blocks_batch.py:163-170), and the
+ *   grouped causal segments of _core_attn_varlen (src/decoding/parcae_blocks.py:435-456).
+ */
+int wfd_attn_prefill(const void* q, const void* k_cache, const void* v_cache, int64_t kv_block_rows,
+                     const int64_t* seg_row_base, const int32_t* seg_q_start, const int32_t* seg_pos0, void* out,
+                     int nseg, int max_seg_len, int H, int Hkv, int Dh, int dtype, float scale,
+                     wfd_stream_t stream);
+
+/*
  * Slot-cache append: cache row flat_row[i] of k_cache / v_cache (layout
  * kv_block_rows) = k[i] / v[i], each (Hkv, Dh).
  * Replaces: StaticKVCache.write_range / write_scatter

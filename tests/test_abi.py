@@ -43,6 +43,9 @@ def test_host_only_entry_points():
     rc = lib.wfd_attn_decode(None, None, None, 512, None, None, None, 1, 16, 16, 64, 1, 0.1, 513, None, 0, None)
     assert rc == -1 and b"kv_block_rows=512" in lib.wfd_last_error()
     assert lib.wfd_kv_append(None, None, None, None, -1, None, 1, 16, 128, 1, None) == -1
+    rc = lib.wfd_attn_prefill(None, None, None, 0, None, None, None, None, 1, 10, 16, 3, 64, 1, 0.1, None)
+    assert rc == -1 and b"wfd_attn_prefill: bad shape" in lib.wfd_last_error()
+    assert lib.wfd_attn_prefill(None, None, None, 0, None, None, None, None, 0, 10, 16, 4, 64, 1, 0.1, None) == 0
     rc = lib.wfd_linear(None, None, 100, None, None, 16, 2, 16, 100, 1, 1, 0, 0, None)
     assert rc == -1
     assert lib.wfd_attn_decode(None, None, None, 0, None, None, None, 0, 16, 16, 64, 1, 0.1, 10, None, 0, None) == 0

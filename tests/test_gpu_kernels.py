@@ -97,6 +97,46 @@ def test_attn_decode_row_invariant(gpu, dtype):
         assert torch.equal(one[0], full[i]), i
 
 
+@pytest.mark.parametrize("blocks", [False, True])
+@pytest.mark.parametrize("H,Hkv,Dh,segs", [
+    (16, 16, 128, [(0, 200)]),                          # one 2048-d-model prompt
+    (16, 4, 128, [(0, 64), (0, 65), (37, 100)]),        # GQA, tile edges, a segment after a cached prefix
+    (4, 4, 64, [(0, 1), (5, 3), (0, 130), (120, 70)]),  # tiny heads, 1-row and ragged segments
+    (16, 16, 64, [(0, 257), (300, 1)]),                 # a lone query over a 300-key prefix
+])
+def test_attn_prefill_matches_oracle(gpu, H, Hkv, Dh, segs, blocks):
+    """MFMA causal prefill: segment (pos0, len) on its own slot, each row
+    attending keys [0, its position]; against the oracle, and both cache
+    layouts give the same bits."""
+    dtype = torch.bfloat16
+    g = torch.Generator().manual_seed(len(segs) * 31 + Dh)
+    S = max(p0 + n for p0, n in segs) + 5
+    n_slots = len(segs) + 1
+    K = torch.randn(n_slots * S, Hkv, Dh, generator=g).to(dtype)
+    V = torch.randn(n_slots * S, Hkv, Dh, generator=g).to(dtype)
+    n = sum(ln for _, ln in segs)
+    q = torch.randn(n, H, Dh, generator=g).to(dtype)
+    seg_rb = torch.tensor([(s + 1) * S for s in range(len(segs))], dtype=torch.int64)
+    qs = torch.tensor(np.cumsum([0] + [ln for _, ln in segs]), dtype=torch.int32)
+    p0 = torch.tensor([p for p, _ in segs], dtype=torch.int32)
+    rb = torch.cat([torch.full((ln,), int(seg_rb[s])) for s, (_, ln) in enumerate(segs)])
+    kl = torch.cat([torch.arange(p + 1, p + ln + 1) for p, ln in segs]).to(torch.int32)
+    print(f"[prefill] H={H} Hkv={Hkv} Dh={Dh} segs={segs} blocks={blocks}", flush=True)
+    Kd, Vd = (_blocks(K, S), _blocks(V, S)) if blocks else (K, V)
+    mx = max(ln for _, ln in segs)
+    out = ops.attn_prefill(q.to(gpu), Kd.to(gpu), Vd.to(gpu), seg_rb.to(gpu), qs.to(gpu), p0.to(gpu), max_seg_len=mx)
+    other = ops.attn_prefill(q.to(gpu), (K if blocks else _blocks(K, S)).to(gpu),
+                             (V if blocks else _blocks(V, S)).to(gpu), seg_rb.to(gpu), qs.to(gpu), p0.to(gpu),
+                             max_seg_len=mx)
+    torch.cuda.synchronize()
+    ref = ok.attention_rows(_np(q), _np(K), _np(V), rb.numpy(), kl.numpy())
+    assert rel_err(_np(out), ref) <= 2e-2
+    assert torch.equal(out, other)
+    # per-row agreement with the decode kernel on the same rows (different arithmetic, same math)
+    dec = ops.attn_decode(q.to(gpu), K.to(gpu), V.to(gpu), rb.to(gpu), kl.to(gpu), kv_len_max=int(kl.max()))
+    assert rel_err(_np(out), _np(dec)) <= 2e-2
+
+
 def test_attn_decode_kv_len_device_data(gpu):
     """Lengths are read from device memory at launch time: changing them in place changes the result."""
     q, K, V, rb, kl = _attn_case(gpu, torch.bfloat16, 2, 16, 16, 128, [600, 600], S=2048)

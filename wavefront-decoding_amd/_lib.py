@@ -35,6 +35,8 @@ SIGNATURES: dict[str, tuple] = {
     "wfd_attn_split_keys": (_i32, []),
     "wfd_attn_decode": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp,
                                _sz, _vp]),
+    "wfd_attn_prefill": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
+                                _vp]),
     "wfd_kv_append": (_i32, [_vp, _vp, _vp, _vp, _i64, _vp, _i32, _i32, _i32, _i32, _vp]),
     "wfd_qkv_rope_append": (_i32, [_vp, _i64, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32,
                                    _i32, _i32, _vp]),

@@ -214,14 +214,23 @@ class LoopedModel:
 
     # -- one SandwichBlock over n rows --------------------------------------------
     def _block(self, prefix: str, n: int, sc, pos_d, kvlen_d, rb_d, fr_d, kv_len_max: int, ws,
-               cache: BatchStaticKVCache, next_norm: torch.Tensor | None, final_out=None, final_rows=None):
+               cache: BatchStaticKVCache, next_norm: torch.Tensor | None, final_out=None, final_rows=None,
+               segments=None):
+        """One SandwichBlock over n rows. `segments` = (seg_row_base, seg_q_start,
+        seg_pos0, max_seg_len) routes attention through the causal prefill
+        kernel (rows grouped by slot at consecutive positions) instead of the
+        per-row decode kernel."""
         c, W = self.cfg, self.W
         x, h = sc["x"], sc["h"]
         q = ops.linear_qkv_rope_append(h, W[prefix + "Wqkv"], pos_d, self.rope_cos, self.rope_sin, fr_d,
                                        cache.flat_k, cache.flat_v, c.n_heads, c.n_kv_heads, c.head_dim, n=n,
                                        q_out=sc["q"][:n])
-        o = ops.attn_decode(q, cache.flat_k, cache.flat_v, rb_d, kvlen_d, kv_len_max=kv_len_max, out=sc["o"][:n],
-                            workspace=ws)
+        if segments is not None:
+            srb, sqs, sp0, smax = segments
+            o = ops.attn_prefill(q, cache.flat_k, cache.flat_v, srb, sqs, sp0, max_seg_len=smax, out=sc["o"][:n])
+        else:
+            o = ops.attn_decode(q, cache.flat_k, cache.flat_v, rb_d, kvlen_d, kv_len_max=kv_len_max,
+                                out=sc["o"][:n], workspace=ws)
         a = ops.linear(o.view(n, -1), W[prefix + "proj"], n=n, out=sc["a"])
         ops.add_rmsnorm(a, W[prefix + "norm_2"], c.norm_eps, res=x, w2=W[prefix + "norm_3"], n=n, x_out=x,
                         h_out=h)
@@ -431,13 +440,19 @@ class LoopedModel:
         D = c.d_model
         pos = np.arange(L, dtype=np.int64)
         n_layers = c.n_prelude + c.T_total * c.n_core + c.n_coda
-        rb = np.repeat(((np.arange(n_layers, dtype=np.int64) * cache.B + b) * cache.S)[:, None], L, axis=1)
+        base = (np.arange(n_layers, dtype=np.int64) * cache.B + b) * cache.S  # slot row base per layer slot
+        rb = np.repeat(base[:, None], L, axis=1)
         fr = rb + pos[None, :]
-        t32, t64, ids_d = self.staging.upload([np.concatenate([pos, pos + 1]).astype(np.int32),
-                                               np.concatenate([rb.reshape(-1), fr.reshape(-1)]), ids])
-        pos_d, kvlen_d = t32[:L], t32[L:]
+        t32, t64, ids_d = self.staging.upload([np.concatenate([pos, pos + 1, [0, L, 0]]).astype(np.int32),
+                                               np.concatenate([rb.reshape(-1), fr.reshape(-1), base]), ids])
+        pos_d, kvlen_d = t32[:L], t32[L:2 * L]
         rb_l = lambda s: t64[s * L: (s + 1) * L]  # noqa: E731
         fr_l = lambda s: t64[(n_layers + s) * L: (n_layers + s + 1) * L]  # noqa: E731
+        # bf16: the whole prompt of a slot is one causal segment for the MFMA
+        # prefill kernel; fp32 keeps the per-row decode kernel
+        flash = self.dtype == torch.bfloat16 and c.head_dim in (64, 128)
+        seg_l = (lambda s: (t64[2 * n_layers * L + s: 2 * n_layers * L + s + 1], t32[2 * L: 2 * L + 2],  # noqa: E731
+                            t32[2 * L + 2: 2 * L + 3], L)) if flash else (lambda s: None)
         sc = self._scratch(L)
         ws = torch.zeros(ops.attn_workspace_bytes(L, c.n_heads, c.head_dim, L), dtype=torch.uint8,
                          device=self.device)
@@ -448,7 +463,7 @@ class LoopedModel:
         for i in range(c.n_prelude):
             nxt = W[f"prelude.{i + 1}.norm_1"] if i + 1 < c.n_prelude else None
             self._block(f"prelude.{i}.", L, sc, pos_d, kvlen_d, rb_l(i), fr_l(i), L, ws, cache, nxt,
-                        final_out=state[:, D:])
+                        final_out=state[:, D:], segments=seg_l(i))
         s0 = initial_state_prefill(c, L, self.state_seed, self.state_init)
         state[:, :D].copy_(s0.to(device=self.device, dtype=self.dtype))
         for r in range(c.T_total):
@@ -458,12 +473,12 @@ class LoopedModel:
                 s = self.slot_core(r, l)
                 nxt = W[f"core.{l + 1}.norm_1"] if l + 1 < c.n_core else None
                 self._block(f"core.{l}.", L, sc, pos_d, kvlen_d, rb_l(s), fr_l(s), L, ws, cache, nxt,
-                            final_out=state[:, :D])
+                            final_out=state[:, :D], segments=seg_l(s))
         ops.add_rmsnorm(state, W["ln_f"], c.norm_eps, w2=W["coda.0.norm_1"], n=L, x_out=sc["x"], h_out=sc["h"])
         for i in range(c.n_coda):
             s = self.slot_coda(i)
             nxt = W[f"coda.{i + 1}.norm_1"] if i + 1 < c.n_coda else W["ln_f"]
-            self._block(f"coda.{i}.", L, sc, pos_d, kvlen_d, rb_l(s), fr_l(s), L, ws, cache, nxt)
+            self._block(f"coda.{i}.", L, sc, pos_d, kvlen_d, rb_l(s), fr_l(s), L, ws, cache, nxt, segments=seg_l(s))
         ops.linear(sc["h"][L - 1: L], W["lm_head"], n=1, out=logits, out_dtype=torch.float32)
         for s in range(n_layers):
             cache.seqlen[s][b] = max(cache.seqlen[s][b], L)

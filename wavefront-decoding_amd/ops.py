@@ -113,6 +113,34 @@ def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, k
     return out
 
 
+def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, seg_row_base: torch.Tensor,
+                 seg_q_start: torch.Tensor, seg_pos0: torch.Tensor, *, max_seg_len: int, scale: float | None = None,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal prefill attention (bf16, MFMA): segment s = q rows
+    [seg_q_start[s], seg_q_start[s+1]) at positions seg_pos0[s] + 0, 1, ... of
+    the slot at cache row seg_row_base[s]; each row attends keys [0, position]."""
+    _need_cuda(q, k_cache, v_cache, seg_row_base, seg_q_start, seg_pos0)
+    _need(q.dim() == 3 and q.is_contiguous(), "q must be contiguous (n, H, Dh)")
+    n, H, Dh = q.shape
+    Hkv, cDh, br = kv_layout(k_cache, v_cache)
+    _need(cDh == Dh and k_cache.dtype == q.dtype, "q/k/v dtype or head_dim mismatch")
+    nseg = seg_row_base.numel()
+    _need(seg_row_base.dtype == torch.int64 and seg_row_base.is_contiguous(), "seg_row_base: int64 (nseg,)")
+    _need(seg_q_start.dtype == torch.int32 and seg_q_start.is_contiguous() and seg_q_start.numel() == nseg + 1,
+          "seg_q_start: int32 (nseg + 1,)")
+    _need(seg_pos0.dtype == torch.int32 and seg_pos0.is_contiguous() and seg_pos0.numel() == nseg,
+          "seg_pos0: int32 (nseg,)")
+    if out is None:
+        out = torch.empty_like(q)
+    _need(out.shape == q.shape and out.dtype == q.dtype and out.is_contiguous(), "bad out")
+    sc = 1.0 / math.sqrt(Dh) if scale is None else float(scale)
+    rc = _lib.load().wfd_attn_prefill(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), br,
+                                      seg_row_base.data_ptr(), seg_q_start.data_ptr(), seg_pos0.data_ptr(),
+                                      out.data_ptr(), nseg, int(max_seg_len), H, Hkv, Dh, _dt(q), sc, _stream())
+    _lib.check(rc, "wfd_attn_prefill")
+    return out
+
+
 # ---------------------------------------------------------------------------
 # slot-cache append
 # ---------------------------------------------------------------------------
