@@ -13,42 +13,49 @@
 // in place from either cache layout (kv_offset). out row r = softmax over the
 // row's causal prefix of (q_r . k) * scale, times V.
 //
-// Work split: a workgroup of 4 waves owns 64 consecutive query rows of one
-// segment and one query head; wave w owns rows 16w..16w+15. Per 64-key tile:
-// the workgroup stages K (row-major) and V (transposed) in LDS; each wave
-// computes S = Q K^T with v_mfma_f32_16x16x32_bf16 (Q fragments held in
-// registers for the whole sweep), runs an online softmax per row (the 16
-// lanes of a row group exchange max and sum by shuffles), rounds P to bf16
-// through its LDS rows into the MFMA A layout, and accumulates O += P V on
-// MFMA. Tiles past the diagonal are never visited; the diagonal tile masks
-// keys past each row's position. Tiles are dispatched longest first.
+// Work split: a workgroup of 8 waves owns 128 consecutive query rows of one
+// segment and one query head; wave w owns rows 16w..16w+15, one per lane
+// column. Per 64-key tile the workgroup stages K (row-major) and V
+// (transposed, d-major) in LDS, with the next tile's global loads issued
+// before the current tile's math so their latency hides under it. Each wave
+// computes S^T = K Q^T on v_mfma_f32_16x16x32_bf16 (K from LDS as the A
+// operand, its Q fragments held in registers for the whole sweep), so a lane
+// holds 16 of its query's 64 scores: the online softmax needs two shuffles per
+// statistic, and P stays in registers as the B operand of O^T = V^T P^T
+// (the k order inside an MFMA step only has to agree between A and B). The
+// lane's output column is then its own query, so the softmax rescale needs no
+// exchange. Tiles past the diagonal are never visited; the diagonal tiles
+// mask keys past each row's position. Query tiles are dispatched longest
+// first.
 #include "wfd_common.h"
 
 namespace wfd {
 
-constexpr int kPfRows = 64;  // query rows per workgroup (4 waves x 16)
-constexpr int kPfKeys = 64;  // keys per tile
+constexpr int kPfWaves = 8;
+constexpr int kPfRows = 16 * kPfWaves;  // query rows per workgroup
+constexpr int kPfKeys = 64;             // keys per tile
 
 template <int DH>
-__global__ __launch_bounds__(256) void attn_prefill_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc,
-                                                           const bf16_t* __restrict__ vc, int64_t block_rows,
-                                                           const int64_t* __restrict__ seg_row_base,
-                                                           const int32_t* __restrict__ seg_q_start,
-                                                           const int32_t* __restrict__ seg_pos0,
-                                                           bf16_t* __restrict__ out, int H, int Hkv,
-                                                           float scale_log2) {
+__global__ __launch_bounds__(64 * kPfWaves) void attn_prefill_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc, const bf16_t* __restrict__ vc, int64_t block_rows,
+    const int64_t* __restrict__ seg_row_base, const int32_t* __restrict__ seg_q_start,
+    const int32_t* __restrict__ seg_pos0, bf16_t* __restrict__ out, int H, int Hkv, float scale_log2) {
+  constexpr int NT = 64 * kPfWaves;   // threads
   constexpr int V = 8;                // bf16 per 16-byte fragment
-  constexpr int NDS = DH / 32;        // MFMA k-steps over Dh (S = Q K^T)
-  constexpr int NCB = DH / 16;        // 16-column blocks of O
-  constexpr int NKB = kPfKeys / 16;   // 16-key column blocks of S
-  constexpr int NPS = kPfKeys / 32;   // MFMA k-steps over keys (O += P V)
+  constexpr int NDS = DH / 32;        // MFMA k-steps over Dh (S^T = K Q^T)
+  constexpr int NDB = DH / 16;        // 16-row blocks of O^T (head dim)
+  constexpr int NKB = kPfKeys / 16;   // 16-key blocks of S^T
+  constexpr int NPS = kPfKeys / 32;   // MFMA k-steps over keys (O^T += V^T P^T)
   constexpr int KP = DH + 8;          // padded LDS row of K (elements)
   constexpr int VP = kPfKeys + 8;     // padded LDS row of V^T
-  constexpr int PP = kPfKeys + 8;     // padded LDS row of P
-  constexpr int CPR = DH / V;         // 16-byte chunks per K/V row
+  constexpr int CPR = DH / V;         // 16-byte chunks per K row
+  constexpr int KCH = kPfKeys * CPR / NT;        // K chunks per thread per tile
+  constexpr int VUN = kPfKeys / 2 * CPR;         // V key-pair chunks per tile
+  constexpr int VCH = VUN >= NT ? VUN / NT : 1;   // ... per thread (Dh 64: waves 0-3 only)
+  static_assert(KCH >= 1 && kPfKeys * CPR % NT == 0 && (VUN % NT == 0 || NT % VUN == 0), "tile split");
+  static_assert(VUN >= NT || VUN % 64 == 0, "V staging must be wave-uniform");
   __shared__ __align__(16) bf16_t k_lds[kPfKeys * KP];
   __shared__ __align__(16) bf16_t vt_lds[DH * VP];
-  __shared__ __align__(16) bf16_t p_lds[4][16 * PP];
 
   const int s = blockIdx.z;
   const int h = blockIdx.y;
@@ -67,12 +74,13 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const bf16_t* __restr
   const int lane = threadIdx.x & 63;
   const int col = lane & 15;
   const int grp = lane >> 4;
-  const int row0 = tq * kPfRows + wave * 16;  // segment row of this wave's first query
+  const int row0 = tq * kPfRows + wave * 16;
   const int last_row = min((tq + 1) * kPfRows, len) - 1;
-  const int kv_hi = pos0 + last_row + 1;      // keys [0, kv_hi) cover every row of the tile
+  const int kv_hi = pos0 + last_row + 1;  // keys [0, kv_hi) cover every row of the tile
   const int ntiles = (kv_hi + kPfKeys - 1) / kPfKeys;
+  const int qpos = pos0 + row0 + col;      // this lane's query position (lane column = query)
 
-  // Q as the MFMA A operand: row col of this wave, k-group grp
+  // Q as the MFMA B operand: column col = query row0 + col, k-group grp
   u32x4 qf[NDS];
   {
     const int r = min(row0 + col, len - 1);
@@ -80,112 +88,140 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const bf16_t* __restr
 #pragma unroll
     for (int k = 0; k < NDS; ++k) qf[k] = ld16(qp + k * 32);
   }
-  float mrun[4], lrun[4];
-  f32x4 o[NCB];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    mrun[r] = -INFINITY;
-    lrun[r] = 0.f;
-  }
-#pragma unroll
-  for (int c = 0; c < NCB; ++c) o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int k0 = t * kPfKeys;
-    // stage the tile: K rows as they are, V transposed (d-major), keys past
-    // kv_hi clamped to the last one (masked below)
+  // staging: thread's K chunks (key, 8 dims) and V key-pair chunks (2 keys, 8 dims)
+  u32x4 kreg[KCH], vreg[VCH][2];
+  auto fetch = [&](int k0) {
 #pragma unroll
-    for (int c = threadIdx.x; c < kPfKeys * CPR; c += 256) {
+    for (int i = 0; i < KCH; ++i) {
+      const int c = threadIdx.x + i * NT;
       const int kr = c / CPR;
-      const int d0 = (c - kr * CPR) * V;
       const int key = min(k0 + kr, kv_hi - 1);
-      const u32x4 kv = ld16(kb + (int64_t)key * rs + d0);
-      const u32x4 vv = ld16(vb + (int64_t)key * rs + d0);
-      *reinterpret_cast<u32x4*>(&k_lds[kr * KP + d0]) = kv;
+      kreg[i] = ld16(kb + (int64_t)key * rs + (c - kr * CPR) * V);
+    }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        reinterpret_cast<uint16_t*>(vt_lds)[(d0 + 2 * e) * VP + kr] = (uint16_t)(vv[e] & 0xffffu);
-        reinterpret_cast<uint16_t*>(vt_lds)[(d0 + 2 * e + 1) * VP + kr] = (uint16_t)(vv[e] >> 16);
+    for (int i = 0; i < VCH; ++i) {
+      const int c = threadIdx.x + i * NT;
+      if (VUN < NT && c >= VUN) break;  // wave-uniform
+      const int kp = c / CPR;
+      const int d0 = (c - kp * CPR) * V;
+      const int key0 = min(k0 + 2 * kp, kv_hi - 1);
+      const int key1 = min(k0 + 2 * kp + 1, kv_hi - 1);
+      vreg[i][0] = ld16(vb + (int64_t)key0 * rs + d0);
+      vreg[i][1] = ld16(vb + (int64_t)key1 * rs + d0);
+    }
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int c = threadIdx.x + i * NT;
+      const int kr = c / CPR;
+      *reinterpret_cast<u32x4*>(&k_lds[kr * KP + (c - kr * CPR) * V]) = kreg[i];
+    }
+#pragma unroll
+    for (int i = 0; i < VCH; ++i) {
+      const int c = threadIdx.x + i * NT;
+      if (VUN < NT && c >= VUN) break;  // wave-uniform
+      const int kp = c / CPR;
+      const int d0 = (c - kp * CPR) * V;
+      uint32_t* vt = reinterpret_cast<uint32_t*>(vt_lds);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {  // dims d0 + 2e, d0 + 2e + 1: (key 2kp, key 2kp+1) pairs
+        const uint32_t a = vreg[i][0][e], b = vreg[i][1][e];
+        vt[((d0 + 2 * e) * VP + 2 * kp) >> 1] = (a & 0xffffu) | (b << 16);
+        vt[((d0 + 2 * e + 1) * VP + 2 * kp) >> 1] = (a >> 16) | (b & 0xffff0000u);
       }
     }
-    __syncthreads();
+  };
 
-    // S = Q K^T: lane holds S[4*grp + r][16*cb + col]
+  float mrun = -INFINITY, lrun = 0.f;
+  f32x4 o[NDB];
+#pragma unroll
+  for (int c = 0; c < NDB; ++c) o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  fetch(0);
+  for (int t = 0; t < ntiles; ++t) {
+    const int k0 = t * kPfKeys;
+    stage();
+    __syncthreads();
+    fetch(k0 + kPfKeys);  // next tile (clamped past the end): in flight under this tile's math
+
+    // S^T = K Q^T: lane holds S[query col][key k0 + 16*cb + 4*grp + r]
     f32x4 sacc[NKB];
 #pragma unroll
     for (int cb = 0; cb < NKB; ++cb) {
       sacc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int k = 0; k < NDS; ++k) {
-        const u32x4 bfr = *reinterpret_cast<const u32x4*>(&k_lds[(16 * cb + col) * KP + 32 * k + grp * V]);
-        sacc[cb] = mfma_step<bf16_t>(qf[k], bfr, sacc[cb]);
+        const u32x4 afr = *reinterpret_cast<const u32x4*>(&k_lds[(16 * cb + col) * KP + 32 * k + grp * V]);
+        sacc[cb] = mfma_step<bf16_t>(afr, qf[k], sacc[cb]);
       }
     }
-    // online softmax over this tile, one row per (grp, r)
-    float corr[4];
+    float mt = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int qpos = pos0 + row0 + 4 * grp + r;
-      float mt = -INFINITY;
+    for (int cb = 0; cb < NKB; ++cb)
 #pragma unroll
-      for (int cb = 0; cb < NKB; ++cb) {
-        const bool ok = k0 + 16 * cb + col <= qpos;
+      for (int r = 0; r < 4; ++r) {
+        const bool ok = k0 + 16 * cb + 4 * grp + r <= qpos;
         const float sv = ok ? sacc[cb][r] * scale_log2 : -INFINITY;
         sacc[cb][r] = sv;
         mt = fmaxf(mt, sv);
       }
+    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float mnew = fmaxf(mrun, mt);
+    const float corr = (mrun == -INFINITY) ? 0.f : exp2f(mrun - mnew);
+    float lt = 0.f;
 #pragma unroll
-      for (int m = 8; m >= 1; m >>= 1) mt = fmaxf(mt, __shfl_xor(mt, m, 64));
-      const float mnew = fmaxf(mrun[r], mt);
-      corr[r] = (mrun[r] == -INFINITY) ? 0.f : exp2f(mrun[r] - mnew);
-      float lt = 0.f;
+    for (int cb = 0; cb < NKB; ++cb)
 #pragma unroll
-      for (int cb = 0; cb < NKB; ++cb) {
+      for (int r = 0; r < 4; ++r) {
         const float p = (sacc[cb][r] == -INFINITY) ? 0.f : exp2f(sacc[cb][r] - mnew);
         sacc[cb][r] = p;
         lt += p;
       }
-#pragma unroll
-      for (int m = 8; m >= 1; m >>= 1) lt += __shfl_xor(lt, m, 64);
-      lrun[r] = fmaf(lrun[r], corr[r], lt);
-      mrun[r] = mnew;
-    }
-    // P (bf16) into this wave's LDS rows, then back as A fragments (row col,
-    // keys 32*k + 8*grp .. +7)
-    uint16_t* pw = reinterpret_cast<uint16_t*>(p_lds[wave]);
-#pragma unroll
-    for (int cb = 0; cb < NKB; ++cb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) pw[(4 * grp + r) * PP + 16 * cb + col] = f32_to_bf16_bits(sacc[cb][r]);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    u32x4 pa[NPS];
-#pragma unroll
-    for (int k = 0; k < NPS; ++k) pa[k] = *reinterpret_cast<const u32x4*>(&pw[col * PP + 32 * k + grp * V]);
+    lt += __shfl_xor(lt, 16, 64);
+    lt += __shfl_xor(lt, 32, 64);
+    lrun = fmaf(lrun, corr, lt);
+    mrun = mnew;
 
-    // O = O * corr + P V: lane holds O[4*grp + r][16*cb + col]
+    // P^T as the B operand of step k: keys k0 + 32k + 4grp + (0..3) then
+    // k0 + 32k + 16 + 4grp + (0..3) -- the order the V^T fragments use below
+    u32x4 pb[NPS];
 #pragma unroll
-    for (int cb = 0; cb < NCB; ++cb) {
+    for (int k = 0; k < NPS; ++k) {
+      pb[k][0] = f32x2_to_bf16x2_bits(sacc[2 * k][0], sacc[2 * k][1]);
+      pb[k][1] = f32x2_to_bf16x2_bits(sacc[2 * k][2], sacc[2 * k][3]);
+      pb[k][2] = f32x2_to_bf16x2_bits(sacc[2 * k + 1][0], sacc[2 * k + 1][1]);
+      pb[k][3] = f32x2_to_bf16x2_bits(sacc[2 * k + 1][2], sacc[2 * k + 1][3]);
+    }
+    // O^T = O^T * corr + V^T P^T: lane holds O[query col][d = 16*db + 4*grp + r]
 #pragma unroll
-      for (int r = 0; r < 4; ++r) o[cb][r] *= corr[r];
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[db][r] *= corr;
 #pragma unroll
       for (int k = 0; k < NPS; ++k) {
-        const u32x4 bfr = *reinterpret_cast<const u32x4*>(&vt_lds[(16 * cb + col) * VP + 32 * k + grp * V]);
-        o[cb] = mfma_step<bf16_t>(pa[k], bfr, o[cb]);
+        const bf16_t* vr = &vt_lds[(16 * db + col) * VP + 32 * k + 4 * grp];
+        const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+        const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
+        const u32x4 afr = {lo.x, lo.y, hi.x, hi.y};
+        o[db] = mfma_step<bf16_t>(afr, pb[k], o[db]);
       }
     }
     __syncthreads();  // K / V^T are restaged by the next tile
   }
 
+  const int row = row0 + col;
+  if (row < len) {
+    const float inv = lrun > 0.f ? 1.f / lrun : 0.f;
+    bf16_t* op = out + ((int64_t)(q0 + row) * H + h) * DH + 4 * grp;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int row = row0 + 4 * grp + r;
-    if (row < len) {
-      bf16_t* op = out + ((int64_t)(q0 + row) * H + h) * DH + col;
-#pragma unroll
-      for (int cb = 0; cb < NCB; ++cb)
-        Elem<bf16_t>::store(op + 16 * cb, lrun[r] > 0.f ? o[cb][r] / lrun[r] : 0.f);
+    for (int db = 0; db < NDB; ++db) {
+      uint2 w;
+      w.x = f32x2_to_bf16x2_bits(o[db][0] * inv, o[db][1] * inv);
+      w.y = f32x2_to_bf16x2_bits(o[db][2] * inv, o[db][3] * inv);
+      *reinterpret_cast<uint2*>(op + 16 * db) = w;
     }
   }
 }
@@ -212,13 +248,14 @@ int wfd_attn_prefill(const void* q, const void* k_cache, const void* v_cache, in
     return kUnsupported;
   }
   const dim3 grid((max_seg_len + kPfRows - 1) / kPfRows, H, nseg);
+  const dim3 block(64 * kPfWaves);
   const float sl2 = scale * 1.4426950408889634f;
   if (Dh == 64)
-    hipLaunchKernelGGL(attn_prefill_kernel<64>, grid, dim3(256), 0, stream, (const bf16_t*)q, (const bf16_t*)k_cache,
+    hipLaunchKernelGGL(attn_prefill_kernel<64>, grid, block, 0, stream, (const bf16_t*)q, (const bf16_t*)k_cache,
                        (const bf16_t*)v_cache, kv_block_rows, seg_row_base, seg_q_start, seg_pos0, (bf16_t*)out, H,
                        Hkv, sl2);
   else
-    hipLaunchKernelGGL(attn_prefill_kernel<128>, grid, dim3(256), 0, stream, (const bf16_t*)q,
+    hipLaunchKernelGGL(attn_prefill_kernel<128>, grid, block, 0, stream, (const bf16_t*)q,
                        (const bf16_t*)k_cache, (const bf16_t*)v_cache, kv_block_rows, seg_row_base, seg_q_start,
                        seg_pos0, (bf16_t*)out, H, Hkv, sl2);
   return launch_status("wfd_attn_prefill");
