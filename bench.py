@@ -16,8 +16,10 @@ measured acceptance rate) and sequentially (AR); bs=32 with ragged prompts
 U[128, 2048] and generation lengths U[64, 512] at emulated alpha 0.5 / 0.7 /
 0.9; the wavefront attention op alone (bf16, 16 heads x 64, W=8,
 L in {1k, 4k, 16k}) and at the decode shapes; a long-context GQA decode tick
-(16 q / 4 kv heads, B=4, 32k context, W=16) over random-filled KV; the
-roofline of the dominant kernel; and the CPU oracle's throughput on a
+(16 q / 4 kv heads, B=4, 32k context, W=16) over random-filled KV; causal
+prefill attention on MFMA (TFLOP/s and fraction of the bf16 peak) and the
+bs=1 prompt's prefill time; the roofline of the dominant kernel; and the CPU
+oracle's throughput on a
 bounded sample of the bs=1 workload on this host's cores.
 """
 from __future__ import annotations
@@ -35,6 +37,7 @@ sys.path.insert(0, REPO)
 
 HBM_PEAK_GBS = 8000.0
 MALL_BYTES = 256e6
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA, MI355X
 
 
 def log(msg: str) -> None:
@@ -48,7 +51,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--quick", action="store_true", help="fewer extras (development)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--only", default="", help="comma list of sections: bs1,roofline,attn,bs32,gqa,cpu")
+    ap.add_argument("--only", default="", help="comma list of sections: bs1,roofline,attn,bs32,prefill,gqa,cpu")
     ap.add_argument("--eager", action="store_true", help="launch every pass eagerly (no hipGraph capture)")
     return ap.parse_args()
 
@@ -305,6 +308,51 @@ def gqa_section(args, dev, res):
     torch.cuda.empty_cache()
 
 
+def prefill_section(args, dev, res):
+    """Causal prefill attention on MFMA (bf16): one prompt per call, all heads,
+    timed with HIP events; TFLOP/s counts 4*H*Dh flops per (query, key) pair
+    of the causal triangle (QK^T and PV), against 2.5 PFLOP/s dense bf16. Also
+    the whole-model prefill of the bs=1 prompt."""
+    import torch
+    from wavefront_decoding_amd import model as M
+    from wavefront_decoding_amd import ops
+    from wavefront_decoding_amd.engine import LoopedModel
+
+    out = {}
+    for name, H, Hkv, Dh, L in [("mha_L2048", 16, 16, 128, 2048), ("gqa_L32768", 16, 4, 128, 32768)]:
+        g = torch.Generator(device=dev).manual_seed(0)
+        K = torch.randn(1, Hkv, L, Dh, device=dev, generator=g).to(torch.bfloat16)
+        V = torch.randn(1, Hkv, L, Dh, device=dev, generator=g).to(torch.bfloat16)
+        q = torch.randn(L, H, Dh, device=dev, generator=g).to(torch.bfloat16)
+        rb = torch.zeros(1, dtype=torch.int64, device=dev)
+        qs = torch.tensor([0, L], dtype=torch.int32, device=dev)
+        p0 = torch.zeros(1, dtype=torch.int32, device=dev)
+        o = torch.empty_like(q)
+        call = lambda i: ops.attn_prefill(q, K, V, rb, qs, p0, max_seg_len=L, out=o)  # noqa: E731
+        call(0)
+        torch.cuda.synchronize()
+        iters = 5 if L > 8192 else 40
+        us = timed(call, iters) * 1e3
+        flops = 4.0 * H * Dh * L * (L + 1) / 2
+        out[name] = {"us": round(us, 1), "TFLOPs": round(flops / us / 1e6, 1),
+                     "frac_of_bf16_peak": round(flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4)}
+        del K, V, q, o
+    res["extra"]["prefill_attention"] = out
+    cfg = M.CONFIGS["looped-2048"]
+    m = LoopedModel(cfg, M.init_weights(cfg, 0), dev, max_seq_len=640, max_batch=1)
+    cache = m.create_cache(1)
+    ids = torch.randint(0, cfg.vocab_size, (512,), generator=torch.Generator().manual_seed(0)).tolist()
+    m.prefill_seq(cache, 0, ids)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    m.prefill_seq(cache, 0, ids)
+    torch.cuda.synchronize()
+    res["extra"]["prefill_bs1_prompt_ms"] = round((time.perf_counter() - t0) * 1e3, 2)
+    log(f"prefill: {out}; bs1 prompt (512 tokens, 68 layer passes) {res['extra']['prefill_bs1_prompt_ms']} ms")
+    del m, cache
+    torch.cuda.empty_cache()
+
+
 def roofline_section(args, dev, res):
     """Dominant kernel of the decode tick: the weight-stream linear. The
     headline figure is its largest stream, the gate|up projection with the
@@ -436,6 +484,8 @@ def main():
         attn_section(args, dev, res)
     if want("bs32") and not args.quick:
         bs32_section(args, dev, res, w)
+    if want("prefill"):
+        prefill_section(args, dev, res)
     if want("gqa"):
         gqa_section(args, dev, res)
     if want("cpu") and not args.no_cpu:
