@@ -6,8 +6,8 @@ parcae-free scheduler modules file by file -- src/decoding/scheduler_batch.py
 and what it imports (batch_state, emu, policy, state, scheduler, blocks,
 acceptance) -- under a private package name, bypassing
 src/decoding/__init__.py (which imports the un-vendored parcae_lm), and drives
-generate_wavefront_batch / ar_generate_batch with the deterministic stub model
-of stub_model.py. The recorded vectors (tokens, counters, union sizes,
+generate_wavefront_batch / ar_generate_batch / generate_dtv_batch with the
+deterministic stub model of stub_model.py. The recorded vectors (tokens, counters, union sizes,
 rollbacks, the per-call (seq, pos, step) schedule, emulated draws) land in
 scheduler_traces.json next to this script.
 
@@ -50,9 +50,10 @@ CASES = dict(
 
 def main() -> None:
     sb, emu_mod, pol_mod = load_reference()
-    out = {"source": "reference src/decoding/scheduler_batch.py generate_wavefront_batch / ar_generate_batch",
+    out = {"source": "reference src/decoding/scheduler_batch.py generate_wavefront_batch / ar_generate_batch / "
+                     "generate_dtv_batch",
            "stub": "tests/golden/stub_model.py (vocab=50, agree_pct=70, salt=0), prompt length 5",
-           "wfd": [], "ar": []}
+           "wfd": [], "ar": [], "dtv": []}
     for B, (T_total, T_draft), N, alpha in itertools.product(*CASES.values()):
         blocks = StubBatchBlocks(T_total, B)
         prompts = stub_prompts(B, 5)
@@ -71,10 +72,22 @@ def main() -> None:
         rec = trace_record(bt, blocks, blocks.last_cache, None)
         rec.update(B=B, T_total=T_total, max_new_tokens=N)
         out["ar"].append(rec)
+    for B, (T_total, T_draft), K, N, alpha in itertools.product(
+            (1, 3), ((4, 1), (4, 2), (8, 2)), (1, 3), (1, 2, 9, 33), (None, 0.0, 0.5, 1.0)):
+        blocks = StubBatchBlocks(T_total, B)
+        emus = None if alpha is None else [emu_mod.EmulatedAcceptance(alpha, seed=1000 + b) for b in range(B)]
+        policy = pol_mod.SsdPolicy(T_total=T_total, T_draft=T_draft)
+        bt = sb.generate_dtv_batch(blocks, stub_prompts(B, 5), N, policy, K, emus)
+        rec = trace_record(bt, blocks, blocks.last_cache, emus)
+        if N > 9:
+            rec["calls"] = None
+        rec.update(B=B, T_total=T_total, T_draft=T_draft, draft_length=K, max_new_tokens=N, alpha=alpha)
+        out["dtv"].append(rec)
     path = os.path.join(HERE, "scheduler_traces.json")
     with open(path, "w") as f:
         json.dump(out, f, separators=(",", ":"))
-    print(f"wrote {len(out['wfd'])} wfd + {len(out['ar'])} ar traces -> {path} ({os.path.getsize(path)} bytes)")
+    print(f"wrote {len(out['wfd'])} wfd + {len(out['ar'])} ar + {len(out['dtv'])} dtv traces -> {path} "
+          f"({os.path.getsize(path)} bytes)")
 
 
 if __name__ == "__main__":

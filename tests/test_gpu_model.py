@@ -26,7 +26,7 @@ from wavefront_decoding_amd.emu import EmulatedAcceptance
 from wavefront_decoding_amd.engine import LoopedModel
 from wavefront_decoding_amd.policy import SsdPolicy
 from wavefront_decoding_amd.scheduler import generate_wavefront_dynamic
-from wavefront_decoding_amd.scheduler_batch import ar_generate_batch, generate_wavefront_batch
+from wavefront_decoding_amd.scheduler_batch import ar_generate_batch, generate_dtv_batch, generate_wavefront_batch
 
 pytestmark = pytest.mark.gpu
 
@@ -246,5 +246,49 @@ def test_token_handles_match_eager_ids(gpu, graphs):
         bt = generate_wavefront_batch(blk, [p.to(gpu) for p in P], [12, 9, 15], SsdPolicy(cfg.T_total, 2), emus)
         ar = ar_generate_batch(blk, [p.to(gpu) for p in P], [6, 8, 5])
         res.append(([(t.tokens, t.counters()) for t in bt.per_seq], [t.tokens for t in ar.per_seq]))
+        assert all(v >= 0 for t in bt.per_seq for v in t.tokens)
+    assert res[0] == res[1]
+
+
+@pytest.mark.parametrize("cfg", [TINY, MINI_BF16, MINI_GQA], ids=lambda c: c.name)
+def test_dtv_is_lossless(gpu, cfg):
+    """Draft-then-verify (single sequence and batch, ragged) commits exactly
+    the sequential tokens: every committed token is a full-depth argmax and
+    every kernel is row-invariant, so verify rows equal sequential rows bit
+    for bit."""
+    from wavefront_decoding_amd.scheduler import generate_draft_then_verify
+
+    w = M.init_weights(cfg, 0)
+    model = LoopedModel(cfg, w, gpu, max_seq_len=256, max_batch=3)
+    blocks = LoopedBlocks(model)
+    ids = _prompt(70, 8, V=cfg.vocab_size).to(gpu)
+    print(f"[{cfg.name}] dtv lossless", flush=True)
+    ar, _ = blocks.ar_generate(ids, 24)
+    for T_draft, K in ((1, 3), (2, 2), (4, 1)):
+        toks, tr = generate_draft_then_verify(blocks, ids, 24, SsdPolicy(cfg.T_total, T_draft), K)
+        assert toks == ar, (T_draft, K)
+        assert tr.n_drafts_proposed > 0
+    P = [_prompt(40, 4, V=cfg.vocab_size), _prompt(25, 5, V=cfg.vocab_size), _prompt(33, 6, V=cfg.vocab_size)]
+    N = [11, 7, 13]
+    bb = LoopedBlocksBatch(model, batch_size=3)
+    bt = generate_dtv_batch(bb, [p.to(gpu) for p in P], N, SsdPolicy(cfg.T_total, 2), 3)
+    ab = ar_generate_batch(bb, [p.to(gpu) for p in P], N)
+    assert [t.tokens for t in bt.per_seq] == [t.tokens for t in ab.per_seq]
+
+
+def test_dtv_token_handles_match_eager_ids(gpu):
+    """Emulated-acceptance DtV keeps every id on the device (drafts feed the
+    next source's prelude as ring handles) and still commits the ids an
+    eager read-back run commits."""
+    cfg = TINY
+    w = M.init_weights(cfg, 0)
+    P = [_prompt(40, 4), _prompt(25, 5), _prompt(33, 6)]
+    res = []
+    for handles in (True, False):
+        bb = LoopedBlocksBatch(LoopedModel(cfg, w, gpu, max_seq_len=128, max_batch=3))
+        blk = bb if handles else _NoHandles(bb)
+        emus = [EmulatedAcceptance(0.6, 3000 + b) for b in range(3)]
+        bt = generate_dtv_batch(blk, [p.to(gpu) for p in P], [12, 9, 15], SsdPolicy(cfg.T_total, 2), 3, emus)
+        res.append([(t.tokens, t.counters()) for t in bt.per_seq])
         assert all(v >= 0 for t in bt.per_seq for v in t.tokens)
     assert res[0] == res[1]

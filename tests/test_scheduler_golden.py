@@ -2,7 +2,7 @@
 
 tests/golden/scheduler_traces.json was produced by
 tests/golden/make_scheduler_traces.py running the reference's
-generate_wavefront_batch / ar_generate_batch over the stub model of
+generate_wavefront_batch / ar_generate_batch / generate_dtv_batch over the stub model of
 tests/golden/stub_model.py. Both this repo's product schedulers and the
 oracle's restatement must reproduce every trace exactly: committed tokens,
 per-sequence and global counters, union sizes, rollback calls, the per-call
@@ -54,6 +54,36 @@ def test_oracle_wfd_batch_matches_reference_trace(ref):
     if ref["calls"] is None:
         got["calls"] = None
     assert got == _strip(ref)
+
+
+def _dtv_id(r):
+    return f"B{r['B']}-T{r['T_total']}/{r['T_draft']}-K{r['draft_length']}-N{r['max_new_tokens']}-a{r['alpha']}"
+
+
+@pytest.mark.parametrize("ref", GOLDEN["dtv"], ids=_dtv_id)
+def test_product_dtv_batch_matches_reference_trace(ref):
+    """Draft-then-verify: the same rounds, drafts, verify cascades, bonus
+    tokens, rollbacks and per-tick unions as the reference's generate_dtv_batch."""
+    blocks = StubBatchBlocks(ref["T_total"], ref["B"])
+    emus = None if ref["alpha"] is None else [EmulatedAcceptance(ref["alpha"], seed=1000 + b) for b in range(ref["B"])]
+    bt = sb.generate_dtv_batch(blocks, stub_prompts(ref["B"], 5), ref["max_new_tokens"],
+                               SsdPolicy(T_total=ref["T_total"], T_draft=ref["T_draft"]), ref["draft_length"], emus)
+    got = trace_record(bt, blocks, blocks.last_cache, emus)
+    if ref["calls"] is None:
+        got["calls"] = None
+    want = {k: v for k, v in _strip(ref).items() if k != "draft_length"}
+    assert got == want
+
+
+def test_reference_dtv_traces_are_lossless():
+    """On the golden data itself: DtV with real comparisons commits exactly
+    the sequential (AR) stub tokens -- verify runs every source to full depth."""
+    for ref in GOLDEN["dtv"]:
+        if ref["alpha"] is not None:
+            continue
+        blocks = StubBatchBlocks(ref["T_total"], ref["B"])
+        bt = sb.ar_generate_batch(blocks, stub_prompts(ref["B"], 5), ref["max_new_tokens"])
+        assert [list(t.tokens) for t in bt.per_seq] == [p["tokens"] for p in ref["per_seq"]], _dtv_id(ref)
 
 
 @pytest.mark.parametrize("ref", GOLDEN["ar"], ids=_case_id)

@@ -21,11 +21,12 @@ from tests.golden.stub_model import StubBatchBlocks, stub_prompts
 from wavefront_decoding_amd.acceptance import RowLogits
 from wavefront_decoding_amd.blocks import LoopedBlocks
 from wavefront_decoding_amd.policy import SsdPolicy
-from wavefront_decoding_amd.scheduler import generate_wavefront_dynamic
+from wavefront_decoding_amd.scheduler import generate_draft_then_verify, generate_wavefront_dynamic
 from wavefront_decoding_amd.state import WavefrontState
 
 GOLDEN = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "scheduler_traces.json")))
 B1 = [r for r in GOLDEN["wfd"] if r["B"] == 1 and r["alpha"] is None]
+B1_DTV = [r for r in GOLDEN["dtv"] if r["B"] == 1 and r["alpha"] is None]
 
 
 class _SingleCache:
@@ -132,3 +133,21 @@ def test_policy_validation():
         SsdPolicy(mode="temperature")
     with pytest.warns(UserWarning):
         SsdPolicy(T_total=5, T_draft=2)
+
+
+@pytest.mark.parametrize("ref", B1_DTV,
+                         ids=lambda r: f"T{r['T_total']}/{r['T_draft']}-K{r['draft_length']}-N{r['max_new_tokens']}")
+def test_dtv_single_matches_batch_b1_trace(ref):
+    """Single-sequence draft-then-verify reproduces the reference batch DtV's
+    B = 1 trace with real greedy comparisons: tokens, counters, rollbacks and
+    the per-call schedule."""
+    blocks = StubSingleBlocks(ref["T_total"])
+    toks, trace = generate_draft_then_verify(blocks, stub_prompts(1, 5)[0], ref["max_new_tokens"],
+                                             SsdPolicy(T_total=ref["T_total"], T_draft=ref["T_draft"]),
+                                             ref["draft_length"])
+    per = ref["per_seq"][0]
+    assert toks == per["tokens"]
+    assert trace.counters() == _counters(per)
+    assert [list(d) for d in blocks.stub.last_cache.drops] == ref["drops"]
+    if ref["calls"] is not None:
+        assert [[k, [list(x) for x in rows]] for k, rows in blocks.stub.calls] == ref["calls"]

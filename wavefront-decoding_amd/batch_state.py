@@ -21,6 +21,19 @@ class SeqState:
     active_p: list[ActiveToken] = field(default_factory=list)
     active_r: list[ActiveToken] = field(default_factory=list)
     active_c: list[ActiveToken] = field(default_factory=list)
+    # draft-then-verify round (src/decoding/batch_state.py:44-56): phase is
+    # "need_p" (the next source needs its embedding), "draft" (the current
+    # source runs depths 0..T_draft) or "verify" (all K+1 sources run on to
+    # T_total); K drafts this round, j = index of the current source
+    phase: str = "need_p"
+    K: int = 0
+    j: int = 0
+    sources: list[ActiveToken] = field(default_factory=list)
+    drafts: list[int] = field(default_factory=list)
+    cur_tok: int = 0
+    cur_pos: int = 0
+    last_token: int = 0
+    p: int = 0
 
     def commit(self, token_id: int) -> None:
         self.committed.append(token_id)
@@ -42,3 +55,5 @@ class SeqState:
 
     def clear_working_state(self) -> None:
         self.active_p, self.active_r, self.active_c = [], [], []
+        self.sources, self.drafts = [], []
+        self.phase = "idle"

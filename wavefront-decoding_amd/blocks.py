@@ -52,6 +52,9 @@ class RecursiveBlocks(ABC):
     def prelude_forward(self, cache, token_id: int, position: int): ...
 
     @abstractmethod
+    def prelude_tokens(self, cache, toks: list) -> None: ...
+
+    @abstractmethod
     def advance_one_step(self, toks: list, cache) -> None: ...
 
     @abstractmethod
@@ -109,6 +112,15 @@ class LoopedBlocks(RecursiveBlocks):
         for t, r in zip(toks, rows.tolist()):
             t.row = r
             t.step = 0
+
+    @property
+    def max_in_flight(self) -> int:
+        """Tokens of one sequence that may be in flight at once (wave-state pool rows per sequence)."""
+        return self.model.R
+
+    def prelude_tokens(self, cache, toks: list[ActiveToken]) -> None:
+        """Prelude these tokens (each gets its wave-state pool row, step 0)."""
+        self._prelude(cache, toks)
 
     def prelude_forward(self, cache, token_id: int, position: int):
         """Prelude one token; returns (hidden, static_state) device views of its pool row."""
@@ -253,6 +265,11 @@ class LoopedBlocksBatch:
         last = torch.stack([self.model.prefill_seq(cache, b, torch.as_tensor(s).reshape(-1).tolist())
                             for b, s in enumerate(seqs)])
         return cache, last
+
+    @property
+    def max_in_flight(self) -> int:
+        """Tokens of one sequence that may be in flight at once (wave-state pool rows per sequence)."""
+        return self.model.R
 
     @torch.no_grad()
     def prelude_union(self, seq_ids, toks, cache) -> None:

@@ -137,3 +137,90 @@ def _finish(trace: GenerationTrace, device, t0: float, warm: float | None):
     trace.walltime_s = t1 - t0
     trace.walltime_steady_s = (t1 - warm) if warm is not None else trace.walltime_s
     return list(trace.tokens), trace
+
+
+@torch.no_grad()
+def generate_draft_then_verify(blocks, prompt_ids: torch.Tensor, max_new_tokens: int, policy: SsdPolicy,
+                               draft_length: int, eos_token_id: int | None = None
+                               ) -> tuple[list[int], GenerationTrace]:
+    """Greedy draft-then-verify with nested reuse for one sequence
+    (src/decoding/scheduler.py:227-367). Each round forwards sources p..p+K one
+    after another at the shallow depth T_draft (a source's shallow argmax is
+    the next source's token and the draft for its position), then continues
+    all K+1 sources together to T_total -- the shallow recurrence is the prefix
+    of the full one, nothing is recomputed -- and verifies the drafts in order
+    against the full-depth argmaxes: the first mismatch commits the gold token
+    and drops every slot row from there on; if all K match, the last source's
+    gold is a free bonus token. Lossless: every committed token is a
+    full-depth argmax. Stops at max_new_tokens or a committed eos_token_id."""
+    if draft_length < 1 or draft_length + 1 > getattr(blocks, "max_in_flight", draft_length + 1):
+        raise ValueError(f"draft_length={draft_length}: a round keeps draft_length + 1 sources in flight, "
+                         f"at most {getattr(blocks, 'max_in_flight', '?')} fit")
+    trace = GenerationTrace()
+    device = prompt_ids.device
+    sampler = policy.make_sampler()
+    t0 = time.perf_counter()
+    state, last_logits = blocks.prefill(prompt_ids.reshape(1, -1), T_total=policy.T_total, T_draft=policy.T_draft)
+    cache = state.kv_cache
+    first = sampler(last_logits, state.prefix_len)
+    state.committed.append(first)
+    state.last_committed_position = state.prefix_len
+    trace.tokens.append(first)
+    warm = None
+
+    def commit(tok: int, pos: int) -> bool:
+        state.committed.append(tok)
+        state.last_committed_position = pos
+        trace.tokens.append(tok)
+        return len(state.committed) >= max_new_tokens or (eos_token_id is not None and tok == eos_token_id)
+
+    stop = len(state.committed) >= max_new_tokens or (eos_token_id is not None and first == eos_token_id)
+    p, last = state.prefix_len, first
+    while not stop:
+        K = min(draft_length, max_new_tokens - len(state.committed))
+        # draft: sources p..p+K at depths 0..T_draft, autoregressively
+        sources, drafts = [], []
+        tok, pos = last, p
+        for j in range(K + 1):
+            src = ActiveToken(token_id=tok, position=pos, role="verify")
+            blocks.prelude_tokens(cache, [src])
+            trace.n_p_calls += 1
+            for _ in range(policy.T_draft):
+                blocks.advance_one_step([src], cache)
+                trace.n_r_calls += 1
+            sources.append(src)
+            nxt, _ = sampler.draft(blocks.coda_logits(state, [src])[0], pos + 1)
+            trace.n_c_calls += 1
+            if j < K:
+                drafts.append(nxt)
+            tok, pos = nxt, pos + 1
+        # verify: all sources from T_draft to T_total together
+        for _ in range(policy.T_total - policy.T_draft):
+            blocks.advance_one_step(sources, cache)
+            trace.n_r_calls += 1
+        golds = blocks.coda_logits(state, sources)
+        trace.n_c_calls += 1
+        rejected = False
+        for i in range(K):
+            ok, gold = sampler.verify(drafts[i], None, golds[i], p + i + 1)
+            trace.n_drafts_proposed += 1
+            if ok:
+                trace.n_drafts_accepted += 1
+                if commit(drafts[i], p + i + 1):
+                    stop = True
+                    break
+            else:
+                trace.n_drafts_rejected += 1
+                trace.n_rollback_events += 1
+                rejected = True
+                stop = commit(gold, p + i + 1)
+                cache.drop_positions_at_and_after(p + i + 1)
+                last, p = gold, p + i + 1
+                break
+        if not rejected and not stop:
+            bonus = sampler(golds[K], p + K + 1)
+            stop = commit(bonus, p + K + 1)
+            last, p = bonus, p + K + 1
+        if warm is None:
+            warm = time.perf_counter()
+    return _finish(trace, device, t0, warm)

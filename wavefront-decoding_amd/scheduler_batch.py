@@ -320,3 +320,138 @@ def generate_wavefront_batch(blocks, prompt_ids, max_new_tokens, policy: SsdPoli
                 s.trace.n_p_calls += 1
             s.active_c = []
     return _finish(bt, seqs, t0, device, cache, blocks, lazy)
+
+
+def _dtv_round(s: SeqState, draft_length: int) -> None:
+    """Open a draft-then-verify round from the last committed token (at s.p)."""
+    s.K = min(draft_length, s.max_new_tokens - len(s.committed))
+    s.j = 0
+    s.sources, s.drafts = [], []
+    s.cur_tok, s.cur_pos = s.last_token, s.p
+    s.phase = "need_p"
+
+
+@torch.no_grad()
+def generate_dtv_batch(blocks, prompt_ids, max_new_tokens, policy: SsdPolicy, draft_length: int, emus=None,
+                       prefilled: SharedPrefill | None = None) -> BatchTrace:
+    """Draft-then-verify with nested reuse, one round state machine per
+    sequence (src/decoding/scheduler_batch.py:368-505).
+
+    A round drafts K tokens: sources p, p+1, ..., p+K each run P and the
+    shallow depths 0..T_draft one after another (a source's shallow argmax is
+    the next source's token), then all K+1 sources continue together from
+    T_draft to T_total -- the draft's recurrence is the prefix of the
+    verify's, nothing is recomputed -- and their full-depth argmaxes verify
+    the drafts in order: the first rejected draft commits the gold token and
+    rolls the sequence back past it; if all K are accepted the last source's
+    gold is a free bonus token. Sequences desync freely: P, R and C run once
+    per tick over the union of what every live sequence needs."""
+    if draft_length < 1 or draft_length + 1 > getattr(blocks, "max_in_flight", draft_length + 1):
+        raise ValueError(f"draft_length={draft_length}: a round keeps draft_length + 1 sources in flight, "
+                         f"at most {getattr(blocks, 'max_in_flight', '?')} fit")
+    device = _device_of(prompt_ids)
+    if device.type == "cuda":
+        torch.cuda.reset_peak_memory_stats()
+    bt = BatchTrace()
+    cache, seqs, t0 = _start(blocks, prompt_ids, emus, max_new_tokens, bt, time.perf_counter(), prefilled)
+    T_total, T_draft = policy.T_total, policy.T_draft
+    lazy = emus is not None and all(e is not None for e in emus) and _lazy_tokens(blocks)
+    for s in seqs:
+        if not s.done:
+            s.last_token, s.p = s.committed[-1], s.prefix_len
+            _dtv_round(s, draft_length)
+
+    max_new = max(s.max_new_tokens for s in seqs)
+    ticks, guard = 0, max_new * ((draft_length + 1) * max(T_draft, 1) + T_total + 4) + 100
+    while True:
+        live = [s for s in seqs if not s.done]
+        if not live:
+            break
+        ticks += 1
+        if ticks > guard:
+            raise RuntimeError(f"dtv batch exceeded tick guard ({guard}) -- scheduler bug?")
+
+        # P: each sequence whose next source needs its embedding
+        pneed = [s for s in live if s.phase == "need_p"]
+        if pneed:
+            new = []
+            for s in pneed:
+                t = ActiveToken(token_id=s.cur_tok, position=s.cur_pos, role="verify")
+                s.sources.append(t)
+                new.append(t)
+                s.trace.n_p_calls += 1
+                s.phase = "draft"
+            blocks.prelude_union([s.idx for s in pneed], new, cache)
+            bt.n_p_calls += 1
+
+        # R: a drafting sequence advances its current source, a verifying one all K+1
+        r_pairs, moved = [], []
+        for s in live:
+            if s.phase == "draft":
+                r_pairs.append((s, s.sources[-1]))
+                moved.append(s)
+            elif s.phase == "verify" and s.sources[0].step < T_total:
+                r_pairs += [(s, t) for t in s.sources]
+                moved.append(s)
+        if r_pairs:
+            blocks.advance_union([s.idx for s, _ in r_pairs], [t for _, t in r_pairs], cache)
+            _record_r(bt, len(r_pairs))
+            for s in moved:
+                s.trace.n_r_calls += 1
+
+        # C: a draft source that reached T_draft, or all sources at T_total
+        entries = []
+        for s in live:
+            if s.phase == "draft" and s.sources[-1].step == T_draft:
+                entries.append((s, "draft", [s.sources[-1]]))
+            elif s.phase == "verify" and s.sources[0].step == T_total:
+                entries.append((s, "verify", list(s.sources)))
+        if not entries:
+            continue
+        c_toks = [t for _, _, ts in entries for t in ts]
+        c_ids = [s.idx for s, _, ts in entries for _ in ts]
+        out = (blocks.coda_argmax_union(c_ids, c_toks, cache, lazy=True) if lazy
+               else blocks.coda_argmax_union(c_ids, c_toks, cache))
+        bt.n_c_calls += 1
+        k = 0
+        for s, kind, ts in entries:
+            ids = out[k: k + len(ts)]
+            k += len(ts)
+            s.trace.n_c_calls += 1
+            if kind == "draft":
+                nxt = ids[0]
+                if s.j < s.K:
+                    s.drafts.append(nxt)  # the draft for position cur_pos + 1
+                s.cur_tok, s.cur_pos = nxt, s.cur_pos + 1
+                s.j += 1
+                s.phase = "need_p" if s.j <= s.K else "verify"
+                continue
+            # verify: source p + i's gold predicts p + i + 1
+            rejected = False
+            for i in range(s.K):
+                s.trace.n_drafts_proposed += 1
+                ok = s.emu.draw() if s.emu is not None else ids[i] == s.drafts[i]
+                if ok:
+                    s.trace.n_drafts_accepted += 1
+                    s.commit(s.drafts[i])
+                    if len(s.committed) >= s.max_new_tokens:
+                        s.done = True
+                        break
+                else:
+                    s.trace.n_drafts_rejected += 1
+                    s.trace.n_rollback_events += 1
+                    rejected = True
+                    s.commit(ids[i])
+                    cache.drop_positions_at_and_after(s.idx, s.p + i + 1)
+                    s.last_token, s.p = ids[i], s.p + i + 1
+                    s.done = len(s.committed) >= s.max_new_tokens
+                    break
+            if not rejected and not s.done:
+                s.commit(ids[s.K])  # all K accepted: the bonus token
+                s.last_token, s.p = ids[s.K], s.p + s.K + 1
+                s.done = len(s.committed) >= s.max_new_tokens
+            if s.done:
+                s.clear_working_state()
+            else:
+                _dtv_round(s, draft_length)
+    return _finish(bt, seqs, t0, device, cache, blocks, lazy)
