@@ -213,6 +213,22 @@ def bs1_section(args, dev, res):
                                       "note": "includes prefill; real argmax acceptance on random-init weights"}
         log(f"bs1: sequential {res['extra']['bs1_sequential_tokens_per_s']:.1f} tok/s; greedy alpha "
             f"{tr.acceptance_rate:.2f}")
+        # draft-then-verify on the same workload (the reference's exp4 comparison:
+        # T_draft = 1, draft lengths 4 and 8, emulated alpha = 0.9)
+        from wavefront_decoding_amd.scheduler_batch import generate_dtv_batch
+        dtv = {}
+        for dl in (4, 8):
+            emus = [EmulatedAcceptance(alpha, 1000)]
+            generate_dtv_batch(bb, prompt.to(dev), 32, SsdPolicy(cfg.T_total, 1), dl, emus, prefilled=pf)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            bt = generate_dtv_batch(bb, prompt.to(dev), N, SsdPolicy(cfg.T_total, 1), dl,
+                                    [EmulatedAcceptance(alpha, 1000)], prefilled=pf)
+            torch.cuda.synchronize()
+            dtv[f"dl{dl}"] = {"tokens_per_s": round(bt.n_tokens / (time.perf_counter() - t0), 1),
+                              "acceptance": round(bt.acceptance_rate, 3), "r_ticks": bt.n_r_calls}
+        res["extra"]["bs1_dtv_alpha0.9_Tdraft1"] = dtv
+        log(f"bs1: DtV {dtv}")
     del model, bb, pf
     torch.cuda.empty_cache()
     return w
