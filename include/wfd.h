@@ -59,12 +59,23 @@ int wfd_abi_version(void);
  * kv_len[i] sizes the grid (and must not exceed a block); workspace >=
  * wfd_attn_workspace_bytes(n, H, Dh, kv_len_max). Dh in {64, 128};
  * H / Hkv in {1, 2, 4}.
+ * group_first (optional, device int32, n + 1 entries): group g = query rows
+ * [group_first[g], group_first[g+1]) -- rows that share one slot (the same
+ * kv_row_base), at most wfd_attn_group_max_rows(H, Hkv) of them; a workgroup
+ * then reads the shared prefix once for the whole group (draft-then-verify
+ * sources, a coda's verify + draft). Entries past the last group repeat
+ * group_first[ngroups] (empty groups). Every row's output bits are the same
+ * with or without grouping. NULL: one row per group.
+ * (wide-wavefront grouping replaces the grouped causal calls of
+ * _core_attn_varlen, src/decoding/parcae_blocks.py:391-456, and the coda
+ * grouping of huginn_blocks_batch.py:331-343.)
  */
 size_t wfd_attn_workspace_bytes(int n, int H, int Dh, int kv_len_max);
 int wfd_attn_split_keys(void);
+int wfd_attn_group_max_rows(int H, int Hkv);
 int wfd_attn_decode(const void* q, const void* k_cache, const void* v_cache, int64_t kv_block_rows,
-                    const int64_t* kv_row_base, const int32_t* kv_len, void* out, int n, int H, int Hkv, int Dh,
-                    int dtype, float scale, int kv_len_max, void* workspace, size_t ws_bytes,
+                    const int64_t* kv_row_base, const int32_t* kv_len, const int32_t* group_first, void* out, int n,
+                    int H, int Hkv, int Dh, int dtype, float scale, int kv_len_max, void* workspace, size_t ws_bytes,
                     wfd_stream_t stream);
 
 /*

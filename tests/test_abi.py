@@ -31,16 +31,17 @@ def test_library_loads_and_exports_every_symbol():
 
 def test_host_only_entry_points():
     lib = _lib.load()
-    assert lib.wfd_abi_version() == 2
+    assert lib.wfd_abi_version() == 3
+    assert [lib.wfd_attn_group_max_rows(16, k) for k in (16, 8, 4, 3)] == [8, 4, 2, 0]
     assert lib.wfd_attn_split_keys() == 2048
     assert lib.wfd_linear_k_multiple(_lib.BF16) == 128 and lib.wfd_linear_k_multiple(_lib.F32) == 64
     # workspace: n*H*splits*(Dh + 2) floats, each array 256-byte aligned
     assert lib.wfd_attn_workspace_bytes(8, 16, 64, 1024) == 8 * 16 * 1 * 64 * 4 + 8 * 16 * 1 * 2 * 4
     # argument validation happens before any device work
-    rc = lib.wfd_attn_decode(None, None, None, 0, None, None, None, 1, 16, 3, 64, 1, 0.1, 10, None, 0, None)
+    rc = lib.wfd_attn_decode(None, None, None, 0, None, None, None, None, 1, 16, 3, 64, 1, 0.1, 10, None, 0, None)
     assert rc == -1 and b"bad shape" in lib.wfd_last_error()
     # head-major blocks: a query's keys must fit one block
-    rc = lib.wfd_attn_decode(None, None, None, 512, None, None, None, 1, 16, 16, 64, 1, 0.1, 513, None, 0, None)
+    rc = lib.wfd_attn_decode(None, None, None, 512, None, None, None, None, 1, 16, 16, 64, 1, 0.1, 513, None, 0, None)
     assert rc == -1 and b"kv_block_rows=512" in lib.wfd_last_error()
     assert lib.wfd_kv_append(None, None, None, None, -1, None, 1, 16, 128, 1, None) == -1
     rc = lib.wfd_attn_prefill(None, None, None, 0, None, None, None, None, 1, 10, 16, 3, 64, 1, 0.1, None)
@@ -48,7 +49,7 @@ def test_host_only_entry_points():
     assert lib.wfd_attn_prefill(None, None, None, 0, None, None, None, None, 0, 10, 16, 4, 64, 1, 0.1, None) == 0
     rc = lib.wfd_linear(None, None, 100, None, None, 16, 2, 16, 100, 1, 1, 0, 0, None)
     assert rc == -1
-    assert lib.wfd_attn_decode(None, None, None, 0, None, None, None, 0, 16, 16, 64, 1, 0.1, 10, None, 0, None) == 0
+    assert lib.wfd_attn_decode(None, None, None, 0, None, None, None, None, 0, 16, 16, 64, 1, 0.1, 10, None, 0, None) == 0
     # packing: shape and aliasing are checked on the host
     assert lib.wfd_linear_pack(8, 16, 24, 128, 1, 0, 0, None) == -1      # N not a multiple of 16
     assert lib.wfd_linear_pack(8, 8, 32, 128, 1, 0, 0, None) == -1       # W_packed aliases W

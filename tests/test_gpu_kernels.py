@@ -137,6 +137,37 @@ def test_attn_prefill_matches_oracle(gpu, H, Hkv, Dh, segs, blocks):
     assert rel_err(_np(out), _np(dec)) <= 2e-2
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("H,Hkv,Dh", [(16, 16, 128), (16, 8, 64), (16, 4, 128), (4, 4, 64)])
+def test_attn_decode_grouped_rows_same_bits(gpu, dtype, H, Hkv, Dh):
+    """Rows that share a slot, grouped (one prefix read per group), give the
+    ungrouped rows' bits exactly -- ragged lengths inside a group, groups that
+    straddle the 2048-key split, a 1-row group, and the oracle agrees."""
+    gmax = ops.attn_group_max_rows(H, Hkv)
+    g = torch.Generator().manual_seed(H * 3 + Hkv + Dh)
+    groups = [[700, 701, 702, 650], [50], [2040, 2048, 2049, 3000, 10, 2100, 1, 4100][:gmax], [2047, 2048][:gmax]]
+    S = 4200
+    n_slots = len(groups) + 1
+    K = torch.randn(n_slots * S, Hkv, Dh, generator=g).to(dtype)
+    V = torch.randn(n_slots * S, Hkv, Dh, generator=g).to(dtype)
+    lens = [ln for grp in groups for ln in grp[:gmax]]
+    rb = torch.tensor([(gi + 1) * S for gi, grp in enumerate(groups) for _ in grp[:gmax]], dtype=torch.int64)
+    first = np.cumsum([0] + [len(grp[:gmax]) for grp in groups]).tolist()
+    n = len(lens)
+    gf = torch.tensor(first + [n] * (n + 1 - len(first)), dtype=torch.int32)
+    q = torch.randn(n, H, Dh, generator=g).to(dtype)
+    kl = torch.tensor(lens, dtype=torch.int32)
+    print(f"[attn grouped] dtype={dtype} H={H} Hkv={Hkv} Dh={Dh} groups={first}", flush=True)
+    Kb, Vb = _blocks(K, S).to(gpu), _blocks(V, S).to(gpu)
+    args = (q.to(gpu), Kb, Vb, rb.to(gpu), kl.to(gpu))
+    plain = ops.attn_decode(*args, kv_len_max=max(lens))
+    grouped = ops.attn_decode(*args, kv_len_max=max(lens), group_first=gf.to(gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(plain, grouped)
+    ref = ok.attention_rows(_np(q), _np(K), _np(V), rb.numpy(), kl.numpy())
+    assert rel_err(_np(grouped), ref) <= TOL[dtype]
+
+
 def test_attn_decode_kv_len_device_data(gpu):
     """Lengths are read from device memory at launch time: changing them in place changes the result."""
     q, K, V, rb, kl = _attn_case(gpu, torch.bfloat16, 2, 16, 16, 128, [600, 600], S=2048)

@@ -292,3 +292,22 @@ def test_dtv_token_handles_match_eager_ids(gpu):
         res.append([(t.tokens, t.counters()) for t in bt.per_seq])
         assert all(v >= 0 for t in bt.per_seq for v in t.tokens)
     assert res[0] == res[1]
+
+
+def test_grouped_attention_keeps_tokens(gpu):
+    """Engines with and without same-slot attention groups (draft-then-verify
+    sources, a coda's verifies + draft) commit the same tokens and counters,
+    eager and captured."""
+    cfg = MINI_BF16
+    w = M.init_weights(cfg, 0)
+    P = [_prompt(40, 4, V=cfg.vocab_size), _prompt(25, 5, V=cfg.vocab_size)]
+    res = []
+    for grouped, graphs in ((False, False), (True, False), (True, True)):
+        m = LoopedModel(cfg, w, gpu, max_seq_len=128, max_batch=2, use_graphs=graphs, group_attention=grouped)
+        bb = LoopedBlocksBatch(m, batch_size=2)
+        emus = [EmulatedAcceptance(0.7, 4000 + b) for b in range(2)]
+        dt = generate_dtv_batch(bb, [p.to(gpu) for p in P], [14, 10], SsdPolicy(cfg.T_total, 1), 4, emus)
+        emus = [EmulatedAcceptance(0.7, 5000 + b) for b in range(2)]
+        wf = generate_wavefront_batch(bb, [p.to(gpu) for p in P], [14, 10], SsdPolicy(cfg.T_total, 2), emus)
+        res.append(([(t.tokens, t.counters()) for t in dt.per_seq], [(t.tokens, t.counters()) for t in wf.per_seq]))
+    assert res[0] == res[1] == res[2]

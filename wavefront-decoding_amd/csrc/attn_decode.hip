@@ -39,11 +39,19 @@ constexpr int kAttnSplit = 2048;  // keys per workgroup
 
 __device__ __forceinline__ float attn_finish(float O, float L) { return L > 0.f ? O / L : 0.f; }
 
-template <typename T, int DH, int G, int NW, int TK>
+// One workgroup = (split, kv head g, group of QG query rows that share a slot).
+// MFMA row m = j * G + r carries query row j of the group at query head
+// g * G + r (NR = QG * G rows; the rest of the 16 are zero padding). Every
+// row's arithmetic -- its scores, its mask (keys < its own kv_len), its
+// online softmax statistics, its P.V accumulation order and the merge -- is
+// the same whichever group it sits in, so grouping changes no bits: a group
+// only reads the shared prefix once instead of once per row.
+template <typename T, int DH, int G, int QG, int NW, int TK>
 __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict__ q, const T* __restrict__ kc,
                                                              const T* __restrict__ vc,
                                                              const int64_t* __restrict__ row_base,
                                                              const int32_t* __restrict__ kv_len,
+                                                             const int32_t* __restrict__ group_first,
                                                              float* __restrict__ part_o, float* __restrict__ part_ml,
                                                              T* __restrict__ out, int H, int Hkv, int max_splits,
                                                              float scale_log2, int64_t block_rows) {
@@ -54,20 +62,29 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict
   constexpr int LPR = DH / V;      // lanes covering one V row
   constexpr int RG = 64 / LPR;     // V row groups per wave
   constexpr int KPL = TK / RG;     // V rows per lane per tile
-  static_assert(DH % KSTEP == 0 && 64 % LPR == 0 && TK % 16 == 0 && TK % RG == 0, "unsupported tile");
+  constexpr int NR = QG * G;       // real MFMA rows
+  static_assert(DH % KSTEP == 0 && 64 % LPR == 0 && TK % 16 == 0 && TK % RG == 0 && NR <= 16, "unsupported tile");
 
-  __shared__ float p_lds[NW][G][TK];
-  __shared__ float o_lds[NW][G][DH];
-  __shared__ float m_lds[NW][G];
-  __shared__ float l_lds[NW][G];
+  __shared__ float p_lds[NW][NR][TK];
+  __shared__ float o_lds[NW][NR][DH];
+  __shared__ float m_lds[NW][NR];
+  __shared__ float l_lds[NW][NR];
 
   const int split = blockIdx.x;
   const int g = blockIdx.y;
-  const int i = blockIdx.z;
-  const int len = kv_len[i];
-  if (split * kAttnSplit >= len) return;  // uniform for the whole workgroup
-  const int kend = min(len, (split + 1) * kAttnSplit);
-  const int ntiles = (kend - split * kAttnSplit + TK - 1) / TK;
+  const int q0 = group_first ? group_first[blockIdx.z] : (int)blockIdx.z;
+  const int qn = group_first ? min(group_first[blockIdx.z + 1] - q0, QG) : 1;
+  if (qn <= 0) return;  // empty group slot (uniform)
+  int lenq[QG];
+  int maxlen = 0;
+#pragma unroll
+  for (int j = 0; j < QG; ++j) {
+    lenq[j] = j < qn ? kv_len[q0 + j] : 0;
+    maxlen = max(maxlen, lenq[j]);
+  }
+  if (split * kAttnSplit >= maxlen) return;  // uniform for the whole workgroup
+  const int kend_max = min(maxlen, (split + 1) * kAttnSplit);
+  const int ntiles = (kend_max - split * kAttnSplit + TK - 1) / TK;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -75,26 +92,42 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict
   const int grp = lane >> 4;
   const int vg = lane / LPR;
   const int dseg = lane % LPR;
-  const int64_t hb = kv_offset(row_base[i], g, Hkv, DH, block_rows);  // position 0, kv head g
-  const int64_t rs = block_rows > 1 ? (int64_t)DH : (int64_t)Hkv * DH;   // key stride
+  const int64_t hb = kv_offset(row_base[q0], g, Hkv, DH, block_rows);  // position 0, kv head g
+  const int64_t rs = block_rows > 1 ? (int64_t)DH : (int64_t)Hkv * DH;  // key stride
   const T* kb = kc + hb;
   const T* vb = vc + hb;
 
-  u32x4 qf[NDS];
-  {
-    const T* qp = q + ((int64_t)i * H + (int64_t)g * G + (col < G ? col : 0)) * DH + grp * V;
+  // this lane's 4 score rows (4*grp + r) and their key bounds in this split
+  int kend4[4];
 #pragma unroll
-    for (int s = 0; s < NDS; ++s) qf[s] = col < G ? ld16(qp + s * KSTEP) : zero16();
+  for (int r = 0; r < 4; ++r) {
+    const int m = 4 * grp + r;
+    int e = -1;  // padding row: every key masked
+#pragma unroll
+    for (int j = 0; j < QG; ++j)
+      if (m < NR && m / G == j && j < qn) e = min(lenq[j], (split + 1) * kAttnSplit);
+    kend4[r] = e;
   }
 
-  // running softmax state of this wave: max (log2 domain), sum, output
-  float mrun[G], lrun[G], o[G][V];
+  u32x4 qf[NDS];
+  {
+    const int m = col;  // A-operand row of this lane
+    const bool real = m < NR && m / G < qn;
+    const int j = real ? m / G : 0;
+    const int hq = g * G + (real ? m % G : 0);
+    const T* qp = q + ((int64_t)(q0 + j) * H + hq) * DH + grp * V;
 #pragma unroll
-  for (int r = 0; r < G; ++r) {
-    mrun[r] = -INFINITY;
-    lrun[r] = 0.f;
+    for (int s = 0; s < NDS; ++s) qf[s] = real ? ld16(qp + s * KSTEP) : zero16();
+  }
+
+  // running softmax state of this wave per row: max (log2 domain), sum, output
+  float mrun[NR], lrun[NR], o[NR][V];
 #pragma unroll
-    for (int e = 0; e < V; ++e) o[r][e] = 0.f;
+  for (int m = 0; m < NR; ++m) {
+    mrun[m] = -INFINITY;
+    lrun[m] = 0.f;
+#pragma unroll
+    for (int e = 0; e < V; ++e) o[m][e] = 0.f;
   }
 
   for (int t = wave; t < ntiles; t += NW) {  // uniform over the wave
@@ -103,7 +136,7 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict
     u32x4 kf[NJ][NDS];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      const int key = min(t0 + 16 * j + col, len - 1);
+      const int key = min(t0 + 16 * j + col, maxlen - 1);
       const T* p = kb + (int64_t)key * rs + grp * V;
 #pragma unroll
       for (int s = 0; s < NDS; ++s) kf[j][s] = ld16(p + s * KSTEP);
@@ -111,11 +144,11 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict
     u32x4 vf[KPL];
 #pragma unroll
     for (int k = 0; k < KPL; ++k) {
-      const int key = min(t0 + RG * k + vg, len - 1);
+      const int key = min(t0 + RG * k + vg, maxlen - 1);
       vf[k] = ld16(vb + (int64_t)key * rs + dseg * V);
     }
 
-    // scores: lane (grp == 0, col) holds S[row r][key 16j + col] in acc[j][r]
+    // scores: lane (grp, col) holds S[row 4*grp + r][key 16j + col] in acc[j][r]
     f32x4 acc[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
@@ -123,46 +156,64 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict
 #pragma unroll
       for (int s = 0; s < NDS; ++s) acc[j] = mfma_step<T>(qf[s], kf[j][s], acc[j]);
     }
-    float corr[G];
+    // per row: the 16 lanes of its group reduce max and sum over the tile's
+    // keys, then every lane takes the row's statistics from the group's first lane
+    float mt4[4], lt4[4];
 #pragma unroll
-    for (int r = 0; r < G; ++r) {
+    for (int r = 0; r < 4; ++r) {
       float mt = -INFINITY;
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        const bool valid = (t0 + 16 * j + col) < kend;
+        const bool valid = (t0 + 16 * j + col) < kend4[r];
         const float sv = valid ? acc[j][r] * scale_log2 : -INFINITY;
         acc[j][r] = sv;
         mt = fmaxf(mt, sv);
       }
 #pragma unroll
-      for (int m = 8; m >= 1; m >>= 1) mt = fmaxf(mt, __shfl_xor(mt, m, 64));
-      // lanes 0-15 hold the real query rows: their statistics are the wave's
-      // (every lane rescales its slice of o with them)
-      mt = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(mt)));
-      const float mnew = fmaxf(mrun[r], mt);
-      corr[r] = (mrun[r] == -INFINITY) ? 0.f : exp2f(mrun[r] - mnew);
+      for (int sh = 8; sh >= 1; sh >>= 1) mt = fmaxf(mt, __shfl_xor(mt, sh, 64));
+      mt4[r] = mt;
+    }
+    float corr[NR];
+    float mnew4[4];
+#pragma unroll
+    for (int m = 0; m < NR; ++m) {
+      const float mt = __uint_as_float(__shfl(__float_as_uint(mt4[m % 4]), 16 * (m / 4), 64));
+      const float mnew = fmaxf(mrun[m], mt);
+      corr[m] = (mrun[m] == -INFINITY) ? 0.f : exp2f(mrun[m] - mnew);
+      mrun[m] = mnew;
+      if (m / 4 == grp) mnew4[m % 4] = mnew;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      // lanes of a padding row group keep mnew4 unset: give them -inf (their p are 0)
+      const float mn = (4 * grp + r < NR) ? mnew4[r] : -INFINITY;
       float lt = 0.f;
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        const float p = (acc[j][r] == -INFINITY) ? 0.f : exp2f(acc[j][r] - mnew);
+        const float p = (acc[j][r] == -INFINITY) ? 0.f : exp2f(acc[j][r] - mn);
         acc[j][r] = p;
         lt += p;
       }
 #pragma unroll
-      for (int m = 8; m >= 1; m >>= 1) lt += __shfl_xor(lt, m, 64);
-      lt = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(lt)));
-      lrun[r] = fmaf(lrun[r], corr[r], lt);
-      mrun[r] = mnew;
+      for (int sh = 8; sh >= 1; sh >>= 1) lt += __shfl_xor(lt, sh, 64);
+      lt4[r] = lt;
+    }
+#pragma unroll
+    for (int m = 0; m < NR; ++m) {
+      const float lt = __uint_as_float(__shfl(__float_as_uint(lt4[m % 4]), 16 * (m / 4), 64));
+      lrun[m] = fmaf(lrun[m], corr[m], lt);
     }
     // P to this wave's LDS rows, in the V lanes' key order
-    if (grp == 0) {
 #pragma unroll
-      for (int r = 0; r < G; ++r)
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * grp + r;
+      if (m < NR) {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
           const int kt = 16 * j + col;  // key within the tile
-          p_lds[wave][r][(kt % RG) * KPL + kt / RG] = acc[j][r];
+          p_lds[wave][m][(kt % RG) * KPL + kt / RG] = acc[j][r];
         }
+      }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -170,18 +221,18 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict
 
     // P.V on the VALU: lane owns V columns [dseg*V, dseg*V+V) of keys RG*k + vg
 #pragma unroll
-    for (int r = 0; r < G; ++r)
+    for (int m = 0; m < NR; ++m)
 #pragma unroll
-      for (int e = 0; e < V; ++e) o[r][e] *= corr[r];
+      for (int e = 0; e < V; ++e) o[m][e] *= corr[m];
 #pragma unroll
     for (int k = 0; k < KPL; ++k) {
       float v[V];
       Elem<T>::unpack(vf[k], v);
 #pragma unroll
-      for (int r = 0; r < G; ++r) {
-        const float p = p_lds[wave][r][vg * KPL + k];
+      for (int m = 0; m < NR; ++m) {
+        const float p = p_lds[wave][m][vg * KPL + k];
 #pragma unroll
-        for (int e = 0; e < V; ++e) o[r][e] = fmaf(p, v[e], o[r][e]);
+        for (int e = 0; e < V; ++e) o[m][e] = fmaf(p, v[e], o[m][e]);
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -189,46 +240,54 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 #pragma unroll
-  for (int m = LPR; m < 64; m <<= 1)
+  for (int sh = LPR; sh < 64; sh <<= 1)
 #pragma unroll
-    for (int r = 0; r < G; ++r)
+    for (int m = 0; m < NR; ++m)
 #pragma unroll
-      for (int e = 0; e < V; ++e) o[r][e] += __shfl_xor(o[r][e], m, 64);
+      for (int e = 0; e < V; ++e) o[m][e] += __shfl_xor(o[m][e], sh, 64);
   if (vg == 0) {
 #pragma unroll
-    for (int r = 0; r < G; ++r)
+    for (int m = 0; m < NR; ++m)
 #pragma unroll
-      for (int e = 0; e < V; ++e) o_lds[wave][r][dseg * V + e] = o[r][e];
+      for (int e = 0; e < V; ++e) o_lds[wave][m][dseg * V + e] = o[m][e];
   }
   if (lane == 0) {
 #pragma unroll
-    for (int r = 0; r < G; ++r) {
-      m_lds[wave][r] = mrun[r];
-      l_lds[wave][r] = lrun[r];
+    for (int m = 0; m < NR; ++m) {
+      m_lds[wave][m] = mrun[m];
+      l_lds[wave][m] = lrun[m];
     }
   }
   __syncthreads();
 
-  // Merge the NW waves in fixed order. One split: finish here (the split merge
-  // over one split, exactly as attn_combine_kernel computes it); otherwise
-  // emit this split's unnormalised partial.
-  int ns = (len + kAttnSplit - 1) / kAttnSplit;
-  ns = ns < max_splits ? ns : max_splits;
-  for (int idx = threadIdx.x; idx < G * DH; idx += 64 * NW) {
-    const int r = idx / DH;
-    const int d = idx - r * DH;
+  // Merge the NW waves in fixed order. A row whose keys fit one split is
+  // finished here (the split merge over one split, exactly as
+  // attn_combine_kernel computes it); otherwise it leaves this split's
+  // unnormalised partial. Rows with no keys in this split write nothing.
+  for (int idx = threadIdx.x; idx < NR * DH; idx += 64 * NW) {
+    const int m = idx / DH;
+    const int d = idx - m * DH;
+    const int j = m / G;
+    int len = 0;
+#pragma unroll
+    for (int jj = 0; jj < QG; ++jj)
+      if (jj == j) len = lenq[jj];
+    if (j >= qn || split * kAttnSplit >= len) continue;
+    int ns = (len + kAttnSplit - 1) / kAttnSplit;
+    ns = ns < max_splits ? ns : max_splits;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, m_lds[w][r]);
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, m_lds[w][m]);
     float O = 0.f, L = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      const float mw = m_lds[w][r];
+      const float mw = m_lds[w][m];
       const float f = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
-      O = fmaf(o_lds[w][r][d], f, O);
-      L = fmaf(l_lds[w][r], f, L);
+      O = fmaf(o_lds[w][m][d], f, O);
+      L = fmaf(l_lds[w][m], f, L);
     }
-    const int h = g * G + r;
+    const int i = q0 + j;
+    const int h = g * G + (m - j * G);
     if (ns == 1) {
       const float f = (M == -INFINITY) ? 0.f : exp2f(M - M);
       Elem<T>::store(out + ((int64_t)i * H + h) * DH + d, attn_finish(fmaf(O, f, 0.f), fmaf(L, f, 0.f)));
@@ -277,27 +336,39 @@ static size_t attn_ws_bytes(int n, int H, int Dh, int kv_len_max) {
   return align256((size_t)n * H * ms * Dh * sizeof(float)) + align256((size_t)n * H * ms * 2 * sizeof(float));
 }
 
+// Largest group of query rows one workgroup takes: 8 MFMA rows (NR = QG * G),
+// what the per-row output registers and LDS of 8 waves hold.
+constexpr int kAttnGroupRows = 8;
+constexpr int group_max_rows(int G) { return G >= kAttnGroupRows ? 1 : kAttnGroupRows / G; }
+
 template <typename T, int DH, int G>
-static void launch_attn(const void* q, const void* kc, const void* vc, const int64_t* rb, const int32_t* kl, void* out,
-                        int n, int H, int Hkv, int ms, float scale, int64_t br, float* po, float* pml,
-                        hipStream_t st) {
+static void launch_attn(const void* q, const void* kc, const void* vc, const int64_t* rb, const int32_t* kl,
+                        const int32_t* gf, void* out, int n, int H, int Hkv, int ms, float scale, int64_t br,
+                        float* po, float* pml, hipStream_t st) {
   const float scale_log2 = scale * 1.4426950408889634f;
   constexpr int TK = DH == 64 ? 64 : 32;  // key tile that fits the registers
   constexpr int NW = 8;  // waves per workgroup: 8 beat 4 and 16 on every measured shape
-  hipLaunchKernelGGL((attn_split_kernel<T, DH, G, NW, TK>), dim3(ms, Hkv, n), dim3(64 * NW), 0, st, (const T*)q,
-                     (const T*)kc, (const T*)vc, rb, kl, po, pml, (T*)out, H, Hkv, ms, scale_log2, br);
+  constexpr int QG = group_max_rows(G);
+  if (gf)
+    hipLaunchKernelGGL((attn_split_kernel<T, DH, G, QG, NW, TK>), dim3(ms, Hkv, n), dim3(64 * NW), 0, st,
+                       (const T*)q, (const T*)kc, (const T*)vc, rb, kl, gf, po, pml, (T*)out, H, Hkv, ms, scale_log2,
+                       br);
+  else
+    hipLaunchKernelGGL((attn_split_kernel<T, DH, G, 1, NW, TK>), dim3(ms, Hkv, n), dim3(64 * NW), 0, st,
+                       (const T*)q, (const T*)kc, (const T*)vc, rb, kl, gf, po, pml, (T*)out, H, Hkv, ms, scale_log2,
+                       br);
   if (ms > 1)  // some query may span several splits
     hipLaunchKernelGGL((attn_combine_kernel<T, DH>), dim3(H, n), dim3(DH), 0, st, po, pml, kl, (T*)out, H, ms);
 }
 
 template <typename T>
 static int dispatch_attn(int Dh, int G, const void* q, const void* kc, const void* vc, const int64_t* rb,
-                         const int32_t* kl, void* out, int n, int H, int Hkv, int ms, float scale, int64_t br,
-                         float* po, float* pml, hipStream_t st) {
-#define WFD_ATTN_CASE(DHV, GV)                                                        \
-  if (Dh == DHV && G == GV) {                                                         \
-    launch_attn<T, DHV, GV>(q, kc, vc, rb, kl, out, n, H, Hkv, ms, scale, br, po, pml, st); \
-    return kOk;                                                                       \
+                         const int32_t* kl, const int32_t* gf, void* out, int n, int H, int Hkv, int ms, float scale,
+                         int64_t br, float* po, float* pml, hipStream_t st) {
+#define WFD_ATTN_CASE(DHV, GV)                                                              \
+  if (Dh == DHV && G == GV) {                                                               \
+    launch_attn<T, DHV, GV>(q, kc, vc, rb, kl, gf, out, n, H, Hkv, ms, scale, br, po, pml, st); \
+    return kOk;                                                                             \
   }
   WFD_ATTN_CASE(64, 1)
   WFD_ATTN_CASE(64, 2)
@@ -320,9 +391,15 @@ size_t wfd_attn_workspace_bytes(int n, int H, int Dh, int kv_len_max) {
 
 int wfd_attn_split_keys(void) { return wfd::kAttnSplit; }
 
+int wfd_attn_group_max_rows(int H, int Hkv) {
+  if (H <= 0 || Hkv <= 0 || H % Hkv != 0) return 0;
+  return wfd::group_max_rows(H / Hkv);
+}
+
 int wfd_attn_decode(const void* q, const void* k_cache, const void* v_cache, int64_t kv_block_rows,
-                    const int64_t* kv_row_base, const int32_t* kv_len, void* out, int n, int H, int Hkv, int Dh,
-                    int dtype, float scale, int kv_len_max, void* workspace, size_t ws_bytes, hipStream_t stream) {
+                    const int64_t* kv_row_base, const int32_t* kv_len, const int32_t* group_first, void* out, int n,
+                    int H, int Hkv, int Dh, int dtype, float scale, int kv_len_max, void* workspace, size_t ws_bytes,
+                    hipStream_t stream) {
   using namespace wfd;
   if (n < 0 || H <= 0 || Hkv <= 0 || H % Hkv != 0 || kv_len_max < 1 || kv_block_rows < 0 ||
       (kv_block_rows > 1 && kv_len_max > kv_block_rows)) {
@@ -346,11 +423,11 @@ int wfd_attn_decode(const void* q, const void* k_cache, const void* v_cache, int
   float* pml = (float*)((char*)workspace + align256((size_t)n * H * ms * Dh * sizeof(float)));
   int rc;
   if (dtype == kBF16)
-    rc = dispatch_attn<bf16_t>(Dh, G, q, k_cache, v_cache, kv_row_base, kv_len, out, n, H, Hkv, ms, scale,
-                               kv_block_rows, po, pml, stream);
+    rc = dispatch_attn<bf16_t>(Dh, G, q, k_cache, v_cache, kv_row_base, kv_len, group_first, out, n, H, Hkv, ms,
+                               scale, kv_block_rows, po, pml, stream);
   else if (dtype == kF32)
-    rc = dispatch_attn<float>(Dh, G, q, k_cache, v_cache, kv_row_base, kv_len, out, n, H, Hkv, ms, scale,
-                              kv_block_rows, po, pml, stream);
+    rc = dispatch_attn<float>(Dh, G, q, k_cache, v_cache, kv_row_base, kv_len, group_first, out, n, H, Hkv, ms,
+                              scale, kv_block_rows, po, pml, stream);
   else
     rc = kUnsupported;
   if (rc != kOk) {

@@ -320,7 +320,7 @@ extern "C" {
 
 const char* wfd_last_error(void) { return wfd::g_err; }
 
-int wfd_abi_version(void) { return 2; }
+int wfd_abi_version(void) { return 3; }
 
 int wfd_add_rmsnorm(const void* a, const int32_t* a_rows, int64_t lda, const void* res, int64_t ldr, const void* w1,
                     const void* w2, void* x_out, const int32_t* out_rows, int64_t ldo, void* h_out, int64_t ldh, int n,

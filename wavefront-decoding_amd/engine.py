@@ -133,7 +133,7 @@ class LoopedModel:
 
     def __init__(self, cfg: LoopedLMConfig, weights: dict[str, torch.Tensor], device="cuda", *, max_seq_len: int,
                  max_batch: int = 1, state_init: str = "random", state_seed: int = 0, use_graphs: bool = False,
-                 max_rows: int | None = None, ring_len: int = 1 << 20):
+                 max_rows: int | None = None, ring_len: int = 1 << 20, group_attention: bool = True):
         self.cfg = cfg
         self.device = torch.device(device)
         self.dtype = cfg.torch_dtype
@@ -142,6 +142,7 @@ class LoopedModel:
         self.state_init = state_init
         self.state_seed = state_seed
         self.use_graphs = use_graphs
+        self.group_attention = group_attention  # rows sharing a slot read its prefix once
         self.W = {}
         for k, v in weights.items():
             w = v.to(device=self.device, dtype=self.dtype).contiguous()
@@ -215,11 +216,12 @@ class LoopedModel:
     # -- one SandwichBlock over n rows --------------------------------------------
     def _block(self, prefix: str, n: int, sc, pos_d, kvlen_d, rb_d, fr_d, kv_len_max: int, ws,
                cache: BatchStaticKVCache, next_norm: torch.Tensor | None, final_out=None, final_rows=None,
-               segments=None):
+               segments=None, group_first=None):
         """One SandwichBlock over n rows. `segments` = (seg_row_base, seg_q_start,
         seg_pos0, max_seg_len) routes attention through the causal prefill
         kernel (rows grouped by slot at consecutive positions) instead of the
-        per-row decode kernel."""
+        per-row decode kernel; `group_first` groups decode rows that share a
+        slot (one prefix read per group, same bits)."""
         c, W = self.cfg, self.W
         x, h = sc["x"], sc["h"]
         q = ops.linear_qkv_rope_append(h, W[prefix + "Wqkv"], pos_d, self.rope_cos, self.rope_sin, fr_d,
@@ -230,7 +232,7 @@ class LoopedModel:
             o = ops.attn_prefill(q, cache.flat_k, cache.flat_v, srb, sqs, sp0, max_seg_len=smax, out=sc["o"][:n])
         else:
             o = ops.attn_decode(q, cache.flat_k, cache.flat_v, rb_d, kvlen_d, kv_len_max=kv_len_max,
-                                out=sc["o"][:n], workspace=ws)
+                                out=sc["o"][:n], workspace=ws, group_first=group_first)
         a = ops.linear(o.view(n, -1), W[prefix + "proj"], n=n, out=sc["a"])
         ops.add_rmsnorm(a, W[prefix + "norm_2"], c.norm_eps, res=x, w2=W[prefix + "norm_3"], n=n, x_out=x,
                         h_out=h)
@@ -246,10 +248,32 @@ class LoopedModel:
         c = self.cfg
         return {"P": c.n_prelude, "R": c.n_core, "C": c.n_coda}[kind]
 
-    def _tables(self, kind: str, cache, seqs, pos, steps, ids, nb: int, ring_base: int | None = None):
-        """int32 [pos | kv_len | pool_row | ring_slot (C only)] and int64
-        [ids (P only) | row_base x L | flat_row x L], each block nb wide; rows
-        n..nb-1 are padding aimed at the trash rows / trash ring slot."""
+    def _groups(self, kind: str, seqs, steps, nb: int) -> np.ndarray | None:
+        """group_first for the attention of a pass (nb + 1 entries): adjacent
+        rows that read the same slots -- same sequence, and for R the same
+        depth (draft-then-verify sources, a coda's verifies and draft) -- form
+        one group of at most attn_group_max_rows rows; padding rows are groups
+        of one. None when every group would hold one row."""
+        n = len(seqs)
+        key = seqs if kind != "R" else seqs * (self.cfg.T_total + 1) + steps
+        if n < 2 or not np.any(key[1:] == key[:-1]):
+            return None
+        gmax = ops.attn_group_max_rows(self.cfg.n_heads, self.cfg.n_kv_heads)
+        first = [0]
+        for i in range(1, n):
+            if key[i] != key[i - 1] or i - first[-1] >= gmax:
+                first.append(i)
+        first += list(range(n, nb + 1))  # padding rows one by one, then the end
+        gf = np.full(nb + 1, nb, dtype=np.int32)
+        gf[:len(first)] = first
+        return gf
+
+    def _tables(self, kind: str, cache, seqs, pos, steps, ids, nb: int, ring_base: int | None = None,
+                groups: np.ndarray | None = None):
+        """int32 [pos | kv_len | pool_row | ring_slot (C only) | group_first
+        (grouped passes, nb + 1)] and int64 [ids (P only) | row_base x L |
+        flat_row x L], each block nb wide; rows n..nb-1 are padding aimed at
+        the trash rows / trash ring slot."""
         c = self.cfg
         n = len(pos)
         L = self._layers(kind)
@@ -263,14 +287,17 @@ class LoopedModel:
         rb[:, :n] = (slots * cache.B + seqs[None, :]) * cache.S
         fr = rb.copy()
         fr[:, :n] += pos[None, :]
-        i32 = np.zeros((4 if kind == "C" else 3) * nb, dtype=np.int32)
+        nblk = 4 if kind == "C" else 3
+        i32 = np.zeros(nblk * nb + (nb + 1 if groups is not None else 0), dtype=np.int32)
+        if groups is not None:
+            i32[nblk * nb:] = groups
         i32[:n] = pos
         i32[nb: nb + n] = pos + 1
         i32[nb + n: 2 * nb] = 1
         i32[2 * nb: 2 * nb + n] = seqs * self.R + pos % self.R
         i32[2 * nb + n: 3 * nb] = self.trash_pool_row
         if kind == "C":
-            i32[3 * nb:] = self.ring_len
+            i32[3 * nb: 4 * nb] = self.ring_len
             if ring_base is not None:
                 i32[3 * nb: 3 * nb + n] = np.arange(ring_base, ring_base + n, dtype=np.int32)
         parts = [rb.reshape(-1), fr.reshape(-1)]
@@ -280,10 +307,13 @@ class LoopedModel:
             parts.insert(0, idp)
         return i32, np.concatenate(parts)
 
-    def _launch(self, kind: str, cache, nb: int, t32: torch.Tensor, t64: torch.Tensor, kv_max: int) -> None:
+    def _launch(self, kind: str, cache, nb: int, t32: torch.Tensor, t64: torch.Tensor, kv_max: int,
+                grouped: bool = False) -> None:
         """The launch sequence of one pass over nb rows (eager or under capture)."""
         c, W, sc, ws = self.cfg, self.W, self.sc, self.attn_ws
         pos_d, kvlen_d, rows_d = t32[:nb], t32[nb: 2 * nb], t32[2 * nb: 3 * nb]
+        nblk = 4 if kind == "C" else 3
+        gf = t32[nblk * nb: nblk * nb + nb + 1] if grouped else None
         L = self._layers(kind)
         off = nb if kind == "P" else 0
         rb = lambda l: t64[off + l * nb: off + (l + 1) * nb]  # noqa: E731
@@ -295,7 +325,7 @@ class LoopedModel:
             for i in range(L):
                 nxt = W[f"prelude.{i + 1}.norm_1"] if i + 1 < L else None
                 self._block(f"prelude.{i}.", nb, sc, pos_d, kvlen_d, rb(i), fr(i), kv_max, ws, cache, nxt,
-                            final_out=static_half, final_rows=rows_d)
+                            final_out=static_half, final_rows=rows_d, group_first=gf)
             ops.copy_rows(self.s0, self.pool, n=nb, width=c.d_model, src_rows=pos_d, dst_rows=rows_d)
         elif kind == "R":
             ops.linear(self.pool, W["adapter"], n=nb, x_rows=rows_d, out=sc["x"])
@@ -303,53 +333,54 @@ class LoopedModel:
             for l in range(L):
                 nxt = W[f"core.{l + 1}.norm_1"] if l + 1 < L else None
                 self._block(f"core.{l}.", nb, sc, pos_d, kvlen_d, rb(l), fr(l), kv_max, ws, cache, nxt,
-                            final_out=self.pool, final_rows=rows_d)
+                            final_out=self.pool, final_rows=rows_d, group_first=gf)
         else:
             ops.add_rmsnorm(self.pool, W["ln_f"], c.norm_eps, w2=W["coda.0.norm_1"], n=nb, a_rows=rows_d,
                             x_out=sc["x"], h_out=sc["h"])
             for i in range(L):
                 nxt = W[f"coda.{i + 1}.norm_1"] if i + 1 < L else W["ln_f"]
-                self._block(f"coda.{i}.", nb, sc, pos_d, kvlen_d, rb(i), fr(i), kv_max, ws, cache, nxt)
+                self._block(f"coda.{i}.", nb, sc, pos_d, kvlen_d, rb(i), fr(i), kv_max, ws, cache, nxt,
+                            group_first=gf)
             ops.linear(sc["h"], W["lm_head"], n=nb, out=sc["logits"], out_dtype=torch.float32)
             ops.argmax(sc["logits"], n=nb, out=sc["ids"], ring=self.tok_ring, ring_rows=t32[3 * nb: 4 * nb])
 
-    def _captured(self, kind: str, nb: int, cache) -> _Captured:
-        key = (kind, nb, id(cache))
+    def _captured(self, kind: str, nb: int, cache, grouped: bool = False) -> _Captured:
+        key = (kind, nb, id(cache), grouped)
         g = self._graphs.get(key)
         if g is not None and g.cache is cache:
             return g
         L = self._layers(kind)
-        g = _Captured(kind, nb, cache, (4 if kind == "C" else 3) * nb, (2 * L + (1 if kind == "P" else 0)) * nb,
-                      self.device)
+        n32 = (4 if kind == "C" else 3) * nb + (nb + 1 if grouped else 0)
+        g = _Captured(kind, nb, cache, n32, (2 * L + (1 if kind == "P" else 0)) * nb, self.device)
         empty = np.zeros(0, dtype=np.int64)
-        i32, i64 = self._tables(kind, cache, empty, empty, empty, empty, nb)   # all padding rows
+        solo = np.arange(nb + 1, dtype=np.int32) if grouped else None            # all padding rows
+        i32, i64 = self._tables(kind, cache, empty, empty, empty, empty, nb, groups=solo)
         g.load(i32, i64)
         torch.cuda.synchronize()
-        self._launch(kind, cache, nb, g.d32, g.d64, cache.S)                   # warm-up, then capture
+        self._launch(kind, cache, nb, g.d32, g.d64, cache.S, grouped)            # warm-up, then capture
         torch.cuda.synchronize()
         g.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g.graph):
-            self._launch(kind, cache, nb, g.d32, g.d64, cache.S)
+            self._launch(kind, cache, nb, g.d32, g.d64, cache.S, grouped)
         torch.cuda.synchronize()
         self._graphs[key] = g
         return g
 
     def _run(self, kind: str, cache, seqs, pos, steps=None, ids=None, ring_base=None) -> None:
         n = len(pos)
+        nb = _bucket(n) if self.use_graphs else n
+        if nb > self.max_rows:
+            raise ValueError(f"union of {n} rows exceeds max_rows={self.max_rows}")
+        groups = self._groups(kind, seqs, steps, nb) if self.group_attention else None
+        grouped = groups is not None
+        i32, i64 = self._tables(kind, cache, seqs, pos, steps, ids, nb, ring_base, groups)
         if self.use_graphs:
-            nb = _bucket(n)
-            if nb > self.max_rows:
-                raise ValueError(f"union of {n} rows exceeds max_rows={self.max_rows}")
-            g = self._captured(kind, nb, cache)
-            i32, i64 = self._tables(kind, cache, seqs, pos, steps, ids, nb, ring_base)
+            g = self._captured(kind, nb, cache, grouped)
             g.load(i32, i64)
             g.graph.replay()
         else:
-            if n > self.max_rows:
-                raise ValueError(f"union of {n} rows exceeds max_rows={self.max_rows}")
-            i32, i64 = self._tables(kind, cache, seqs, pos, steps, ids, n, ring_base)
             t32, t64 = self.staging.upload([i32, i64])
-            self._launch(kind, cache, n, t32, t64, int(pos.max()) + 1)
+            self._launch(kind, cache, n, t32, t64, int(pos.max()) + 1, grouped)
 
     def _check(self, cache, seqs, pos):
         if len(pos) and (pos.min() < 0 or pos.max() >= cache.S):

@@ -83,13 +83,20 @@ def kv_layout(k_cache: torch.Tensor, v_cache: torch.Tensor) -> tuple[int, int, i
     return k_cache.shape[1], k_cache.shape[3], k_cache.shape[2]
 
 
+def attn_group_max_rows(H: int, Hkv: int) -> int:
+    """Most query rows one attention group may hold for this head shape."""
+    return int(_lib.load().wfd_attn_group_max_rows(H, Hkv))
+
+
 def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, kv_row_base: torch.Tensor,
                 kv_len: torch.Tensor, *, kv_len_max: int, scale: float | None = None,
-                out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+                out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                group_first: torch.Tensor | None = None) -> torch.Tensor:
     """Wavefront decode attention: q (n, H, Dh) over slot rows of the KV
     caches (layout: kv_layout); query i reads cache rows
-    kv_row_base[i] + [0, kv_len[i])."""
-    _need_cuda(q, k_cache, v_cache, kv_row_base, kv_len)
+    kv_row_base[i] + [0, kv_len[i]). `group_first` (int32, n + 1) groups rows
+    that share a slot so the prefix is read once per group (same bits)."""
+    _need_cuda(q, k_cache, v_cache, kv_row_base, kv_len, group_first)
     _need(q.dim() == 3 and q.is_contiguous(), "q must be contiguous (n, H, Dh)")
     n, H, Dh = q.shape
     Hkv, cDh, br = kv_layout(k_cache, v_cache)
@@ -99,6 +106,8 @@ def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, k
           "kv_row_base: int64 (n,)")
     _need(kv_len.dtype == torch.int32 and kv_len.numel() >= n and kv_len.is_contiguous(), "kv_len: int32 (n,)")
     _need(kv_len_max >= 1, "kv_len_max must be >= 1")
+    _need(group_first is None or (group_first.dtype == torch.int32 and group_first.is_contiguous()
+                                  and group_first.numel() >= n + 1), "group_first: int32 (n + 1,)")
     if out is None:
         out = torch.empty_like(q)
     _need(out.shape == q.shape and out.dtype == q.dtype and out.is_contiguous(), "bad out")
@@ -107,7 +116,7 @@ def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, k
     sc = 1.0 / math.sqrt(Dh) if scale is None else float(scale)
     rc = _lib.load().wfd_attn_decode(
         q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), br, kv_row_base.data_ptr(), kv_len.data_ptr(),
-        out.data_ptr(), n, H, Hkv, Dh, _dt(q), sc, int(kv_len_max), workspace.data_ptr(),
+        _p(group_first), out.data_ptr(), n, H, Hkv, Dh, _dt(q), sc, int(kv_len_max), workspace.data_ptr(),
         workspace.numel() * workspace.element_size(), _stream())
     _lib.check(rc, "wfd_attn_decode")
     return out
