@@ -272,6 +272,15 @@ def bs32_section(args, dev, res, w=None):
     res["extra"]["bs32"] = out
     res["extra"]["bs32_workload"] = ("32 sequences, prompts U[128,2048], generation U[64,512] (seed 0), "
                                      "T_total=16, T_draft=2, emulated acceptance seeds 1000+b, prefill excluded")
+    # draft-then-verify on the same batch (the reference's exp4 setting: T_draft = 1,
+    # draft length 4); its verify sources share slots, so their attention is grouped
+    from wavefront_decoding_amd.scheduler_batch import generate_dtv_batch
+    emus = [EmulatedAcceptance(0.9, 1000 + b) for b in range(B)]
+    bt = generate_dtv_batch(bb, prompts, glen, SsdPolicy(cfg.T_total, 1), 4, emus, prefilled=pf)
+    res["extra"]["bs32_dtv_alpha0.9_Tdraft1_dl4"] = {
+        "decode_tokens_per_s": round(bt.n_tokens / max(bt.walltime_decode_s, 1e-9), 1), "tokens": bt.n_tokens,
+        "r_ticks": bt.n_r_calls, "r_union_mean": round(bt.r_union_mean, 1), "acceptance": round(bt.acceptance_rate, 3)}
+    log(f"bs32: DtV {res['extra']['bs32_dtv_alpha0.9_Tdraft1_dl4']}")
     del model, bb, pf
     torch.cuda.empty_cache()
 

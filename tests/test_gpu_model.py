@@ -304,6 +304,7 @@ def test_grouped_attention_keeps_tokens(gpu):
     res = []
     for grouped, graphs in ((False, False), (True, False), (True, True)):
         m = LoopedModel(cfg, w, gpu, max_seq_len=128, max_batch=2, use_graphs=graphs, group_attention=grouped)
+        m.group_min_workgroups = 0  # group even these small unions
         bb = LoopedBlocksBatch(m, batch_size=2)
         emus = [EmulatedAcceptance(0.7, 4000 + b) for b in range(2)]
         dt = generate_dtv_batch(bb, [p.to(gpu) for p in P], [14, 10], SsdPolicy(cfg.T_total, 1), 4, emus)
