@@ -56,6 +56,7 @@ constexpr int kWideWaves = 16;
 constexpr int kWideMaxChunksPerWave = 3;
 constexpr int kWideMaxRows = 16;
 constexpr int kHalfTileMax = 256;  // wide launches of at most this many tiles use half tiles
+constexpr int kResidentWide = 512;  // 1024-thread workgroups resident at once (two per CU)
 enum Epilogue : int { kEpiPlain = 0, kEpiSwiGLU = 1, kEpiRope = 2 };
 
 // Operands of the QKV-RoPE-append epilogue (unused by the others).
@@ -201,14 +202,17 @@ __device__ __forceinline__ void chunk_mma(f32x4 (&acc)[NT], const u32x4 (&xf)[kC
 }
 
 // ---------------------------------------------------------------------------
-// wide: grid (tiles << HALF), 1024 threads; MC chunks per wave. HALF: two
+// wide: grid (tiles << HALF), WW waves (16, or 8 for launches of more tiles
+// than 1024-thread workgroups can keep resident at once: two per CU); MC
+// chunks per wave. Which wave computes a chunk does not change the chunk-order
+// sum, so WW changes no bits. HALF: two
 // workgroups per tile, each owning 8 of its 16 columns (its other lanes load
 // zero weights through an invalid buffer offset: no memory traffic), so a
 // 2048-column projection spreads over 256 workgroups instead of 128. The MFMA
 // output of a column does not depend on the other columns' operands, so both
 // forms give the same bits.
-template <typename T, typename TO, int EPI, int MC, bool HALF>
-__global__ __launch_bounds__(64 * kWideWaves) void linear_wide_kernel(
+template <typename T, typename TO, int EPI, int MC, bool HALF, int WW>
+__global__ __launch_bounds__(64 * WW) void linear_wide_kernel(
     const T* __restrict__ x, const int32_t* __restrict__ x_rows, int64_t ldx, const T* __restrict__ W,
     TO* __restrict__ y, int64_t ldy, int n, int K, int pair_off, const RopeArgs ra) {
   extern __shared__ f32x4 red[];  // [P][64 lanes]
@@ -232,7 +236,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void linear_wide_kernel(
   u32x4 xf[MC][kChunkSteps];
 #pragma unroll
   for (int j = 0; j < MC; ++j) {
-    const int p = wave + kWideWaves * j;
+    const int p = wave + WW * j;
     const int pc = p < P ? p : P - 1;
     if (HALF) {
       const bool mine = (col >> 3) == half;
@@ -248,7 +252,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void linear_wide_kernel(
   }
 #pragma unroll
   for (int j = 0; j < MC; ++j) {
-    const int p = wave + kWideWaves * j;
+    const int p = wave + WW * j;
     if (p < P) {
       f32x4 acc[1];
       chunk_mma<T, 1>(acc, xf[j], wf[j]);
@@ -356,20 +360,36 @@ static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const v
   // fewer tiles than half the chip's 256 CUs x 2: split tiles into column halves
   // (not for SwiGLU, whose partner column c ^ 8 lies in the other half)
   const bool half = EPI != kEpiSwiGLU && tiles <= kHalfTileMax;
-#define WFD_WIDE(MCV)                                                                                            \
-  if (half)                                                                                                      \
-    hipLaunchKernelGGL((linear_wide_kernel<T, TO, EPI, MCV, true>), dim3(2 * tiles), dim3(64 * kWideWaves), lds, \
-                       st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra);                  \
-  else                                                                                                           \
-    hipLaunchKernelGGL((linear_wide_kernel<T, TO, EPI, MCV, false>), dim3(tiles), dim3(64 * kWideWaves), lds, st, \
-                       (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra);
-  if (wide && mc == 1) {
+  // more tiles than two 1024-thread workgroups per CU hold: 8-wave workgroups
+  // (four per CU), so the whole launch is resident in one round (gate|up at
+  // 704 tiles: 11.5 -> 10.4 us)
+  const int mc8 = (P + 7) / 8;
+  const bool ww8 = !half && tiles > kResidentWide && mc8 <= kWideMaxChunksPerWave;
+#define WFD_WIDE(MCV)                                                                                             \
+  if (half)                                                                                                       \
+    hipLaunchKernelGGL((linear_wide_kernel<T, TO, EPI, MCV, true, kWideWaves>), dim3(2 * tiles),                 \
+                       dim3(64 * kWideWaves), lds, st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K,     \
+                       pair_off, ra);                                                                             \
+  else                                                                                                            \
+    hipLaunchKernelGGL((linear_wide_kernel<T, TO, EPI, MCV, false, kWideWaves>), dim3(tiles), dim3(64 * kWideWaves), \
+                       lds, st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra);
+#define WFD_WIDE8(MCV)                                                                                          \
+  hipLaunchKernelGGL((linear_wide_kernel<T, TO, EPI, MCV, false, 8>), dim3(tiles), dim3(64 * 8), lds, st,      \
+                     (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra);
+  if (wide && ww8 && mc8 == 1) {
+    WFD_WIDE8(1)
+  } else if (wide && ww8 && mc8 == 2) {
+    WFD_WIDE8(2)
+  } else if (wide && ww8) {
+    WFD_WIDE8(3)
+  } else if (wide && mc == 1) {
     WFD_WIDE(1)
   } else if (wide && mc == 2) {
     WFD_WIDE(2)
   } else if (wide) {
     WFD_WIDE(3)
   } else {
+#undef WFD_WIDE8
 #undef WFD_WIDE
     constexpr int NB = 2;
     hipLaunchKernelGGL((linear_tile_kernel<T, TO, EPI, NB>), dim3((n + 63) / 64, (tiles + NB - 1) / NB), dim3(256),
