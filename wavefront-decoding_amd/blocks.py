@@ -301,6 +301,35 @@ class LoopedBlocksBatch:
             return list(self.model.last_c_handles)
         return ids.tolist()
 
+    @torch.no_grad()
+    def run_passes(self, passes, cache, lazy: bool = False) -> list[int] | None:
+        """A tick's passes -- [(kind, seq_ids, toks)] with kind "P", "R" or "C"
+        (C last) -- as one launch sequence (one graph replay, one table upload),
+        with the token bookkeeping prelude_union / advance_union /
+        coda_argmax_union would do. Returns the C pass's ids (or handles)."""
+        eng, R = [], self.model.R
+        for kind, seq_ids, toks in passes:
+            if not toks:
+                continue
+            pos = [t.position for t in toks]
+            if kind == "P":
+                eng.append(("P", seq_ids, pos, [t.token_id for t in toks]))
+                for b, t in zip(seq_ids, toks):
+                    t.row = int(b) * R + t.position % R
+                    t.step = 0
+            elif kind == "R":
+                eng.append(("R", seq_ids, pos, [t.step for t in toks]))
+                for t in toks:
+                    t.step += 1
+            else:
+                eng.append(("C", seq_ids, pos, None))
+        out = self.model.run_passes(cache, eng) if eng else None
+        if out is None:
+            return None
+        if lazy and self.model.last_c_handles is not None:
+            return list(self.model.last_c_handles)
+        return out[1].tolist()
+
     def reset_token_ring(self) -> None:
         self.model.reset_token_ring()
 

@@ -354,43 +354,65 @@ class LoopedModel:
             ops.linear(sc["h"], W["lm_head"], n=nb, out=sc["logits"], out_dtype=torch.float32)
             ops.argmax(sc["logits"], n=nb, out=sc["ids"], ring=self.tok_ring, ring_rows=t32[3 * nb: 4 * nb])
 
-    def _captured(self, kind: str, nb: int, cache, grouped: bool = False) -> _Captured:
-        key = (kind, nb, id(cache), grouped)
-        g = self._graphs.get(key)
-        if g is not None and g.cache is cache:
-            return g
-        L = self._layers(kind)
-        n32 = (4 if kind == "C" else 3) * nb + (nb + 1 if grouped else 0)
-        g = _Captured(kind, nb, cache, n32, (2 * L + (1 if kind == "P" else 0)) * nb, self.device)
-        empty = np.zeros(0, dtype=np.int64)
-        solo = np.arange(nb + 1, dtype=np.int32) if grouped else None            # all padding rows
-        i32, i64 = self._tables(kind, cache, empty, empty, empty, empty, nb, groups=solo)
-        g.load(i32, i64)
-        torch.cuda.synchronize()
-        self._launch(kind, cache, nb, g.d32, g.d64, cache.S, grouped)            # warm-up, then capture
-        torch.cuda.synchronize()
-        g.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g.graph):
-            self._launch(kind, cache, nb, g.d32, g.d64, cache.S, grouped)
-        torch.cuda.synchronize()
-        self._graphs[key] = g
-        return g
-
-    def _run(self, kind: str, cache, seqs, pos, steps=None, ids=None, ring_base=None) -> None:
+    def _plan(self, kind: str, cache, seqs, pos, steps=None, ids=None, ring_base=None) -> dict:
+        """Tables and launch shape of one pass (padded to its row bucket under graphs)."""
         n = len(pos)
         nb = _bucket(n) if self.use_graphs else n
         if nb > self.max_rows:
             raise ValueError(f"union of {n} rows exceeds max_rows={self.max_rows}")
         groups = self._groups(kind, seqs, steps, nb) if self.group_attention else None
-        grouped = groups is not None
         i32, i64 = self._tables(kind, cache, seqs, pos, steps, ids, nb, ring_base, groups)
+        return dict(kind=kind, nb=nb, grouped=groups is not None, i32=i32, i64=i64, kv_max=int(pos.max()) + 1)
+
+    def _launch_plans(self, cache, plans, t32: torch.Tensor, t64: torch.Tensor, kv_max: int | None = None) -> None:
+        """Launch the passes in order, each on its slice of the joint tables."""
+        o32 = o64 = 0
+        for p in plans:
+            n32, n64 = len(p["i32"]), len(p["i64"])
+            self._launch(p["kind"], cache, p["nb"], t32[o32: o32 + n32], t64[o64: o64 + n64],
+                         kv_max if kv_max is not None else p["kv_max"], p["grouped"])
+            o32 += n32
+            o64 += n64
+
+    def _captured(self, cache, plans) -> _Captured:
+        """The graph of a pass sequence: one per (cache, [(kind, bucket, grouped)])."""
+        key = (id(cache),) + tuple((p["kind"], p["nb"], p["grouped"]) for p in plans)
+        g = self._graphs.get(key)
+        if g is not None and g.cache is cache:
+            return g
+        empty = np.zeros(0, dtype=np.int64)
+        pad = []  # the same shapes with every row a padding row
+        for p in plans:
+            solo = np.arange(p["nb"] + 1, dtype=np.int32) if p["grouped"] else None
+            i32, i64 = self._tables(p["kind"], cache, empty, empty, empty, empty, p["nb"], groups=solo)
+            pad.append(dict(p, i32=i32, i64=i64))
+        g = _Captured("+".join(p["kind"] for p in plans), plans[0]["nb"], cache, sum(len(p["i32"]) for p in pad),
+                      sum(len(p["i64"]) for p in pad), self.device)
+        g.load(np.concatenate([p["i32"] for p in pad]), np.concatenate([p["i64"] for p in pad]))
+        torch.cuda.synchronize()
+        self._launch_plans(cache, pad, g.d32, g.d64, cache.S)                   # warm-up, then capture
+        torch.cuda.synchronize()
+        g.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g.graph):
+            self._launch_plans(cache, pad, g.d32, g.d64, cache.S)
+        torch.cuda.synchronize()
+        self._graphs[key] = g
+        return g
+
+    def _run_plans(self, cache, plans) -> None:
+        """One replay (graphs) or one table upload + launches (eager) for the whole sequence."""
+        i32 = np.concatenate([p["i32"] for p in plans])
+        i64 = np.concatenate([p["i64"] for p in plans])
         if self.use_graphs:
-            g = self._captured(kind, nb, cache, grouped)
+            g = self._captured(cache, plans)
             g.load(i32, i64)
             g.graph.replay()
         else:
             t32, t64 = self.staging.upload([i32, i64])
-            self._launch(kind, cache, n, t32, t64, int(pos.max()) + 1, grouped)
+            self._launch_plans(cache, plans, t32, t64)
+
+    def _run(self, kind: str, cache, seqs, pos, steps=None, ids=None, ring_base=None) -> None:
+        self._run_plans(cache, [self._plan(kind, cache, seqs, pos, steps, ids, ring_base)])
 
     def _check(self, cache, seqs, pos):
         if len(pos) and (pos.min() < 0 or pos.max() >= cache.S):
@@ -401,6 +423,62 @@ class LoopedModel:
             raise ValueError("cache longer than the engine's tables (max_seq_len)")
 
     # -- P / R / C ---------------------------------------------------------------------
+    def _prepare(self, cache, kind: str, seqs, positions, extra=None):
+        """Validated plan + bookkeeping closure of one pass. extra: token ids (P),
+        steps (R). A C pass takes its token-ring slots here."""
+        c = self.cfg
+        seqs = np.asarray(seqs, dtype=np.int64)
+        pos = np.asarray(positions, dtype=np.int64)
+        self._check(cache, seqs, pos)
+        if kind == "P":
+            plan = self._plan("P", cache, seqs, pos, ids=np.asarray(extra, dtype=np.int64))
+            writes = [(self.slot_prelude(i), b, p) for b, p in zip(seqs.tolist(), pos.tolist())
+                      for i in range(c.n_prelude)]
+            return plan, writes, None
+        if kind == "R":
+            st = np.asarray(extra, dtype=np.int64)
+            if st.min() < 0 or st.max() >= c.T_total:
+                raise ValueError(f"core step out of range [0, {c.T_total})")
+            plan = self._plan("R", cache, seqs, pos, steps=st)
+            writes = [(self.slot_core(s_, l), b, p) for b, p, s_ in zip(seqs.tolist(), pos.tolist(), st.tolist())
+                      for l in range(c.n_core)]
+            return plan, writes, None
+        n = len(pos)
+        base = None
+        if self._ring_next + n <= self.ring_len:
+            base = self._ring_next
+            self._ring_next += n
+        plan = self._plan("C", cache, seqs, pos, ring_base=base)
+        writes = [(self.slot_coda(i), b, p) for b, p in zip(seqs.tolist(), pos.tolist()) for i in range(c.n_coda)]
+        return plan, writes, (None if base is None else [-(base + i) - 1 for i in range(n)])
+
+    def run_passes(self, cache, passes) -> tuple[torch.Tensor, torch.Tensor] | None:
+        """Several passes as one launch sequence -- one graph replay and one
+        table upload -- in order: passes = [(kind, seqs, positions, extra)],
+        kind "P" (extra = token ids or ring handles), "R" (extra = steps) or
+        "C" (extra unused; at most one, last). A scheduler tick (P, R, C) or a
+        whole sequential token (P, T_total x R, C) then costs one replay.
+        Returns what coda_union returns for the C pass, else None."""
+        plans, writes, handles, n_c = [], [], None, 0
+        for kind, seqs, positions, extra in passes:
+            if len(positions) == 0:
+                continue
+            if kind == "C" and passes[-1][0] != "C":
+                raise ValueError("the C pass must come last")
+            plan, w, h = self._prepare(cache, kind, seqs, positions, extra)
+            plans.append(plan)
+            writes += w
+            if kind == "C":
+                handles, n_c = h, len(positions)
+        if plans:
+            self._run_plans(cache, plans)
+        for slot, b, p in writes:
+            cache.note_write(slot, b, p)
+        if n_c:
+            self.last_c_handles = handles
+            return self.sc["logits"][:n_c], self.sc["ids"][:n_c]
+        return None
+
     def prelude_union(self, cache, seqs, positions, token_ids) -> np.ndarray:
         """Embed + prelude blocks for n new tokens; fills pool[row] = [s0(pos) | e].
         Returns the pool rows."""
@@ -408,48 +486,23 @@ class LoopedModel:
         pos = np.asarray(positions, dtype=np.int64)
         if len(pos) == 0:
             return np.zeros(0, dtype=np.int64)
-        self._check(cache, seqs, pos)
-        self._run("P", cache, seqs, pos, ids=np.asarray(token_ids, dtype=np.int64))
-        for b, p in zip(seqs.tolist(), pos.tolist()):
-            for i in range(self.cfg.n_prelude):
-                cache.note_write(self.slot_prelude(i), b, p)
+        self.run_passes(cache, [("P", seqs, pos, token_ids)])
         return seqs * self.R + pos % self.R
 
     def core_union(self, cache, seqs, positions, steps) -> None:
         """One recurrence for n rows at their own depths: pool[row][:D] advances one step."""
-        c = self.cfg
-        seqs = np.asarray(seqs, dtype=np.int64)
-        pos = np.asarray(positions, dtype=np.int64)
-        st = np.asarray(steps, dtype=np.int64)
-        if len(pos) == 0:
-            return
-        self._check(cache, seqs, pos)
-        if st.min() < 0 or st.max() >= c.T_total:
-            raise ValueError(f"core step out of range [0, {c.T_total})")
-        self._run("R", cache, seqs, pos, steps=st)
-        for b, p, s in zip(seqs.tolist(), pos.tolist(), st.tolist()):
-            for l in range(c.n_core):
-                cache.note_write(self.slot_core(s, l), b, p)
+        self.run_passes(cache, [("R", seqs, positions, steps)])
 
     def coda_union(self, cache, seqs, positions) -> tuple[torch.Tensor, torch.Tensor]:
         """ln_f -> coda blocks -> ln_f -> lm_head -> argmax for n rows. Returns
         (logits (n, V) float32, argmax ids (n,) int64), both device views that
         the next call overwrites. The ids also land in the token ring:
         `last_c_handles` lists their handles (None when the ring is full)."""
-        seqs = np.asarray(seqs, dtype=np.int64)
-        pos = np.asarray(positions, dtype=np.int64)
-        n = len(pos)
-        self._check(cache, seqs, pos)
-        base = None
-        if self._ring_next + n <= self.ring_len:
-            base = self._ring_next
-            self._ring_next += n
-        self._run("C", cache, seqs, pos, ring_base=base)
-        self.last_c_handles = None if base is None else [-(base + i) - 1 for i in range(n)]
-        for b, p in zip(seqs.tolist(), pos.tolist()):
-            for i in range(self.cfg.n_coda):
-                cache.note_write(self.slot_coda(i), b, p)
-        return self.sc["logits"][:n], self.sc["ids"][:n]
+        out = self.run_passes(cache, [("C", seqs, positions, None)])
+        if out is None:  # empty union
+            self.last_c_handles = []
+            return self.sc["logits"][:0], self.sc["ids"][:0]
+        return out
 
     # -- token ring --------------------------------------------------------------------
     def reset_token_ring(self) -> None:

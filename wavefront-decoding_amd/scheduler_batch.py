@@ -158,6 +158,27 @@ def _finish(bt: BatchTrace, seqs, t0: float, device, cache, blocks=None, lazy: b
     return bt
 
 
+def _passes(blocks, cache, passes, lazy: bool):
+    """A tick's P / R / C passes, [(kind, seq_ids, toks)] in order. Blocks
+    that can fuse them run the tick as one launch sequence; others get one
+    call per pass. Returns the C pass's ids (or token handles), else None."""
+    fused = getattr(blocks, "run_passes", None)
+    if fused is not None:
+        return fused([p for p in passes if p[2]], cache, lazy)
+    out = None
+    for kind, ids, toks in passes:
+        if not toks:
+            continue
+        if kind == "P":
+            blocks.prelude_union(ids, toks, cache)
+        elif kind == "R":
+            blocks.advance_union(ids, toks, cache)
+        else:
+            out = blocks.coda_argmax_union(ids, toks, cache, lazy=True) if lazy else blocks.coda_argmax_union(
+                ids, toks, cache)
+    return out
+
+
 def _record_r(bt: BatchTrace, n: int) -> None:
     bt.n_r_calls += 1
     bt.r_union_total += n
@@ -183,15 +204,14 @@ def ar_generate_batch(blocks, prompt_ids, max_new_tokens, prefilled: SharedPrefi
                                     role="verify"))
             s.trace.n_p_calls += 1
         ids = [s.idx for s in act]
-        blocks.prelude_union(ids, toks, cache)
+        # the whole token: P, T_total R passes and C as one launch sequence
+        out = _passes(blocks, cache, [("P", ids, toks)] + [("R", ids, toks)] * blocks.T_total + [("C", ids, toks)],
+                      lazy)
         bt.n_p_calls += 1
         for _ in range(blocks.T_total):
-            blocks.advance_union(ids, toks, cache)
             _record_r(bt, len(toks))
             for s in act:
                 s.trace.n_r_calls += 1
-        out = blocks.coda_argmax_union(ids, toks, cache, lazy=True) if lazy else blocks.coda_argmax_union(
-            ids, toks, cache)
         bt.n_c_calls += 1
         for s, nid in zip(act, out):
             s.trace.n_c_calls += 1
@@ -227,42 +247,33 @@ def generate_wavefront_batch(blocks, prompt_ids, max_new_tokens, policy: SsdPoli
         if ticks > guard:
             raise RuntimeError(f"wfd batch exceeded tick guard ({guard}) -- scheduler bug?")
 
-        # P: everything queued by the previous settle
+        # P: everything queued by the previous settle; it joins the R union
         p_pairs = [(s, t) for s in live for t in s.active_p]
-        if p_pairs:
-            blocks.prelude_union([s.idx for s, _ in p_pairs], [t for _, t in p_pairs], cache)
-            for s, t in p_pairs:
-                s.active_r.append(t)
-            for s in live:
-                s.active_p = []
-            bt.n_p_calls += 1
-
+        for s, t in p_pairs:
+            s.active_r.append(t)
+        for s in live:
+            s.active_p = []
         # R: one tick for every live wave
         r_pairs = [(s, t) for s in live for t in s.active_r if t.is_alive]
-        if r_pairs:
-            blocks.advance_union([s.idx for s, _ in r_pairs], [t for _, t in r_pairs], cache)
-            _record_r(bt, len(r_pairs))
-            for s in live:
-                if any(t.is_alive for t in s.active_r):
-                    s.trace.n_r_calls += 1
-
-        # routing: commit point -> verify (moved); draft point -> draft (copied)
+        # routing by the depth each token reaches in this tick's R: commit
+        # point -> verify (moved); draft point -> draft (copied)
         for s in live:
             keep = []
             for t in s.active_r:
                 if not t.is_alive:
                     continue
-                if t.step == T_total:
+                after = t.step + 1
+                if after == T_total:
                     t.role = "verify"
                     s.active_c.append(t)
                 else:
                     keep.append(t)
-                    if t.step == T_draft:
+                    if after == T_draft:
                         d = copy.copy(t)
                         d.role = "draft"
+                        d.step = after
                         s.active_c.append(d)
             s.active_r = keep
-
         # C: one union over every sequence's verifies + draft
         plan, c_toks, c_ids = [], [], []
         for s in live:
@@ -272,10 +283,18 @@ def generate_wavefront_batch(blocks, prompt_ids, max_new_tokens, policy: SsdPoli
                 plan.append((s, vs, ds))
                 c_toks += vs + ds
                 c_ids += [s.idx] * (len(vs) + len(ds))
+        golds = _passes(blocks, cache, [("P", [s.idx for s, _ in p_pairs], [t for _, t in p_pairs]),
+                                        ("R", [s.idx for s, _ in r_pairs], [t for _, t in r_pairs]),
+                                        ("C", c_ids, c_toks)], lazy)
+        if p_pairs:
+            bt.n_p_calls += 1
+        if r_pairs:
+            _record_r(bt, len(r_pairs))
+            for s in live:
+                if any(t.is_alive for t in s.active_r) or any(t.role == "verify" for t in s.active_c):
+                    s.trace.n_r_calls += 1
         gold_of: dict[int, int] = {}
         if c_toks:
-            golds = (blocks.coda_argmax_union(c_ids, c_toks, cache, lazy=True) if lazy
-                     else blocks.coda_argmax_union(c_ids, c_toks, cache))
             gold_of = {id(t): g for t, g in zip(c_toks, golds)}
             bt.n_c_calls += 1
             for s, _, _ in plan:
@@ -373,17 +392,13 @@ def generate_dtv_batch(blocks, prompt_ids, max_new_tokens, policy: SsdPolicy, dr
 
         # P: each sequence whose next source needs its embedding
         pneed = [s for s in live if s.phase == "need_p"]
-        if pneed:
-            new = []
-            for s in pneed:
-                t = ActiveToken(token_id=s.cur_tok, position=s.cur_pos, role="verify")
-                s.sources.append(t)
-                new.append(t)
-                s.trace.n_p_calls += 1
-                s.phase = "draft"
-            blocks.prelude_union([s.idx for s in pneed], new, cache)
-            bt.n_p_calls += 1
-
+        new = []
+        for s in pneed:
+            t = ActiveToken(token_id=s.cur_tok, position=s.cur_pos, role="verify")
+            s.sources.append(t)
+            new.append(t)
+            s.trace.n_p_calls += 1
+            s.phase = "draft"
         # R: a drafting sequence advances its current source, a verifying one all K+1
         r_pairs, moved = [], []
         for s in live:
@@ -393,25 +408,28 @@ def generate_dtv_batch(blocks, prompt_ids, max_new_tokens, policy: SsdPolicy, dr
             elif s.phase == "verify" and s.sources[0].step < T_total:
                 r_pairs += [(s, t) for t in s.sources]
                 moved.append(s)
+        # C: a draft source that reaches T_draft in this R, or all sources at T_total
+        stepped = {id(t) for _, t in r_pairs}
+        after = lambda t: t.step + (id(t) in stepped)  # noqa: E731
+        entries = []
+        for s in live:
+            if s.phase == "draft" and after(s.sources[-1]) == T_draft:
+                entries.append((s, "draft", [s.sources[-1]]))
+            elif s.phase == "verify" and after(s.sources[0]) == T_total:
+                entries.append((s, "verify", list(s.sources)))
+        c_toks = [t for _, _, ts in entries for t in ts]
+        c_ids = [s.idx for s, _, ts in entries for _ in ts]
+        out = _passes(blocks, cache, [("P", [s.idx for s in pneed], new),
+                                      ("R", [s.idx for s, _ in r_pairs], [t for _, t in r_pairs]),
+                                      ("C", c_ids, c_toks)], lazy)
+        if pneed:
+            bt.n_p_calls += 1
         if r_pairs:
-            blocks.advance_union([s.idx for s, _ in r_pairs], [t for _, t in r_pairs], cache)
             _record_r(bt, len(r_pairs))
             for s in moved:
                 s.trace.n_r_calls += 1
-
-        # C: a draft source that reached T_draft, or all sources at T_total
-        entries = []
-        for s in live:
-            if s.phase == "draft" and s.sources[-1].step == T_draft:
-                entries.append((s, "draft", [s.sources[-1]]))
-            elif s.phase == "verify" and s.sources[0].step == T_total:
-                entries.append((s, "verify", list(s.sources)))
         if not entries:
             continue
-        c_toks = [t for _, _, ts in entries for t in ts]
-        c_ids = [s.idx for s, _, ts in entries for _ in ts]
-        out = (blocks.coda_argmax_union(c_ids, c_toks, cache, lazy=True) if lazy
-               else blocks.coda_argmax_union(c_ids, c_toks, cache))
         bt.n_c_calls += 1
         k = 0
         for s, kind, ts in entries:
