@@ -51,7 +51,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--quick", action="store_true", help="fewer extras (development)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--only", default="", help="comma list of sections: bs1,roofline,attn,bs32,prefill,gqa,cpu")
+    ap.add_argument("--only", default="", help="comma list of sections: bs1,roofline,attn,bs32,prefill,c5,gqa,cpu")
     ap.add_argument("--eager", action="store_true", help="launch every pass eagerly (no hipGraph capture)")
     return ap.parse_args()
 
@@ -378,6 +378,46 @@ def prefill_section(args, dev, res):
     torch.cuda.empty_cache()
 
 
+def c5_section(args, dev, res):
+    """The long-context configuration end to end: the GQA looped model (16 q /
+    4 kv heads, 4-layer core x 32), 4 sequences of 32768 uniform-random prompt
+    tokens prefilled on the GPU (MFMA causal attention), then 128 new tokens
+    each by WFD with T_draft = 2 (wavefront width 16) at emulated alpha = 0.9."""
+    import torch
+    from wavefront_decoding_amd import model as M
+    from wavefront_decoding_amd.blocks import LoopedBlocksBatch
+    from wavefront_decoding_amd.emu import EmulatedAcceptance
+    from wavefront_decoding_amd.engine import LoopedModel
+    from wavefront_decoding_amd.policy import SsdPolicy
+    from wavefront_decoding_amd.scheduler_batch import generate_wavefront_batch, prefill_once
+
+    cfg = M.CONFIGS["looped-2048-gqa"]
+    B, ctx, N = 4, 32768, 128
+    g = torch.Generator().manual_seed(0)
+    prompts = [torch.randint(0, cfg.vocab_size, (ctx,), generator=g).to(dev) for _ in range(B)]
+    model = LoopedModel(cfg, M.init_weights(cfg, 0), dev, max_seq_len=ctx + N + 16, max_batch=B,
+                        use_graphs=not args.eager)
+    bb = LoopedBlocksBatch(model, batch_size=B)
+    t0 = time.perf_counter()
+    pf = prefill_once(bb, prompts)
+    prefill_s = time.perf_counter() - t0
+    log(f"c5: prefill of {B} x {ctx} tokens in {prefill_s:.1f} s")
+    policy = SsdPolicy(cfg.T_total, 2)
+    generate_wavefront_batch(bb, prompts, [4] * B, policy, [EmulatedAcceptance(0.9, 1000 + b) for b in range(B)],
+                             prefilled=pf)  # warm-up (graph capture)
+    bt = generate_wavefront_batch(bb, prompts, N, policy, [EmulatedAcceptance(0.9, 1000 + b) for b in range(B)],
+                                  prefilled=pf)
+    res["extra"]["c5_long_context"] = {
+        "decode_tokens_per_s": round(bt.n_tokens / max(bt.walltime_decode_s, 1e-9), 1), "tokens": bt.n_tokens,
+        "r_ticks": bt.n_r_calls, "r_union_mean": round(bt.r_union_mean, 1), "acceptance": round(bt.acceptance_rate, 3),
+        "prefill_s": round(prefill_s, 2), "kv_cache_GB": round(pf.cache.nbytes / 1e9, 1),
+        "workload": "GQA 16q/4kv looped model, B=4 x 32768-token prompts, 128 new tokens each, T_total=32, "
+                    "T_draft=2 (W=16), emulated alpha 0.9; decode rate excludes prefill"}
+    log(f"c5: {res['extra']['c5_long_context']}")
+    del model, bb, pf
+    torch.cuda.empty_cache()
+
+
 def roofline_section(args, dev, res):
     """Dominant kernel of the decode tick: the weight-stream linear. The
     headline figure is its largest stream, the gate|up projection with the
@@ -511,6 +551,8 @@ def main():
         bs32_section(args, dev, res, w)
     if want("prefill"):
         prefill_section(args, dev, res)
+    if want("c5") and not args.quick:
+        c5_section(args, dev, res)
     if want("gqa"):
         gqa_section(args, dev, res)
     if want("cpu") and not args.no_cpu:

@@ -548,8 +548,8 @@ class LoopedModel:
         seg_l = (lambda s: (t64[2 * n_layers * L + s: 2 * n_layers * L + s + 1], t32[2 * L: 2 * L + 2],  # noqa: E731
                             t32[2 * L + 2: 2 * L + 3], L)) if flash else (lambda s: None)
         sc = self._scratch(L)
-        ws = torch.zeros(ops.attn_workspace_bytes(L, c.n_heads, c.head_dim, L), dtype=torch.uint8,
-                         device=self.device)
+        ws = None if flash else torch.zeros(ops.attn_workspace_bytes(L, c.n_heads, c.head_dim, L),
+                                            dtype=torch.uint8, device=self.device)
         logits = torch.empty(1, c.vocab_size, dtype=torch.float32, device=self.device)
         state = torch.empty(L, 2 * D, dtype=self.dtype, device=self.device)  # [s | e] per prompt row
         ops.embed(ids_d, W["wte"], c.emb_scale, out=sc["x"])
