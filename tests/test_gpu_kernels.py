@@ -214,13 +214,19 @@ def test_linear_swiglu_fp32_out_and_row_gather(gpu, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_linear_row_invariant(gpu, dtype):
-    """Row m of y is bit-identical for every batch size and position in the batch."""
+@pytest.mark.parametrize("N", [384, 4112, 11280])
+def test_linear_row_invariant(gpu, dtype, N):
+    """Row m of y is bit-identical for every batch size and position in the
+    batch, whichever kernel a row count selects. N = 24, 257 and 705 column
+    tiles: at 300 rows, per-wave weight streaming, then weights shared through
+    LDS 2 and 4 tiles per workgroup (both with a ragged tail)."""
     g = torch.Generator().manual_seed(5)
-    K, N = 2048, 384
+    K = 2048
+    print(f"[linear row invariance] dtype={dtype} N={N}", flush=True)
     X = torch.randn(300, K, generator=g).to(dtype).to(gpu)
     W = (0.02 * torch.randn(N, K, generator=g)).to(dtype).to(gpu)
     full = ops.linear(X, W)
+    assert rel_err(_np(full), ok.linear(_np(X), _np(W))) <= TOL[dtype]
     for n in (1, 5, 16, 17, 33, 64, 65, 300):
         part = ops.linear(X[:n].contiguous(), W)
         assert torch.equal(part, full[:n]), n

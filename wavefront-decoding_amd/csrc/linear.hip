@@ -57,6 +57,10 @@ constexpr int kWideMaxChunksPerWave = 3;
 constexpr int kWideMaxRows = 16;
 constexpr int kHalfTileMax = 256;  // wide launches of at most this many tiles use half tiles
 constexpr int kResidentWide = 512;  // 1024-thread workgroups resident at once (two per CU)
+// (64-row block, weight tile) pairs up to which a many-row launch lets each
+// wave stream its own weights (tile kernel) rather than share them through
+// LDS (gemm kernel): measured crossover on the 2048-d model's projections
+constexpr int kGemmMinBlockTiles = 512;
 enum Epilogue : int { kEpiPlain = 0, kEpiSwiGLU = 1, kEpiRope = 2 };
 
 // Operands of the QKV-RoPE-append epilogue (unused by the others).
@@ -349,6 +353,98 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ 
   }
 }
 
+// ---------------------------------------------------------------------------
+// gemm: grid (ceil(n/64), ceil(tiles/BT)), 256 threads; wave = 16 rows of x,
+// workgroup = 64 rows x BT weight tiles. Each chunk's BT weight tiles go
+// through LDS once (double-buffered: the next chunk's fragments load while
+// this one's MFMAs run) and all 4 waves read them there, so a weight byte
+// crosses L2 once per 64 rows instead of once per 16. Same per-chunk
+// arithmetic as the wide and tile kernels, so the same bits.
+template <typename T, typename TO, int EPI, int BT>
+__global__ __launch_bounds__(256) void linear_gemm_kernel(const T* __restrict__ x, const int32_t* __restrict__ x_rows,
+                                                          int64_t ldx, const T* __restrict__ W, TO* __restrict__ y,
+                                                          int64_t ldy, int n, int K, int pair_off, int tiles,
+                                                          const RopeArgs ra) {
+  constexpr int V = LinTraits<T>::V;
+  constexpr int FR = BT * kChunkSteps;  // 1 KB fragments per chunk: (tile, step)
+  constexpr int FPW = FR / 4;           // fragments each wave stages per chunk
+  __shared__ __align__(16) u32x4 wl[2][FR][64];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const int row0 = (blockIdx.x * 4 + wave) * 16;
+  const int P = K / LinTraits<T>::KC;
+  // a wave past the last row still stages weights and meets every barrier;
+  // its x loads read zeros and it stores nothing
+  const uint32_t xoff = row0 < n ? x_offset<T>(x_rows, ldx, row0, col, grp, n) : kBufInvalid;
+  const __amdgpu_buffer_rsrc_t xrs = buf_rsrc(x);
+
+  // the fragments this wave stages: f = wave * FPW + i -> (tile f / 4, step f % 4)
+  const T* wsrc[FPW];
+#pragma unroll
+  for (int i = 0; i < FPW; ++i) {
+    const int f = wave * FPW + i;
+    const int g = blockIdx.y * BT + f / kChunkSteps;
+    wsrc[i] = W + packed_off<T>(g < tiles ? g : tiles - 1, 0, P, lane) + (int64_t)(f % kChunkSteps) * 64 * V;
+  }
+  const int64_t pstride = (int64_t)kChunkSteps * 64 * V;  // elements from one chunk to the next in a tile
+  u32x4 wreg[FPW];
+  auto fetch_w = [&](int p) {
+#pragma unroll
+    for (int i = 0; i < FPW; ++i) wreg[i] = ld16(wsrc[i] + p * pstride);
+  };
+  auto stage_w = [&](int b) {
+#pragma unroll
+    for (int i = 0; i < FPW; ++i) wl[b][wave * FPW + i][lane] = wreg[i];
+  };
+
+  f32x4 tot[BT];
+#pragma unroll
+  for (int t = 0; t < BT; ++t) tot[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  u32x4 xa[kChunkSteps], xb[kChunkSteps];
+  fetch_w(0);
+  load_x<T>(xa, xrs, xoff, 0);
+  stage_w(0);
+  __syncthreads();
+  for (int p = 0; p < P; ++p) {
+    const int b = p & 1;
+    const int pn = p + 1 < P ? p + 1 : P - 1;  // every load unconditional: the last chunk re-reads itself
+    fetch_w(pn);
+    load_x<T>(xb, xrs, xoff, pn);
+    f32x4 acc[BT];
+#pragma unroll
+    for (int t = 0; t < BT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < kChunkSteps; ++st)
+#pragma unroll
+      for (int t = 0; t < BT; ++t) acc[t] = mfma_step<T>(xa[st], wl[b][t * kChunkSteps + st][lane], acc[t]);
+#pragma unroll
+    for (int t = 0; t < BT; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) tot[t][r] += acc[t][r];
+    stage_w(b ^ 1);  // that buffer was last read in chunk p - 1, before the barrier closing it
+    __syncthreads();
+#pragma unroll
+    for (int st = 0; st < kChunkSteps; ++st) xa[st] = xb[st];
+  }
+  if (row0 >= n) return;  // after the last barrier
+#pragma unroll
+  for (int t = 0; t < BT; ++t) {
+    const int g = blockIdx.y * BT + t;
+    if (g >= tiles) continue;  // uniform over the workgroup
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int orow = row0 + 4 * grp + r;
+      // column col ^ 1 lives in lane ^ 1, column col ^ 8 in lane ^ 8 (the whole wave takes part)
+      const float partner = EPI == kEpiRope     ? __shfl_xor(tot[t][r], 1, 64)
+                            : EPI == kEpiSwiGLU ? __shfl_xor(tot[t][r], 8, 64)
+                                                : 0.f;
+      if (orow < n) store_out<TO, EPI>(y, ldy, ra, orow, g, col, tot[t][r], partner);
+    }
+  }
+}
+
 template <typename T, typename TO, int EPI>
 static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const void* W, void* y, int64_t ldy, int n,
                           int N, int K, int pair_off, const RopeArgs& ra, hipStream_t st) {
@@ -391,9 +487,22 @@ static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const v
   } else {
 #undef WFD_WIDE8
 #undef WFD_WIDE
-    constexpr int NB = 2;
-    hipLaunchKernelGGL((linear_tile_kernel<T, TO, EPI, NB>), dim3((n + 63) / 64, (tiles + NB - 1) / NB), dim3(256),
-                       0, st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra);
+    const int rb = (n + 63) / 64;
+    if (rb * tiles <= kGemmMinBlockTiles) {
+      // few (row block, tile) pairs: every wave streams its own weights, no barriers
+      constexpr int NB = 2;
+      hipLaunchKernelGGL((linear_tile_kernel<T, TO, EPI, NB>), dim3(rb, (tiles + NB - 1) / NB), dim3(256), 0, st,
+                         (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra);
+      return;
+    }
+    // weights through LDS, shared by the 4 waves: 4 tiles per workgroup
+    // while that still leaves >= 512 workgroups, else 2 (>= 256 of them)
+    if (rb * ((tiles + 3) / 4) >= 512)
+      hipLaunchKernelGGL((linear_gemm_kernel<T, TO, EPI, 4>), dim3(rb, (tiles + 3) / 4), dim3(256), 0, st,
+                         (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra);
+    else
+      hipLaunchKernelGGL((linear_gemm_kernel<T, TO, EPI, 2>), dim3(rb, (tiles + 1) / 2), dim3(256), 0, st,
+                         (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra);
   }
 }
 
