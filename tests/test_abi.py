@@ -33,7 +33,7 @@ def test_host_only_entry_points():
     lib = _lib.load()
     assert lib.wfd_abi_version() == 3
     assert [lib.wfd_attn_group_max_rows(16, k) for k in (16, 8, 4, 3)] == [8, 4, 2, 0]
-    assert lib.wfd_attn_split_keys() == 2048
+    assert lib.wfd_attn_split_keys() == 1024
     assert lib.wfd_linear_k_multiple(_lib.BF16) == 128 and lib.wfd_linear_k_multiple(_lib.F32) == 64
     # workspace: n*H*splits*(Dh + 2) floats, each array 256-byte aligned
     assert lib.wfd_attn_workspace_bytes(8, 16, 64, 1024) == 8 * 16 * 1 * 64 * 4 + 8 * 16 * 1 * 2 * 4

@@ -142,10 +142,12 @@ def test_attn_prefill_matches_oracle(gpu, H, Hkv, Dh, segs, blocks):
 def test_attn_decode_grouped_rows_same_bits(gpu, dtype, H, Hkv, Dh):
     """Rows that share a slot, grouped (one prefix read per group), give the
     ungrouped rows' bits exactly -- ragged lengths inside a group, groups that
-    straddle the 2048-key split, a 1-row group, and the oracle agrees."""
+    straddle the 1024- and 2048-key split edges, a 1-row group, and the oracle
+    agrees."""
     gmax = ops.attn_group_max_rows(H, Hkv)
     g = torch.Generator().manual_seed(H * 3 + Hkv + Dh)
-    groups = [[700, 701, 702, 650], [50], [2040, 2048, 2049, 3000, 10, 2100, 1, 4100][:gmax], [2047, 2048][:gmax]]
+    groups = [[700, 701, 702, 650], [50], [2040, 2048, 2049, 3000, 10, 2100, 1, 4100][:gmax], [2047, 2048][:gmax],
+              [1023, 1024, 1025, 1026][:gmax]]
     S = 4200
     n_slots = len(groups) + 1
     K = torch.randn(n_slots * S, Hkv, Dh, generator=g).to(dtype)
