@@ -216,12 +216,13 @@ def test_linear_swiglu_fp32_out_and_row_gather(gpu, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("N", [384, 4112, 11280])
+@pytest.mark.parametrize("N", [384, 4096, 4112, 11280])
 def test_linear_row_invariant(gpu, dtype, N):
     """Row m of y is bit-identical for every batch size and position in the
-    batch, whichever kernel a row count selects. N = 24, 257 and 705 column
-    tiles: at 300 rows, per-wave weight streaming, then weights shared through
-    LDS 2 and 4 tiles per workgroup (both with a ragged tail)."""
+    batch, whichever kernel a row count selects. N = 24, 256, 257 and 705
+    column tiles: at 300 rows, the LDS-pipelined stream kernel with 1 and 2
+    tiles per workgroup, then weights shared through LDS 2 and 4 tiles per
+    workgroup (both with a ragged tail); gathered rows at 3 and 40 rows."""
     g = torch.Generator().manual_seed(5)
     K = 2048
     print(f"[linear row invariance] dtype={dtype} N={N}", flush=True)
@@ -233,6 +234,9 @@ def test_linear_row_invariant(gpu, dtype, N):
         part = ops.linear(X[:n].contiguous(), W)
         assert torch.equal(part, full[:n]), n
     rows = torch.tensor([299, 0, 150], dtype=torch.int32, device=gpu)
+    gathered = ops.linear(X, W, x_rows=rows)
+    assert torch.equal(gathered, full[rows.long()])
+    rows = torch.randperm(300, generator=g)[:40].to(torch.int32).to(gpu)
     gathered = ops.linear(X, W, x_rows=rows)
     assert torch.equal(gathered, full[rows.long()])
     sw = torch.cat([W, W.flip(0)])

@@ -61,6 +61,10 @@ constexpr int kResidentWide = 512;  // 1024-thread workgroups resident at once (
 // wave stream its own weights (tile kernel) rather than share them through
 // LDS (gemm kernel): measured crossover on the 2048-d model's projections
 constexpr int kGemmMinBlockTiles = 512;
+// Launches of at most this many weight tiles (2048 output columns) use the
+// stream kernel, with this many LDS stages
+constexpr int kStreamMaxTiles = 256;
+constexpr int kStreamStages = 4;
 enum Epilogue : int { kEpiPlain = 0, kEpiSwiGLU = 1, kEpiRope = 2 };
 
 // Operands of the QKV-RoPE-append epilogue (unused by the others).
@@ -445,6 +449,149 @@ __global__ __launch_bounds__(256) void linear_gemm_kernel(const T* __restrict__ 
   }
 }
 
+// ---------------------------------------------------------------------------
+// stream: grid (ceil(n/64), ceil(tiles/BT)), 256 threads; wave = 16 rows of x,
+// workgroup = 64 rows x BT weight tiles. Weights and x move global -> LDS
+// with the 16-byte direct-to-LDS load (lane l's 16 bytes land at the wave's
+// LDS base + 16 l), NS - 1 chunks ahead of the MFMAs, through a ring of NS
+// LDS stages: no registers hold data in flight, so the depth of the pipeline
+// costs LDS, not VGPRs, and a K-sequential workgroup keeps NS - 1 chunks of
+// loads outstanding instead of paying the memory latency once per chunk. The
+// weight tiles of a stage are read by all 4 waves; each wave reads only its
+// own x rows. Same per-chunk arithmetic as the other kernels, same bits.
+//
+// Ordering (per wave; vector-memory loads complete in issue order): before
+// the barrier of chunk p a wave waits until only the loads of the chunks
+// after p remain; the barrier then publishes every wave's chunk p, and
+// retires every wave's reads of chunk p - 1, whose stage the loads of chunk
+// p + NS - 1 issued right after it overwrite.
+// The loads are issued through inline assembly so that the compiler, which
+// does not know they write LDS, adds no wait of its own before the LDS reads
+// (it would wait for every outstanding load); the waits are the explicit ones
+// below. M0 holds the wave's LDS byte address; one wait state separates its
+// write from the load that reads it.
+__device__ __forceinline__ void load16_lds(const void* src, const u32x4* lds_wave_base) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_wave_base;
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src) : "memory", "m0");
+}
+
+// Wait until at most N of this wave's loads are outstanding and its LDS reads
+// have completed, then the workgroup barrier.
+template <int N>
+__device__ __forceinline__ void wait_vmem_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// Row pointer of lane `col` in the 16-row block at `base` (lane group grp's
+// first element); padding lanes (col >= rows left) take the block's first
+// row: their MFMA rows are never stored and never mix with real rows.
+template <typename T>
+__device__ __forceinline__ const T* x_row_ptr(const T* __restrict__ x, const int32_t* __restrict__ x_rows,
+                                              int64_t ldx, int base, int col, int grp, int n) {
+  const int m = n - base < 16 ? n - base : 16;
+  int r = base + (col < m ? col : 0);
+  if (x_rows) {
+    int v0 = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int v = x_rows[base + (j < m ? j : 0)];
+      v0 = (col < m ? col : 0) == j ? v : v0;
+    }
+    r = v0;
+  }
+  return x + (int64_t)r * ldx + grp * Chunk<T>::V;
+}
+
+template <typename T, typename TO, int EPI, int BT, int NS>
+__global__ __launch_bounds__(256) void linear_stream_kernel(const T* __restrict__ x, const int32_t* __restrict__ x_rows,
+                                                            int64_t ldx, const T* __restrict__ W, TO* __restrict__ y,
+                                                            int64_t ldy, int n, int K, int pair_off, int tiles,
+                                                            const RopeArgs ra) {
+  constexpr int V = LinTraits<T>::V;
+  constexpr int KSTEP = LinTraits<T>::KSTEP;
+  constexpr int KC = LinTraits<T>::KC;
+  constexpr int FR = BT * kChunkSteps;   // weight fragments (tile, step) per chunk, 1 KB each
+  constexpr int FPW = BT;                // of which each wave loads FR / 4
+  constexpr int LW = FPW;                // loads per chunk of a wave without rows
+  constexpr int LX = FPW + kChunkSteps;  // ... and of a wave with rows
+  __shared__ __align__(16) u32x4 wst[NS][FR][64];
+  __shared__ __align__(16) u32x4 xst[NS][4][kChunkSteps][64];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const int row0 = (blockIdx.x * 4 + wave) * 16;
+  const bool rows = row0 < n;  // uniform over the wave
+  const int P = K / KC;
+  const T* xsrc = rows ? x_row_ptr<T>(x, x_rows, ldx, row0, col, grp, n) : x;
+  const T* wsrc[FPW];
+#pragma unroll
+  for (int i = 0; i < FPW; ++i) {
+    const int f = wave * FPW + i;
+    const int g = blockIdx.y * BT + f / kChunkSteps;
+    wsrc[i] = W + packed_off<T>(g < tiles ? g : tiles - 1, 0, P, lane) + (int64_t)(f % kChunkSteps) * 64 * V;
+  }
+  const int64_t pstride = (int64_t)kChunkSteps * 64 * V;
+  auto issue = [&](int p) {
+    const int st = p % NS;
+#pragma unroll
+    for (int i = 0; i < FPW; ++i) load16_lds(wsrc[i] + p * pstride, &wst[st][wave * FPW + i][0]);
+    if (rows) {
+#pragma unroll
+      for (int s = 0; s < kChunkSteps; ++s) load16_lds(xsrc + (int64_t)p * KC + s * KSTEP, &xst[st][wave][s][0]);
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < NS - 1; ++u)
+    if (u < P) issue(u);
+
+  f32x4 tot[BT];
+#pragma unroll
+  for (int t = 0; t < BT; ++t) tot[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int p = 0; p < P; ++p) {
+    // this wave's chunk p is in LDS once at most the later chunks' loads are outstanding
+    if (p + NS - 2 < P) {
+      if (rows) wait_vmem_barrier<(NS - 2) * LX>();
+      else wait_vmem_barrier<(NS - 2) * LW>();
+    } else {
+      wait_vmem_barrier<0>();
+    }
+    if (p + NS - 1 < P) issue(p + NS - 1);
+    if (rows) {
+      const int st = p % NS;
+      f32x4 acc[BT];
+#pragma unroll
+      for (int t = 0; t < BT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < kChunkSteps; ++s) {
+        const u32x4 xf = xst[st][wave][s][lane];
+#pragma unroll
+        for (int t = 0; t < BT; ++t) acc[t] = mfma_step<T>(xf, wst[st][t * kChunkSteps + s][lane], acc[t]);
+      }
+#pragma unroll
+      for (int t = 0; t < BT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) tot[t][r] += acc[t][r];
+    }
+  }
+  if (!rows) return;  // after the last barrier; every load of this wave has completed
+#pragma unroll
+  for (int t = 0; t < BT; ++t) {
+    const int g = blockIdx.y * BT + t;
+    if (g >= tiles) continue;  // uniform over the workgroup
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int orow = row0 + 4 * grp + r;
+      // column col ^ 1 lives in lane ^ 1, column col ^ 8 in lane ^ 8 (the whole wave takes part)
+      const float partner = EPI == kEpiRope     ? __shfl_xor(tot[t][r], 1, 64)
+                            : EPI == kEpiSwiGLU ? __shfl_xor(tot[t][r], 8, 64)
+                                                : 0.f;
+      if (orow < n) store_out<TO, EPI>(y, ldy, ra, orow, g, col, tot[t][r], partner);
+    }
+  }
+}
+
 template <typename T, typename TO, int EPI>
 static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const void* W, void* y, int64_t ldy, int n,
                           int N, int K, int pair_off, const RopeArgs& ra, hipStream_t st) {
@@ -488,6 +635,18 @@ static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const v
 #undef WFD_WIDE8
 #undef WFD_WIDE
     const int rb = (n + 63) / 64;
+    if (tiles <= kStreamMaxTiles) {
+      // few weight tiles: each workgroup walks all of K, so its chunk chain is
+      // the launch's critical path; keep kStreamStages - 1 chunks in flight.
+      // Two tiles per workgroup while that still leaves >= 256 workgroups.
+      if (rb * ((tiles + 1) / 2) >= 256)
+        hipLaunchKernelGGL((linear_stream_kernel<T, TO, EPI, 2, kStreamStages>), dim3(rb, (tiles + 1) / 2), dim3(256),
+                           0, st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra);
+      else
+        hipLaunchKernelGGL((linear_stream_kernel<T, TO, EPI, 1, kStreamStages>), dim3(rb, tiles), dim3(256), 0, st,
+                           (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra);
+      return;
+    }
     if (rb * tiles <= kGemmMinBlockTiles) {
       // few (row block, tile) pairs: every wave streams its own weights, no barriers
       constexpr int NB = 2;
