@@ -14,41 +14,54 @@
 // row's causal prefix of (q_r . k) * scale, times V.
 //
 // Work split: a workgroup of 4 waves owns 128 consecutive query rows of one
-// segment and one query head; wave w owns rows 32w..32w+31 as two blocks of
-// 16, one query per lane column in each. Per 64-key tile the workgroup stages
-// K (row-major) and V (transposed, d-major) in LDS, with the next tile's
-// global loads (32-bit buffer offsets, nothing read past the segment's last
-// key) issued before the current tile's math so their latency hides under
-// it. Each wave computes S^T = K Q^T on v_mfma_f32_16x16x32_bf16 -- every K
-// fragment read from LDS feeds both query blocks -- so a lane holds 16 of its
-// query's 64 scores: the online softmax needs two shuffles per statistic (the
-// scale folds into the exponent's FMA), and P stays in registers as the B
-// operand of O^T = V^T P^T (the k order inside an MFMA step only has to agree
-// between A and B; each V^T fragment again feeds both blocks). The lane's
-// output column is its own query, so the softmax rescale needs no exchange.
-// Tiles past the diagonal are never visited; the diagonal tiles mask keys
-// past each row's position (tiles below them skip the mask). Query tiles are
-// dispatched longest first.
+// segment and one query head; wave w owns rows 32w..32w+31, one query per
+// lane column of the 32x32 MFMA tiles. Per 64-key tile the workgroup stages K
+// (row-major) and V (transposed, d-major) in LDS, with the next tile's global
+// loads (32-bit buffer offsets, nothing read past the segment's last key)
+// issued before the current tile's math so their latency hides under it.
+// Each wave computes S^T = K Q^T on v_mfma_f32_32x32x16_bf16 (two 32-key
+// blocks x Dh/16 steps), then O^T = V^T P^T on the same instruction. Against
+// 16-query blocks on the 16x16x32 MFMA this halves the LDS bytes read per
+// flop: every K and V^T fragment a wave reads feeds 32 queries.
+//
+// Key order inside a 32-key block: MFMA row r (lane half hf = lane / 32 holds
+// rows 8i + 4hf + j, i, j < 4) reads K row pi(r) = 16(i / 2) + 8hf + 4(i % 2)
+// + j, so result register rr of a lane holds key 16(rr / 8) + 8hf + rr % 8 --
+// exactly the 8 consecutive keys the B operand of a 16-key P^T step wants in
+// that lane. P thus goes from the S^T accumulators to the B operand of
+// O^T = V^T P^T by packing to bf16, with no exchange, and the V^T fragment of
+// the same lane half is 8 consecutive keys of one d row (one 16-byte LDS
+// read). A lane's output column is its query, so the online softmax's max and
+// sum need one shuffle (the other lane half) and the rescale none; the scale
+// folds into the exponent's FMA. Tiles past the diagonal are never visited;
+// the diagonal tiles mask keys past each row's position (tiles below them
+// skip the mask). Query tiles are dispatched longest first.
 #include "wfd_common.h"
 
 namespace wfd {
 
-constexpr int kPfWaves = 8;
-constexpr int kPfQB = 1;                        // 16-query blocks per wave
-constexpr int kPfRows = 16 * kPfQB * kPfWaves;  // query rows per workgroup
-constexpr int kPfKeys = 64;                     // keys per tile
+constexpr int kPfWaves = 4;
+constexpr int kPfRows = 32 * kPfWaves;  // query rows per workgroup
+constexpr int kPfKeys = 64;             // keys per tile
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, f32x16 acc) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), acc,
+                                                 0, 0, 0);
+}
 
 template <int DH>
-__global__ __launch_bounds__(64 * kPfWaves) void attn_prefill_kernel(
+__global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2))) void attn_prefill_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ kc, const bf16_t* __restrict__ vc, int64_t block_rows,
     const int64_t* __restrict__ seg_row_base, const int32_t* __restrict__ seg_q_start,
     const int32_t* __restrict__ seg_pos0, bf16_t* __restrict__ out, int H, int Hkv, float scale_log2) {
   constexpr int NT = 64 * kPfWaves;   // threads
   constexpr int V = 8;                // bf16 per 16-byte fragment
-  constexpr int NDS = DH / 32;        // MFMA k-steps over Dh (S^T = K Q^T)
-  constexpr int NDB = DH / 16;        // 16-row blocks of O^T (head dim)
-  constexpr int NKB = kPfKeys / 16;   // 16-key blocks of S^T
-  constexpr int NPS = kPfKeys / 32;   // MFMA k-steps over keys (O^T += V^T P^T)
+  constexpr int NDS = DH / 16;        // MFMA k-steps over Dh (S^T = K Q^T)
+  constexpr int NDB = DH / 32;        // 32-row blocks of O^T (head dim)
+  constexpr int NKB = kPfKeys / 32;   // 32-key blocks of S^T
+  constexpr int NPS = kPfKeys / 16;   // MFMA k-steps over keys (O^T += V^T P^T)
   constexpr int KP = DH + 8;          // padded LDS row of K (elements)
   constexpr int VP = kPfKeys + 8;     // padded LDS row of V^T
   constexpr int CPR = DH / V;         // 16-byte chunks per K row
@@ -57,8 +70,8 @@ __global__ __launch_bounds__(64 * kPfWaves) void attn_prefill_kernel(
   constexpr int VCH = VUN >= NT ? VUN / NT : 1;  // ... per thread (fewer chunks than threads: the first waves)
   static_assert(KCH >= 1 && kPfKeys * CPR % NT == 0 && (VUN % NT == 0 || NT % VUN == 0), "tile split");
   static_assert(VUN >= NT || VUN % 64 == 0, "V staging must be wave-uniform");
-  __shared__ __align__(16) bf16_t k_lds[kPfKeys * KP];
-  __shared__ __align__(16) bf16_t vt_lds[DH * VP];
+  __shared__ __align__(16) bf16_t k_lds[2][kPfKeys * KP];  // double-buffered: one barrier per tile
+  __shared__ __align__(16) bf16_t vt_lds[2][DH * VP];
 
   const int s = blockIdx.z;
   const int h = blockIdx.y;
@@ -73,9 +86,9 @@ __global__ __launch_bounds__(64 * kPfWaves) void attn_prefill_kernel(
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const int col = lane & 15;
-  const int grp = lane >> 4;
-  const int row0 = tq * kPfRows + wave * 16 * kPfQB;
+  const int col = lane & 31;  // query of this lane
+  const int hf = lane >> 5;   // lane half
+  const int row0 = tq * kPfRows + wave * 32;
   const int last_row = min((tq + 1) * kPfRows, len) - 1;
   const int kv_hi = pos0 + last_row + 1;  // keys [0, kv_hi) cover every row of the tile
   const int ntiles = (kv_hi + kPfKeys - 1) / kPfKeys;
@@ -87,15 +100,16 @@ __global__ __launch_bounds__(64 * kPfWaves) void attn_prefill_kernel(
   const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(vc + hb), (short)0, span,
                                                                       0x00020000);
 
-  // Q as the MFMA B operand: column col of block qb = query row0 + 16 qb + col, k-group grp
-  u32x4 qf[kPfQB][NDS];
+  // Q as the MFMA B operand: column col = query row0 + col, dims 16k + 8hf + (0..7)
+  u32x4 qf[NDS];
+  {
+    const int r = min(row0 + col, len - 1);
+    const bf16_t* qp = q + ((int64_t)(q0 + r) * H + h) * DH + hf * V;
 #pragma unroll
-  for (int qb = 0; qb < kPfQB; ++qb) {
-    const int r = min(row0 + 16 * qb + col, len - 1);
-    const bf16_t* qp = q + ((int64_t)(q0 + r) * H + h) * DH + grp * V;
-#pragma unroll
-    for (int k = 0; k < NDS; ++k) qf[qb][k] = ld16(qp + k * 32);
+    for (int k = 0; k < NDS; ++k) qf[k] = ld16(qp + k * 16);
   }
+  // K row of MFMA row col within a 32-key block (the permutation above)
+  const int krow = 16 * ((col >> 3) >> 1) + 8 * ((col >> 2) & 1) + 4 * ((col >> 3) & 1) + (col & 3);
 
   // staging: thread's K chunks (key, 8 dims) and V key-pair chunks (2 keys, 8 dims)
   u32x4 kreg[KCH], vreg[VCH][2];
@@ -116,14 +130,14 @@ __global__ __launch_bounds__(64 * kPfWaves) void attn_prefill_kernel(
       vreg[i][1] = buf_ld16(vr, off + rsb);
     }
   };
-  auto stage = [&]() {
+  auto stage = [&](int b) {
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
       const int c = threadIdx.x + i * NT;
       const int kr_ = c / CPR;
-      *reinterpret_cast<u32x4*>(&k_lds[kr_ * KP + (c - kr_ * CPR) * V]) = kreg[i];
+      *reinterpret_cast<u32x4*>(&k_lds[b][kr_ * KP + (c - kr_ * CPR) * V]) = kreg[i];
     }
-    uint32_t* vt = reinterpret_cast<uint32_t*>(vt_lds);
+    uint32_t* vt = reinterpret_cast<uint32_t*>(vt_lds[b]);
 #pragma unroll
     for (int i = 0; i < VCH; ++i) {
       const int c = threadIdx.x + i * NT;
@@ -139,115 +153,114 @@ __global__ __launch_bounds__(64 * kPfWaves) void attn_prefill_kernel(
     }
   };
 
-  float mrun[kPfQB], lrun[kPfQB];
-  f32x4 o[kPfQB][NDB];
+  float mrun = -INFINITY, lrun = 0.f;
+  f32x16 o[NDB];
 #pragma unroll
-  for (int qb = 0; qb < kPfQB; ++qb) {
-    mrun[qb] = -INFINITY;
-    lrun[qb] = 0.f;
+  for (int c = 0; c < NDB; ++c)
 #pragma unroll
-    for (int c = 0; c < NDB; ++c) o[qb][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
+    for (int r = 0; r < 16; ++r) o[c][r] = 0.f;
+  const int qpos = pos0 + row0 + col;
 
+  // tile t lives in buffer t & 1; the registers hold tile t + 1 while tile t
+  // is computed, and are staged into the other buffer after it (that buffer
+  // was last read in tile t - 1, before the barrier that closed it)
   fetch(0);
+  stage(0);
+  fetch(kPfKeys);
+  __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
     const int k0 = t * kPfKeys;
-    stage();
-    __syncthreads();
-    fetch(k0 + kPfKeys);  // next tile (zeros past the last key): in flight under this tile's math
+    const int b = t & 1;
     // keys past some row's position only in the diagonal tiles (uniform per wave)
     const bool full = k0 + kPfKeys - 1 <= pos0 + row0;
 
-    // S^T = K Q^T: lane holds S[query 16 qb + col][key k0 + 16 cb + 4 grp + r]
-    f32x4 sacc[kPfQB][NKB];
+    // S^T = K Q^T: register rr of block kb holds S[query col][key k0 + 32 kb + 16 (rr / 8) + 8 hf + rr % 8]
+    f32x16 sacc[NKB];
 #pragma unroll
-    for (int cb = 0; cb < NKB; ++cb) {
+    for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
-      for (int qb = 0; qb < kPfQB; ++qb) sacc[qb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
 #pragma unroll
       for (int k = 0; k < NDS; ++k) {
-        const u32x4 afr = *reinterpret_cast<const u32x4*>(&k_lds[(16 * cb + col) * KP + 32 * k + grp * V]);
-#pragma unroll
-        for (int qb = 0; qb < kPfQB; ++qb) sacc[qb][cb] = mfma_step<bf16_t>(afr, qf[qb][k], sacc[qb][cb]);
+        const u32x4 afr = *reinterpret_cast<const u32x4*>(&k_lds[b][(32 * kb + krow) * KP + 16 * k + hf * V]);
+        sacc[kb] = mfma32(afr, qf[k], sacc[kb]);
       }
     }
-    // online softmax per query (log2 domain: p = 2^(s * scale_log2 - m)); the
-    // first tile holds key 0 for every row, so m is finite from then on and
-    // masked scores (-inf) give p = 0 without a test
-    u32x4 pb[kPfQB][NPS];
-    float corr[kPfQB];
+    // online softmax (log2 domain: p = 2^(s * scale_log2 - m)); the first tile
+    // holds key 0 for every row, so m is finite from then on and masked
+    // scores (-inf) give p = 0 without a test
+    if (!full) {  // a diagonal tile (uniform over the wave)
 #pragma unroll
-    for (int qb = 0; qb < kPfQB; ++qb) {
-      const int qpos = pos0 + row0 + 16 * qb + col;
-      float mt = -INFINITY;
+      for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-      for (int cb = 0; cb < NKB; ++cb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          if (!full && k0 + 16 * cb + 4 * grp + r > qpos) sacc[qb][cb][r] = -INFINITY;
-          mt = fmaxf(mt, sacc[qb][cb][r]);
-        }
-      mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-      const float mnew = fmaxf(mrun[qb], mt * scale_log2);
-      corr[qb] = exp2f(mrun[qb] - mnew);
-      float lt = 0.f;
-#pragma unroll
-      for (int cb = 0; cb < NKB; ++cb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float p = exp2f(fmaf(sacc[qb][cb][r], scale_log2, -mnew));
-          sacc[qb][cb][r] = p;
-          lt += p;
-        }
-      lt += __shfl_xor(lt, 16, 64);
-      lt += __shfl_xor(lt, 32, 64);
-      lrun[qb] = fmaf(lrun[qb], corr[qb], lt);
-      mrun[qb] = mnew;
-      // P^T as the B operand of step k: keys k0 + 32k + 4grp + (0..3) then
-      // k0 + 32k + 16 + 4grp + (0..3) -- the order the V^T fragments use below
-#pragma unroll
-      for (int k = 0; k < NPS; ++k) {
-        pb[qb][k][0] = f32x2_to_bf16x2_bits(sacc[qb][2 * k][0], sacc[qb][2 * k][1]);
-        pb[qb][k][1] = f32x2_to_bf16x2_bits(sacc[qb][2 * k][2], sacc[qb][2 * k][3]);
-        pb[qb][k][2] = f32x2_to_bf16x2_bits(sacc[qb][2 * k + 1][0], sacc[qb][2 * k + 1][1]);
-        pb[qb][k][3] = f32x2_to_bf16x2_bits(sacc[qb][2 * k + 1][2], sacc[qb][2 * k + 1][3]);
-      }
+        for (int r = 0; r < 16; ++r)
+          if (k0 + 32 * kb + 16 * (r >> 3) + 8 * hf + (r & 7) > qpos) sacc[kb][r] = -INFINITY;
     }
-    // O^T = O^T * corr + V^T P^T: lane holds O[query 16 qb + col][d = 16 db + 4 grp + r]
+    float mt = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[kb][r]);
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float mnew = fmaxf(mrun, mt * scale_log2);
+    // the hardware 2^x (v_exp_f32): results below 2^-126 flush to zero, which
+    // only drops probabilities far below bf16 resolution of the row's sum
+    const float corr = __builtin_amdgcn_exp2f(mrun - mnew);
+    float lt = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(sacc[kb][r], scale_log2, -mnew));
+        sacc[kb][r] = p;
+        lt += p;
+      }
+    lt += __shfl_xor(lt, 32, 64);
+    lrun = fmaf(lrun, corr, lt);
+    mrun = mnew;
+    // P^T as the B operand of key step k: keys k0 + 16k + 8hf + (0..7)
+    u32x4 pb[NPS];
+#pragma unroll
+    for (int k = 0; k < NPS; ++k)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        pb[k][e] = f32x2_to_bf16x2_bits(sacc[k >> 1][8 * (k & 1) + 2 * e], sacc[k >> 1][8 * (k & 1) + 2 * e + 1]);
+    // O^T = O^T * corr + V^T P^T: register rr of block db holds O[query col][d = 32 db + 8 (rr / 4) + 4 hf + rr % 4];
+    // once the running maxima settle most tiles change none of the wave's (corr == 1 exactly)
+    if (__builtin_amdgcn_ballot_w64(corr != 1.f)) {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= corr;
+    }
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
 #pragma unroll
-      for (int qb = 0; qb < kPfQB; ++qb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) o[qb][db][r] *= corr[qb];
-#pragma unroll
       for (int k = 0; k < NPS; ++k) {
-        const bf16_t* vp = &vt_lds[(16 * db + col) * VP + 32 * k + 4 * grp];
-        const uint2 lo = *reinterpret_cast<const uint2*>(vp);
-        const uint2 hi = *reinterpret_cast<const uint2*>(vp + 16);
-        const u32x4 afr = {lo.x, lo.y, hi.x, hi.y};
-#pragma unroll
-        for (int qb = 0; qb < kPfQB; ++qb) o[qb][db] = mfma_step<bf16_t>(afr, pb[qb][k], o[qb][db]);
+        const u32x4 afr = *reinterpret_cast<const u32x4*>(&vt_lds[b][(32 * db + col) * VP + 16 * k + 8 * hf]);
+        o[db] = mfma32(afr, pb[k], o[db]);
       }
     }
-    __syncthreads();  // K / V^T are restaged by the next tile
+    if (t + 1 < ntiles) {  // uniform
+      stage(b ^ 1);
+      fetch(k0 + 2 * kPfKeys);  // zeros past the last key
+    }
+    __syncthreads();
   }
 
+  const int row = row0 + col;
+  if (row < len) {
+    const float inv = lrun > 0.f ? 1.f / lrun : 0.f;
+    bf16_t* op = out + ((int64_t)(q0 + row) * H + h) * DH + 4 * hf;
 #pragma unroll
-  for (int qb = 0; qb < kPfQB; ++qb) {
-    const int row = row0 + 16 * qb + col;
-    if (row < len) {
-      const float inv = lrun[qb] > 0.f ? 1.f / lrun[qb] : 0.f;
-      bf16_t* op = out + ((int64_t)(q0 + row) * H + h) * DH + 4 * grp;
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) {
+      for (int i = 0; i < 4; ++i) {
         uint2 w;
-        w.x = f32x2_to_bf16x2_bits(o[qb][db][0] * inv, o[qb][db][1] * inv);
-        w.y = f32x2_to_bf16x2_bits(o[qb][db][2] * inv, o[qb][db][3] * inv);
-        *reinterpret_cast<uint2*>(op + 16 * db) = w;
+        w.x = f32x2_to_bf16x2_bits(o[db][4 * i] * inv, o[db][4 * i + 1] * inv);
+        w.y = f32x2_to_bf16x2_bits(o[db][4 * i + 2] * inv, o[db][4 * i + 3] * inv);
+        *reinterpret_cast<uint2*>(op + 32 * db + 8 * i) = w;
       }
-    }
   }
 }
 
