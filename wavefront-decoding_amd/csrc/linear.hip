@@ -358,14 +358,39 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------
-// gemm: grid (ceil(n/64), ceil(tiles/BT)), 256 threads; wave = 16 rows of x,
+// XCD-aware work mapping for the many-row kernels. Workgroups are handed to
+// the 8 XCDs round-robin by linear id, and each XCD has its own L2. The row
+// blocks that share a group of weight tiles are put on one XCD, so the group's
+// weights cross the fabric once and the other row blocks read them from that
+// XCD's L2 (with the plain 2-D grid they land on R different XCDs and every
+// weight byte crosses the fabric R = ceil(n / 64) times). Linear id i:
+// XCD i % 8, j = i / 8, row block j % R, tile group (j / R) * 8 + i % 8; the
+// grid is R x (tile groups rounded up to 8) and the padding ids return.
+constexpr int kXcds = 8;
+
+__host__ __device__ constexpr int xcd_grid(int rb, int groups) {
+  return rb * ((groups + kXcds - 1) / kXcds) * kXcds;
+}
+
+template <int BT>
+__device__ __forceinline__ bool xcd_block(int n, int tiles, int& rbk, int& tg) {
+  const int R = (n + 63) / 64;
+  const int i = blockIdx.x;
+  const int j = i / kXcds;
+  rbk = j % R;
+  tg = (j / R) * kXcds + i % kXcds;
+  return tg * BT < tiles;
+}
+
+// gemm: grid xcd_grid(ceil(n/64), ceil(tiles/BT)), 256 threads; wave = 16 rows of x,
 // workgroup = 64 rows x BT weight tiles. Each chunk's BT weight tiles go
-// through LDS once (double-buffered: the next chunk's fragments load while
-// this one's MFMAs run) and all 4 waves read them there, so a weight byte
-// crosses L2 once per 64 rows instead of once per 16. Same per-chunk
+// through LDS once (double-buffered) and all 4 waves read them there, so a
+// weight byte crosses L2 once per 64 rows instead of once per 16. Weights and
+// x are loaded into registers two chunks ahead of their use, so a chunk's
+// memory latency overlaps the MFMAs of the two before it. Same per-chunk
 // arithmetic as the wide and tile kernels, so the same bits.
 template <typename T, typename TO, int EPI, int BT>
-__global__ __launch_bounds__(256) void linear_gemm_kernel(const T* __restrict__ x, const int32_t* __restrict__ x_rows,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void linear_gemm_kernel(const T* __restrict__ x, const int32_t* __restrict__ x_rows,
                                                           int64_t ldx, const T* __restrict__ W, TO* __restrict__ y,
                                                           int64_t ldy, int n, int K, int pair_off, int tiles,
                                                           const RopeArgs ra) {
@@ -373,11 +398,13 @@ __global__ __launch_bounds__(256) void linear_gemm_kernel(const T* __restrict__ 
   constexpr int FR = BT * kChunkSteps;  // 1 KB fragments per chunk: (tile, step)
   constexpr int FPW = FR / 4;           // fragments each wave stages per chunk
   __shared__ __align__(16) u32x4 wl[2][FR][64];
+  int rbk, tg;
+  if (!xcd_block<BT>(n, tiles, rbk, tg)) return;  // padding workgroup (uniform, before any barrier)
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int col = lane & 15;
   const int grp = lane >> 4;
-  const int row0 = (blockIdx.x * 4 + wave) * 16;
+  const int row0 = (rbk * 4 + wave) * 16;
   const int P = K / LinTraits<T>::KC;
   // a wave past the last row still stages weights and meets every barrier;
   // its x loads read zeros and it stores nothing
@@ -389,53 +416,79 @@ __global__ __launch_bounds__(256) void linear_gemm_kernel(const T* __restrict__ 
 #pragma unroll
   for (int i = 0; i < FPW; ++i) {
     const int f = wave * FPW + i;
-    const int g = blockIdx.y * BT + f / kChunkSteps;
+    const int g = tg * BT + f / kChunkSteps;
     wsrc[i] = W + packed_off<T>(g < tiles ? g : tiles - 1, 0, P, lane) + (int64_t)(f % kChunkSteps) * 64 * V;
   }
   const int64_t pstride = (int64_t)kChunkSteps * 64 * V;  // elements from one chunk to the next in a tile
-  u32x4 wreg[FPW];
-  auto fetch_w = [&](int p) {
+  // every load unconditional: chunks past the last re-read it, never used
+  auto cl = [&](int p) { return p < P ? p : P - 1; };
+  auto fetch_w = [&](u32x4 (&wr)[FPW], int p) {
 #pragma unroll
-    for (int i = 0; i < FPW; ++i) wreg[i] = ld16(wsrc[i] + p * pstride);
+    for (int i = 0; i < FPW; ++i) wr[i] = ld16(wsrc[i] + cl(p) * pstride);
   };
-  auto stage_w = [&](int b) {
+  auto stage_w = [&](const u32x4 (&wr)[FPW], int b) {
 #pragma unroll
-    for (int i = 0; i < FPW; ++i) wl[b][wave * FPW + i][lane] = wreg[i];
+    for (int i = 0; i < FPW; ++i) wl[b][wave * FPW + i][lane] = wr[i];
   };
-
   f32x4 tot[BT];
 #pragma unroll
   for (int t = 0; t < BT; ++t) tot[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  u32x4 xa[kChunkSteps], xb[kChunkSteps];
-  fetch_w(0);
-  load_x<T>(xa, xrs, xoff, 0);
-  stage_w(0);
-  __syncthreads();
-  for (int p = 0; p < P; ++p) {
-    const int b = p & 1;
-    const int pn = p + 1 < P ? p + 1 : P - 1;  // every load unconditional: the last chunk re-reads itself
-    fetch_w(pn);
-    load_x<T>(xb, xrs, xoff, pn);
+  auto mma = [&](const u32x4 (&xf)[kChunkSteps], int b) {
     f32x4 acc[BT];
 #pragma unroll
     for (int t = 0; t < BT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // step st's BT weight fragments are read from LDS while step st - 1's MFMAs run
+    u32x4 wf[2][BT];
 #pragma unroll
-    for (int st = 0; st < kChunkSteps; ++st)
+    for (int t = 0; t < BT; ++t) wf[0][t] = wl[b][t * kChunkSteps][lane];
 #pragma unroll
-      for (int t = 0; t < BT; ++t) acc[t] = mfma_step<T>(xa[st], wl[b][t * kChunkSteps + st][lane], acc[t]);
+    for (int st = 0; st < kChunkSteps; ++st) {
+      if (st + 1 < kChunkSteps) {
+#pragma unroll
+        for (int t = 0; t < BT; ++t) wf[(st + 1) & 1][t] = wl[b][t * kChunkSteps + st + 1][lane];
+      }
+#pragma unroll
+      for (int t = 0; t < BT; ++t) acc[t] = mfma_step<T>(xf[st], wf[st & 1][t], acc[t]);
+    }
 #pragma unroll
     for (int t = 0; t < BT; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) tot[t][r] += acc[t][r];
-    stage_w(b ^ 1);  // that buffer was last read in chunk p - 1, before the barrier closing it
+  };
+
+  // Register rings, statically unrolled by two (no copies, no exit inside
+  // the loop): chunk q's weights are fetched two half-iterations before they
+  // are staged into LDS stage q & 1, and its x two half-iterations before
+  // its MFMAs. Issue order at the top of every pair, oldest first:
+  // x0 (chunk p), w1 (p + 1), x1 (p + 1), w0 (p + 2); the prologue builds
+  // the same order so the compiler's wait counts are the steady-state ones.
+  u32x4 w0[FPW], w1[FPW], x0[kChunkSteps], x1[kChunkSteps];
+  fetch_w(w0, 0);
+  load_x<T>(x0, xrs, xoff, 0);
+  fetch_w(w1, 1);
+  load_x<T>(x1, xrs, xoff, cl(1));
+  stage_w(w0, 0);
+  __syncthreads();
+  fetch_w(w0, 2);
+  for (int p = 0; p + 1 < P; p += 2) {
+    // chunk p: LDS stage 0, x0
+    mma(x0, 0);
+    load_x<T>(x0, xrs, xoff, cl(p + 2));
+    stage_w(w1, 1);  // chunk p + 1; stage 1 was last read by chunk p - 1, before the previous barrier
     __syncthreads();
-#pragma unroll
-    for (int st = 0; st < kChunkSteps; ++st) xa[st] = xb[st];
+    fetch_w(w1, p + 3);
+    // chunk p + 1: LDS stage 1, x1
+    mma(x1, 1);
+    load_x<T>(x1, xrs, xoff, cl(p + 3));
+    stage_w(w0, 0);  // chunk p + 2; stage 0 was last read by chunk p, before the barrier above
+    __syncthreads();
+    fetch_w(w0, p + 4);
   }
+  if (P & 1) mma(x0, 0);  // chunk P - 1, staged by the last pair (or the prologue)
   if (row0 >= n) return;  // after the last barrier
 #pragma unroll
   for (int t = 0; t < BT; ++t) {
-    const int g = blockIdx.y * BT + t;
+    const int g = tg * BT + t;
     if (g >= tiles) continue;  // uniform over the workgroup
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -657,10 +710,10 @@ static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const v
     // weights through LDS, shared by the 4 waves: 4 tiles per workgroup
     // while that still leaves >= 512 workgroups, else 2 (>= 256 of them)
     if (rb * ((tiles + 3) / 4) >= 512)
-      hipLaunchKernelGGL((linear_gemm_kernel<T, TO, EPI, 4>), dim3(rb, (tiles + 3) / 4), dim3(256), 0, st,
+      hipLaunchKernelGGL((linear_gemm_kernel<T, TO, EPI, 4>), dim3(xcd_grid(rb, (tiles + 3) / 4)), dim3(256), 0, st,
                          (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra);
     else
-      hipLaunchKernelGGL((linear_gemm_kernel<T, TO, EPI, 2>), dim3(rb, (tiles + 1) / 2), dim3(256), 0, st,
+      hipLaunchKernelGGL((linear_gemm_kernel<T, TO, EPI, 2>), dim3(xcd_grid(rb, (tiles + 1) / 2)), dim3(256), 0, st,
                          (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra);
   }
 }
