@@ -16,13 +16,15 @@
 // Work split: a workgroup of 4 waves owns 128 consecutive query rows of one
 // segment and one query head; wave w owns rows 32w..32w+31, one query per
 // lane column of the 32x32 MFMA tiles. Per 64-key tile the workgroup stages K
-// (row-major) and V (transposed, d-major) in LDS, with the next tile's global
-// loads (32-bit buffer offsets, nothing read past the segment's last key)
-// issued before the current tile's math so their latency hides under it.
+// and V row-major in LDS (16-byte stores, no transpose), with the next tile's
+// global loads (32-bit buffer offsets, nothing read past the segment's last
+// key) issued before the current tile's math so their latency hides under it.
 // Each wave computes S^T = K Q^T on v_mfma_f32_32x32x16_bf16 (two 32-key
-// blocks x Dh/16 steps), then O^T = V^T P^T on the same instruction. Against
-// 16-query blocks on the 16x16x32 MFMA this halves the LDS bytes read per
-// flop: every K and V^T fragment a wave reads feeds 32 queries.
+// blocks x Dh/16 steps), then O^T = V^T P^T on the same instruction, its V^T
+// operand read straight from the row-major V tile with the LDS transposing
+// read (ds_read_b64_tr_b16, two per fragment). Against 16-query blocks on the
+// 16x16x32 MFMA this halves the LDS bytes read per flop: every K and V^T
+// fragment a wave reads feeds 32 queries.
 //
 // Key order inside a 32-key block: MFMA row r (lane half hf = lane / 32 holds
 // rows 8i + 4hf + j, i, j < 4) reads K row pi(r) = 16(i / 2) + 8hf + 4(i % 2)
@@ -30,12 +32,13 @@
 // exactly the 8 consecutive keys the B operand of a 16-key P^T step wants in
 // that lane. P thus goes from the S^T accumulators to the B operand of
 // O^T = V^T P^T by packing to bf16, with no exchange, and the V^T fragment of
-// the same lane half is 8 consecutive keys of one d row (one 16-byte LDS
-// read). A lane's output column is its query, so the online softmax's max and
-// sum need one shuffle (the other lane half) and the rescale none; the scale
-// folds into the exponent's FMA. Tiles past the diagonal are never visited;
-// the diagonal tiles mask keys past each row's position (tiles below them
-// skip the mask). Query tiles are dispatched longest first.
+// the same lane half is 8 consecutive keys of one d column (two transposing
+// LDS reads of 4 keys). A lane's output column is its query, so the online
+// softmax's max and sum need one shuffle (the other lane half) and the
+// rescale none; the scale folds into the exponent's FMA. Tiles past the
+// diagonal are never visited; the diagonal tiles mask keys past each row's
+// position (tiles below them skip the mask). Query tiles are dispatched
+// longest first.
 #include "wfd_common.h"
 
 namespace wfd {
@@ -63,15 +66,15 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2
   constexpr int NKB = kPfKeys / 32;   // 32-key blocks of S^T
   constexpr int NPS = kPfKeys / 16;   // MFMA k-steps over keys (O^T += V^T P^T)
   constexpr int KP = DH + 8;          // padded LDS row of K (elements)
-  constexpr int VP = kPfKeys + 8;     // padded LDS row of V^T
-  constexpr int CPR = DH / V;         // 16-byte chunks per K row
-  constexpr int KCH = kPfKeys * CPR / NT;      // K chunks per thread per tile
-  constexpr int VUN = kPfKeys / 2 * CPR;       // V key-pair chunks per tile
-  constexpr int VCH = VUN >= NT ? VUN / NT : 1;  // ... per thread (fewer chunks than threads: the first waves)
-  static_assert(KCH >= 1 && kPfKeys * CPR % NT == 0 && (VUN % NT == 0 || NT % VUN == 0), "tile split");
-  static_assert(VUN >= NT || VUN % 64 == 0, "V staging must be wave-uniform");
+  // padded LDS row of V: a transposing read takes 4 rows x 64 bytes per 32
+  // lanes, which a row of DH + 32 elements (2 DH + 64 bytes) spreads over all
+  // 64 banks for DH = 64 and 128
+  constexpr int VRP = DH + 32;
+  constexpr int CPR = DH / V;         // 16-byte chunks per K / V row
+  constexpr int KCH = kPfKeys * CPR / NT;      // K (and V) chunks per thread per tile
+  static_assert(KCH >= 1 && kPfKeys * CPR % NT == 0, "tile split");
   __shared__ __align__(16) bf16_t k_lds[2][kPfKeys * KP];  // double-buffered: one barrier per tile
-  __shared__ __align__(16) bf16_t vt_lds[2][DH * VP];
+  __shared__ __align__(16) bf16_t v_lds[2][kPfKeys * VRP];
 
   const int s = blockIdx.z;
   const int h = blockIdx.y;
@@ -111,23 +114,16 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2
   // K row of MFMA row col within a 32-key block (the permutation above)
   const int krow = 16 * ((col >> 3) >> 1) + 8 * ((col >> 2) & 1) + 4 * ((col >> 3) & 1) + (col & 3);
 
-  // staging: thread's K chunks (key, 8 dims) and V key-pair chunks (2 keys, 8 dims)
-  u32x4 kreg[KCH], vreg[VCH][2];
+  // staging: thread's K and V chunks (key, 8 dims), both stored row-major
+  u32x4 kreg[KCH], vreg[KCH];
   auto fetch = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
       const int c = threadIdx.x + i * NT;
       const int kr_ = c / CPR;
-      kreg[i] = buf_ld16(kr, (uint32_t)(k0 + kr_) * rsb + (uint32_t)((c - kr_ * CPR) * V * sizeof(bf16_t)));
-    }
-#pragma unroll
-    for (int i = 0; i < VCH; ++i) {
-      const int c = threadIdx.x + i * NT;
-      if (VUN < NT && c >= VUN) break;  // wave-uniform
-      const int kp = c / CPR;
-      const uint32_t off = (uint32_t)(k0 + 2 * kp) * rsb + (uint32_t)((c - kp * CPR) * V * sizeof(bf16_t));
-      vreg[i][0] = buf_ld16(vr, off);
-      vreg[i][1] = buf_ld16(vr, off + rsb);
+      const uint32_t off = (uint32_t)(k0 + kr_) * rsb + (uint32_t)((c - kr_ * CPR) * V * sizeof(bf16_t));
+      kreg[i] = buf_ld16(kr, off);
+      vreg[i] = buf_ld16(vr, off);
     }
   };
   auto stage = [&](int b) {
@@ -136,21 +132,27 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2
       const int c = threadIdx.x + i * NT;
       const int kr_ = c / CPR;
       *reinterpret_cast<u32x4*>(&k_lds[b][kr_ * KP + (c - kr_ * CPR) * V]) = kreg[i];
+      *reinterpret_cast<u32x4*>(&v_lds[b][kr_ * VRP + (c - kr_ * CPR) * V]) = vreg[i];
     }
-    uint32_t* vt = reinterpret_cast<uint32_t*>(vt_lds[b]);
-#pragma unroll
-    for (int i = 0; i < VCH; ++i) {
-      const int c = threadIdx.x + i * NT;
-      if (VUN < NT && c >= VUN) break;  // wave-uniform
-      const int kp = c / CPR;
-      const int d0 = (c - kp * CPR) * V;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {  // dims d0 + 2e, d0 + 2e + 1: (key 2kp, key 2kp+1) pairs
-        const uint32_t a = vreg[i][0][e], b = vreg[i][1][e];
-        vt[((d0 + 2 * e) * VP + 2 * kp) >> 1] = (a & 0xffffu) | (b << 16);
-        vt[((d0 + 2 * e + 1) * VP + 2 * kp) >> 1] = (a >> 16) | (b & 0xffff0000u);
-      }
-    }
+  };
+  // V^T fragment of d-block db, key step k (the A operand of O^T += V^T P^T:
+  // lane l holds d = 32 db + l % 32, keys 16 k + 8 (l / 32) + 0..7) from the
+  // row-major V tile with two transposing reads. Within each 16-lane group
+  // the read hands lane i element i % 4 of the 8-byte chunks that lanes
+  // i / 4, 4 + i / 4, 8 + i / 4, 12 + i / 4 address; lane j addressing V[key0 +
+  // j / 4][dbase + 4 (j % 4)] thus yields V[key0 + 0..3][dbase + i] in lane i.
+  const int tg = lane >> 4;  // 16-lane group: bit 0 picks d + 16, bit 1 keys + 8
+  const int ti = lane & 15;
+  const int v_lane = ((tg >> 1) * 8 + (ti >> 2)) * VRP + 16 * (tg & 1) + 4 * (ti & 3);
+  auto vt_frag = [&](int b, int db, int k) {
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    typedef const __attribute__((address_space(3))) void* lds_ptr;
+    const bf16_t* p = &v_lds[b][v_lane + 16 * k * VRP + 32 * db];
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr)p);
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr)(p + 4 * VRP));
+    const uint2 a = __builtin_bit_cast(uint2, lo), c = __builtin_bit_cast(uint2, hi);
+    return u32x4{a.x, a.y, c.x, c.y};
   };
 
   float mrun = -INFINITY, lrun = 0.f;
@@ -236,10 +238,7 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
 #pragma unroll
-      for (int k = 0; k < NPS; ++k) {
-        const u32x4 afr = *reinterpret_cast<const u32x4*>(&vt_lds[b][(32 * db + col) * VP + 16 * k + 8 * hf]);
-        o[db] = mfma32(afr, pb[k], o[db]);
-      }
+      for (int k = 0; k < NPS; ++k) o[db] = mfma32(vt_frag(b, db, k), pb[k], o[db]);
     }
     if (t + 1 < ntiles) {  // uniform
       stage(b ^ 1);
