@@ -177,17 +177,23 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2
     const bool full = k0 + kPfKeys - 1 <= pos0 + row0;
 
     // S^T = K Q^T: register rr of block kb holds S[query col][key k0 + 32 kb + 16 (rr / 8) + 8 hf + rr % 8]
+    // (the two 32-key blocks' chains interleaved: back-to-back MFMAs are
+    // independent; the wave's priority is raised while it issues MFMAs so a
+    // wave in its softmax fills the MFMA shadows, not the other way round)
     f32x16 sacc[NKB];
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
+    for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-      for (int k = 0; k < NDS; ++k) {
+    for (int k = 0; k < NDS; ++k)
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
         const u32x4 afr = *reinterpret_cast<const u32x4*>(&k_lds[b][(32 * kb + krow) * KP + 16 * k + hf * V]);
         sacc[kb] = mfma32(afr, qf[k], sacc[kb]);
       }
-    }
+    __builtin_amdgcn_s_setprio(0);
     // online softmax (log2 domain: p = 2^(s * scale_log2 - m)); the first tile
     // holds key 0 for every row, so m is finite from then on and masked
     // scores (-inf) give p = 0 without a test
@@ -235,11 +241,12 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[db][r] *= corr;
     }
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) {
+    for (int k = 0; k < NPS; ++k)
 #pragma unroll
-      for (int k = 0; k < NPS; ++k) o[db] = mfma32(vt_frag(b, db, k), pb[k], o[db]);
-    }
+      for (int db = 0; db < NDB; ++db) o[db] = mfma32(vt_frag(b, db, k), pb[k], o[db]);
+    __builtin_amdgcn_s_setprio(0);
     if (t + 1 < ntiles) {  // uniform
       stage(b ^ 1);
       fetch(k0 + 2 * kPfKeys);  // zeros past the last key
