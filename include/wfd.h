@@ -107,6 +107,18 @@ int wfd_kv_append(const void* k, const void* v, void* k_cache, void* v_cache, in
                   const int64_t* flat_row, int n, int Hkv, int Dh, int dtype, wfd_stream_t stream);
 
 /*
+ * SwiGLU of n rows laid out [gate (F) | up (F)] with row stride ldg:
+ * out[i][j] = silu(gu[i][j]) * gu[i][F + j] (silu(v) = v / (1 + e^-v)) in
+ * fp32, rounded once to `dtype`, row stride ldo. F, ldg and ldo are
+ * multiples of 8 (bf16) / 4 (fp32) elements and both pointers 16-byte
+ * aligned. The linear layer's SwiGLU epilogue for a gate|up product made
+ * elsewhere (the prompt pass's library GEMM).
+ * Replaces: the gated MLP's silu(gate) * up inside block.mlp in the prompt
+ *   pass (src/decoding/huginn_blocks_batch.py:159-161,163-170).
+ */
+int wfd_swiglu(const void* gu, int64_t ldg, void* out, int64_t ldo, int n, int F, int dtype, wfd_stream_t stream);
+
+/*
  * Fused QKV epilogue: split qkv rows (n, (H + 2*Hkv) * Dh) into q|k|v, rotate
  * q and k by RoPE at pos[i] (interleaved pairs (2j, 2j+1), angle
  * pos * base^(-2j/Dh), tables (rope_rows, Dh/2) fp32), write q to q_out

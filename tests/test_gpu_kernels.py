@@ -251,6 +251,26 @@ def test_linear_row_invariant(gpu, dtype, N):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_swiglu_matches_reference(gpu, dtype):
+    """silu(gate) * up of [gate | up] rows in fp32, rounded once: against an fp32
+    torch reference on the same rounded inputs (bit-exact up to the last
+    rounding: one ulp of the element type), with a strided, padded gu."""
+    g = torch.Generator().manual_seed(2)
+    n, F = 37, 5632 // 4
+    gu = (3 * torch.randn(n, 2 * F + 64, generator=g)).to(dtype).to(gpu)[:, :2 * F]
+    out = ops.swiglu(gu)
+    gf, uf = gu[:, :F].float(), gu[:, F:].float()
+    ref = (gf / (1 + torch.exp(-gf)) * uf).to(dtype)
+    diff = (out.float() - ref.float()).abs()
+    ulp = ref.float().abs() * (2 ** -7 if dtype == torch.bfloat16 else 2 ** -22) + 1e-30
+    assert bool((diff <= ulp).all()), float((diff / ulp).max())
+    # n rows of a larger buffer; the rows past n are untouched
+    buf = torch.full((n + 3, F), 7.0, dtype=dtype, device=gpu)
+    ops.swiglu(gu, n=n, out=buf)
+    assert torch.equal(buf[:n], out) and bool((buf[n:] == 7).all())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_add_rmsnorm(gpu, dtype):
     g = torch.Generator().manual_seed(3)
     n, D = 6, 2048

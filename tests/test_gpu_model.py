@@ -77,6 +77,32 @@ def test_tiny_prefill_logits_match_oracle(tiny):
     assert rel_err(logits.cpu().numpy(), ref[0]) <= 1e-4
 
 
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_prompt_pass_library_gemm_matches_kernels(gpu, dtype):
+    """The prompt pass with library GEMMs (the default) against the same pass
+    on the packed linear kernels: the same slot caches and last-position logits
+    up to the GEMMs' summation order (rows that are computed once and never
+    compared bit for bit with decode rows), and the oracle agrees."""
+    import dataclasses
+    cfg = dataclasses.replace(TINY, dtype=dtype)
+    w = M.init_weights(cfg, 0)
+    ids = _prompt(100).tolist()
+    outs = []
+    for dense in (True, False):
+        m = LoopedModel(cfg, w, gpu, max_seq_len=128, max_batch=1, dense_prompt=dense)
+        cache = m.create_cache(1)
+        logits = m.prefill_seq(cache, 0, ids)
+        torch.cuda.synchronize()
+        outs.append((logits.float().cpu().numpy(), cache.flat_k.float().cpu().numpy(),
+                     cache.flat_v.float().cpu().numpy()))
+    tol = 1e-4 if dtype == "float32" else 5e-2  # bf16: roundings of the two GEMM orders compound over the loop
+    for a, b in zip(outs[0], outs[1]):
+        assert rel_err(a, b) <= tol
+    if dtype == "float32":
+        ref = _oracle(cfg, w, 128).prefill([ids])[1][0]
+        assert rel_err(outs[0][0], ref) <= tol
+
+
 @pytest.mark.parametrize("T_draft", [1, 2])
 def test_tiny_wfd_matches_oracle_and_sequential(tiny, T_draft):
     w, model = tiny

@@ -39,6 +39,7 @@ SIGNATURES: dict[str, tuple] = {
     "wfd_attn_prefill": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
                                 _vp]),
     "wfd_kv_append": (_i32, [_vp, _vp, _vp, _vp, _i64, _vp, _i32, _i32, _i32, _i32, _vp]),
+    "wfd_swiglu": (_i32, [_vp, _i64, _vp, _i64, _i32, _i32, _i32, _vp]),
     "wfd_qkv_rope_append": (_i32, [_vp, _i64, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32,
                                    _i32, _i32, _vp]),
     "wfd_linear_k_multiple": (_i32, [_i32]),

@@ -314,13 +314,35 @@ __global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float* __rest
   }
 }
 
+// SwiGLU of rows laid out [gate (F) | up (F)]: out[i][j] = silu(gate) * up,
+// silu(v) = v / (1 + e^-v), in fp32 from the stored (rounded) gate and up,
+// rounded once -- the linear layer's SwiGLU epilogue for a gate|up product
+// computed elsewhere (the prompt pass's library GEMM). One 16-byte vector of
+// each half per thread.
+template <typename T>
+__global__ __launch_bounds__(256) void swiglu_kernel(const T* __restrict__ gu, int64_t ldg, T* __restrict__ out,
+                                                     int64_t ldo, int n, int F) {
+  constexpr int V = Elem<T>::kVec;
+  const int per_row = F / V;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (int64_t)n * per_row) return;
+  const int i = (int)(t / per_row);
+  const int j = (int)(t - (int64_t)i * per_row) * V;
+  float g[V], u[V], o[V];
+  Elem<T>::unpack(ld16(gu + (int64_t)i * ldg + j), g);
+  Elem<T>::unpack(ld16(gu + (int64_t)i * ldg + F + j), u);
+#pragma unroll
+  for (int e = 0; e < V; ++e) o[e] = (g[e] / (1.0f + expf(-g[e]))) * u[e];
+  *reinterpret_cast<u32x4*>(out + (int64_t)i * ldo + j) = Elem<T>::pack(o);
+}
+
 }  // namespace wfd
 
 extern "C" {
 
 const char* wfd_last_error(void) { return wfd::g_err; }
 
-int wfd_abi_version(void) { return 3; }
+int wfd_abi_version(void) { return 4; }
 
 int wfd_add_rmsnorm(const void* a, const int32_t* a_rows, int64_t lda, const void* res, int64_t ldr, const void* w1,
                     const void* w2, void* x_out, const int32_t* out_rows, int64_t ldo, void* h_out, int64_t ldh, int n,
@@ -379,6 +401,34 @@ int wfd_qkv_rope_append(const void* qkv, int64_t ldq, const int32_t* pos, const 
     return kUnsupported;
   }
   return launch_status("wfd_qkv_rope_append");
+}
+
+int wfd_swiglu(const void* gu, int64_t ldg, void* out, int64_t ldo, int n, int F, int dtype, hipStream_t stream) {
+  using namespace wfd;
+  const int vec = dtype == kBF16 ? Elem<bf16_t>::kVec : Elem<float>::kVec;
+  if (dtype != kBF16 && dtype != kF32) {
+    set_error("wfd_swiglu: unsupported dtype %d", dtype);
+    return kUnsupported;
+  }
+  if (n < 0 || F <= 0 || F % vec || ldg < 2 * (int64_t)F || ldo < F || ldg % vec || ldo % vec) {
+    set_error("wfd_swiglu: bad shape n=%d F=%d ldg=%lld ldo=%lld (F and strides multiples of %d)", n, F,
+              (long long)ldg, (long long)ldo, vec);
+    return kBadArg;
+  }
+  if (n == 0) return kOk;
+  if (!gu || !out || ((uintptr_t)gu & 15) || ((uintptr_t)out & 15)) {
+    set_error("wfd_swiglu: null or unaligned pointer (16-byte alignment)");
+    return kBadArg;
+  }
+  const int64_t threads = (int64_t)n * (F / vec);
+  const dim3 grid((unsigned)((threads + 255) / 256));
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(swiglu_kernel<bf16_t>, grid, dim3(256), 0, stream, (const bf16_t*)gu, ldg, (bf16_t*)out, ldo,
+                       n, F);
+  else
+    hipLaunchKernelGGL(swiglu_kernel<float>, grid, dim3(256), 0, stream, (const float*)gu, ldg, (float*)out, ldo, n,
+                       F);
+  return launch_status("wfd_swiglu");
 }
 
 int wfd_kv_append(const void* k, const void* v, void* k_cache, void* v_cache, int64_t kv_block_rows,

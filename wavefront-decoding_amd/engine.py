@@ -137,7 +137,8 @@ class LoopedModel:
 
     def __init__(self, cfg: LoopedLMConfig, weights: dict[str, torch.Tensor], device="cuda", *, max_seq_len: int,
                  max_batch: int = 1, state_init: str = "random", state_seed: int = 0, use_graphs: bool = False,
-                 max_rows: int | None = None, ring_len: int = 1 << 20, group_attention: bool = True):
+                 max_rows: int | None = None, ring_len: int = 1 << 20, group_attention: bool = True,
+                 dense_prompt: bool = True):
         self.cfg = cfg
         self.device = torch.device(device)
         self.dtype = cfg.torch_dtype
@@ -149,10 +150,18 @@ class LoopedModel:
         self.group_attention = group_attention  # rows sharing a slot read its prefix once
         self.group_min_workgroups = _GROUP_MIN_WORKGROUPS
         self.W = {}
+        # the prompt pass (prefill_seq) runs its linears as plain library GEMMs
+        # over row-major copies of the block weights: its rows are computed once
+        # and never compared bit for bit with decode rows, and at hundreds to
+        # tens of thousands of rows the library GEMM is 2-9x faster
+        self.dense_prompt = dense_prompt
+        self.Wd: dict[str, torch.Tensor] = {}
         for k, v in weights.items():
             w = v.to(device=self.device, dtype=self.dtype).contiguous()
             leaf = k.rsplit(".", 1)[-1]
-            if leaf in _LINEAR_WEIGHTS:  # stored once, in the kernels' packed layout
+            if leaf in _LINEAR_WEIGHTS:  # the kernels' packed layout
+                if dense_prompt and leaf != "lm_head":
+                    self.Wd[k] = w
                 w = ops.pack_linear(w, swiglu=leaf == "fc")
             self.W[k] = w
         cos, sin = rope_tables(max_seq_len, cfg.head_dim, cfg.rope_base)
@@ -210,39 +219,58 @@ class LoopedModel:
         self._graphs.clear()
 
     # -- scratch -----------------------------------------------------------------
-    def _scratch(self, cap: int) -> dict[str, torch.Tensor]:
+    def _scratch(self, cap: int, dense: bool = False) -> dict[str, torch.Tensor]:
         c = self.cfg
         mk = lambda w: torch.empty(cap, w, dtype=self.dtype, device=self.device)  # noqa: E731
-        return dict(x=mk(c.d_model), h=mk(c.d_model),
-                    q=torch.empty(cap, c.n_heads, c.head_dim, dtype=self.dtype, device=self.device),
-                    o=torch.empty(cap, c.n_heads, c.head_dim, dtype=self.dtype, device=self.device),
-                    a=mk(c.d_model), u=mk(c.ffn), m=mk(c.d_model))
+        sc = dict(x=mk(c.d_model), h=mk(c.d_model),
+                  q=torch.empty(cap, c.n_heads, c.head_dim, dtype=self.dtype, device=self.device),
+                  o=torch.empty(cap, c.n_heads, c.head_dim, dtype=self.dtype, device=self.device),
+                  a=mk(c.d_model), u=mk(c.ffn), m=mk(c.d_model))
+        if dense:  # the library GEMMs' unfused outputs: q|k|v rows, gate|up rows
+            sc["qkv"] = mk((c.n_heads + 2 * c.n_kv_heads) * c.head_dim)
+            sc["gu"] = mk(2 * c.ffn)
+        return sc
 
     # -- one SandwichBlock over n rows --------------------------------------------
     def _block(self, prefix: str, n: int, sc, pos_d, kvlen_d, rb_d, fr_d, kv_len_max: int, ws,
                cache: BatchStaticKVCache, next_norm: torch.Tensor | None, final_out=None, final_rows=None,
-               segments=None, group_first=None):
+               segments=None, group_first=None, dense: bool = False):
         """One SandwichBlock over n rows. `segments` = (seg_row_base, seg_q_start,
         seg_pos0, max_seg_len) routes attention through the causal prefill
         kernel (rows grouped by slot at consecutive positions) instead of the
         per-row decode kernel; `group_first` groups decode rows that share a
-        slot (one prefix read per group, same bits)."""
+        slot (one prefix read per group, same bits). `dense` (the prompt pass)
+        runs the four linears as library GEMMs over the row-major weights, with
+        the RoPE/append and SwiGLU epilogues as their own kernels."""
         c, W = self.cfg, self.W
         x, h = sc["x"], sc["h"]
-        q = ops.linear_qkv_rope_append(h, W[prefix + "Wqkv"], pos_d, self.rope_cos, self.rope_sin, fr_d,
-                                       cache.flat_k, cache.flat_v, c.n_heads, c.n_kv_heads, c.head_dim, n=n,
-                                       q_out=sc["q"][:n])
+        if dense:
+            qkv = torch.mm(h[:n], self.Wd[prefix + "Wqkv"].t(), out=sc["qkv"][:n])
+            q = ops.qkv_rope_append(qkv, pos_d, self.rope_cos, self.rope_sin, fr_d, cache.flat_k, cache.flat_v,
+                                    c.n_heads, c.n_kv_heads, c.head_dim, q_out=sc["q"][:n])
+        else:
+            q = ops.linear_qkv_rope_append(h, W[prefix + "Wqkv"], pos_d, self.rope_cos, self.rope_sin, fr_d,
+                                           cache.flat_k, cache.flat_v, c.n_heads, c.n_kv_heads, c.head_dim, n=n,
+                                           q_out=sc["q"][:n])
         if segments is not None:
             srb, sqs, sp0, smax = segments
             o = ops.attn_prefill(q, cache.flat_k, cache.flat_v, srb, sqs, sp0, max_seg_len=smax, out=sc["o"][:n])
         else:
             o = ops.attn_decode(q, cache.flat_k, cache.flat_v, rb_d, kvlen_d, kv_len_max=kv_len_max,
                                 out=sc["o"][:n], workspace=ws, group_first=group_first)
-        a = ops.linear(o.view(n, -1), W[prefix + "proj"], n=n, out=sc["a"])
+        if dense:
+            a = torch.mm(o.view(n, -1), self.Wd[prefix + "proj"].t(), out=sc["a"][:n])
+        else:
+            a = ops.linear(o.view(n, -1), W[prefix + "proj"], n=n, out=sc["a"])
         ops.add_rmsnorm(a, W[prefix + "norm_2"], c.norm_eps, res=x, w2=W[prefix + "norm_3"], n=n, x_out=x,
                         h_out=h)
-        u = ops.linear(h, W[prefix + "fc"], n=n, out=sc["u"], swiglu=True)
-        m = ops.linear(u, W[prefix + "mlp_proj"], n=n, out=sc["m"])
+        if dense:
+            gu = torch.mm(h[:n], self.Wd[prefix + "fc"].t(), out=sc["gu"][:n])
+            u = ops.swiglu(gu, n=n, out=sc["u"][:n])
+            m = torch.mm(u, self.Wd[prefix + "mlp_proj"].t(), out=sc["m"][:n])
+        else:
+            u = ops.linear(h, W[prefix + "fc"], n=n, out=sc["u"], swiglu=True)
+            m = ops.linear(u, W[prefix + "mlp_proj"], n=n, out=sc["m"])
         if next_norm is not None:
             ops.add_rmsnorm(m, W[prefix + "norm_4"], c.norm_eps, res=x, w2=next_norm, n=n, x_out=x, h_out=h)
         else:
@@ -523,7 +551,8 @@ class LoopedModel:
     def prefill_seq(self, cache, b: int, token_ids) -> torch.Tensor:
         """Whole prompt of sequence b at positions [0, L): fills every slot's
         [0, L) and returns the last position's logits (V,) float32. Runs eagerly
-        with its own L-row scratch."""
+        with its own L-row scratch; with dense_prompt its linears are library
+        GEMMs (see __init__), the last position's lm_head row the packed kernel."""
         c, W = self.cfg, self.W
         ids = np.asarray(token_ids, dtype=np.int64).reshape(-1)
         L = len(ids)
@@ -547,7 +576,8 @@ class LoopedModel:
         flash = self.dtype == torch.bfloat16 and c.head_dim in (64, 128)
         seg_l = (lambda s: (t64[2 * n_layers * L + s: 2 * n_layers * L + s + 1], t32[2 * L: 2 * L + 2],  # noqa: E731
                             t32[2 * L + 2: 2 * L + 3], L)) if flash else (lambda s: None)
-        sc = self._scratch(L)
+        dense = self.dense_prompt
+        sc = self._scratch(L, dense=dense)
         ws = None if flash else torch.zeros(ops.attn_workspace_bytes(L, c.n_heads, c.head_dim, L),
                                             dtype=torch.uint8, device=self.device)
         logits = torch.empty(1, c.vocab_size, dtype=torch.float32, device=self.device)
@@ -557,22 +587,26 @@ class LoopedModel:
         for i in range(c.n_prelude):
             nxt = W[f"prelude.{i + 1}.norm_1"] if i + 1 < c.n_prelude else None
             self._block(f"prelude.{i}.", L, sc, pos_d, kvlen_d, rb_l(i), fr_l(i), L, ws, cache, nxt,
-                        final_out=state[:, D:], segments=seg_l(i))
+                        final_out=state[:, D:], segments=seg_l(i), dense=dense)
         s0 = initial_state_prefill(c, L, self.state_seed, self.state_init)
         state[:, :D].copy_(s0.to(device=self.device, dtype=self.dtype))
         for r in range(c.T_total):
-            ops.linear(state, W["adapter"], n=L, out=sc["x"])
+            if dense:
+                torch.mm(state, self.Wd["adapter"].t(), out=sc["x"][:L])
+            else:
+                ops.linear(state, W["adapter"], n=L, out=sc["x"])
             ops.rmsnorm(sc["x"], W["core.0.norm_1"], c.norm_eps, n=L, x_out=sc["h"])
             for l in range(c.n_core):
                 s = self.slot_core(r, l)
                 nxt = W[f"core.{l + 1}.norm_1"] if l + 1 < c.n_core else None
                 self._block(f"core.{l}.", L, sc, pos_d, kvlen_d, rb_l(s), fr_l(s), L, ws, cache, nxt,
-                            final_out=state[:, :D], segments=seg_l(s))
+                            final_out=state[:, :D], segments=seg_l(s), dense=dense)
         ops.add_rmsnorm(state, W["ln_f"], c.norm_eps, w2=W["coda.0.norm_1"], n=L, x_out=sc["x"], h_out=sc["h"])
         for i in range(c.n_coda):
             s = self.slot_coda(i)
             nxt = W[f"coda.{i + 1}.norm_1"] if i + 1 < c.n_coda else W["ln_f"]
-            self._block(f"coda.{i}.", L, sc, pos_d, kvlen_d, rb_l(s), fr_l(s), L, ws, cache, nxt, segments=seg_l(s))
+            self._block(f"coda.{i}.", L, sc, pos_d, kvlen_d, rb_l(s), fr_l(s), L, ws, cache, nxt, segments=seg_l(s),
+                        dense=dense)
         ops.linear(sc["h"][L - 1: L], W["lm_head"], n=1, out=logits, out_dtype=torch.float32)
         for s in range(n_layers):
             cache.seqlen[s][b] = max(cache.seqlen[s][b], L)

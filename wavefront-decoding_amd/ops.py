@@ -168,6 +168,23 @@ def kv_append(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: 
     _lib.check(rc, "wfd_kv_append")
 
 
+def swiglu(gu: torch.Tensor, *, n: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """silu(gate) * up of rows gu = [gate (F) | up (F)] (wfd_swiglu): the
+    linear layer's SwiGLU epilogue for a gate|up product computed elsewhere."""
+    _need_cuda(gu)
+    _need(gu.dim() == 2 and gu.stride(1) == 1 and gu.shape[1] % 2 == 0, "gu: (n, 2F) with unit column stride")
+    n = gu.shape[0] if n is None else n
+    F = gu.shape[1] // 2
+    if out is None:
+        out = torch.empty(n, F, dtype=gu.dtype, device=gu.device)
+    _need_cuda(out)
+    _need(out.dtype == gu.dtype and out.dim() == 2 and out.stride(1) == 1 and out.shape[1] == F, "out: (n, F)")
+    _need(0 <= n <= min(gu.shape[0], out.shape[0]), "n: within the rows of gu and out")
+    rc = _lib.load().wfd_swiglu(gu.data_ptr(), gu.stride(0), out.data_ptr(), out.stride(0), n, F, _dt(gu), _stream())
+    _lib.check(rc, "wfd_swiglu")
+    return out
+
+
 def qkv_rope_append(qkv: torch.Tensor, pos: torch.Tensor, rope_cos: torch.Tensor, rope_sin: torch.Tensor,
                     flat_row: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, H: int, Hkv: int, Dh: int,
                     q_out: torch.Tensor | None = None) -> torch.Tensor:
