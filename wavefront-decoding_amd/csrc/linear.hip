@@ -16,18 +16,23 @@
 // the work is split): K is cut into P = K / KC chunks of 4 MFMA k-steps
 // (KC = 128 bf16 / 64 fp32 elements); a chunk partial is the MFMA chain over
 // its 4 steps starting from zero; y = epilogue(((0 + c_0) + c_1) + ... + c_{P-1})
-// in fp32. Two kernels honour it bit for bit:
+// in fp32. Four kernels honour it bit for bit:
 //
-//  * wide (n <= 16): one 1024-thread workgroup per tile; its 16 waves take
-//    the chunks round-robin (all loads of a wave issued together), park the
+//  * wide (n <= 16): one 16-wave workgroup per tile (or column half of a
+//    tile), 8 waves when there are more than 512 tiles; its waves take the
+//    chunks round-robin (all loads of a wave issued together), park the
 //    chunk partials in LDS, and threads sum them in chunk order. No
 //    cross-workgroup synchronization: a tile's whole K is reduced inside one
 //    workgroup.
-//  * tile (n > 16): a workgroup owns 64 rows of x and 2 tiles; each of its 4
-//    waves walks the chunks in order for one 16-row block of x and both
-//    tiles, with a two-stage register pipeline (chunk p+1 in flight while
-//    chunk p runs on MFMA). The waves of a workgroup read the same weight
-//    fragments, so the weights stream from HBM once per 64 rows.
+//  * tile (n > 16, few row-block x tile pairs): a workgroup owns 64 rows of x
+//    and 2 tiles; each of its 4 waves walks the chunks in order for one
+//    16-row block of x and both tiles, with a two-stage register pipeline.
+//  * gemm (n > 16, many pairs): 64 rows x 2 or 4 tiles per workgroup, the
+//    tiles' weights staged once in LDS for the 4 waves, weights and x loaded
+//    two chunks ahead, an XCD-aware grid.
+//  * stream (n > 16, at most 256 tiles): 64 rows x 1 or 2 tiles per
+//    workgroup, weights and x moved global -> LDS by direct-to-LDS loads
+//    through a 4-stage ring (3 chunks in flight without registers).
 //
 // So y[m] is bit-identical whatever n is and wherever row m sits -- the
 // property that keeps wavefront decode token-identical to sequential decode.
