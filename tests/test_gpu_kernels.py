@@ -227,7 +227,8 @@ def test_linear_row_invariant(gpu, dtype, N):
     batch, whichever kernel a row count selects. N = 24, 256, 257 and 705
     column tiles: at 300 rows, the LDS-pipelined stream kernel with 1 and 2
     tiles per workgroup, then weights shared through LDS 2 and 4 tiles per
-    workgroup (both with a ragged tail); gathered rows at 3 and 40 rows."""
+    workgroup (both with a ragged tail); gathered rows at 3 and 40 rows; x
+    read at a row pitch of K + 64 bytes (the engine's activation buffers)."""
     g = torch.Generator().manual_seed(5)
     K = 2048
     print(f"[linear row invariance] dtype={dtype} N={N}", flush=True)
@@ -238,6 +239,10 @@ def test_linear_row_invariant(gpu, dtype, N):
     for n in (1, 5, 16, 17, 33, 64, 65, 300):
         part = ops.linear(X[:n].contiguous(), W)
         assert torch.equal(part, full[:n]), n
+    pitched = torch.empty(300, K + 64 // X.element_size(), dtype=dtype, device=gpu)[:, :K]
+    pitched.copy_(X)
+    for n in (5, 64, 300):
+        assert torch.equal(ops.linear(pitched, W, n=n), full[:n]), n
     rows = torch.tensor([299, 0, 150], dtype=torch.int32, device=gpu)
     gathered = ops.linear(X, W, x_rows=rows)
     assert torch.equal(gathered, full[rows.long()])
