@@ -157,7 +157,8 @@ int wfd_linear_pack(const void* W, void* W_packed, int N, int K, int dtype, int 
  * wfd_linear_k_multiple(dtype), N of 16. K is summed in fixed 128 (bf16) /
  * 64 (fp32) element chunks, chunk partials added in chunk order, so y[m] does
  * not depend on n or on where row m sits. Every x row read (x_rows[m] * ldx)
- * must lie within the first 2 GiB of x.
+ * must lie within the first 2 GiB of x. x, W and the x row pitch (ldx
+ * elements) must be 16-byte aligned.
  * Replaces: the nn.Linear calls of the block forwards -- Wqkv, proj, the gated
  *   MLP, adapter, lm_head (src/decoding/huginn_blocks.py:79,100-102,216,291;
  *   huginn_blocks_batch.py:149,160-161,299,345).

@@ -51,6 +51,14 @@ def test_host_only_entry_points():
     assert lib.wfd_attn_prefill(None, None, None, 0, None, None, None, None, 0, 10, 16, 4, 64, 1, 0.1, None) == 0
     rc = lib.wfd_linear(None, None, 100, None, None, 16, 2, 16, 100, 1, 1, 0, 0, None)
     assert rc == -1
+    # 16-byte loads of x rows and packed weights: pointers and the x pitch are checked
+    rc = lib.wfd_linear(4096 + 8, None, 128, 8192, 8192, 16, 2, 16, 128, 1, 1, 0, 0, None)
+    assert rc == -1 and b"16-byte aligned" in lib.wfd_last_error()
+    rc = lib.wfd_linear(4096, None, 132, 8192, 8192, 16, 2, 16, 128, 1, 1, 0, 0, None)
+    assert rc == -1 and b"16-byte aligned" in lib.wfd_last_error()
+    rc = lib.wfd_linear_qkv_rope_append(4096, None, 132, 8192, 2, 128, 16, 16, 16, 8, 16, 16, 16, 16, 0, 1, 1, 16, 1,
+                                        None)
+    assert rc == -1 and b"16-byte aligned" in lib.wfd_last_error()
     assert lib.wfd_attn_decode(None, None, None, 0, None, None, None, None, 0, 16, 16, 64, 1, 0.1, 10, None, 0, None) == 0
     # packing: shape and aliasing are checked on the host
     assert lib.wfd_linear_pack(8, 16, 24, 128, 1, 0, 0, None) == -1      # N not a multiple of 16

@@ -791,6 +791,10 @@ int wfd_linear(const void* x, const int32_t* x_rows, int64_t ldx, const void* W,
     set_error("wfd_linear: the x operand must span less than 2 GiB");
     return kBadArg;
   }
+  if ((((uintptr_t)x | (uintptr_t)W) & 15) || ((ldx * esz) & 15)) {
+    set_error("wfd_linear: x rows and W must be 16-byte aligned (ldx=%lld)", (long long)ldx);
+    return kBadArg;
+  }
   const int kmul = wfd_linear_k_multiple(dtype);
   if (K % kmul != 0 || N % 16 != 0) {
     set_error("wfd_linear: K=%d must be a multiple of %d and N=%d of 16", K, kmul, N);
@@ -846,8 +850,13 @@ int wfd_linear_qkv_rope_append(const void* x, const int32_t* x_rows, int64_t ldx
     set_error("wfd_linear_qkv_rope_append: null pointer argument");
     return kBadArg;
   }
-  if (!x_rows && (int64_t)n * ldx * (dtype == kBF16 ? 2 : 4) >= (int64_t)kBufInvalid) {
+  const int64_t esz = dtype == kBF16 ? 2 : 4;
+  if (!x_rows && (int64_t)n * ldx * esz >= (int64_t)kBufInvalid) {
     set_error("wfd_linear_qkv_rope_append: the x operand must span less than 2 GiB");
+    return kBadArg;
+  }
+  if ((((uintptr_t)x | (uintptr_t)Wqkv) & 15) || ((ldx * esz) & 15)) {
+    set_error("wfd_linear_qkv_rope_append: x rows and Wqkv must be 16-byte aligned (ldx=%lld)", (long long)ldx);
     return kBadArg;
   }
   const int kmul = wfd_linear_k_multiple(dtype);
