@@ -58,7 +58,7 @@ int wfd_abi_version(void);
  * kv_len[i] - 1 (with blocks, rows of one block). kv_len_max >= every
  * kv_len[i] sizes the grid (and must not exceed a block); workspace >=
  * wfd_attn_workspace_bytes(n, H, Dh, kv_len_max). Dh in {64, 128};
- * H / Hkv in {1, 2, 4}.
+ * H / Hkv in {1, 2, 4}. q, the caches, out and workspace are 16-byte aligned.
  * group_first (optional, device int32, n + 1 entries): group g = query rows
  * [group_first[g], group_first[g+1]) -- rows that share one slot (the same
  * kv_row_base), at most wfd_attn_group_max_rows(H, Hkv) of them; a workgroup
@@ -85,7 +85,7 @@ int wfd_attn_decode(const void* q, const void* k_cache, const void* v_cache, int
  * start at seg_row_base[s]; query row j attends that slot's keys [0, its
  * position] (bottom-right causal), which must already be appended. out: (n, H,
  * Dh). max_seg_len >= every segment length sizes the grid. Tables are device
- * data.
+ * data. q, the caches and out are 16-byte aligned.
  * Replaces: attn_dense(q, k, v, causal=True) (src/decoding/fa4_attention.py:189-215)
  *   from _block_dense (src/decoding/huginn_blocks_batch.py:163-170), and the
  *   grouped causal segments of _core_attn_varlen (src/decoding/parcae_blocks.py:435-456).

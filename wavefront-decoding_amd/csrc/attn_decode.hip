@@ -440,6 +440,10 @@ int wfd_attn_decode(const void* q, const void* k_cache, const void* v_cache, int
     set_error("wfd_attn_decode: null pointer argument");
     return kBadArg;
   }
+  if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out | (uintptr_t)workspace) & 15) {
+    set_error("wfd_attn_decode: q, the caches, out and workspace must be 16-byte aligned");
+    return kBadArg;
+  }
   const int G = H / Hkv;
   const int ms = max_splits_for(kv_len_max);
   const size_t need = attn_ws_bytes(n, H, Dh, kv_len_max);

@@ -287,6 +287,10 @@ int wfd_attn_prefill(const void* q, const void* k_cache, const void* v_cache, in
     set_error("wfd_attn_prefill: null pointer argument");
     return kBadArg;
   }
+  if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out) & 15) {
+    set_error("wfd_attn_prefill: q, the caches and out must be 16-byte aligned");
+    return kBadArg;
+  }
   if (dtype != kBF16 || (Dh != 64 && Dh != 128)) {
     set_error("wfd_attn_prefill: unsupported dtype=%d Dh=%d (bf16, Dh 64/128)", dtype, Dh);
     return kUnsupported;
