@@ -226,8 +226,9 @@ def test_linear_row_invariant(gpu, dtype, N):
     """Row m of y is bit-identical for every batch size and position in the
     batch, whichever kernel a row count selects. N = 24, 256, 257 and 705
     column tiles: at 300 rows, the LDS-pipelined stream kernel with 1 and 2
-    tiles per workgroup, then weights shared through LDS 2 and 4 tiles per
-    workgroup (both with a ragged tail); gathered rows at 3 and 40 rows; x
+    tiles per workgroup, then weights shared through LDS 4 tiles per
+    workgroup (2 at 33-65 rows; both with a ragged tail); gathered rows at 3
+    and 40 rows; x
     read at a row pitch of K + 64 bytes (the engine's activation buffers)."""
     g = torch.Generator().manual_seed(5)
     K = 2048

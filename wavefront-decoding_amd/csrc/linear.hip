@@ -696,8 +696,10 @@ static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const v
     if (tiles <= kStreamMaxTiles) {
       // few weight tiles: each workgroup walks all of K, so its chunk chain is
       // the launch's critical path; keep kStreamStages - 1 chunks in flight.
-      // Two tiles per workgroup while that still leaves >= 256 workgroups.
-      if (rb * ((tiles + 1) / 2) >= 256)
+      // One tile per workgroup while that makes at most 256 workgroups, else
+      // two (at 192 rows x 128 tiles, 384 one-tile workgroups took ~1.5x as
+      // long as 192 two-tile ones).
+      if (rb * tiles > 256)
         hipLaunchKernelGGL((linear_stream_kernel<T, TO, EPI, 2, kStreamStages>), dim3(rb, (tiles + 1) / 2), dim3(256),
                            0, st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra);
       else
@@ -713,8 +715,9 @@ static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const v
       return;
     }
     // weights through LDS, shared by the 4 waves: 4 tiles per workgroup
-    // while that still leaves >= 512 workgroups, else 2 (>= 256 of them)
-    if (rb * ((tiles + 3) / 4) >= 512)
+    // while that still leaves >= 256 workgroups, else 2 (lm_head at 64 rows:
+    // 500 four-tile workgroups 34 us, 1000 two-tile ones 42 us)
+    if (rb * ((tiles + 3) / 4) >= 256)
       hipLaunchKernelGGL((linear_gemm_kernel<T, TO, EPI, 4>), dim3(xcd_grid(rb, (tiles + 3) / 4)), dim3(256), 0, st,
                          (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra);
     else
