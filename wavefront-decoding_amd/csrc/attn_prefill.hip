@@ -76,11 +76,14 @@ __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2
   __shared__ __align__(16) bf16_t k_lds[2][kPfKeys * KP];  // double-buffered: one barrier per tile
   __shared__ __align__(16) bf16_t v_lds[2][kPfKeys * VRP];
 
+  // the head is the fastest grid dimension, so the launch hands out the
+  // longest query tiles of every head before any shorter one (longest first
+  // over the whole launch, not per head: a head's long tiles never start last)
   const int s = blockIdx.z;
-  const int h = blockIdx.y;
+  const int h = blockIdx.x;
   const int q0 = seg_q_start[s];
   const int len = seg_q_start[s + 1] - q0;
-  const int tq = (len + kPfRows - 1) / kPfRows - 1 - (int)blockIdx.x;  // longest tiles first
+  const int tq = (len + kPfRows - 1) / kPfRows - 1 - (int)blockIdx.y;
   if (tq < 0) return;  // uniform for the workgroup
   const int pos0 = seg_pos0[s];
   const int g = h / (H / Hkv);
@@ -295,7 +298,12 @@ int wfd_attn_prefill(const void* q, const void* k_cache, const void* v_cache, in
     set_error("wfd_attn_prefill: unsupported dtype=%d Dh=%d (bf16, Dh 64/128)", dtype, Dh);
     return kUnsupported;
   }
-  const dim3 grid((max_seg_len + kPfRows - 1) / kPfRows, H, nseg);
+  const int qtiles = (max_seg_len + kPfRows - 1) / kPfRows;
+  if (qtiles > 65535 || nseg > 65535) {
+    set_error("wfd_attn_prefill: max_seg_len=%d / nseg=%d beyond the grid", max_seg_len, nseg);
+    return kUnsupported;
+  }
+  const dim3 grid(H, qtiles, nseg);
   const dim3 block(64 * kPfWaves);
   const float sl2 = scale * 1.4426950408889634f;
   if (Dh == 64)
