@@ -64,6 +64,9 @@ def test_host_only_entry_points():
     assert rc == -1 and b"16-byte aligned" in lib.wfd_last_error()
     rc = lib.wfd_attn_prefill(4096, 4096, 4096, 0, 16, 16, 16, 4096 + 2, 1, 10, 16, 16, 64, 1, 0.1, None)
     assert rc == -1 and b"16-byte aligned" in lib.wfd_last_error()
+    # one grid row per 128-query tile: at most 65535 of them
+    rc = lib.wfd_attn_prefill(4096, 4096, 4096, 0, 16, 16, 16, 4096, 1, 65535 * 128 + 1, 16, 16, 64, 1, 0.1, None)
+    assert rc < 0 and b"beyond the grid" in lib.wfd_last_error()
     # packing: shape and aliasing are checked on the host
     assert lib.wfd_linear_pack(8, 16, 24, 128, 1, 0, 0, None) == -1      # N not a multiple of 16
     assert lib.wfd_linear_pack(8, 8, 32, 128, 1, 0, 0, None) == -1       # W_packed aliases W
