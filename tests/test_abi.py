@@ -5,6 +5,9 @@ import os
 import re
 import subprocess
 
+import pytest
+import torch
+
 from wavefront_decoding_amd import _lib
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -51,6 +54,19 @@ def test_host_only_entry_points():
     assert lib.wfd_attn_prefill(None, None, None, 0, None, None, None, None, 0, 10, 16, 4, 64, 1, 0.1, None) == 0
     rc = lib.wfd_linear(None, None, 100, None, None, 16, 2, 16, 100, 1, 1, 0, 0, None)
     assert rc == -1
+    # packing: shape and aliasing are checked on the host
+    assert lib.wfd_linear_pack(8, 16, 24, 128, 1, 0, 0, None) == -1      # N not a multiple of 16
+    assert lib.wfd_linear_pack(8, 8, 32, 128, 1, 0, 0, None) == -1       # W_packed aliases W
+    assert lib.wfd_linear_pack(8, 16, 32, 128, 1, 1, 12, None) == -1     # swiglu pair_off mismatch
+
+
+@pytest.mark.skipif(torch.cuda.device_count() > 0, reason="made-up device addresses: run only where no GPU is "
+                    "visible, so a regressed check cannot launch a kernel on them")
+def test_alignment_and_grid_checks_reject_before_launch():
+    """Checks whose outcome depends on a pointer's value (16-byte alignment)
+    or on the grid bound. The addresses are made up (4096, 8192): rejection
+    happens on the host, before any launch."""
+    lib = _lib.load()
     # 16-byte loads of x rows and packed weights: pointers and the x pitch are checked
     rc = lib.wfd_linear(4096 + 8, None, 128, 8192, 8192, 16, 2, 16, 128, 1, 1, 0, 0, None)
     assert rc == -1 and b"16-byte aligned" in lib.wfd_last_error()
@@ -67,7 +83,3 @@ def test_host_only_entry_points():
     # one grid row per 128-query tile: at most 65535 of them
     rc = lib.wfd_attn_prefill(4096, 4096, 4096, 0, 16, 16, 16, 4096, 1, 65535 * 128 + 1, 16, 16, 64, 1, 0.1, None)
     assert rc < 0 and b"beyond the grid" in lib.wfd_last_error()
-    # packing: shape and aliasing are checked on the host
-    assert lib.wfd_linear_pack(8, 16, 24, 128, 1, 0, 0, None) == -1      # N not a multiple of 16
-    assert lib.wfd_linear_pack(8, 8, 32, 128, 1, 0, 0, None) == -1       # W_packed aliases W
-    assert lib.wfd_linear_pack(8, 16, 32, 128, 1, 1, 12, None) == -1     # swiglu pair_off mismatch

@@ -5,6 +5,12 @@ HIP kernel on torch's current stream through libwfd.so. Nothing here computes
 on the host and nothing falls back to torch math: a missing library raises.
 Outputs may be passed in (`out=`) so a caller can keep every buffer at a fixed
 address for hipGraph capture; otherwise they are allocated with torch.
+
+What the host checks: dtypes, devices, widths, contiguity, and that every
+buffer addressed by plain row number (no row table) holds at least the rows
+the launch touches. Row tables (x_rows, a_rows, out_rows, src_rows, ...) are
+device data and are trusted, as the C ABI states: their entries are not read
+back, so the caller guarantees they index inside the buffers passed.
 """
 from __future__ import annotations
 
@@ -199,6 +205,8 @@ def qkv_rope_append(qkv: torch.Tensor, pos: torch.Tensor, rope_cos: torch.Tensor
     _need((cHkv, cDh) == (Hkv, Dh) and k_cache.dtype == qkv.dtype, "cache shape/dtype mismatch")
     if q_out is None:
         q_out = torch.empty(n, H, Dh, dtype=qkv.dtype, device=qkv.device)
+    _need_cuda(q_out)
+    _need(q_out.is_contiguous() and q_out.numel() >= n * H * Dh and q_out.dtype == qkv.dtype, "q_out (n, H, Dh)")
     rc = _lib.load().wfd_qkv_rope_append(qkv.data_ptr(), qkv.stride(0), pos.data_ptr(), rope_cos.data_ptr(),
                                          rope_sin.data_ptr(), rope_cos.shape[0], flat_row.data_ptr(),
                                          q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), br, n, H, Hkv,
@@ -219,6 +227,7 @@ def linear_qkv_rope_append(x: torch.Tensor, Wqkv: torch.Tensor, pos: torch.Tenso
     _rows(x_rows, n, "x_rows")
     K = Wp.K
     _need(x.dim() == 2 and x.stride(1) == 1 and x.shape[1] >= K and x.dtype == Wp.dtype, "x (rows, K+)")
+    _need(n >= 0 and (x_rows is not None or x.shape[0] >= n), f"x holds {x.shape[0]} rows < n={n}")
     _need(Wp.N == (H + 2 * Hkv) * Dh, "Wqkv ((H+2Hkv)Dh, K)")
     _need(pos.dtype == torch.int32 and pos.numel() >= n and pos.is_contiguous(), "pos: int32")
     _need(flat_row.dtype == torch.int64 and flat_row.numel() >= n and flat_row.is_contiguous(), "flat_row: int64")
@@ -303,6 +312,7 @@ def linear(x: torch.Tensor, W, *, n: int | None = None, x_rows: torch.Tensor | N
     n = x.shape[0] if (n is None and x_rows is None) else (n if n is not None else x_rows.numel())
     _rows(x_rows, n, "x_rows")
     _need(x.shape[1] >= K and x.dtype == Wp.dtype, f"x width {x.shape[1]} < K={K} or dtype mismatch")
+    _need(n >= 0 and (x_rows is not None or x.shape[0] >= n), f"x holds {x.shape[0]} rows < n={n}")
     od = out_dtype or x.dtype
     width = N // 2 if swiglu else N
     if out is None:
@@ -328,12 +338,20 @@ def add_rmsnorm(a: torch.Tensor, w1: torch.Tensor, eps: float, *, res: torch.Ten
     _rows(a_rows, n, "a_rows")
     _rows(out_rows, n, "out_rows")
     _need(a.dim() == 2 and a.stride(1) == 1 and a.shape[1] >= D, "a (rows, D+)")
+    _need(n >= 0 and (a_rows is not None or a.shape[0] >= n), f"a holds {a.shape[0]} rows < n={n}")
     if res is not None:
-        _need(res.dim() == 2 and res.stride(1) == 1 and res.shape[0] >= n and res.dtype == a.dtype, "bad res")
+        _need(res.dim() == 2 and res.stride(1) == 1 and res.shape[0] >= n and res.shape[1] >= D
+              and res.dtype == a.dtype, "bad res")
     if x_out is None:
         x_out = torch.empty(n, D, dtype=a.dtype, device=a.device)
     if w2 is not None and h_out is None:
         h_out = torch.empty(n, D, dtype=a.dtype, device=a.device)
+    if x_out is not None:
+        _need(x_out.dim() == 2 and x_out.stride(1) == 1 and x_out.shape[1] >= D and x_out.dtype == a.dtype
+              and (out_rows is not None or x_out.shape[0] >= n), "x_out: (>= n rows, D+) of a's dtype")
+    if h_out is not None:
+        _need(h_out.dim() == 2 and h_out.stride(1) == 1 and h_out.shape[1] >= D and h_out.shape[0] >= n
+              and h_out.dtype == a.dtype, "h_out: (>= n rows, D+) of a's dtype")
     rc = _lib.load().wfd_add_rmsnorm(a.data_ptr(), _p(a_rows), a.stride(0), _p(res),
                                      res.stride(0) if res is not None else 0, w1.data_ptr(), _p(w2),
                                      x_out.data_ptr(), _p(out_rows), x_out.stride(0), _p(h_out),
@@ -356,8 +374,11 @@ def embed(ids: torch.Tensor, table: torch.Tensor, scale: float = 1.0, *, out: to
         _need(ring.dtype == torch.int64 and ring.is_contiguous(), "ring: int64 contiguous")
     n = ids.numel()
     Vocab, D = table.shape
+    _need(table.dim() == 2 and table.is_contiguous(), "table: contiguous (vocab, D)")
     if out is None:
         out = torch.empty(n, D, dtype=table.dtype, device=table.device)
+    _need(out.dim() == 2 and out.stride(1) == 1 and out.shape[0] >= n and out.shape[1] >= D
+          and out.dtype == table.dtype, "out: (>= n rows, D+) of the table's dtype")
     rc = _lib.load().wfd_embed(ids.data_ptr(), _p(ring), ring.numel() if ring is not None else 0, table.data_ptr(),
                                float(scale), out.data_ptr(), out.stride(0), n, Vocab, D, _dt(table), _stream())
     _lib.check(rc, "wfd_embed")
@@ -370,6 +391,10 @@ def copy_rows(src: torch.Tensor, dst: torch.Tensor, *, n: int, width: int, src_r
     _need(src.dtype == dst.dtype and src.stride(-1) == 1 and dst.stride(-1) == 1, "copy_rows dtype/layout")
     _rows(src_rows, n, "src_rows")
     _rows(dst_rows, n, "dst_rows")
+    _need(src.dim() == 2 and dst.dim() == 2 and 0 <= width <= min(src.shape[1], dst.shape[1]) and n >= 0,
+          "copy_rows: 2-D src/dst at least `width` wide")
+    _need(src_rows is not None or src.shape[0] >= n, f"src holds {src.shape[0]} rows < n={n}")
+    _need(dst_rows is not None or dst.shape[0] >= n, f"dst holds {dst.shape[0]} rows < n={n}")
     rc = _lib.load().wfd_copy_rows(src.data_ptr(), _p(src_rows), src.stride(0), dst.data_ptr(), _p(dst_rows),
                                    dst.stride(0), n, width, _dt(src), _stream())
     _lib.check(rc, "wfd_copy_rows")
@@ -382,12 +407,14 @@ def argmax(logits: torch.Tensor, *, n: int | None = None, out: torch.Tensor | No
     _need_cuda(logits, out, ring, ring_rows)
     _need(logits.dtype == torch.float32 and logits.dim() == 2 and logits.stride(1) == 1, "logits: float32 (n, V)")
     n = logits.shape[0] if n is None else n
+    _need(0 <= n <= logits.shape[0], f"n={n} outside the {logits.shape[0]} logits rows")
     if ring is not None:
         _need(ring.dtype == torch.int64 and ring.is_contiguous(), "ring: int64 contiguous")
         _rows(ring_rows, n, "ring_rows")
         _need(ring_rows is not None, "ring needs ring_rows")
     if out is None:
         out = torch.empty(n, dtype=torch.int64, device=logits.device)
+    _need(out.dtype == torch.int64 and out.is_contiguous() and out.numel() >= n, "out: int64 (>= n,)")
     rc = _lib.load().wfd_argmax(logits.data_ptr(), logits.stride(0), out.data_ptr(), _p(ring), _p(ring_rows),
                                 ring.numel() if ring is not None else 0, n, logits.shape[1], _stream())
     _lib.check(rc, "wfd_argmax")
