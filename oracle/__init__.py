@@ -26,7 +26,15 @@ tests/test_oracle_*.py):
                       own batch scheduler (tests/golden/); WFD == sequential
                       tokens; T_draft == T_total == sequential call for call;
                       alpha = 1 -> no rejects; alpha = 0 -> every draft rejected.
-  model (P/R/C)       composed only of the pinned pieces above; the block
-                      structure itself (sandwich norms, concat adapter) has
-                      no reference vector: parity unpinned beyond its parts.
+  model (P/R/C)       the composition (tests/test_oracle_composition.py):
+                      closed forms (Wqkv = fc = 0 -> norm_4(norm_2(x)); a
+                      lone key returns its value, so a block at position 0 is
+                      a fixed chain of library calls), the adapter's halves
+                      ([I | 0] reads s, [0 | I] reads e), and a dense causal
+                      formulation in torch over whole prompts (library
+                      RMSNorm / linear / SiLU / SDPA, complex-number RoPE)
+                      that must reproduce the per-slot oracle's logits and
+                      slot caches; planted wiring slips (residual after the
+                      norm, swapped norms, swapped adapter halves or gate/up,
+                      a missing coda ln_f, a transposed slot map) each fail.
 """

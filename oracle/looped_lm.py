@@ -9,9 +9,11 @@ single token row, so a token's numbers never depend on what else is in
 flight -- the oracle is batch-invariant by construction.
 
 The block structure (sandwich norms, concat adapter, interleaved-pair RoPE,
-SwiGLU) is this build's written spec of the looped model: the reference's
-Huginn arithmetic lives in absent external model code, so beyond its pinned
-pieces (oracle/kernels.py) the block forward is parity unpinned.
+SwiGLU) follows the reference's own block code (huginn_blocks.py:93-103,216,
+261-292); the Huginn module internals it calls live in absent external model
+code. The per-op pieces are pinned in tests/test_oracle_kernels.py, and the
+composition here in tests/test_oracle_composition.py (closed forms, the
+adapter's halves, and a dense causal torch formulation over whole prompts).
 
 `OracleBatchBlocks` exposes the union API that oracle/scheduler.py drives.
 """
