@@ -57,7 +57,8 @@ int wfd_abi_version(void);
  * out: (n, H, Dh). Query i attends rows kv_row_base[i] .. kv_row_base[i] +
  * kv_len[i] - 1 (with blocks, rows of one block). kv_len_max >= every
  * kv_len[i] sizes the grid (and must not exceed a block); workspace >=
- * wfd_attn_workspace_bytes(n, H, Dh, kv_len_max). Dh in {64, 128};
+ * wfd_attn_workspace_bytes(n, H, Dh, kv_len_max). A query with kv_len <= 0
+ * gets a zero output row. Dh in {64, 128};
  * H / Hkv in {1, 2, 4}. q, the caches, out and workspace are 16-byte aligned.
  * group_first (optional, device int32, n + 1 entries): group g = query rows
  * [group_first[g], group_first[g+1]) -- rows that share one slot (the same
@@ -77,6 +78,22 @@ int wfd_attn_decode(const void* q, const void* k_cache, const void* v_cache, int
                     const int64_t* kv_row_base, const int32_t* kv_len, const int32_t* group_first, void* out, int n,
                     int H, int Hkv, int Dh, int dtype, float scale, int kv_len_max, void* workspace, size_t ws_bytes,
                     wfd_stream_t stream);
+
+/*
+ * Row tables of a packed varlen attention call, built on the device: query
+ * row r of segment s (rows [cu_q[s], cu_q[s+1]) of q; keys [cu_k[s],
+ * cu_k[s+1]) of a token-major K / V) gets kv_row_base[r] = cu_k[s] and
+ * kv_len[r] = k_len (causal == 0) or max(k_len - q_len + (r - cu_q[s]) + 1, 0)
+ * (causal != 0: bottom-right per segment, the FA varlen convention; a row
+ * with no keys yields a zero output row from wfd_attn_decode). Rows at or
+ * past cu_q[nseg] get kv_len 0. cu_q, cu_k: int32 (nseg + 1), device data;
+ * the outputs then feed wfd_attn_decode with kv_block_rows = 0, so the whole
+ * call never reads a length back to the host.
+ * Replaces: the cu_seqlens handling of fa4_attention.attn_varlen /
+ *   _attn_varlen_torch (src/decoding/fa4_attention.py:301-317,348-366).
+ */
+int wfd_attn_varlen_rows(const int32_t* cu_q, const int32_t* cu_k, int nseg, int total_q, int causal,
+                         int64_t* kv_row_base, int32_t* kv_len, wfd_stream_t stream);
 
 /*
  * Causal prefill attention on MFMA (bf16; Dh 64 or 128; any H / Hkv).

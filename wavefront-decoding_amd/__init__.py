@@ -8,14 +8,15 @@ Layers, bottom-up:
   _lib, ops         ctypes binding + torch-tensor front end (no host fallback)
   attention         the reference's attention-backend API (attn_dense,
                     attn_cutoff_multi, attn_varlen, attn_varlen_q1_padded,
-                    set_backend/backend) routed to the decode kernel
+                    set_backend/backend, compute_qkv) on the HIP kernels
   kv_cache          StaticKVCache / BatchStaticKVCache over one flat device buffer
   model             synthetic looped-LM configs and seeded random-init weights
+  engine            the device engine: P / R / C unions as fused launch
+                    sequences, captured as hipGraphs (one replay per tick)
   blocks            P / R / C block forwards (single sequence and batch union)
   state, policy, acceptance, emu, batch_state
-  scheduler         generate_wavefront_dynamic, ar_generate
-  scheduler_batch   generate_wavefront_batch, ar_generate_batch
-  graph             hipGraph step engine (captured decode ticks)
+  scheduler         generate_wavefront_dynamic, generate_draft_then_verify
+  scheduler_batch   generate_wavefront_batch, ar_generate_batch, generate_dtv_batch
 """
 from __future__ import annotations
 

@@ -85,7 +85,15 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict
     lenq[j] = j < qn ? kv_len[q0 + j] : 0;
     maxlen = max(maxlen, lenq[j]);
   }
-  if (split * kAttnSplit >= maxlen) return;  // uniform for the whole workgroup
+  if (split * kAttnSplit >= maxlen) {  // uniform for the whole workgroup
+    // a group whose rows have no keys at all (kv_len <= 0): its first split
+    // writes their zero rows (the flash-attention convention for a query that
+    // attends nothing)
+    if (split == 0)
+      for (int idx = threadIdx.x; idx < qn * G * DH; idx += 64 * NW)
+        Elem<T>::store(out + ((int64_t)(q0 + idx / (G * DH)) * H + g * G + (idx / DH) % G) * DH + idx % DH, 0.f);
+    return;
+  }
   const int kend_max = min(maxlen, (split + 1) * kAttnSplit);
   const int ntiles = (kend_max - split * kAttnSplit + TK - 1) / TK;
 
@@ -275,7 +283,12 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict
 #pragma unroll
     for (int jj = 0; jj < QG; ++jj)
       if (jj == j) len = lenq[jj];
-    if (j >= qn || split * kAttnSplit >= len) continue;
+    if (j >= qn) continue;
+    if (len <= 0) {  // no keys: a zero row, written once
+      if (split == 0) Elem<T>::store(out + ((int64_t)(q0 + j) * H + g * G + (m - j * G)) * DH + d, 0.f);
+      continue;
+    }
+    if (split * kAttnSplit >= len) continue;
     int ns = (len + kAttnSplit - 1) / kAttnSplit;
     ns = ns < max_splits ? ns : max_splits;
     float M = -INFINITY;
@@ -355,6 +368,36 @@ __global__ __launch_bounds__(DH) void attn_combine_kernel(const float* __restric
   Elem<T>::store(out + ((int64_t)i * H + h) * DH + d, attn_finish(O, L));
 }
 
+// Per-row tables of a packed varlen call (the FA varlen convention): query
+// row r of segment s (rows [cu_q[s], cu_q[s+1]), keys [cu_k[s], cu_k[s+1]) of
+// a token-major K / V) reads keys from row cu_k[s]; non-causal it reads the
+// whole segment, causal (bottom-right) keys [0, k_len - q_len + r - cu_q[s]].
+// Rows at or past cu_q[nseg] get no keys. One thread per row, a binary search
+// over cu_q: the tables never leave the device.
+__global__ void varlen_rows_kernel(const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k, int nseg,
+                                   int total_q, int causal, int64_t* __restrict__ row_base,
+                                   int32_t* __restrict__ kv_len) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= total_q) return;
+  int lo = 0, hi = nseg;  // find the last s with cu_q[s] <= r
+  if (nseg <= 0 || r >= cu_q[nseg] || r < cu_q[0]) {
+    row_base[r] = 0;
+    kv_len[r] = 0;
+    return;
+  }
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (cu_q[mid] <= r)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  const int qs = cu_q[lo], ql = cu_q[lo + 1] - qs;
+  const int ks = cu_k[lo], kl = cu_k[lo + 1] - ks;
+  row_base[r] = ks;
+  kv_len[r] = causal ? max(kl - ql + (r - qs) + 1, 0) : kl;
+}
+
 static int max_splits_for(int kv_len_max) { return kv_len_max <= 0 ? 1 : (kv_len_max + kAttnSplit - 1) / kAttnSplit; }
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -411,6 +454,23 @@ static int dispatch_attn(int Dh, int G, const void* q, const void* kc, const voi
 }  // namespace wfd
 
 extern "C" {
+
+int wfd_attn_varlen_rows(const int32_t* cu_q, const int32_t* cu_k, int nseg, int total_q, int causal,
+                         int64_t* kv_row_base, int32_t* kv_len, hipStream_t stream) {
+  using namespace wfd;
+  if (nseg < 0 || total_q < 0) {
+    set_error("wfd_attn_varlen_rows: bad shape nseg=%d total_q=%d", nseg, total_q);
+    return kBadArg;
+  }
+  if (total_q == 0) return kOk;
+  if (!cu_q || !cu_k || !kv_row_base || !kv_len) {
+    set_error("wfd_attn_varlen_rows: null pointer argument");
+    return kBadArg;
+  }
+  hipLaunchKernelGGL(varlen_rows_kernel, dim3((total_q + 255) / 256), dim3(256), 0, stream, cu_q, cu_k, nseg, total_q,
+                     causal ? 1 : 0, kv_row_base, kv_len);
+  return launch_status("wfd_attn_varlen_rows");
+}
 
 size_t wfd_attn_workspace_bytes(int n, int H, int Dh, int kv_len_max) {
   if (n < 0 || H <= 0 || Dh <= 0) return 0;

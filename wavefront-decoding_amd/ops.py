@@ -128,6 +128,29 @@ def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, k
     return out
 
 
+def attn_varlen_rows(cu_q: torch.Tensor, cu_k: torch.Tensor, total_q: int, *, causal: bool,
+                     kv_row_base: torch.Tensor | None = None, kv_len: torch.Tensor | None = None):
+    """Per-row (kv_row_base int64, kv_len int32) tables of a packed varlen call,
+    built on the device from cu_q / cu_k (int32, nseg + 1): row r of segment s
+    reads keys from row cu_k[s] of a token-major K / V; all of the segment, or
+    (causal) keys [0, k_len - q_len + r - cu_q[s]]."""
+    _need_cuda(cu_q, cu_k, kv_row_base, kv_len)
+    _need(cu_q.dtype == torch.int32 and cu_k.dtype == torch.int32 and cu_q.is_contiguous() and cu_k.is_contiguous()
+          and cu_q.numel() == cu_k.numel() and cu_q.numel() >= 1, "cu_q / cu_k: int32 (nseg + 1,)")
+    if kv_row_base is None:
+        kv_row_base = torch.empty(total_q, dtype=torch.int64, device=cu_q.device)
+    if kv_len is None:
+        kv_len = torch.empty(total_q, dtype=torch.int32, device=cu_q.device)
+    _need(kv_row_base.dtype == torch.int64 and kv_row_base.is_contiguous() and kv_row_base.numel() >= total_q,
+          "kv_row_base: int64 (>= total_q,)")
+    _need(kv_len.dtype == torch.int32 and kv_len.is_contiguous() and kv_len.numel() >= total_q,
+          "kv_len: int32 (>= total_q,)")
+    rc = _lib.load().wfd_attn_varlen_rows(cu_q.data_ptr(), cu_k.data_ptr(), cu_q.numel() - 1, int(total_q),
+                                          1 if causal else 0, kv_row_base.data_ptr(), kv_len.data_ptr(), _stream())
+    _lib.check(rc, "wfd_attn_varlen_rows")
+    return kv_row_base, kv_len
+
+
 def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, seg_row_base: torch.Tensor,
                  seg_q_start: torch.Tensor, seg_pos0: torch.Tensor, *, max_seg_len: int, scale: float | None = None,
                  out: torch.Tensor | None = None) -> torch.Tensor:
