@@ -1,0 +1,304 @@
+"""Each benchmark configuration's own workload on the GPU, against the oracle
+or against sequential decode (GPU).
+
+* C1 (tiny fp32, 128-token prompt, 64 tokens): WFD at T_draft 1 and 2 commits
+  the oracle's sequential tokens with the oracle's counters; captured graphs
+  and the device token ring give the same tokens and counters as the oracle.
+* Accepted drafts under real greedy acceptance: an adapter [c R | I]
+  (R the random init block) makes shallow drafts agree with the full depth
+  (c = 0: every loop step sees e, so every draft is exact; c = 1 on the tiny
+  model: a mix of accepts and rejects); WFD and draft-then-verify still
+  commit exactly the sequential tokens, eager and captured.
+* C3 (2048-d bf16, 512-token prompt): greedy WFD with T_draft = 2 (W = 8) for
+  64 tokens commits exactly the sequential tokens, eager and captured, on the
+  random-init model (drafts rejected) and on the accepting variant.
+* C4 (2048-d bf16, B = 32, ragged prompts): the reference's batch gates
+  (experiments/exp4_emu/verify_batch.py:88-141): each sequence's tokens and
+  counters equal its solo run (emulated alpha = 0.7), replicas of one prompt
+  commit the same tokens, alpha = 0 next to alpha = 1 leaves the alpha = 1
+  sequence untouched, batch prefill equals single-sequence prefill, AR R calls
+  = (N - 1) T_total, and real greedy batch WFD equals sequential decode.
+* C5 (GQA 16 q / 4 kv, Dh 128): decode attention over 32k-key prefixes
+  (33 splits + the combine) against the oracle, and one R tick of the GQA
+  model (16 rows at depths 0..30) against the oracle.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kernels as ok
+from oracle import scheduler as osched
+from oracle import state_init
+from oracle.looped_lm import OracleBatchBlocks, OracleLM
+from tests.conftest import rel_err
+from wavefront_decoding_amd import model as M
+from wavefront_decoding_amd import ops
+from wavefront_decoding_amd.blocks import LoopedBlocks, LoopedBlocksBatch
+from wavefront_decoding_amd.emu import EmulatedAcceptance
+from wavefront_decoding_amd.engine import LoopedModel
+from wavefront_decoding_amd.policy import SsdPolicy
+from wavefront_decoding_amd.scheduler import generate_draft_then_verify, generate_wavefront_dynamic
+from wavefront_decoding_amd.scheduler_batch import ar_generate_batch, generate_wavefront_batch
+
+pytestmark = pytest.mark.gpu
+
+TINY = M.CONFIGS["tiny"]
+C3 = M.CONFIGS["looped-2048"]
+GQA = M.CONFIGS["looped-2048-gqa"]
+MINI_BF16 = M.LoopedLMConfig("mini-bf16", 4096, 512, 4, 4, 128, 1536, 1, 2, 1, 8)
+
+
+def _prompt(L, seed=0, V=4096):
+    return torch.randint(0, V, (L,), generator=torch.Generator().manual_seed(seed))
+
+
+def _round(a, cfg):
+    return torch.from_numpy(a).to(cfg.torch_dtype).float().numpy()
+
+
+def _oracle(cfg, w, S, B=1):
+    wn = M.weights_numpy(w)
+    s0t = lambda p: _round(state_init.s0_token(cfg.d_model, cfg.state_std, cfg.emb_scale, 0, p), cfg)  # noqa: E731
+    s0p = lambda L: _round(state_init.s0_prefill(cfg.d_model, cfg.state_std, cfg.emb_scale, 0, L), cfg)  # noqa: E731
+    return OracleBatchBlocks(OracleLM(cfg, wn, S, B, s0t, s0p))
+
+
+def accepting(cfg, w, c: float) -> dict:
+    """The same weights with adapter [c R | I]: R the random block acting on
+    s, identity on e. c = 0 makes every loop step's input e, so the hidden
+    state (and the draft) is the same at every depth."""
+    D = cfg.d_model
+    ad = w["adapter"].clone()
+    ad[:, D:] = torch.eye(D)
+    ad[:, :D] *= c
+    return dict(w, adapter=ad.to(cfg.torch_dtype).float())
+
+
+# ---------------------------------------------------------------------------
+# C1: tiny fp32, 128-token prompt, 64 tokens
+# ---------------------------------------------------------------------------
+@pytest.fixture(scope="module")
+def tiny_w():
+    return M.init_weights(TINY, 0)
+
+
+@pytest.mark.parametrize("graphs", [False, True])
+@pytest.mark.parametrize("T_draft", [1, 2])
+def test_c1_wfd_64_tokens_match_oracle(gpu, tiny_w, T_draft, graphs):
+    ids = _prompt(128)
+    N = 64
+    print(f"[C1] T_draft={T_draft} graphs={graphs}", flush=True)
+    blocks = LoopedBlocks(LoopedModel(TINY, tiny_w, gpu, max_seq_len=256, use_graphs=graphs))
+    toks, trace = generate_wavefront_dynamic(blocks, ids.to(gpu), N, SsdPolicy(TINY.T_total, T_draft))
+    oc = osched.wfd_single(_oracle(TINY, tiny_w, 256), ids.tolist(), N, TINY.T_total, T_draft)
+    assert toks == oc.tokens and len(toks) == N
+    assert trace.counters() == {k: getattr(oc, k) for k in trace.counters()}
+    assert toks == osched.ar_single(_oracle(TINY, tiny_w, 256), ids.tolist(), N, TINY.T_total)
+
+
+def test_graph_batch_and_token_ring_match_oracle(gpu, tiny_w):
+    """Captured batch WFD with ids kept in the device token ring (emulated
+    acceptance) against the oracle's batch restatement: tokens, per-sequence
+    counters and union sizes."""
+    P = [_prompt(40, 4), _prompt(25, 5), _prompt(33, 6)]
+    bb = LoopedBlocksBatch(LoopedModel(TINY, tiny_w, gpu, max_seq_len=128, max_batch=3, use_graphs=True))
+    emus = [EmulatedAcceptance(0.6, 1000 + b) for b in range(3)]
+    bt = generate_wavefront_batch(bb, [p.to(gpu) for p in P], [12, 9, 15], SsdPolicy(TINY.T_total, 2), emus)
+    res = osched.wfd_batch(_oracle(TINY, tiny_w, 128, B=3), [p.tolist() for p in P], [12, 9, 15], TINY.T_total, 2,
+                           [osched.Emu(0.6, 1000 + b) for b in range(3)])
+    for b in range(3):
+        assert bt.per_seq[b].tokens == res.per_seq[b].tokens
+        assert bt.per_seq[b].counters() == {k: getattr(res.per_seq[b], k) for k in bt.per_seq[b].counters()}
+    assert (bt.n_r_calls, bt.r_union_total, bt.r_union_max) == (res.n_r_calls, res.r_union_total, res.r_union_max)
+
+
+# ---------------------------------------------------------------------------
+# accepted drafts under real greedy acceptance
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("graphs", [False, True])
+def test_accepted_and_rejected_drafts_tiny(gpu, tiny_w, graphs):
+    """c = 1 on the tiny model: some drafts accepted, some rejected; tokens
+    and counters equal the oracle's, tokens equal sequential decode."""
+    w = accepting(TINY, tiny_w, 1.0)
+    ids = _prompt(32)
+    blocks = LoopedBlocks(LoopedModel(TINY, w, gpu, max_seq_len=128, use_graphs=graphs))
+    toks, tr = generate_wavefront_dynamic(blocks, ids.to(gpu), 30, SsdPolicy(TINY.T_total, 2))
+    assert tr.n_drafts_accepted > 0 and tr.n_drafts_rejected > 0, tr.counters()
+    oc = osched.wfd_single(_oracle(TINY, w, 128), ids.tolist(), 30, TINY.T_total, 2)
+    assert toks == oc.tokens
+    assert tr.counters() == {k: getattr(oc, k) for k in tr.counters()}
+    ar, _ = blocks.ar_generate(ids.to(gpu), 30)
+    assert toks == ar
+
+
+@pytest.mark.parametrize("graphs", [False, True])
+def test_accepted_drafts_bf16_wfd_and_dtv_lossless(gpu, graphs):
+    """c = 0 on a bf16 model with the 2048-d head shape: every draft is
+    accepted (WFD keeps its speculative rows and commits them), draft-then-
+    verify commits every draft plus the bonus tokens; both equal sequential."""
+    w = accepting(MINI_BF16, M.init_weights(MINI_BF16, 0), 0.0)
+    blocks = LoopedBlocks(LoopedModel(MINI_BF16, w, gpu, max_seq_len=256, use_graphs=graphs))
+    ids = _prompt(90, 3).to(gpu)
+    ar, _ = blocks.ar_generate(ids, 40)
+    for T_draft in (1, 2):
+        toks, tr = generate_wavefront_dynamic(blocks, ids, 40, SsdPolicy(MINI_BF16.T_total, T_draft))
+        assert toks == ar, T_draft
+        assert tr.n_drafts_accepted == tr.n_drafts_proposed > 0 and tr.n_drafts_rejected == 0
+    toks, tr = generate_draft_then_verify(blocks, ids, 40, SsdPolicy(MINI_BF16.T_total, 1), 3)
+    assert toks == ar
+    assert tr.n_drafts_accepted == tr.n_drafts_proposed > 0
+
+
+# ---------------------------------------------------------------------------
+# C3: the 2048-d model, 512-token prompt, greedy WFD at W = 8
+# ---------------------------------------------------------------------------
+@pytest.fixture(scope="module")
+def w2048():
+    return M.init_weights(C3, 0)
+
+
+@pytest.mark.parametrize("variant", ["random_init", "accepting"])
+def test_c3_greedy_wfd_is_lossless(gpu, w2048, variant):
+    """64 tokens of greedy WFD (T_total 16, T_draft 2) from the 512-token
+    prompt equal sequential looped decode, eager and captured."""
+    w = w2048 if variant == "random_init" else accepting(C3, w2048, 0.0)
+    ids = _prompt(512, 0, C3.vocab_size).to(gpu)
+    N = 64
+    ref = None
+    for graphs in (False, True):
+        print(f"[C3] {variant} graphs={graphs}", flush=True)
+        blocks = LoopedBlocks(LoopedModel(C3, w, gpu, max_seq_len=512 + N + 16, use_graphs=graphs))
+        ar, _ = blocks.ar_generate(ids, N)
+        toks, tr = generate_wavefront_dynamic(blocks, ids, N, SsdPolicy(C3.T_total, 2))
+        assert toks == ar and len(toks) == N
+        if variant == "accepting":
+            assert tr.n_drafts_accepted == tr.n_drafts_proposed > 0
+        ref = ar if ref is None else ref
+        assert ar == ref  # eager and captured decode agree
+        del blocks
+        torch.cuda.empty_cache()
+
+
+# ---------------------------------------------------------------------------
+# C4: the 2048-d model at B = 32, ragged prompts
+# ---------------------------------------------------------------------------
+B4 = 32
+
+
+@pytest.fixture(scope="module")
+def c4(gpu, w2048):
+    g = torch.Generator().manual_seed(0)
+    plen = torch.randint(16, 97, (B4,), generator=g).tolist()
+    glen = torch.randint(8, 25, (B4,), generator=g).tolist()
+    prompts = [torch.randint(0, C3.vocab_size, (p,), generator=g).to(gpu) for p in plen]
+    model = LoopedModel(C3, w2048, gpu, max_seq_len=max(plen) + max(glen) + 16, max_batch=B4)
+    yield model, prompts, glen
+    del model
+    torch.cuda.empty_cache()
+
+
+def test_c4_batch_equals_solo_runs(gpu, c4):
+    """Emulated alpha = 0.7 (seeds 1000 + b): every sequence of the 32-wide
+    batch commits its solo run's tokens with its solo run's counters."""
+    model, prompts, glen = c4
+    policy = SsdPolicy(C3.T_total, 2)
+    print("[C4] batch of 32", flush=True)
+    bt = generate_wavefront_batch(LoopedBlocksBatch(model, batch_size=B4), prompts, glen, policy,
+                                  [EmulatedAcceptance(0.7, 1000 + b) for b in range(B4)])
+    assert bt.r_union_max > 100  # the sequences' waves really shared unions
+    solo_blocks = LoopedBlocksBatch(model, batch_size=1)
+    for b in range(B4):
+        solo = generate_wavefront_batch(solo_blocks, [prompts[b]], [glen[b]], policy,
+                                        [EmulatedAcceptance(0.7, 1000 + b)])
+        assert bt.per_seq[b].tokens == solo.per_seq[0].tokens, b
+        assert bt.per_seq[b].counters() == solo.per_seq[0].counters(), b
+
+
+def test_c4_greedy_batch_equals_sequential(gpu, c4):
+    """Real greedy acceptance over the ragged 32-wide batch commits exactly
+    the lockstep sequential decode's tokens; AR R calls = (N - 1) T_total."""
+    model, prompts, glen = c4
+    bb = LoopedBlocksBatch(model, batch_size=B4)
+    print("[C4] greedy batch vs sequential", flush=True)
+    wfd = generate_wavefront_batch(bb, prompts, glen, SsdPolicy(C3.T_total, 2))
+    ar = ar_generate_batch(bb, prompts, glen)
+    assert [t.tokens for t in wfd.per_seq] == [t.tokens for t in ar.per_seq]
+    for t, n in zip(ar.per_seq, glen):
+        assert t.n_r_calls == (n - 1) * C3.T_total and len(t.tokens) == n
+
+
+def test_c4_replicas_isolation_and_prefill(gpu, c4):
+    """Replicas of one prompt commit identical tokens and counters; an
+    alpha = 0 neighbour leaves an alpha = 1 sequence's run unchanged; batch
+    prefill logits equal the single-sequence prefill's."""
+    model, prompts, glen = c4
+    policy = SsdPolicy(C3.T_total, 1)
+    bb4 = LoopedBlocksBatch(model, batch_size=4)
+    bt = generate_wavefront_batch(bb4, [prompts[0]] * 4, 12, policy, [EmulatedAcceptance(1.0, 11) for _ in range(4)])
+    assert all(t.tokens == bt.per_seq[0].tokens and t.counters() == bt.per_seq[0].counters() for t in bt.per_seq)
+    bb1 = LoopedBlocksBatch(model, batch_size=1)
+    solo = generate_wavefront_batch(bb1, [prompts[1]], 12, policy, [EmulatedAcceptance(1.0, 31)])
+    bb2 = LoopedBlocksBatch(model, batch_size=2)
+    mix = generate_wavefront_batch(bb2, [prompts[1]] * 2, 12, policy,
+                                   [EmulatedAcceptance(0.0, 99), EmulatedAcceptance(1.0, 31)])
+    assert solo.per_seq[0].counters() == mix.per_seq[1].counters()
+    assert solo.per_seq[0].tokens == mix.per_seq[1].tokens
+    t0 = mix.per_seq[0]
+    assert t0.n_drafts_proposed > 0 and t0.n_drafts_accepted == 0 and len(t0.tokens) == 12
+    _, lb = bb2.prefill([prompts[2], prompts[2]])
+    _, ls = LoopedBlocks(model).prefill(prompts[2], C3.T_total, 2)
+    assert rel_err(lb[0].cpu().numpy(), ls.cpu().numpy()) <= 1e-6
+
+
+# ---------------------------------------------------------------------------
+# C5: GQA 16 q / 4 kv heads, 32k context
+# ---------------------------------------------------------------------------
+def test_c5_attention_32k_matches_oracle(gpu):
+    """8 decode rows over two 32k-key slots in the engine's head-major block
+    layout: 33 splits per row plus the split combine, against the oracle."""
+    S = 32800
+    lens = [32768, 32769, 32770, 32775, 32700, 30000, 32799, 31744]
+    g = torch.Generator().manual_seed(32)
+    K = torch.randn(2 * S, 4, 128, generator=g).to(torch.bfloat16)
+    V = torch.randn(2 * S, 4, 128, generator=g).to(torch.bfloat16)
+    q = torch.randn(8, 16, 128, generator=g).to(torch.bfloat16)
+    rb = torch.tensor([(i % 2) * S for i in range(8)], dtype=torch.int64)
+    kl = torch.tensor(lens, dtype=torch.int32)
+    blocks = lambda t: t.view(2, S, 4, 128).permute(0, 2, 1, 3).contiguous()  # noqa: E731
+    print("[C5] attention 32k", flush=True)
+    out = ops.attn_decode(q.to(gpu), blocks(K).to(gpu), blocks(V).to(gpu), rb.to(gpu), kl.to(gpu), kv_len_max=S)
+    assert ops.attn_workspace_bytes(8, 16, 128, S) > 0
+    ref = ok.attention_rows(q.float().numpy(), K.float().numpy(), V.float().numpy(), rb.numpy(), kl.numpy())
+    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-2
+
+
+def test_c5_gqa_core_tick_matches_oracle(gpu):
+    """One R tick of the GQA looped model (16 rows = W at depths 0, 2, ..., 30
+    of one sequence, random K/V prefixes at a reduced 2k context) against the
+    fp32 oracle fed the same bf16 values: <= 2e-2."""
+    cfg = GQA
+    w = M.init_weights(cfg, 0)
+    S = 2048
+    model = LoopedModel(cfg, w, gpu, max_seq_len=S, max_batch=1)
+    cache = model.create_cache(1)
+    g = torch.Generator().manual_seed(5)
+    for t in (cache.flat_k, cache.flat_v):
+        t.copy_(torch.randn(t.shape, generator=g).to(torch.bfloat16))
+    pos = [2000 - i for i in range(16)]
+    steps = [2 * i for i in range(16)]
+    rows = [model.pool_row(0, p) for p in pos]
+    state = torch.randn(16, 2 * cfg.d_model, generator=g).to(torch.bfloat16)
+    model.pool[rows] = state.to(gpu)
+    print("[C5] GQA core tick", flush=True)
+    model.core_union(cache, [0] * 16, pos, steps)
+    got = model.pool[rows, : cfg.d_model].float().cpu().numpy()
+    lm = OracleLM(cfg, M.weights_numpy(w), S, 1, None, None)
+    lm.Kc[:] = cache.K.float().cpu().numpy()
+    lm.Vc[:] = cache.V.float().cpu().numpy()
+    st = state.float().numpy()
+    ref = np.stack([lm.core(0, pos[i], steps[i], st[i, : cfg.d_model], st[i, cfg.d_model:]) for i in range(16)])
+    assert rel_err(got, ref) <= 2e-2
+    del model, cache
+    torch.cuda.empty_cache()
