@@ -41,6 +41,8 @@ enum { WFD_EPI_PLAIN = 0, WFD_EPI_SWIGLU = 1 };
 
 /* Message for the last failing call on this thread. */
 const char* wfd_last_error(void);
+/* Bumped whenever an entry point's signature changes (5: wfd_argmax's accept flags,
+   wfd_attn_varlen_rows). */
 int wfd_abi_version(void);
 
 /*
@@ -238,13 +240,18 @@ int wfd_copy_rows(const void* src, const int32_t* src_rows, int64_t lds, void* d
 /*
  * out[i] = argmax_j logits[i, j] (first index on ties), logits fp32, 16-byte
  * aligned; with a ring, also ring[ring_rows[i]] = out[i] (rows outside
- * [0, ring_len) are skipped).
- * Replaces: greedy_sample's argmax and its .item() (src/decoding/acceptance.py:40-44)
- *   and coda_argmax_union's argmax + .tolist() (src/decoding/huginn_blocks_batch.py:345-346):
- *   with the ring, ids stay on the device until the caller reads them.
+ * [0, ring_len) are skipped). With expect / accept (both or neither):
+ * accept[i] = 1 if out[i] equals the expected token -- expect[i] >= 0 a plain
+ * id, -ring_len <= expect[i] < 0 a ring handle -(slot + 1) whose id an
+ * earlier pass wrote -- else 0 (also for any other expect[i]: no comparison).
+ * Replaces: greedy_sample's argmax and its .item() (src/decoding/acceptance.py:40-44),
+ *   greedy_accept's draft == argmax comparison (acceptance.py:47-58), and
+ *   coda_argmax_union's argmax + .tolist() (src/decoding/huginn_blocks_batch.py:345-346):
+ *   with the ring and the accept flags, ids stay on the device and a greedy
+ *   verify reads back one flag per row.
  */
 int wfd_argmax(const float* logits, int64_t ld, int64_t* out, int64_t* ring, const int32_t* ring_rows,
-               int64_t ring_len, int n, int vocab, wfd_stream_t stream);
+               int64_t ring_len, const int64_t* expect, int32_t* accept, int n, int vocab, wfd_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -34,7 +34,7 @@ def test_library_loads_and_exports_every_symbol():
 
 def test_host_only_entry_points():
     lib = _lib.load()
-    assert lib.wfd_abi_version() == 4
+    assert lib.wfd_abi_version() == 5
     assert lib.wfd_swiglu(None, 16, None, 8, 1, 12, 1, None) == -1  # F not a multiple of 8 (bf16)
     assert lib.wfd_swiglu(None, 16, None, 8, 0, 8, 1, None) == 0
     assert [lib.wfd_attn_group_max_rows(16, k) for k in (16, 8, 4, 3)] == [8, 4, 2, 0]

@@ -151,6 +151,41 @@ def test_accepted_drafts_bf16_wfd_and_dtv_lossless(gpu, graphs):
     assert tr.n_drafts_accepted == tr.n_drafts_proposed > 0
 
 
+class _HostCompare:
+    """The same blocks without device-side comparison or token handles: the
+    batch scheduler then reads every argmax back and compares on the host."""
+
+    def __init__(self, inner):
+        self._inner = inner
+
+    def __getattr__(self, name):
+        if name in ("resolve_tokens", "reset_token_ring", "device_accept"):
+            raise AttributeError(name)
+        return getattr(self._inner, name)
+
+
+@pytest.mark.parametrize("graphs", [False, True])
+def test_device_greedy_verify_matches_host_compare(gpu, tiny_w, graphs):
+    """Greedy batch WFD with the accept decision made on the device (one flag
+    per verify row, ids kept in the token ring) commits the tokens and counters
+    of the host comparison and of the oracle, over accepts and rejects."""
+    w = accepting(TINY, tiny_w, 1.0)
+    P = [_prompt(32), _prompt(21, 5), _prompt(40, 6)]
+    N = [30, 17, 25]
+    res = []
+    for host in (False, True):
+        bb = LoopedBlocksBatch(LoopedModel(TINY, w, gpu, max_seq_len=128, max_batch=3, use_graphs=graphs))
+        bt = generate_wavefront_batch(_HostCompare(bb) if host else bb, [p.to(gpu) for p in P], N,
+                                      SsdPolicy(TINY.T_total, 2))
+        res.append([(t.tokens, t.counters()) for t in bt.per_seq])
+    assert res[0] == res[1]
+    acc = sum(c["n_drafts_accepted"] for _, c in res[0])
+    rej = sum(c["n_drafts_rejected"] for _, c in res[0])
+    assert acc > 0 and rej > 0, (acc, rej)
+    oc = osched.wfd_batch(_oracle(TINY, w, 128, B=3), [p.tolist() for p in P], N, TINY.T_total, 2)
+    assert [t for t, _ in res[0]] == [t.tokens for t in oc.per_seq]
+
+
 # ---------------------------------------------------------------------------
 # C3: the 2048-d model, 512-token prompt, greedy WFD at W = 8
 # ---------------------------------------------------------------------------
@@ -177,7 +212,12 @@ def test_c3_greedy_wfd_is_lossless(gpu, w2048, variant):
             assert tr.n_drafts_accepted == tr.n_drafts_proposed > 0
         ref = ar if ref is None else ref
         assert ar == ref  # eager and captured decode agree
-        del blocks
+        # the batch scheduler at B = 1 with the verify on the device (the bench's path)
+        bb = LoopedBlocksBatch(blocks.model, batch_size=1)
+        bt = generate_wavefront_batch(bb, [ids], N, SsdPolicy(C3.T_total, 2))
+        assert bt.per_seq[0].tokens == ar
+        assert bt.per_seq[0].counters() == tr.counters()
+        del blocks, bb
         torch.cuda.empty_cache()
 
 

@@ -52,7 +52,7 @@ SIGNATURES: dict[str, tuple] = {
                                _i32, _vp]),
     "wfd_embed": (_i32, [_vp, _vp, _i64, _vp, _f32, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
     "wfd_copy_rows": (_i32, [_vp, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _i32, _vp]),
-    "wfd_argmax": (_i32, [_vp, _i64, _vp, _vp, _vp, _i64, _i32, _i32, _vp]),
+    "wfd_argmax": (_i32, [_vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i32, _i32, _vp]),
 }
 
 _LIB: ctypes.CDLL | None = None

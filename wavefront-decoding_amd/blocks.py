@@ -23,7 +23,7 @@ import numpy as np
 import torch
 
 from .acceptance import GREEDY, RowLogits
-from .engine import LoopedModel
+from .engine import NO_EXPECT, LoopedModel
 from .kv_cache import BatchStaticKVCache, StaticKVCache
 from .state import ActiveToken, WavefrontState
 
@@ -301,12 +301,19 @@ class LoopedBlocksBatch:
             return list(self.model.last_c_handles)
         return ids.tolist()
 
+    # the C pass can compare each row's argmax with the token speculated at
+    # the next position on the device (wfd_argmax's accept flags)
+    device_accept = True
+
     @torch.no_grad()
-    def run_passes(self, passes, cache, lazy: bool = False) -> list[int] | None:
+    def run_passes(self, passes, cache, lazy: bool = False, expect=None) -> list[int] | None:
         """A tick's passes -- [(kind, seq_ids, toks)] with kind "P", "R" or "C"
         (C last) -- as one launch sequence (one graph replay, one table upload),
         with the token bookkeeping prelude_union / advance_union /
-        coda_argmax_union would do. Returns the C pass's ids (or handles)."""
+        coda_argmax_union would do. Returns the C pass's ids (or handles).
+        `expect` (C rows, each a plain id, a ring handle or None): the C pass
+        also compares every row's argmax with it on the device, and
+        `last_accept` receives the flags (one device->host read for the tick)."""
         eng, R = [], self.model.R
         for kind, seq_ids, toks in passes:
             if not toks:
@@ -322,10 +329,14 @@ class LoopedBlocksBatch:
                 for t in toks:
                     t.step += 1
             else:
-                eng.append(("C", seq_ids, pos, None))
+                exp = None if expect is None else [NO_EXPECT if e is None else e for e in expect]
+                eng.append(("C", seq_ids, pos, exp))
         out = self.model.run_passes(cache, eng) if eng else None
+        self.last_accept = None
         if out is None:
             return None
+        if expect is not None:
+            self.last_accept = [bool(f) for f in self.model.last_accept.tolist()]
         if lazy and self.model.last_c_handles is not None:
             return list(self.model.last_c_handles)
         return out[1].tolist()

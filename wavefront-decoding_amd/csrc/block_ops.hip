@@ -276,7 +276,8 @@ __device__ __forceinline__ void argmax_merge(float& bv, int& bi, float ov, int o
 __global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float* __restrict__ logits, int64_t ld,
                                                             int64_t* __restrict__ out, int64_t* __restrict__ ring,
                                                             const int32_t* __restrict__ ring_rows, int64_t ring_len,
-                                                            int Vocab) {
+                                                            const int64_t* __restrict__ expect,
+                                                            int32_t* __restrict__ accept, int Vocab) {
   __shared__ float sv[kArgThreads / 64];
   __shared__ int si[kArgThreads / 64];
   const int i = blockIdx.x;
@@ -307,6 +308,18 @@ __global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float* __rest
     int ix = si[0];
     for (int w = 1; w < kArgThreads / 64; ++w) argmax_merge(b, ix, sv[w], si[w]);
     out[i] = (int64_t)ix;
+    if (accept) {
+      // greedy acceptance on the device: the token speculated at the next
+      // position is a plain id (>= 0) or a ring handle -(slot + 1) written by
+      // an earlier pass; anything else is "nothing to compare" (reads 0)
+      const int64_t e = expect[i];
+      int64_t want = -1;
+      if (e >= 0)
+        want = e;
+      else if (ring && e >= -ring_len)
+        want = ring[-e - 1];
+      accept[i] = want == (int64_t)ix ? 1 : 0;
+    }
     if (ring) {
       const int32_t r = ring_rows[i];
       if (r >= 0 && r < ring_len) ring[r] = (int64_t)ix;
@@ -342,7 +355,7 @@ extern "C" {
 
 const char* wfd_last_error(void) { return wfd::g_err; }
 
-int wfd_abi_version(void) { return 4; }
+int wfd_abi_version(void) { return 5; }
 
 int wfd_add_rmsnorm(const void* a, const int32_t* a_rows, int64_t lda, const void* res, int64_t ldr, const void* w1,
                     const void* w2, void* x_out, const int32_t* out_rows, int64_t ldo, void* h_out, int64_t ldh, int n,
@@ -507,15 +520,15 @@ int wfd_copy_rows(const void* src, const int32_t* src_rows, int64_t lds, void* d
 }
 
 int wfd_argmax(const float* logits, int64_t ld, int64_t* out, int64_t* ring, const int32_t* ring_rows,
-               int64_t ring_len, int n, int vocab, hipStream_t stream) {
+               int64_t ring_len, const int64_t* expect, int32_t* accept, int n, int vocab, hipStream_t stream) {
   using namespace wfd;
   if (n < 0 || vocab <= 0 || ld < vocab) {
     set_error("wfd_argmax: bad shape n=%d vocab=%d", n, vocab);
     return kBadArg;
   }
   if (n == 0) return kOk;
-  if (!logits || !out || (ring && (!ring_rows || ring_len <= 0))) {
-    set_error("wfd_argmax: null pointer argument (ring needs ring_rows and a length)");
+  if (!logits || !out || (ring && (!ring_rows || ring_len <= 0)) || (!expect != !accept)) {
+    set_error("wfd_argmax: null pointer argument (ring needs ring_rows and a length; expect and accept go together)");
     return kBadArg;
   }
   if (((uintptr_t)logits) & 15) {
@@ -523,7 +536,7 @@ int wfd_argmax(const float* logits, int64_t ld, int64_t* out, int64_t* ring, con
     return kBadArg;
   }
   hipLaunchKernelGGL(argmax_kernel, dim3(n), dim3(kArgThreads), 0, stream, logits, ld, out, ring, ring_rows,
-                     ring_len, vocab);
+                     ring_len, expect, accept, vocab);
   return launch_status("wfd_argmax");
 }
 

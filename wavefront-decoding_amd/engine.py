@@ -124,6 +124,9 @@ _LINEAR_WEIGHTS = frozenset({"Wqkv", "proj", "fc", "mlp_proj", "adapter", "lm_he
 # grouped attention only when at least this many (group, kv head) workgroups remain
 _GROUP_MIN_WORKGROUPS = 256
 
+# a C row's expected-token entry that asks for no comparison (below every ring handle)
+NO_EXPECT = -(1 << 62)
+
 
 def _bucket(n: int) -> int:
     b = 1
@@ -184,6 +187,7 @@ class LoopedModel:
         self.sc = self._scratch(self.max_rows)
         self.sc["logits"] = torch.empty(self.max_rows, cfg.vocab_size, dtype=torch.float32, device=self.device)
         self.sc["ids"] = torch.empty(self.max_rows, dtype=torch.int64, device=self.device)
+        self.sc["accept"] = torch.zeros(self.max_rows, dtype=torch.int32, device=self.device)
         self.attn_ws = torch.zeros(ops.attn_workspace_bytes(self.max_rows, cfg.n_heads, cfg.head_dim, max_seq_len),
                                    dtype=torch.uint8, device=self.device)
         self.staging = _Staging(self.device)
@@ -196,6 +200,9 @@ class LoopedModel:
         self.tok_ring = torch.zeros(ring_len + 1, dtype=torch.int64, device=self.device)
         self._ring_next = 0
         self.last_c_handles: list[int] | None = None
+        self.last_accept: torch.Tensor | None = None
+        # algorithmic HBM bytes of every pass launched (see pass_bytes)
+        self.bytes_moved = 0
 
     # -- slots / rows ----------------------------------------------------------
     def slot_prelude(self, i: int) -> int:
@@ -321,8 +328,10 @@ class LoopedModel:
                 groups: np.ndarray | None = None):
         """int32 [pos | kv_len | pool_row | ring_slot (C only) | group_first
         (grouped passes, nb + 1)] and int64 [ids (P only) | row_base x L |
-        flat_row x L], each block nb wide; rows n..nb-1 are padding aimed at
-        the trash rows / trash ring slot."""
+        flat_row x L | expected token (C only)], each block nb wide; rows
+        n..nb-1 are padding aimed at the trash rows / trash ring slot. For C,
+        `ids` carries the expected tokens of a device-side greedy verify
+        (NO_EXPECT: no comparison)."""
         c = self.cfg
         n = len(pos)
         L = self._layers(kind)
@@ -354,6 +363,11 @@ class LoopedModel:
             idp = np.zeros(nb, dtype=np.int64)
             idp[:n] = ids
             parts.insert(0, idp)
+        elif kind == "C":
+            exp = np.full(nb, NO_EXPECT, dtype=np.int64)
+            if ids is not None and len(ids):
+                exp[:n] = ids
+            parts.append(exp)
         return i32, np.concatenate(parts)
 
     def _launch(self, kind: str, cache, nb: int, t32: torch.Tensor, t64: torch.Tensor, kv_max: int,
@@ -391,9 +405,11 @@ class LoopedModel:
                 self._block(f"coda.{i}.", nb, sc, pos_d, kvlen_d, rb(i), fr(i), kv_max, ws, cache, nxt,
                             group_first=gf)
             ops.linear(sc["h"], W["lm_head"], n=nb, out=sc["logits"], out_dtype=torch.float32)
-            ops.argmax(sc["logits"], n=nb, out=sc["ids"], ring=self.tok_ring, ring_rows=t32[3 * nb: 4 * nb])
+            ops.argmax(sc["logits"], n=nb, out=sc["ids"], ring=self.tok_ring, ring_rows=t32[3 * nb: 4 * nb],
+                       expect=t64[2 * L * nb: 2 * L * nb + nb], accept=sc["accept"])
 
     def _plan(self, kind: str, cache, seqs, pos, steps=None, ids=None, ring_base=None) -> dict:
+        # ids: token ids / handles (P) or expected tokens (C)
         """Tables and launch shape of one pass (padded to its row bucket under graphs)."""
         n = len(pos)
         nb = _bucket(n) if self.use_graphs else n
@@ -461,6 +477,35 @@ class LoopedModel:
         if cache.S > self.max_seq_len:
             raise ValueError("cache longer than the engine's tables (max_seq_len)")
 
+    # -- traffic accounting ------------------------------------------------------------
+    def pass_bytes(self, kind: str, positions) -> int:
+        """Algorithmic HBM bytes of one pass over rows at `positions`: every
+        weight byte of its layers once (plus the embedding rows for P, the
+        adapter for R, ln_f and lm_head for C), each row's slot prefix (K and V
+        of keys [0, position]) per layer, its K/V append, and the activation
+        rows the layers read and write (x into each linear, its output, the
+        norms' inputs and outputs). Padding rows of a captured launch are not
+        counted: they are not part of the work."""
+        c = self.cfg
+        el = torch.empty(0, dtype=self.dtype).element_size()
+        D, F, Hd, Kd = c.d_model, c.ffn, c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
+        layer_w = (c.qkv_dim * D + D * Hd + 2 * F * D + D * F + 4 * D) * el
+        n = len(positions)
+        kv_keys = sum(int(p) + 1 for p in positions)
+        layer_kv = (kv_keys * 2 * Kd + n * 2 * Kd) * el
+        # per row: Wqkv x -> q; attention q -> o; proj o -> a; norm (a, x) -> (x, h);
+        # fc h -> u; mlp_proj u -> m; norm (m, x) -> (x, h)
+        layer_act = n * (12 * D + 4 * Hd + 2 * F) * el
+        L = self._layers(kind)
+        total = L * (layer_w + layer_kv + layer_act)
+        if kind == "P":
+            total += n * D * el + n * 2 * D * el + n * D * el  # embedding rows, pool rows written, s0 rows
+        elif kind == "R":
+            total += 2 * D * D * el + n * (2 * D + D) * el  # adapter weights, its x rows and output
+        else:
+            total += (c.vocab_size * D + D) * el + n * (D + c.vocab_size * 4 + 8)  # lm_head, ln_f, logits, ids
+        return int(total)
+
     # -- P / R / C ---------------------------------------------------------------------
     def _prepare(self, cache, kind: str, seqs, positions, extra=None):
         """Validated plan + bookkeeping closure of one pass. extra: token ids (P),
@@ -487,7 +532,8 @@ class LoopedModel:
         if self._ring_next + n <= self.ring_len:
             base = self._ring_next
             self._ring_next += n
-        plan = self._plan("C", cache, seqs, pos, ring_base=base)
+        expect = None if extra is None else np.asarray(extra, dtype=np.int64)
+        plan = self._plan("C", cache, seqs, pos, ids=expect, ring_base=base)
         writes = [(self.slot_coda(i), b, p) for b, p in zip(seqs.tolist(), pos.tolist()) for i in range(c.n_coda)]
         return plan, writes, (None if base is None else [-(base + i) - 1 for i in range(n)])
 
@@ -495,9 +541,12 @@ class LoopedModel:
         """Several passes as one launch sequence -- one graph replay and one
         table upload -- in order: passes = [(kind, seqs, positions, extra)],
         kind "P" (extra = token ids or ring handles), "R" (extra = steps) or
-        "C" (extra unused; at most one, last). A scheduler tick (P, R, C) or a
-        whole sequential token (P, T_total x R, C) then costs one replay.
-        Returns what coda_union returns for the C pass, else None."""
+        "C" (extra = None, or per row the token expected from its argmax -- a
+        plain id, a ring handle, or NO_EXPECT -- for a device-side greedy
+        verify whose flags land in `last_accept`; at most one C, last). A
+        scheduler tick (P, R, C) or a whole sequential token (P, T_total x R,
+        C) then costs one replay. Returns what coda_union returns for the C
+        pass, else None."""
         plans, writes, handles, n_c = [], [], None, 0
         for kind, seqs, positions, extra in passes:
             if len(positions) == 0:
@@ -506,6 +555,7 @@ class LoopedModel:
                 raise ValueError("the C pass must come last")
             plan, w, h = self._prepare(cache, kind, seqs, positions, extra)
             plans.append(plan)
+            self.bytes_moved += self.pass_bytes(kind, positions)
             writes += w
             if kind == "C":
                 handles, n_c = h, len(positions)
@@ -515,6 +565,7 @@ class LoopedModel:
             cache.note_write(slot, b, p)
         if n_c:
             self.last_c_handles = handles
+            self.last_accept = self.sc["accept"][:n_c]
             return self.sc["logits"][:n_c], self.sc["ids"][:n_c]
         return None
 

@@ -424,10 +424,13 @@ def copy_rows(src: torch.Tensor, dst: torch.Tensor, *, n: int, width: int, src_r
 
 
 def argmax(logits: torch.Tensor, *, n: int | None = None, out: torch.Tensor | None = None,
-           ring: torch.Tensor | None = None, ring_rows: torch.Tensor | None = None) -> torch.Tensor:
+           ring: torch.Tensor | None = None, ring_rows: torch.Tensor | None = None,
+           expect: torch.Tensor | None = None, accept: torch.Tensor | None = None) -> torch.Tensor:
     """out[i] = argmax logits[i] (first index on ties); with `ring`, also
-    ring[ring_rows[i]] = out[i]."""
-    _need_cuda(logits, out, ring, ring_rows)
+    ring[ring_rows[i]] = out[i]; with `expect` (int64: a plain id, a ring
+    handle, or anything below -len(ring) for no comparison) also
+    accept[i] = int32(out[i] == expected token)."""
+    _need_cuda(logits, out, ring, ring_rows, expect, accept)
     _need(logits.dtype == torch.float32 and logits.dim() == 2 and logits.stride(1) == 1, "logits: float32 (n, V)")
     n = logits.shape[0] if n is None else n
     _need(0 <= n <= logits.shape[0], f"n={n} outside the {logits.shape[0]} logits rows")
@@ -438,7 +441,12 @@ def argmax(logits: torch.Tensor, *, n: int | None = None, out: torch.Tensor | No
     if out is None:
         out = torch.empty(n, dtype=torch.int64, device=logits.device)
     _need(out.dtype == torch.int64 and out.is_contiguous() and out.numel() >= n, "out: int64 (>= n,)")
+    _need((expect is None) == (accept is None), "expect and accept go together")
+    if expect is not None:
+        _need(expect.dtype == torch.int64 and expect.is_contiguous() and expect.numel() >= n, "expect: int64 (>= n,)")
+        _need(accept.dtype == torch.int32 and accept.is_contiguous() and accept.numel() >= n, "accept: int32 (>= n,)")
     rc = _lib.load().wfd_argmax(logits.data_ptr(), logits.stride(0), out.data_ptr(), _p(ring), _p(ring_rows),
-                                ring.numel() if ring is not None else 0, n, logits.shape[1], _stream())
+                                ring.numel() if ring is not None else 0, _p(expect), _p(accept), n, logits.shape[1],
+                                _stream())
     _lib.check(rc, "wfd_argmax")
     return out

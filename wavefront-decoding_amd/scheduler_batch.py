@@ -13,8 +13,10 @@ Extensions over the reference (its behaviour is the default): prompts may
 have different lengths (a list of 1-D id sequences; the reference needs
 equal lengths, huginn_blocks_batch.py:180-185), and max_new_tokens may be a
 per-sequence list (the reference takes one value, scheduler_batch.py:348-349).
-When every decision is emulated (or nothing is decided, AR), sampled ids stay
-on the device as token handles and are read back once at the end.
+Sampled ids stay on the device as token handles, read back once at the end,
+whenever nothing on the host needs their values: emulated decisions, AR, and
+greedy WFD on blocks that compare the argmaxes on the device (then a tick
+reads back one accept flag per C row instead of the ids).
 """
 from __future__ import annotations
 
@@ -136,20 +138,29 @@ class _BatchRun:
         self.handles = handles and hasattr(blocks, "resolve_tokens") and hasattr(blocks, "reset_token_ring")
         if self.handles:
             blocks.reset_token_ring()
+        self.accept_flags: list[bool] | None = None
 
     def live(self) -> list[Lane]:
         return [lane for lane in self.lanes if not lane.done]
 
-    def launch(self, p_rows, r_rows, c_rows, r_repeat: int = 1):
+    def launch(self, p_rows, r_rows, c_rows, r_repeat: int = 1, expect=None):
         """P, R (r_repeat times) and C over [(lane, token)] rows as one launch
         sequence when the blocks fuse passes; returns the C rows' ids (or token
-        handles) and updates the whole-batch counters."""
+        handles) and updates the whole-batch counters. `expect` (one entry per
+        C row: the token speculated at the row's next position, or None) asks
+        for the greedy comparisons on the device; their flags land in
+        `accept_flags`."""
         passes = [("P", p_rows)] + [("R", r_rows)] * r_repeat + [("C", c_rows)]
         passes = [(kind, [lane.index for lane, _ in rows], [t for _, t in rows]) for kind, rows in passes if rows]
         ids = None
+        self.accept_flags = None
         fused = getattr(self.blocks, "run_passes", None)
         if fused is not None and passes:
-            ids = fused(passes, self.cache, self.handles)
+            if expect is not None and c_rows:
+                ids = fused(passes, self.cache, self.handles, expect=expect)
+                self.accept_flags = self.blocks.last_accept
+            else:
+                ids = fused(passes, self.cache, self.handles)
         else:
             for kind, seqs, toks in passes:
                 if kind == "P":
@@ -231,7 +242,7 @@ def _route(lane: Lane, T_total: int, T_draft: int):
     return verifies, draft
 
 
-def _settle(lane: Lane, verifies, draft, gold: dict, cache) -> None:
+def _settle(lane: Lane, verifies, draft, gold: dict, cache, decide) -> None:
     """Walk a lane's verify chain in position order. Verify v finalizes
     position v + 1 against the token speculated there: accept commits it;
     reject commits the full-depth argmax, truncates the lane from there and
@@ -251,7 +262,7 @@ def _settle(lane: Lane, verifies, draft, gold: dict, cache) -> None:
         else:
             edge = False
             lane.trace.n_drafts_proposed += 1
-            if lane.accepts(g, nxt.token_id):
+            if decide(v, g, nxt):
                 lane.trace.n_drafts_accepted += 1
                 lane.commit(nxt.token_id)
             else:
@@ -272,9 +283,17 @@ def _settle(lane: Lane, verifies, draft, gold: dict, cache) -> None:
 @torch.no_grad()
 def generate_wavefront_batch(blocks, prompt_ids, max_new_tokens, policy: SsdPolicy, emus=None,
                              prefilled: SharedPrefill | None = None) -> BatchTrace:
-    """One independent wave per sequence; P, R and C once per tick over the union."""
+    """One independent wave per sequence; P, R and C once per tick over the union.
+
+    Greedy (no emulated streams) on blocks that compare on the device: each
+    verify row carries the token speculated at its next position, the argmax
+    kernel compares them, and the tick reads back one accept flag per C row
+    while every id stays on the device (read once at the end). Other blocks
+    compare the ids on the host."""
     emulated = emus is not None and all(e is not None for e in emus)
-    run = _BatchRun(blocks, prompt_ids, max_new_tokens, emus, prefilled, handles=emulated)
+    greedy = emus is None or all(e is None for e in emus)
+    on_device = greedy and getattr(blocks, "device_accept", False) and hasattr(blocks, "run_passes")
+    run = _BatchRun(blocks, prompt_ids, max_new_tokens, emus, prefilled, handles=emulated or on_device)
     T_total, T_draft = policy.T_total, policy.T_draft
     for lane in run.live():
         lane.enqueue(lane.committed[-1], lane.prompt_len)
@@ -297,11 +316,25 @@ def generate_wavefront_batch(blocks, prompt_ids, max_new_tokens, policy: SsdPoli
             if verifies or draft is not None:
                 plan.append((lane, verifies, draft))
         c_rows = [(lane, t) for lane, vs, d in plan for t in vs + ([d] if d is not None else [])]
-        ids = run.launch(p_rows, r_rows, c_rows)
+        expect = None
+        if on_device and c_rows:
+            expect = []
+            for lane, vs, d in plan:
+                for i, v in enumerate(vs):
+                    nxt = vs[i + 1] if i + 1 < len(vs) else lane.token_at(v.position + 1)
+                    expect.append(None if nxt is None else nxt.token_id)
+                if d is not None:
+                    expect.append(None)
+        ids = run.launch(p_rows, r_rows, c_rows, expect=expect)
         gold = {id(t): g for (_, t), g in zip(c_rows, ids or [])}
+        if expect is not None:
+            flag = {id(t): f for (_, t), f in zip(c_rows, run.accept_flags)}
+            decide = lambda v, g, nxt: flag[id(v)]  # noqa: E731
         for lane, verifies, draft in plan:
             lane.trace.n_c_calls += 1
-            _settle(lane, verifies, draft, gold, run.cache)
+            if expect is None:
+                decide = lambda v, g, nxt, lane=lane: lane.accepts(g, nxt.token_id)  # noqa: E731
+            _settle(lane, verifies, draft, gold, run.cache, decide)
     return run.finish()
 
 
