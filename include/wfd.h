@@ -82,6 +82,26 @@ int wfd_attn_decode(const void* q, const void* k_cache, const void* v_cache, int
                     wfd_stream_t stream);
 
 /*
+ * wfd_attn_decode without a workspace argument: the split partials go to a
+ * static scratch array inside the library (WFD_ATTN_NOALLOC_MAX_BYTES per
+ * device, held by every device the library runs on until the process ends),
+ * so the call allocates nothing, for callers that cannot allocate (code
+ * under hipGraph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). It has no counterpart in the reference. Same arguments, same
+ * kernels and the same output bits as wfd_attn_decode; a launch whose
+ * partials need more than the maximum (wfd_attn_workspace_bytes(n, H, Dh,
+ * kv_len_max) > WFD_ATTN_NOALLOC_MAX_BYTES) is rejected with WFD_WORKSPACE.
+ * Every call on a device shares that device's scratch: calls that overlap on
+ * one device (concurrent streams) race. Nothing in it needs clearing: a
+ * launch writes every partial it reads.
+ */
+#define WFD_ATTN_NOALLOC_MAX_BYTES (32u << 20)
+int wfd_attn_decode_noalloc(const void* q, const void* k_cache, const void* v_cache, int64_t kv_block_rows,
+                            const int64_t* kv_row_base, const int32_t* kv_len, const int32_t* group_first, void* out,
+                            int n, int H, int Hkv, int Dh, int dtype, float scale, int kv_len_max,
+                            wfd_stream_t stream);
+
+/*
  * Row tables of a packed varlen attention call, built on the device: query
  * row r of segment s (rows [cu_q[s], cu_q[s+1]) of q; keys [cu_k[s],
  * cu_k[s+1]) of a token-major K / V) gets kv_row_base[r] = cu_k[s] and

@@ -36,6 +36,8 @@ SIGNATURES: dict[str, tuple] = {
     "wfd_attn_group_max_rows": (_i32, [_i32, _i32]),
     "wfd_attn_decode": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _f32, _i32,
                                _vp, _sz, _vp]),
+    "wfd_attn_decode_noalloc": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _f32,
+                                       _i32, _vp]),
     "wfd_attn_varlen_rows": (_i32, [_vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp]),
     "wfd_attn_prefill": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
                                 _vp]),

@@ -34,6 +34,8 @@
 // 1024 rather than 2048 keys per split: with ragged lengths (the batched
 // decode) the longest workgroups set the launch's tail, and halving them made
 // the B=32 decode 13 % faster; uniform long prefixes lose ~2-3 %.
+#include <mutex>
+
 #include "wfd_common.h"
 
 namespace wfd {
@@ -451,6 +453,40 @@ static int dispatch_attn(int Dh, int G, const void* q, const void* kc, const voi
   return kUnsupported;
 }
 
+// Scratch of wfd_attn_decode_noalloc: the split partials of one launch live
+// in this file-scope device array instead of a caller's workspace. Each
+// device that runs the library holds its own copy until the process ends.
+// Host code never passes the array's name to a kernel (on the host it is only
+// a stand-in for the symbol): it resolves the device address once per device
+// with hipGetSymbolAddress and passes that.
+constexpr size_t kAttnScratchBytes = (size_t)WFD_ATTN_NOALLOC_MAX_BYTES;
+__device__ __align__(256) unsigned char scratch[kAttnScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_addr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (resolved on the first
+// call per device), or nullptr with the error set.
+static void* attn_scratch(void) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("wfd_attn_decode_noalloc: no current device (or device index %d beyond %d)", dev, kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error("wfd_attn_decode_noalloc: hipGetSymbolAddress failed on device %d: %s", dev, hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_addr[dev] = p;
+  }
+  return g_scratch_addr[dev];
+}
+
 }  // namespace wfd
 
 extern "C" {
@@ -527,6 +563,33 @@ int wfd_attn_decode(const void* q, const void* k_cache, const void* v_cache, int
     return rc;
   }
   return launch_status("wfd_attn_decode");
+}
+
+
+
+int wfd_attn_decode_noalloc(const void* q, const void* k_cache, const void* v_cache, int64_t kv_block_rows,
+                            const int64_t* kv_row_base, const int32_t* kv_len, const int32_t* group_first, void* out,
+                            int n, int H, int Hkv, int Dh, int dtype, float scale, int kv_len_max,
+                            hipStream_t stream) {
+  using namespace wfd;
+  if (n > 0 && H > 0 && Dh > 0 && kv_len_max >= 1) {
+    const size_t need = attn_ws_bytes(n, H, Dh, kv_len_max);
+    if (need > kAttnScratchBytes) {
+      set_error("wfd_attn_decode_noalloc: this launch needs %zu bytes of split partials, more than the %zu-byte "
+                "static scratch (n=%d H=%d Dh=%d kv_len_max=%d); use wfd_attn_decode with a workspace",
+                need, kAttnScratchBytes, n, H, Dh, kv_len_max);
+      return kWorkspace;
+    }
+  }
+  if (n == 0) return wfd_attn_decode(q, k_cache, v_cache, kv_block_rows, kv_row_base, kv_len, group_first, out, n,
+                                     H, Hkv, Dh, dtype, scale, kv_len_max, nullptr, 0, stream);
+  void* ws = nullptr;
+  if (n > 0 && H > 0 && Dh > 0) {  // shape errors are reported by the shared path below
+    ws = attn_scratch();
+    if (!ws) return kLaunch;
+  }
+  return wfd_attn_decode(q, k_cache, v_cache, kv_block_rows, kv_row_base, kv_len, group_first, out, n, H, Hkv, Dh,
+                         dtype, scale, kv_len_max, ws, kAttnScratchBytes, stream);
 }
 
 }  // extern "C"
