@@ -194,8 +194,11 @@ int wfd_linear_pack(const void* W, void* W_packed, int N, int K, int dtype, int 
  * g_j = row j, u_j = row pair_off + j of the product. out_dtype may be
  * WFD_F32 for bf16 inputs (logits). K must be a multiple of
  * wfd_linear_k_multiple(dtype), N of 16. K is summed in fixed 128 (bf16) /
- * 64 (fp32) element chunks, chunk partials added in chunk order, so y[m] does
- * not depend on n or on where row m sits. Every x row read (x_rows[m] * ldx)
+ * 64 (fp32) element chunks: the P chunks form wfd_linear_slices(K) slices of
+ * ceil(P / 4) chunks, chunk partials are added in chunk order within a slice
+ * and slice sums in slice order from zero, so y[m] does not depend on n, on
+ * where row m sits, or on whether the slices ran in one workgroup or in
+ * several (wfd_linear_partials). Every x row read (x_rows[m] * ldx)
  * must lie within the first 2 GiB of x. x, W and the x row pitch (ldx
  * elements) must be 16-byte aligned.
  * Replaces: the nn.Linear calls of the block forwards -- Wqkv, proj, the gated
@@ -204,6 +207,25 @@ int wfd_linear_pack(const void* W, void* W_packed, int N, int K, int dtype, int 
  */
 int wfd_linear(const void* x, const int32_t* x_rows, int64_t ldx, const void* W, void* y, int64_t ldy, int n, int N,
                int K, int dtype, int out_dtype, int epilogue, int pair_off, wfd_stream_t stream);
+
+/* Number of K slices of wfd_linear's arithmetic contract for this K (1..4);
+ * 0 if K is not a positive multiple of wfd_linear_k_multiple(dtype). */
+int wfd_linear_slices(int K, int dtype);
+
+/*
+ * Split-K form of wfd_linear (plain epilogue): one workgroup per (64 rows,
+ * 32 or 64 columns, K slice), so a many-row projection with few output
+ * columns fills the chip and reads each x row once per 32-64 columns. Writes
+ * the fp32 slice sums part[(q * n + m) * N + j] for q < wfd_linear_slices(K);
+ * adding them in slice order from zero and rounding to dtype gives wfd_linear's
+ * y[m, j] bit for bit (wfd_add_rmsnorm_split does exactly that). Shapes,
+ * x_rows and alignment as for wfd_linear; part 16-byte aligned.
+ * Replaces: the same nn.Linear calls as wfd_linear where the output feeds a
+ *   residual norm -- proj, the MLP down projection and the adapter
+ *   (src/decoding/huginn_blocks.py:100-102,216; huginn_blocks_batch.py:159-161,299).
+ */
+int wfd_linear_partials(const void* x, const int32_t* x_rows, int64_t ldx, const void* W, float* part, int n, int N,
+                        int K, int dtype, wfd_stream_t stream);
 
 /*
  * The fused q|k|v projection with wfd_qkv_rope_append as its epilogue:
@@ -237,6 +259,22 @@ int wfd_linear_qkv_rope_append(const void* x, const int32_t* x_rows, int64_t ldx
 int wfd_add_rmsnorm(const void* a, const int32_t* a_rows, int64_t lda, const void* res, int64_t ldr, const void* w1,
                     const void* w2, void* x_out, const int32_t* out_rows, int64_t ldo, void* h_out, int64_t ldh, int n,
                     int D, float eps, int dtype, wfd_stream_t stream);
+
+/*
+ * wfd_add_rmsnorm whose `a` rows come from wfd_linear_partials: row i of `a`
+ * is sum_{q < nslices} part[q * slice_stride + i * D + :], added in slice order
+ * from zero and rounded to dtype -- wfd_linear's output row, bit for bit. If
+ * a_out is given, that row is also stored there (a_out[i * lda_out]); the
+ * rest is wfd_add_rmsnorm's math on the same values (a_rows is implicitly
+ * the identity). slice_stride >= n * D.
+ * Replaces: the residual norms after proj, the MLP down projection and the
+ *   adapter (src/decoding/huginn_blocks.py:95,101-102,216;
+ *   huginn_blocks_batch.py:160-161,299) with their linear's K reduction.
+ */
+int wfd_add_rmsnorm_split(const float* part, int64_t slice_stride, int nslices, void* a_out, int64_t lda_out,
+                          const void* res, int64_t ldr, const void* w1, const void* w2, void* x_out,
+                          const int32_t* out_rows, int64_t ldo, void* h_out, int64_t ldh, int n, int D, float eps,
+                          int dtype, wfd_stream_t stream);
 
 /*
  * out[i] = table[id_i] * scale, id_i = ids[i]; a negative ids[i] with a ring

@@ -257,6 +257,50 @@ def test_linear_row_invariant(gpu, dtype, N):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("N,K", [(2048, 2048), (2048, 5632), (2048, 4096), (256, 1024), (512, 384), (128, 128)])
+def test_linear_split_k_same_bits(gpu, dtype, N, K):
+    """Split-K projections: the slice sums of linear_partials, added in slice
+    order in fp32 and rounded, equal the one-launch linear bit for bit (1 to 4
+    slices: K = 128 .. 5632), over contiguous and gathered rows; the norm that
+    reduces them (add_rmsnorm_split) equals linear + add_rmsnorm, including
+    the kept linear rows (a_out), and matches the oracle."""
+    if K % ops.linear_k_multiple(dtype):
+        pytest.skip("K not a multiple of the kernel granularity")
+    g = torch.Generator().manual_seed(N + K)
+    print(f"[split-K] dtype={dtype} N={N} K={K}", flush=True)
+    X = torch.randn(300, K, generator=g).to(dtype).to(gpu)
+    Wm = (0.02 * torch.randn(N, K, generator=g)).to(dtype).to(gpu)
+    W = ops.pack_linear(Wm)
+    r = torch.randn(300, N, generator=g).to(dtype).to(gpu)
+    w1 = (1 + 0.1 * torch.randn(N, generator=g)).to(dtype).to(gpu)
+    w2 = (1 + 0.1 * torch.randn(N, generator=g)).to(dtype).to(gpu)
+    part = torch.empty(4 * 300 * N, dtype=torch.float32, device=gpu)
+    S = ops.linear_slices(K, dtype)
+    P = K // ops.linear_k_multiple(dtype)
+    assert S == -(-P // -(-P // 4))  # ceil(P / Q) slices of Q = ceil(P / 4) chunks
+    norm_ok = N % ops.linear_k_multiple(dtype) == 0
+    for n, rows in ((1, None), (17, None), (64, None), (113, None), (300, None),
+                    (40, torch.randperm(300, generator=g)[:40].to(torch.int32).to(gpu))):
+        y = ops.linear(X, W, n=n, x_rows=rows)
+        assert ops.linear_partials(X, W, part, n=n, x_rows=rows) == S
+        sl = part[: S * n * N].view(S, n, N)
+        acc = torch.zeros(n, N, dtype=torch.float32, device=gpu)
+        for q in range(S):
+            acc = acc + sl[q]
+        assert torch.equal(acc.to(dtype), y), n
+        if not norm_ok:
+            continue
+        keep = torch.empty(n, N, dtype=dtype, device=gpu)
+        x1, h1 = ops.add_rmsnorm_split(part, S, n, w1, 1e-6, dtype=dtype, res=r, w2=w2, a_out=keep)
+        x0, h0 = ops.add_rmsnorm(y, w1, 1e-6, res=r, w2=w2, n=n)
+        assert torch.equal(keep, y) and torch.equal(x1, x0) and torch.equal(h1, h0), n
+        h2 = ops.add_rmsnorm_split(part, S, n, w1, 1e-6, dtype=dtype)
+        assert torch.equal(h2, ops.rmsnorm(y, w1, 1e-6, n=n)), n
+    # the last case (gathered rows) against the oracle
+    assert rel_err(_np(y), ok.linear(_np(X)[rows.long().cpu().numpy()], _np(Wm))) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_swiglu_matches_reference(gpu, dtype):
     """silu(gate) * up of [gate | up] rows in fp32, rounded once: against an fp32
     torch reference on the same rounded inputs (bit-exact up to the last

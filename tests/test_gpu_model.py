@@ -181,6 +181,41 @@ def test_core_tick_row_invariant(gpu):
         assert torch.equal(model.pool[rows[i]], union[i]), i
 
 
+@pytest.mark.parametrize("cfg", [MINI_BF16, M.CONFIGS["looped-2048"]], ids=lambda c: c.name)
+def test_split_k_projections_same_bits(gpu, cfg):
+    """proj, the MLP down projection and the adapter split over K (slice sums
+    reduced in the next norm) give the bits of the one-launch linears: an R
+    tick over 40 mixed-depth rows of 4 sequences (distinct pool rows) and a C
+    pass over the same rows, with the split path on (its default row range)
+    and off."""
+    w = M.init_weights(cfg, 2)
+    B, n = 4, 40
+    model = LoopedModel(cfg, w, gpu, max_seq_len=64, max_batch=B, max_rows=64)
+    assert model.split_rows[0] <= n <= model.split_rows[1]
+    cache = model.create_cache(B)
+    g = torch.Generator().manual_seed(6)
+    kv = torch.randn(2, *cache.flat_k.shape, generator=g).to(cache.flat_k.dtype).to(gpu)
+    seqs = [i // 10 for i in range(n)]
+    pos = [60 - i % 10 for i in range(n)]
+    steps = [i % cfg.T_total for i in range(n)]
+    rows = [model.pool_row(b, p) for b, p in zip(seqs, pos)]
+    assert len(set(rows)) == n
+    model.pool.copy_(torch.randn(model.pool.shape, generator=g).to(model.pool.dtype))
+    init = model.pool.clone()
+    out = {}
+    for split in (True, False):
+        print(f"[split-K model] {cfg.name} split={split}", flush=True)
+        model.split_rows = (17, 512) if split else (1 << 30, 1 << 30)
+        model.pool.copy_(init)
+        cache.flat_k.copy_(kv[0])
+        cache.flat_v.copy_(kv[1])
+        model.core_union(cache, seqs, pos, steps)
+        logits, _ = model.coda_union(cache, seqs, pos)
+        out[split] = (model.pool[rows].clone(), logits.clone())
+    assert torch.equal(out[True][0], out[False][0])
+    assert torch.equal(out[True][1], out[False][1])
+
+
 def test_2048_core_tick_matches_oracle(gpu):
     """One R tick of the 2048-d bf16 model (8 rows, depths 0..14, slot prefixes
     of random K/V) against the fp32 oracle fed the same bf16 values: <= 2e-2."""

@@ -52,6 +52,10 @@ SIGNATURES: dict[str, tuple] = {
                                           _i64, _i32, _i32, _i32, _i32, _vp]),
     "wfd_add_rmsnorm": (_i32, [_vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i32, _i32, _f32,
                                _i32, _vp]),
+    "wfd_linear_slices": (_i32, [_i32, _i32]),
+    "wfd_linear_partials": (_i32, [_vp, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _vp]),
+    "wfd_add_rmsnorm_split": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _i64,
+                                     _i32, _i32, _f32, _i32, _vp]),
     "wfd_embed": (_i32, [_vp, _vp, _i64, _vp, _f32, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
     "wfd_copy_rows": (_i32, [_vp, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _i32, _vp]),
     "wfd_argmax": (_i32, [_vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i32, _i32, _vp]),

@@ -45,6 +45,7 @@ int launch_status(const char* what) {
 
 constexpr int kRowThreads = 256;
 constexpr int kNormMaxD = 4096;
+constexpr int kNormRowsPerCuLaunch = 1024;  // rows from which the norm packs 4 rows per workgroup
 
 // One wave per row, 16-byte vector loads. The row is cut into the linear
 // layer's K chunks (KC elements); lane (j = lane / 16, c = lane % 16) holds,
@@ -53,15 +54,32 @@ constexpr int kNormMaxD = 4096;
 // the library's one order (chunk_sumsq, then chunks in order). Every load is
 // unconditional, and the residual / second-norm variants are compile-time, so
 // no load sits behind a data-dependent branch (whose join would wait for it).
-template <typename T, bool RES, bool TWO, int MAXR>
+//
+// SPLIT: `a` is not a row but the fp32 slice partials of a split-K linear
+// (wfd_linear_partials: slice q of row i at part + q * slice_stride + i * D);
+// the kernel adds them in slice order from zero -- the linear's arithmetic
+// contract -- and rounds to T as the linear's store would, optionally keeps
+// that row (a_out), and continues as the plain kernel from the same values.
+constexpr int kSplitMaxSlices = 4;  // the linear's K slices (at most 4)
+
+struct SplitArgs {
+  const float* part;
+  int64_t slice_stride;
+  int nslices;
+  void* a_out;
+  int64_t lda_out;
+};
+
+template <typename T, bool RES, bool TWO, int MAXR, bool SPLIT>
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
     const T* __restrict__ a, const int32_t* __restrict__ a_rows, int64_t lda, const T* __restrict__ res,
     int64_t ldr, const T* __restrict__ w1, const T* __restrict__ w2, T* __restrict__ x_out,
-    const int32_t* __restrict__ out_rows, int64_t ldo, T* __restrict__ h_out, int64_t ldh, int n, int D, float eps) {
+    const int32_t* __restrict__ out_rows, int64_t ldo, T* __restrict__ h_out, int64_t ldh, int n, int D, float eps,
+    const SplitArgs sp) {
   constexpr int V = Chunk<T>::V;
   constexpr int KSTEP = Chunk<T>::KSTEP;
   constexpr int KC = Chunk<T>::KC;
-  const int i = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int i = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int c = lane & 15;
   const int j = lane >> 4;
@@ -72,21 +90,68 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
   // P-1 (its sum is never used, nothing is stored for it)
   float v[MAXR][kChunkSteps][V];
   u32x4 wa[MAXR][kChunkSteps], wb[MAXR][kChunkSteps];
+  [[maybe_unused]] u32x4 wr[SPLIT ? MAXR : 1][SPLIT ? kChunkSteps : 1];
 #pragma unroll
   for (int r = 0; r < MAXR; ++r) {
     const int p = r * 16 + c < P ? r * 16 + c : P - 1;
 #pragma unroll
     for (int s = 0; s < kChunkSteps; ++s) {
       const int64_t off = (int64_t)p * KC + s * KSTEP + j * V;
-      Elem<T>::unpack(ld16(a + ar * lda + off), v[r][s]);
+      if constexpr (SPLIT) {
+        // branch-free, so every load can be issued before the first add: a
+        // slice past nslices re-reads slice 0 and adds +0 in its place (the
+        // sum starts at +0 and so is never -0: adding +0 leaves its bits)
+        float sum[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) sum[e] = 0.f;
+#pragma unroll
+        for (int q = 0; q < kSplitMaxSlices; ++q) {
+          const bool live = q < sp.nslices;
+          const float* src = sp.part + (live ? q : 0) * sp.slice_stride + (int64_t)i * D + off;
+#pragma unroll
+          for (int h = 0; h < V / 4; ++h) {
+            const u32x4 w = ld16(src + 4 * h);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sum[4 * h + e] += live ? __uint_as_float(w[e]) : 0.f;
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < V; ++e) v[r][s][e] = Elem<T>::round(sum[e]);
+      } else {
+        Elem<T>::unpack(ld16(a + ar * lda + off), v[r][s]);
+      }
       wa[r][s] = ld16(w1 + off);
       if constexpr (TWO) wb[r][s] = ld16(w2 + off);
-      if constexpr (RES) {
+      if constexpr (RES && SPLIT) {
+        wr[r][s] = ld16(res + (int64_t)i * ldr + off);  // added after a_out is stored
+      } else if constexpr (RES) {
         float q[V];
         Elem<T>::unpack(ld16(res + (int64_t)i * ldr + off), q);
 #pragma unroll
         for (int e = 0; e < V; ++e) v[r][s][e] += q[e];
       }
+    }
+  }
+  if constexpr (SPLIT) {
+    if (sp.a_out) {  // the linear's output rows, when the caller keeps them
+#pragma unroll
+      for (int r = 0; r < MAXR; ++r)
+#pragma unroll
+        for (int s = 0; s < kChunkSteps; ++s)
+          if (r * 16 + c < P)
+            *reinterpret_cast<u32x4*>((T*)sp.a_out + (int64_t)i * sp.lda_out + (int64_t)(r * 16 + c) * KC +
+                                      s * KSTEP + j * V) = Elem<T>::pack(v[r][s]);
+    }
+    if constexpr (RES) {
+#pragma unroll
+      for (int r = 0; r < MAXR; ++r)
+#pragma unroll
+        for (int s = 0; s < kChunkSteps; ++s) {
+          float q[V];
+          Elem<T>::unpack(wr[r][s], q);
+#pragma unroll
+          for (int e = 0; e < V; ++e) v[r][s][e] += q[e];
+        }
     }
   }
   // first norm
@@ -140,47 +205,62 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
   }
 }
 
-template <typename T, int MAXR>
+template <typename T, int MAXR, bool SPLIT>
 static void launch_norm_r(const void* a, const int32_t* a_rows, int64_t lda, const void* res, int64_t ldr,
                           const void* w1, const void* w2, void* x_out, const int32_t* out_rows, int64_t ldo,
-                          void* h_out, int64_t ldh, int n, int D, float eps, hipStream_t stream) {
-  const dim3 grid((n + 3) / 4), block(256);
+                          void* h_out, int64_t ldh, int n, int D, float eps, const SplitArgs& sp,
+                          hipStream_t stream) {
+  // one row (wave) per workgroup unless there are rows enough to fill every
+  // CU four times over: a CU streams its waves' rows at a bounded rate, so a
+  // few hundred rows finish sooner spread one per CU
+  const int rpw = n >= kNormRowsPerCuLaunch ? 4 : 1;
+  const dim3 grid((n + rpw - 1) / rpw), block(64 * rpw);
   const T *at = (const T*)a, *rt = (const T*)res, *w1t = (const T*)w1, *w2t = (const T*)w2;
   T *xo = (T*)x_out, *ho = (T*)h_out;
   if (res && w2)
-    hipLaunchKernelGGL((add_rmsnorm_kernel<T, true, true, MAXR>), grid, block, 0, stream, at, a_rows, lda, rt, ldr,
-                       w1t, w2t, xo, out_rows, ldo, ho, ldh, n, D, eps);
+    hipLaunchKernelGGL((add_rmsnorm_kernel<T, true, true, MAXR, SPLIT>), grid, block, 0, stream, at, a_rows, lda, rt,
+                       ldr, w1t, w2t, xo, out_rows, ldo, ho, ldh, n, D, eps, sp);
   else if (res)
-    hipLaunchKernelGGL((add_rmsnorm_kernel<T, true, false, MAXR>), grid, block, 0, stream, at, a_rows, lda, rt, ldr,
-                       w1t, w2t, xo, out_rows, ldo, ho, ldh, n, D, eps);
+    hipLaunchKernelGGL((add_rmsnorm_kernel<T, true, false, MAXR, SPLIT>), grid, block, 0, stream, at, a_rows, lda, rt,
+                       ldr, w1t, w2t, xo, out_rows, ldo, ho, ldh, n, D, eps, sp);
   else if (w2)
-    hipLaunchKernelGGL((add_rmsnorm_kernel<T, false, true, MAXR>), grid, block, 0, stream, at, a_rows, lda, rt, ldr,
-                       w1t, w2t, xo, out_rows, ldo, ho, ldh, n, D, eps);
+    hipLaunchKernelGGL((add_rmsnorm_kernel<T, false, true, MAXR, SPLIT>), grid, block, 0, stream, at, a_rows, lda, rt,
+                       ldr, w1t, w2t, xo, out_rows, ldo, ho, ldh, n, D, eps, sp);
   else
-    hipLaunchKernelGGL((add_rmsnorm_kernel<T, false, false, MAXR>), grid, block, 0, stream, at, a_rows, lda, rt, ldr,
-                       w1t, w2t, xo, out_rows, ldo, ho, ldh, n, D, eps);
+    hipLaunchKernelGGL((add_rmsnorm_kernel<T, false, false, MAXR, SPLIT>), grid, block, 0, stream, at, a_rows, lda, rt,
+                       ldr, w1t, w2t, xo, out_rows, ldo, ho, ldh, n, D, eps, sp);
 }
 
 // Rounds of 16 chunks per lane: a row of up to 16 chunks needs one (the usual
 // d_model), wider rows up to kNormMaxD take the general form.
-template <typename T>
+template <typename T, bool SPLIT>
 static void launch_norm_t(const void* a, const int32_t* a_rows, int64_t lda, const void* res, int64_t ldr,
                           const void* w1, const void* w2, void* x_out, const int32_t* out_rows, int64_t ldo,
-                          void* h_out, int64_t ldh, int n, int D, float eps, hipStream_t stream) {
+                          void* h_out, int64_t ldh, int n, int D, float eps, const SplitArgs& sp, hipStream_t stream) {
   if (D <= 16 * Chunk<T>::KC)
-    launch_norm_r<T, 1>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, stream);
+    launch_norm_r<T, 1, SPLIT>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, sp,
+                               stream);
   else
-    launch_norm_r<T, kNormMaxD / (16 * Chunk<T>::KC)>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out,
-                                                       ldh, n, D, eps, stream);
+    launch_norm_r<T, kNormMaxD / (16 * Chunk<T>::KC), SPLIT>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo,
+                                                              h_out, ldh, n, D, eps, sp, stream);
 }
 
 static void launch_add_rmsnorm(int dtype, const void* a, const int32_t* a_rows, int64_t lda, const void* res, int64_t ldr,
                         const void* w1, const void* w2, void* x_out, const int32_t* out_rows, int64_t ldo,
-                        void* h_out, int64_t ldh, int n, int D, float eps, hipStream_t stream) {
-  if (dtype == kBF16)
-    launch_norm_t<bf16_t>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, stream);
+                        void* h_out, int64_t ldh, int n, int D, float eps, const SplitArgs* sp, hipStream_t stream) {
+  const SplitArgs none{};
+  if (dtype == kBF16 && sp)
+    launch_norm_t<bf16_t, true>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, *sp,
+                                stream);
+  else if (dtype == kBF16)
+    launch_norm_t<bf16_t, false>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, none,
+                                 stream);
+  else if (sp)
+    launch_norm_t<float, true>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, *sp,
+                               stream);
   else
-    launch_norm_t<float>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, stream);
+    launch_norm_t<float, false>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, none,
+                                stream);
 }
 
 template <typename T>
@@ -382,8 +462,43 @@ int wfd_add_rmsnorm(const void* a, const int32_t* a_rows, int64_t lda, const voi
     set_error("wfd_add_rmsnorm: null pointer argument");
     return kBadArg;
   }
-  launch_add_rmsnorm(dtype, a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, stream);
+  launch_add_rmsnorm(dtype, a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, nullptr,
+                     stream);
   return launch_status("wfd_add_rmsnorm");
+}
+
+int wfd_add_rmsnorm_split(const float* part, int64_t slice_stride, int nslices, void* a_out, int64_t lda_out,
+                          const void* res, int64_t ldr, const void* w1, const void* w2, void* x_out,
+                          const int32_t* out_rows, int64_t ldo, void* h_out, int64_t ldh, int n, int D, float eps,
+                          int dtype, hipStream_t stream) {
+  using namespace wfd;
+  if (dtype != kBF16 && dtype != kF32) {
+    set_error("wfd_add_rmsnorm_split: unsupported dtype %d", dtype);
+    return kUnsupported;
+  }
+  const int kc = dtype == kBF16 ? Chunk<bf16_t>::KC : Chunk<float>::KC;
+  if (n < 0 || D <= 0 || D > kNormMaxD || D % kc != 0 || nslices < 1 || nslices > kSplitMaxSlices ||
+      slice_stride < (int64_t)n * D) {
+    set_error("wfd_add_rmsnorm_split: bad shape n=%d D=%d nslices=%d slice_stride=%lld", n, D, nslices,
+              (long long)slice_stride);
+    return kBadArg;
+  }
+  const int esz = dtype == kBF16 ? 2 : 4;
+  if ((((uintptr_t)part | (uintptr_t)a_out | (uintptr_t)res | (uintptr_t)w1 | (uintptr_t)w2 | (uintptr_t)x_out |
+        (uintptr_t)h_out) & 15) || ((slice_stride * 4) & 15) || (a_out && ((lda_out * esz) & 15)) ||
+      (res && ((ldr * esz) & 15)) || (x_out && ((ldo * esz) & 15)) || (h_out && ((ldh * esz) & 15))) {
+    set_error("wfd_add_rmsnorm_split: rows must be 16-byte aligned");
+    return kBadArg;
+  }
+  if (n == 0) return kOk;
+  if (!part || !w1 || (w2 && !h_out) || (!w2 && !x_out)) {
+    set_error("wfd_add_rmsnorm_split: null pointer argument");
+    return kBadArg;
+  }
+  const SplitArgs sp{part, slice_stride, nslices, a_out, lda_out};
+  launch_add_rmsnorm(dtype, nullptr, nullptr, 0, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, &sp,
+                     stream);
+  return launch_status("wfd_add_rmsnorm_split");
 }
 
 int wfd_qkv_rope_append(const void* qkv, int64_t ldq, const int32_t* pos, const float* rope_cos,

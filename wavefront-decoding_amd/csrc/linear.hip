@@ -14,9 +14,14 @@
 //
 // Arithmetic contract (depends on K and the dtype only, never on n or on how
 // the work is split): K is cut into P = K / KC chunks of 4 MFMA k-steps
-// (KC = 128 bf16 / 64 fp32 elements); a chunk partial is the MFMA chain over
-// its 4 steps starting from zero; y = epilogue(((0 + c_0) + c_1) + ... + c_{P-1})
-// in fp32. Four kernels honour it bit for bit:
+// (KC = 128 bf16 / 64 fp32 elements), and the chunks into at most kSlices
+// consecutive slices of Q = ceil(P / kSlices) chunks. A chunk partial is the
+// MFMA chain over its 4 steps starting from zero; a slice partial is
+// ((0 + c_a) + c_a+1) + ... over its chunks in order; y = epilogue(((0 + s_0)
+// + s_1) + ...) over the slices in order, in fp32. The slices let a many-row
+// launch split K across workgroups (wfd_linear_partials writes the slice
+// partials; the consumer adds them in slice order) with the same bits as a
+// launch that walks all of K. Five kernels honour it bit for bit:
 //
 //  * wide (n <= 16): one 16-wave workgroup per tile (or column half of a
 //    tile), 8 waves when there are more than 512 tiles; its waves take the
@@ -33,6 +38,8 @@
 //  * stream (n > 16, at most 256 tiles): 64 rows x 1 or 2 tiles per
 //    workgroup, weights and x moved global -> LDS by direct-to-LDS loads
 //    through a 4-stage ring (3 chunks in flight without registers).
+//  * gemm, slice form (wfd_linear_partials): the gemm kernel over one slice
+//    of K per workgroup (grid y = slice), storing fp32 slice partials.
 //
 // So y[m] is bit-identical whatever n is and wherever row m sits -- the
 // property that keeps wavefront decode token-identical to sequential decode.
@@ -71,6 +78,14 @@ constexpr int kGemmMinBlockTiles = 512;
 constexpr int kStreamMaxTiles = 256;
 constexpr int kStreamStages = 4;
 enum Epilogue : int { kEpiPlain = 0, kEpiSwiGLU = 1, kEpiRope = 2 };
+
+// K slices of the arithmetic contract (see the header): Q = ceil(P / kSlices)
+// chunks per slice, at most kSlices slices.
+constexpr int kSlices = 4;
+__host__ __device__ constexpr int slice_chunks(int P) { return (P + kSlices - 1) / kSlices; }
+__host__ __device__ constexpr int slice_count(int P) { return (P + slice_chunks(P) - 1) / slice_chunks(P); }
+// true after the last chunk of a slice
+__device__ __forceinline__ bool slice_end(int p, int P, int Q) { return (p + 1) % Q == 0 || p + 1 == P; }
 
 // Operands of the QKV-RoPE-append epilogue (unused by the others).
 struct RopeArgs {
@@ -274,14 +289,21 @@ __global__ __launch_bounds__(64 * WW) void linear_wide_kernel(
   }
   __syncthreads();
 
-  // threads 0..255: one (lane', r) output each; sum chunk partials in chunk order
+  // threads 0..255: one (lane', r) output each; chunk partials summed slice by slice, in order
   if (threadIdx.x < 256) {
     const int ln = threadIdx.x >> 2;
     const int r = threadIdx.x & 3;
     const int row = 4 * (ln >> 4) + r;
     const float* rf = reinterpret_cast<const float*>(red);
-    float v = 0.f;
-    for (int p = 0; p < P; ++p) v += rf[(p * 64 + ln) * 4 + r];
+    const int Q = slice_chunks(P);
+    float v = 0.f, sl = 0.f;
+    for (int p = 0; p < P; ++p) {
+      sl += rf[(p * 64 + ln) * 4 + r];
+      if (slice_end(p, P, Q)) {
+        v += sl;
+        sl = 0.f;
+      }
+    }
     // column ln ^ 1 lives in thread threadIdx.x ^ 4, column ln ^ 8 in threadIdx.x ^ 32
     const float partner = EPI == kEpiRope     ? __shfl_xor(v, 4, 64)
                           : EPI == kEpiSwiGLU ? __shfl_xor(v, 32, 64)
@@ -320,9 +342,25 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ 
 
   // two-stage register pipeline; every load is unconditional (the stage past
   // the last chunk re-reads chunk P-1 and is never used)
-  f32x4 tot[NB];
+  const int Q = slice_chunks(P);
+  f32x4 tot[NB], sl[NB];
 #pragma unroll
-  for (int c = 0; c < NB; ++c) tot[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < NB; ++c) tot[c] = sl[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // chunk p's partial into its slice; at the slice's end the slice into the total
+  auto add = [&](const f32x4 (&acc)[NB], int p) {
+#pragma unroll
+    for (int c = 0; c < NB; ++c)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sl[c][r] += acc[c][r];
+    if (slice_end(p, P, Q)) {
+#pragma unroll
+      for (int c = 0; c < NB; ++c) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) tot[c][r] += sl[c][r];
+        sl[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  };
   u32x4 wa[NB][kChunkSteps], wb[NB][kChunkSteps], xa[kChunkSteps], xb[kChunkSteps];
   load_w<T, NB>(wa, wtile, P, 0, lane);
   load_x<T>(xa, xrs, xoff, 0);
@@ -332,19 +370,13 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ 
     load_x<T>(xb, xrs, xoff, p1);
     f32x4 acc[NB];
     chunk_mma<T, NB>(acc, xa, wa);
-#pragma unroll
-    for (int c = 0; c < NB; ++c)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) tot[c][r] += acc[c][r];
+    add(acc, p);
     if (p + 1 >= P) break;
     const int p2 = p + 2 < P ? p + 2 : P - 1;
     load_w<T, NB>(wa, wtile, P, p2, lane);
     load_x<T>(xa, xrs, xoff, p2);
     chunk_mma<T, NB>(acc, xb, wb);
-#pragma unroll
-    for (int c = 0; c < NB; ++c)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) tot[c][r] += acc[c][r];
+    add(acc, p + 1);
   }
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
@@ -394,11 +426,17 @@ __device__ __forceinline__ bool xcd_block(int n, int tiles, int& rbk, int& tg) {
 // x are loaded into registers two chunks ahead of their use, so a chunk's
 // memory latency overlaps the MFMAs of the two before it. Same per-chunk
 // arithmetic as the wide and tile kernels, so the same bits.
-template <typename T, typename TO, int EPI, int BT>
+//
+// PART (the slice form behind wfd_linear_partials): grid y = slice; the
+// workgroup walks only its slice's chunks and stores the fp32 slice partial of
+// every (row, column) at part[(slice * n + row) * 16 * tiles + column], with no
+// epilogue. Adding the slices in slice order from zero gives the bits of a
+// launch that walks all of K.
+template <typename T, typename TO, int EPI, int BT, bool PART>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void linear_gemm_kernel(const T* __restrict__ x, const int32_t* __restrict__ x_rows,
                                                           int64_t ldx, const T* __restrict__ W, TO* __restrict__ y,
                                                           int64_t ldy, int n, int K, int pair_off, int tiles,
-                                                          const RopeArgs ra) {
+                                                          const RopeArgs ra, float* __restrict__ part) {
   constexpr int V = LinTraits<T>::V;
   constexpr int FR = BT * kChunkSteps;  // 1 KB fragments per chunk: (tile, step)
   constexpr int FPW = FR / 4;           // fragments each wave stages per chunk
@@ -411,6 +449,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
   const int grp = lane >> 4;
   const int row0 = (rbk * 4 + wave) * 16;
   const int P = K / LinTraits<T>::KC;
+  const int Q = slice_chunks(P);
+  // chunks [pb, pe): all of K, or the slice of this workgroup
+  const int pb = PART ? (int)blockIdx.y * Q : 0;
+  const int pe = PART ? min(P, pb + Q) : P;
   // a wave past the last row still stages weights and meets every barrier;
   // its x loads read zeros and it stores nothing
   const uint32_t xoff = row0 < n ? x_offset<T>(x_rows, ldx, row0, col, grp, n) : kBufInvalid;
@@ -426,7 +468,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
   }
   const int64_t pstride = (int64_t)kChunkSteps * 64 * V;  // elements from one chunk to the next in a tile
   // every load unconditional: chunks past the last re-read it, never used
-  auto cl = [&](int p) { return p < P ? p : P - 1; };
+  auto cl = [&](int p) { return p < pe ? p : pe - 1; };
   auto fetch_w = [&](u32x4 (&wr)[FPW], int p) {
 #pragma unroll
     for (int i = 0; i < FPW; ++i) wr[i] = ld16(wsrc[i] + cl(p) * pstride);
@@ -435,10 +477,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
 #pragma unroll
     for (int i = 0; i < FPW; ++i) wl[b][wave * FPW + i][lane] = wr[i];
   };
-  f32x4 tot[BT];
+  f32x4 tot[BT], sl[BT];
 #pragma unroll
-  for (int t = 0; t < BT; ++t) tot[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  auto mma = [&](const u32x4 (&xf)[kChunkSteps], int b) {
+  for (int t = 0; t < BT; ++t) tot[t] = sl[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // chunk p from LDS stage b: its partial into the slice; at the slice's end
+  // (full-K form) the slice into the total
+  auto mma = [&](const u32x4 (&xf)[kChunkSteps], int b, int p) {
     f32x4 acc[BT];
 #pragma unroll
     for (int t = 0; t < BT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -458,7 +502,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
 #pragma unroll
     for (int t = 0; t < BT; ++t)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) tot[t][r] += acc[t][r];
+      for (int r = 0; r < 4; ++r) sl[t][r] += acc[t][r];
+    if (!PART && slice_end(p, P, Q)) {
+#pragma unroll
+      for (int t = 0; t < BT; ++t) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) tot[t][r] += sl[t][r];
+        sl[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
   };
 
   // Register rings, statically unrolled by two (no copies, no exit inside
@@ -468,29 +520,43 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
   // x0 (chunk p), w1 (p + 1), x1 (p + 1), w0 (p + 2); the prologue builds
   // the same order so the compiler's wait counts are the steady-state ones.
   u32x4 w0[FPW], w1[FPW], x0[kChunkSteps], x1[kChunkSteps];
-  fetch_w(w0, 0);
-  load_x<T>(x0, xrs, xoff, 0);
-  fetch_w(w1, 1);
-  load_x<T>(x1, xrs, xoff, cl(1));
+  fetch_w(w0, pb);
+  load_x<T>(x0, xrs, xoff, pb);
+  fetch_w(w1, pb + 1);
+  load_x<T>(x1, xrs, xoff, cl(pb + 1));
   stage_w(w0, 0);
   __syncthreads();
-  fetch_w(w0, 2);
-  for (int p = 0; p + 1 < P; p += 2) {
+  fetch_w(w0, pb + 2);
+  for (int p = pb; p + 1 < pe; p += 2) {
     // chunk p: LDS stage 0, x0
-    mma(x0, 0);
+    mma(x0, 0, p);
     load_x<T>(x0, xrs, xoff, cl(p + 2));
     stage_w(w1, 1);  // chunk p + 1; stage 1 was last read by chunk p - 1, before the previous barrier
     __syncthreads();
     fetch_w(w1, p + 3);
     // chunk p + 1: LDS stage 1, x1
-    mma(x1, 1);
+    mma(x1, 1, p + 1);
     load_x<T>(x1, xrs, xoff, cl(p + 3));
     stage_w(w0, 0);  // chunk p + 2; stage 0 was last read by chunk p, before the barrier above
     __syncthreads();
     fetch_w(w0, p + 4);
   }
-  if (P & 1) mma(x0, 0);  // chunk P - 1, staged by the last pair (or the prologue)
+  if ((pe - pb) & 1) mma(x0, 0, pe - 1);  // the last chunk, staged by the last pair (or the prologue)
   if (row0 >= n) return;  // after the last barrier
+  if constexpr (PART) {
+    const int N = 16 * tiles;
+#pragma unroll
+    for (int t = 0; t < BT; ++t) {
+      const int g = tg * BT + t;
+      if (g >= tiles) continue;  // uniform over the workgroup
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int orow = row0 + 4 * grp + r;
+        if (orow < n) part[((int64_t)blockIdx.y * n + orow) * N + 16 * g + col] = sl[t][r];
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int t = 0; t < BT; ++t) {
     const int g = tg * BT + t;
@@ -604,9 +670,10 @@ __global__ __launch_bounds__(256) void linear_stream_kernel(const T* __restrict_
   for (int u = 0; u < NS - 1; ++u)
     if (u < P) issue(u);
 
-  f32x4 tot[BT];
+  const int Q = slice_chunks(P);
+  f32x4 tot[BT], sl[BT];
 #pragma unroll
-  for (int t = 0; t < BT; ++t) tot[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < BT; ++t) tot[t] = sl[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int p = 0; p < P; ++p) {
     // this wave's chunk p is in LDS once at most the later chunks' loads are outstanding
     if (p + NS - 2 < P) {
@@ -630,7 +697,15 @@ __global__ __launch_bounds__(256) void linear_stream_kernel(const T* __restrict_
 #pragma unroll
       for (int t = 0; t < BT; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) tot[t][r] += acc[t][r];
+        for (int r = 0; r < 4; ++r) sl[t][r] += acc[t][r];
+      if (slice_end(p, P, Q)) {
+#pragma unroll
+        for (int t = 0; t < BT; ++t) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) tot[t][r] += sl[t][r];
+          sl[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
     }
   }
   if (!rows) return;  // after the last barrier; every load of this wave has completed
@@ -718,17 +793,74 @@ static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const v
     // while that still leaves >= 256 workgroups, else 2 (lm_head at 64 rows:
     // 500 four-tile workgroups 34 us, 1000 two-tile ones 42 us)
     if (rb * ((tiles + 3) / 4) >= 256)
-      hipLaunchKernelGGL((linear_gemm_kernel<T, TO, EPI, 4>), dim3(xcd_grid(rb, (tiles + 3) / 4)), dim3(256), 0, st,
-                         (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra);
+      hipLaunchKernelGGL((linear_gemm_kernel<T, TO, EPI, 4, false>), dim3(xcd_grid(rb, (tiles + 3) / 4)), dim3(256), 0,
+                         st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra, nullptr);
     else
-      hipLaunchKernelGGL((linear_gemm_kernel<T, TO, EPI, 2>), dim3(xcd_grid(rb, (tiles + 1) / 2)), dim3(256), 0, st,
-                         (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra);
+      hipLaunchKernelGGL((linear_gemm_kernel<T, TO, EPI, 2, false>), dim3(xcd_grid(rb, (tiles + 1) / 2)), dim3(256), 0,
+                         st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra, nullptr);
   }
+}
+
+// The slice form: grid (xcd-mapped row blocks x tile groups, slices). Four
+// tiles per workgroup while that leaves >= 256 workgroups, else two: each
+// workgroup then reads its 64 rows of x once for 64 (or 32) output columns
+// and only its slice of K, where the stream kernel reads them for 16 columns
+// and all of K.
+template <typename T>
+static void launch_linear_partials(const void* x, const int32_t* xr, int64_t ldx, const void* W, float* part, int n,
+                                   int N, int K, hipStream_t st) {
+  const int tiles = N / 16;
+  const int P = K / LinTraits<T>::KC;
+  const int S = slice_count(P);
+  const int rb = (n + 63) / 64;
+  const RopeArgs ra{};
+  if (rb * ((tiles + 3) / 4) * S >= 256)
+    hipLaunchKernelGGL((linear_gemm_kernel<T, T, kEpiPlain, 4, true>), dim3(xcd_grid(rb, (tiles + 3) / 4), S),
+                       dim3(256), 0, st, (const T*)x, xr, ldx, (const T*)W, (T*)nullptr, 0, n, K, 0, tiles, ra, part);
+  else
+    hipLaunchKernelGGL((linear_gemm_kernel<T, T, kEpiPlain, 2, true>), dim3(xcd_grid(rb, (tiles + 1) / 2), S),
+                       dim3(256), 0, st, (const T*)x, xr, ldx, (const T*)W, (T*)nullptr, 0, n, K, 0, tiles, ra, part);
 }
 
 }  // namespace wfd
 
 extern "C" {
+
+int wfd_linear_slices(int K, int dtype) {
+  using namespace wfd;
+  const int kc = dtype == kBF16 ? LinTraits<bf16_t>::KC : LinTraits<float>::KC;
+  if (K <= 0 || K % kc) return 0;
+  return slice_count(K / kc);
+}
+
+int wfd_linear_partials(const void* x, const int32_t* x_rows, int64_t ldx, const void* W, float* part, int n, int N,
+                        int K, int dtype, hipStream_t stream) {
+  using namespace wfd;
+  const int kc = dtype == kBF16 ? LinTraits<bf16_t>::KC : LinTraits<float>::KC;
+  if (n < 0 || N <= 0 || N % 16 || K <= 0 || K % kc || ldx < K || (dtype != kBF16 && dtype != kF32)) {
+    set_error("wfd_linear_partials: bad shape n=%d N=%d K=%d ldx=%lld dtype=%d", n, N, K, (long long)ldx, dtype);
+    return kBadArg;
+  }
+  if (n == 0) return kOk;
+  if (!x || !W || !part) {
+    set_error("wfd_linear_partials: null pointer argument");
+    return kBadArg;
+  }
+  const int64_t es = dtype == kBF16 ? 2 : 4;
+  if (!x_rows && (int64_t)n * ldx * es >= (int64_t)kBufInvalid) {
+    set_error("wfd_linear_partials: the x operand must span less than 2 GiB");
+    return kBadArg;
+  }
+  if (((uintptr_t)x | (uintptr_t)W | (uintptr_t)part | (uintptr_t)(ldx * es)) & 15) {
+    set_error("wfd_linear_partials: x, W, part and the x row pitch must be 16-byte aligned");
+    return kBadArg;
+  }
+  if (dtype == kBF16)
+    launch_linear_partials<bf16_t>(x, x_rows, ldx, W, part, n, N, K, stream);
+  else
+    launch_linear_partials<float>(x, x_rows, ldx, W, part, n, N, K, stream);
+  return launch_status("wfd_linear_partials");
+}
 
 int wfd_linear_k_multiple(int dtype) {
   using namespace wfd;

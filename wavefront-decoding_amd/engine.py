@@ -127,6 +127,10 @@ _GROUP_MIN_WORKGROUPS = 256
 # a C row's expected-token entry that asks for no comparison (below every ring handle)
 NO_EXPECT = -(1 << 62)
 
+# (min, max) rows of a d_model-output projection that runs split-K; up to 16
+# rows one workgroup per tile already walks K in parallel (wide kernel)
+_SPLIT_ROWS = (17, 512)
+
 
 def _bucket(n: int) -> int:
     b = 1
@@ -152,6 +156,10 @@ class LoopedModel:
         self.use_graphs = use_graphs
         self.group_attention = group_attention  # rows sharing a slot read its prefix once
         self.group_min_workgroups = _GROUP_MIN_WORKGROUPS
+        # row counts at which proj, the MLP down projection and the adapter run
+        # split-K (linear_partials) with their K reduction in the next norm:
+        # same bits as the one-launch linear, more workgroups per launch
+        self.split_rows = _SPLIT_ROWS
         self.W = {}
         # the prompt pass (prefill_seq) runs its linears as plain library GEMMs
         # over row-major copies of the block weights: its rows are computed once
@@ -244,6 +252,9 @@ class LoopedModel:
                   q=torch.empty(cap, c.n_heads, c.head_dim, dtype=self.dtype, device=self.device),
                   o=torch.empty(cap, c.n_heads, c.head_dim, dtype=self.dtype, device=self.device),
                   a=mk(c.d_model), u=self._pitched(cap, c.ffn), m=mk(c.d_model))
+        # fp32 slice sums of the split-K projections (at most 4 slices)
+        sc["part"] = torch.empty(4 * min(cap, self.split_rows[1]) * c.d_model, dtype=torch.float32,
+                                 device=self.device)
         if dense:  # the library GEMMs' unfused outputs: q|k|v rows, gate|up rows
             sc["qkv"] = mk((c.n_heads + 2 * c.n_kv_heads) * c.head_dim)
             sc["gu"] = mk(2 * c.ffn)
@@ -278,21 +289,44 @@ class LoopedModel:
                                 out=sc["o"][:n], workspace=ws, group_first=group_first)
         if dense:
             a = torch.mm(o.view(n, -1), self.Wd[prefix + "proj"].t(), out=sc["a"][:n])
+            ops.add_rmsnorm(a, W[prefix + "norm_2"], c.norm_eps, res=x, w2=W[prefix + "norm_3"], n=n, x_out=x,
+                            h_out=h)
         else:
-            a = ops.linear(o.view(n, -1), W[prefix + "proj"], n=n, out=sc["a"])
-        ops.add_rmsnorm(a, W[prefix + "norm_2"], c.norm_eps, res=x, w2=W[prefix + "norm_3"], n=n, x_out=x,
-                        h_out=h)
+            self._linear_norm(o.view(n, -1), W[prefix + "proj"], n, sc, "a", W[prefix + "norm_2"], res=x,
+                              w2=W[prefix + "norm_3"], x_out=x, h_out=h)
         if dense:
             gu = torch.mm(h[:n], self.Wd[prefix + "fc"].t(), out=sc["gu"][:n])
             u = ops.swiglu(gu, n=n, out=sc["u"][:n])
             m = torch.mm(u, self.Wd[prefix + "mlp_proj"].t(), out=sc["m"][:n])
+            if next_norm is not None:
+                ops.add_rmsnorm(m, W[prefix + "norm_4"], c.norm_eps, res=x, w2=next_norm, n=n, x_out=x, h_out=h)
+            else:
+                ops.add_rmsnorm(m, W[prefix + "norm_4"], c.norm_eps, res=x, n=n, x_out=final_out,
+                                out_rows=final_rows)
         else:
             u = ops.linear(h, W[prefix + "fc"], n=n, out=sc["u"], swiglu=True)
-            m = ops.linear(u, W[prefix + "mlp_proj"], n=n, out=sc["m"])
-        if next_norm is not None:
-            ops.add_rmsnorm(m, W[prefix + "norm_4"], c.norm_eps, res=x, w2=next_norm, n=n, x_out=x, h_out=h)
+            if next_norm is not None:
+                self._linear_norm(u, W[prefix + "mlp_proj"], n, sc, "m", W[prefix + "norm_4"], res=x,
+                                  w2=next_norm, x_out=x, h_out=h)
+            else:
+                self._linear_norm(u, W[prefix + "mlp_proj"], n, sc, "m", W[prefix + "norm_4"], res=x,
+                                  x_out=final_out, out_rows=final_rows)
+
+    def _linear_norm(self, xin: torch.Tensor, Wp, n: int, sc, tmp: str, w1: torch.Tensor, *, x_rows=None,
+                     keep=None, **norm) -> None:
+        """norm(linear(xin) [+ res]) for a d_model-output projection: split-K
+        (slice sums, reduced inside the norm) for n in split_rows, else the
+        linear into sc[tmp] then the norm -- the same bits either way. `keep`
+        also receives the linear's output rows (the adapter's, which are the
+        core block's residual)."""
+        lo, hi = self.split_rows
+        eps = self.cfg.norm_eps
+        if lo <= n <= hi:
+            S = ops.linear_partials(xin, Wp, sc["part"], n=n, x_rows=x_rows)
+            ops.add_rmsnorm_split(sc["part"], S, n, w1, eps, dtype=self.dtype, a_out=keep, **norm)
         else:
-            ops.add_rmsnorm(m, W[prefix + "norm_4"], c.norm_eps, res=x, n=n, x_out=final_out, out_rows=final_rows)
+            y = ops.linear(xin, Wp, n=n, x_rows=x_rows, out=keep if keep is not None else sc[tmp])
+            ops.add_rmsnorm(y, w1, eps, n=n, **norm)
 
     # -- row tables ------------------------------------------------------------------
     def _layers(self, kind: str) -> int:
@@ -391,8 +425,9 @@ class LoopedModel:
                             final_out=static_half, final_rows=rows_d, group_first=gf)
             ops.copy_rows(self.s0, self.pool, n=nb, width=c.d_model, src_rows=pos_d, dst_rows=rows_d)
         elif kind == "R":
-            ops.linear(self.pool, W["adapter"], n=nb, x_rows=rows_d, out=sc["x"])
-            ops.rmsnorm(sc["x"], W["core.0.norm_1"], c.norm_eps, n=nb, x_out=sc["h"])
+            # adapter -> x (the first core block's residual), core.0.norm_1 -> h
+            self._linear_norm(self.pool, W["adapter"], nb, sc, "x", W["core.0.norm_1"], x_rows=rows_d,
+                              keep=sc["x"], x_out=sc["h"])
             for l in range(L):
                 nxt = W[f"core.{l + 1}.norm_1"] if l + 1 < L else None
                 self._block(f"core.{l}.", nb, sc, pos_d, kvlen_d, rb(l), fr(l), kv_max, ws, cache, nxt,

@@ -387,6 +387,71 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, **kw) -> torch.Tensor:
     return add_rmsnorm(x, w, eps, **kw)
 
 
+def linear_slices(K: int, dtype: torch.dtype) -> int:
+    """K slices of the linear's arithmetic contract for this K (1..4)."""
+    s = _lib.load().wfd_linear_slices(K, _DT[dtype])
+    _need(s > 0, f"K={K} is not a multiple of the linear's chunk")
+    return s
+
+
+def linear_partials(x: torch.Tensor, W, part: torch.Tensor, *, n: int | None = None,
+                    x_rows: torch.Tensor | None = None) -> int:
+    """Split-K linear: part (flat fp32, >= slices * n * N) receives the slice
+    sums, slice q of row m at part[(q * n + m) * N:]. Returns the number of
+    slices; add_rmsnorm_split turns them into the linear's output rows."""
+    _need_cuda(x, x_rows, part)
+    Wp = _packed(W, False)
+    _need_cuda(Wp.data)
+    _need(x.dim() == 2 and x.stride(1) == 1, "x (rows, K+)")
+    N, K = Wp.N, Wp.K
+    n = x.shape[0] if (n is None and x_rows is None) else (n if n is not None else x_rows.numel())
+    _rows(x_rows, n, "x_rows")
+    _need(x.shape[1] >= K and x.dtype == Wp.dtype, f"x width {x.shape[1]} < K={K} or dtype mismatch")
+    _need(n >= 0 and (x_rows is not None or x.shape[0] >= n), f"x holds {x.shape[0]} rows < n={n}")
+    S = linear_slices(K, x.dtype)
+    _need(part.dtype == torch.float32 and part.is_contiguous() and part.numel() >= S * n * N,
+          f"part: contiguous fp32 of >= {S}*{n}*{N} elements")
+    rc = _lib.load().wfd_linear_partials(x.data_ptr(), _p(x_rows), x.stride(0), Wp.data.data_ptr(),
+                                         part.data_ptr(), n, N, K, _dt(x), _stream())
+    _lib.check(rc, "wfd_linear_partials")
+    return S
+
+
+def add_rmsnorm_split(part: torch.Tensor, nslices: int, n: int, w1: torch.Tensor, eps: float, *,
+                      dtype: torch.dtype, res: torch.Tensor | None = None, w2: torch.Tensor | None = None,
+                      a_out: torch.Tensor | None = None, x_out: torch.Tensor | None = None,
+                      out_rows: torch.Tensor | None = None, h_out: torch.Tensor | None = None):
+    """add_rmsnorm whose `a` rows are the slice sums linear_partials left in
+    `part` (n rows, D = w1.numel() columns), added in slice order and rounded
+    to `dtype`; a_out, if given, keeps those rows. Returns like add_rmsnorm."""
+    _need_cuda(part, w1, res, w2, a_out, x_out, out_rows, h_out)
+    D = w1.numel()
+    _rows(out_rows, n, "out_rows")
+    _need(n >= 0 and 1 <= nslices <= 4, f"n={n} nslices={nslices}")
+    _need(part.dtype == torch.float32 and part.is_contiguous() and part.numel() >= nslices * n * D,
+          f"part: contiguous fp32 of >= {nslices}*{n}*{D} elements")
+    for name, t in (("res", res), ("a_out", a_out)):
+        if t is not None:
+            _need(t.dim() == 2 and t.stride(1) == 1 and t.shape[0] >= n and t.shape[1] >= D and t.dtype == dtype,
+                  f"bad {name}")
+    if x_out is None:
+        x_out = torch.empty(n, D, dtype=dtype, device=part.device)
+    if w2 is not None and h_out is None:
+        h_out = torch.empty(n, D, dtype=dtype, device=part.device)
+    _need(x_out.dim() == 2 and x_out.stride(1) == 1 and x_out.shape[1] >= D and x_out.dtype == dtype
+          and (out_rows is not None or x_out.shape[0] >= n), "x_out: (>= n rows, D+)")
+    if h_out is not None:
+        _need(h_out.dim() == 2 and h_out.stride(1) == 1 and h_out.shape[1] >= D and h_out.shape[0] >= n
+              and h_out.dtype == dtype, "h_out: (>= n rows, D+)")
+    rc = _lib.load().wfd_add_rmsnorm_split(
+        part.data_ptr(), n * D, nslices, _p(a_out), a_out.stride(0) if a_out is not None else 0, _p(res),
+        res.stride(0) if res is not None else 0, w1.data_ptr(), _p(w2), x_out.data_ptr(), _p(out_rows),
+        x_out.stride(0), _p(h_out), h_out.stride(0) if h_out is not None else 0, n, D, float(eps), _DT[dtype],
+        _stream())
+    _lib.check(rc, "wfd_add_rmsnorm_split")
+    return (x_out, h_out) if w2 is not None else x_out
+
+
 def embed(ids: torch.Tensor, table: torch.Tensor, scale: float = 1.0, *, out: torch.Tensor | None = None,
           ring: torch.Tensor | None = None):
     """out[i] = table[id_i] * scale; with `ring`, a negative ids[i] = -(slot + 1)
