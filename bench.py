@@ -20,10 +20,18 @@ draft-then-verify; greedy decode on the same model with an adapter that makes
 every draft exact; bs=32 with ragged prompts U[128, 2048] and generation
 lengths U[64, 512] at emulated alpha 0.5 / 0.7 / 0.9 and greedy; the
 wavefront attention op alone (bf16, 16 heads x 64, W=8, L in {1k, 4k, 16k})
-and at the 2048-d decode shape (its roofline object); a long-context GQA
-decode tick and the long-context configuration end to end; causal prefill
-attention on MFMA; the roofline of the dominant kernel; and the CPU oracle on
-bounded samples of the workloads on this host's cores.
+and at the 2048-d decode shapes; a long-context GQA decode tick and the
+long-context configuration end to end; causal prefill attention on MFMA; the
+per-shape weight-stream linears at 8 rows; and the CPU oracle on bounded
+samples of the workloads on this host's cores.
+
+`roofline` is the wavefront attention kernel at the headline's shape (one
+layer tick of the 2048-d model at bs=1: 8 rows x 16 heads x Dh 128 over
+512..778-key prefixes), the kernel the decode target is stated for;
+`extra.roofline_linear` is the largest single kernel of that tick, the
+gate|up projection with the SwiGLU epilogue at 8 rows. Both take `achieved`
+from HIP events around graph replays on the launch stream and `traffic` from
+the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes.
 """
 from __future__ import annotations
 
@@ -366,18 +374,14 @@ def attn_section(args, dev, res):
                      "frac": round(by / us / 1e3 / HBM_PEAK_GBS, 4)}
     res["extra"]["wavefront_attention"] = out
     t = out["decode_2048d_layer_tick"]
-    res["roofline_wavefront_attention"] = {
+    res["roofline"] = {
         "bound": "hbm", "achieved": t["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": t["frac"],
-        "traffic": None, "kernel": "wfd::attn_split_kernel (2048-d model, one bs=1 layer tick: 8 rows x 16 heads x "
-                                   "Dh 128, prefixes 512..778 keys)",
+        "traffic": None, "kernel": "wfd::attn_split_kernel<bf16_t, 128, 1, 1, 8, 32> (2048-d model, one bs=1 "
+                                   "layer tick: 8 rows x 16 heads x Dh 128, prefixes 512..778 keys, one split each)",
         "bytes_per_launch": int(t["MB"] * 1e6), "avg_launch_us": t["us"]}
-    tpath = os.path.join(REPO, "profiles", "wavefront_attention_2048d_traffic.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            tr = json.load(f)
-        res["roofline_wavefront_attention"]["traffic"] = tr["traffic_bytes"]
-        res["roofline_wavefront_attention"]["traffic_source"] = tr["source"]
+    _attach_traffic(res["roofline"], "wavefront_attention_c3_tick_traffic.json")
     log(f"attn: {out}")
+    _calibration_copy(dev)
 
 
 def gqa_section(args, dev, res):
@@ -509,26 +513,36 @@ def roofline_section(args, dev, res):
     lin = linear_roofline(dev, M.CONFIGS["looped-2048"], 8)
     us, by = lin["fc_swiglu"]
     ach = by / (us * 1e-6) / 1e9
-    res["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                       "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-                       "kernel": "wfd::linear_wide_kernel<bf16_t, bf16_t, 1, 2, false, 8> (gate|up 11264x2048 + SwiGLU, "
-                                 "n=8 rows)",
-                       "bytes_per_launch": int(by), "avg_launch_us": round(us, 2)}
-    # HBM bytes per launch of this kernel at this shape, from the committed
-    # rocprofv3 FETCH_SIZE / WRITE_SIZE passes (a counter run cannot time itself)
-    tpath = os.path.join(REPO, "profiles", "linear_swiglu_n8_traffic.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            t = json.load(f)
-        if t.get("kernel", "") in res["roofline"]["kernel"]:
-            res["roofline"]["traffic"] = t["traffic_bytes"]
-            res["roofline"]["traffic_source"] = t["source"]
+    rl = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+          "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+          "kernel": "wfd::linear_wide_kernel<bf16_t, bf16_t, 1, 2, false, 8> (gate|up 11264x2048 + SwiGLU, n=8 rows)",
+          "bytes_per_launch": int(by), "avg_launch_us": round(us, 2)}
+    _attach_traffic(rl, "linear_swiglu_n8_traffic.json")
+    res["extra"]["roofline_linear"] = rl
     res["extra"]["linear_shapes_n8"] = {k: {"us": round(u, 2), "MB": round(b / 1e6, 2),
                                             "GBs": round(b / (u * 1e-6) / 1e9, 1)} for k, (u, b) in lin.items()}
     log(f"roofline: fc+SwiGLU linear {ach:.0f} GB/s over {us:.2f} us avg launch; shapes "
         f"{res['extra']['linear_shapes_n8']}")
-    # a plain device copy of known size (256 MiB read + 256 MiB written): the
-    # scale for HBM byte counters (FETCH_SIZE / WRITE_SIZE) read in the same run
+    _calibration_copy(dev)
+
+
+def _attach_traffic(rl: dict, name: str) -> None:
+    """HBM bytes per launch of the roofline kernel at its shape, from the
+    committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes (a counter run cannot
+    time itself), when the profile names the same kernel."""
+    tpath = os.path.join(REPO, "profiles", name)
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            t = json.load(f)
+        if t.get("kernel", "") and rl["kernel"].startswith(t["kernel"]):
+            rl["traffic"] = t["traffic_bytes"]
+            rl["traffic_source"] = t["source"]
+
+
+def _calibration_copy(dev) -> None:
+    """A plain device copy of known size (256 MiB read + 256 MiB written):
+    the scale for the HBM byte counters (FETCH_SIZE / WRITE_SIZE) read in the
+    same run."""
     import torch
 
     a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)

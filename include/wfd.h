@@ -195,10 +195,12 @@ int wfd_linear_pack(const void* W, void* W_packed, int N, int K, int dtype, int 
  * WFD_F32 for bf16 inputs (logits). K must be a multiple of
  * wfd_linear_k_multiple(dtype), N of 16. K is summed in fixed 128 (bf16) /
  * 64 (fp32) element chunks: the P chunks form wfd_linear_slices(K) slices of
- * ceil(P / 4) chunks, chunk partials are added in chunk order within a slice
- * and slice sums in slice order from zero, so y[m] does not depend on n, on
- * where row m sits, or on whether the slices ran in one workgroup or in
- * several (wfd_linear_partials). Every x row read (x_rows[m] * ldx)
+ * Q = ceil(P / 4) chunks, each slice up to 4 sub-slices of ceil(Q / 4)
+ * chunks; chunk partials are added in chunk order within a sub-slice,
+ * sub-slice sums in order within a slice and slice sums in slice order, each
+ * sum from zero in fp32, so y[m] does not depend on n, on where row m sits,
+ * or on whether the slices ran in one workgroup or in several
+ * (wfd_linear_partials). Every x row read (x_rows[m] * ldx)
  * must lie within the first 2 GiB of x. x, W and the x row pitch (ldx
  * elements) must be 16-byte aligned.
  * Replaces: the nn.Linear calls of the block forwards -- Wqkv, proj, the gated

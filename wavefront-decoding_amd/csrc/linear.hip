@@ -14,21 +14,25 @@
 //
 // Arithmetic contract (depends on K and the dtype only, never on n or on how
 // the work is split): K is cut into P = K / KC chunks of 4 MFMA k-steps
-// (KC = 128 bf16 / 64 fp32 elements), and the chunks into at most kSlices
-// consecutive slices of Q = ceil(P / kSlices) chunks. A chunk partial is the
-// MFMA chain over its 4 steps starting from zero; a slice partial is
-// ((0 + c_a) + c_a+1) + ... over its chunks in order; y = epilogue(((0 + s_0)
-// + s_1) + ...) over the slices in order, in fp32. The slices let a many-row
-// launch split K across workgroups (wfd_linear_partials writes the slice
-// partials; the consumer adds them in slice order) with the same bits as a
-// launch that walks all of K. Five kernels honour it bit for bit:
+// (KC = 128 bf16 / 64 fp32 elements); the chunks into at most 4 consecutive
+// slices of Q = ceil(P / 4) chunks, and each slice into at most 4 consecutive
+// sub-slices of R = ceil(Q / 4) chunks. A chunk partial is the MFMA chain over
+// its 4 steps starting from zero; a sub-slice sum is ((0 + c_a) + c_a+1) + ...
+// over its chunks in order, a slice sum ((0 + u_0) + u_1) + ... over its
+// sub-slices in order, and y = epilogue(((0 + s_0) + s_1) + ...) over the
+// slices in order, all in fp32. The slices let a many-row launch split K
+// across workgroups (wfd_linear_partials writes the slice sums; the consumer
+// adds them in slice order); the sub-slices (at most 16) let a few-row launch
+// give each wave one run of chunks to sum in registers. Every sum starts at
+// +0 and so is never -0: adding a +0 for an empty (sub-)slice leaves its bits.
+// Five kernels honour the contract bit for bit:
 //
 //  * wide (n <= 16): one 16-wave workgroup per tile (or column half of a
-//    tile), 8 waves when there are more than 512 tiles; its waves take the
-//    chunks round-robin (all loads of a wave issued together), park the
-//    chunk partials in LDS, and threads sum them in chunk order. No
-//    cross-workgroup synchronization: a tile's whole K is reduced inside one
-//    workgroup.
+//    tile), 8 waves when there are more than 512 tiles; wave w sums sub-slice
+//    w (and w + 8 with 8 waves) in registers (all loads of a wave issued
+//    together), parks it in LDS, and threads add the 16 sub-slice sums in
+//    contract order. No cross-workgroup synchronization: a tile's whole K is
+//    reduced inside one workgroup.
 //  * tile (n > 16, few row-block x tile pairs): a workgroup owns 64 rows of x
 //    and 2 tiles; each of its 4 waves walks the chunks in order for one
 //    16-row block of x and both tiles, with a two-stage register pipeline.
@@ -79,13 +83,63 @@ constexpr int kStreamMaxTiles = 256;
 constexpr int kStreamStages = 4;
 enum Epilogue : int { kEpiPlain = 0, kEpiSwiGLU = 1, kEpiRope = 2 };
 
-// K slices of the arithmetic contract (see the header): Q = ceil(P / kSlices)
-// chunks per slice, at most kSlices slices.
+// K slices and sub-slices of the arithmetic contract (see the header): at most
+// 4 slices of Q = ceil(P / 4) chunks, each of at most 4 sub-slices of
+// R = ceil(Q / 4) = ceil(P / 16) chunks.
 constexpr int kSlices = 4;
+constexpr int kSubSlices = 4;  // per slice
 __host__ __device__ constexpr int slice_chunks(int P) { return (P + kSlices - 1) / kSlices; }
 __host__ __device__ constexpr int slice_count(int P) { return (P + slice_chunks(P) - 1) / slice_chunks(P); }
-// true after the last chunk of a slice
-__device__ __forceinline__ bool slice_end(int p, int P, int Q) { return (p + 1) % Q == 0 || p + 1 == P; }
+__host__ __device__ constexpr int sub_chunks(int P) { return (slice_chunks(P) + kSubSlices - 1) / kSubSlices; }
+
+// Where a kernel that walks chunks in order (from the start of a slice)
+// closes a sub-slice or a slice: a running boundary, not a modulo (a chunk
+// loop that tests p % Q pays an integer division per chunk).
+struct SliceWalk {
+  int P, Q, R, nsl, nsub;
+  __device__ __forceinline__ SliceWalk(int P_, int p0)
+      : P(P_), Q(slice_chunks(P_)), R(sub_chunks(P_)), nsl(p0 + slice_chunks(P_)), nsub(p0 + sub_chunks(P_)) {}
+  // after chunk p: 0 inside a sub-slice, 1 a sub-slice ended, 2 a slice ended
+  __device__ __forceinline__ int end(int p) {
+    const int e = p + 1;
+    if (e == nsl || e == P) {
+      nsl += Q;
+      nsub = e + R;
+      return 2;
+    }
+    if (e == nsub) {
+      nsub += R;
+      return 1;
+    }
+    return 0;
+  }
+};
+
+// Chunk partials into the contract's running sums: sub-slice, slice, total.
+template <int NT>
+__device__ __forceinline__ void contract_add(f32x4 (&sub)[NT], f32x4 (&sl)[NT], f32x4 (&tot)[NT],
+                                             const f32x4 (&acc)[NT], int lvl) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sub[t][r] += acc[t][r];
+  if (lvl >= 1) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sl[t][r] += sub[t][r];
+      sub[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  if (lvl == 2) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) tot[t][r] += sl[t][r];
+      sl[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+}
 
 // Operands of the QKV-RoPE-append epilogue (unused by the others).
 struct RopeArgs {
@@ -231,21 +285,27 @@ __device__ __forceinline__ void chunk_mma(f32x4 (&acc)[NT], const u32x4 (&xf)[kC
 
 // ---------------------------------------------------------------------------
 // wide: grid (tiles << HALF), WW waves (16, or 8 for launches of more tiles
-// than 1024-thread workgroups can keep resident at once: two per CU); MC
-// chunks per wave. Which wave computes a chunk does not change the chunk-order
-// sum, so WW changes no bits. HALF: two
-// workgroups per tile, each owning 8 of its 16 columns (its other lanes load
-// zero weights through an invalid buffer offset: no memory traffic), so a
-// 2048-column projection spreads over 256 workgroups instead of 128. The MFMA
-// output of a column does not depend on the other columns' operands, so both
-// forms give the same bits.
-template <typename T, typename TO, int EPI, int MC, bool HALF, int WW>
+// than 1024-thread workgroups can keep resident at once: two per CU). Wave w
+// owns sub-slice w of the contract (with 8 waves also w + 8): RM >= R chunks
+// per sub-slice, summed in chunk order in registers, so each wave parks one
+// f32x4 per sub-slice in LDS and the tile's 16 sub-slice sums are added by
+// threads 0..255 in contract order (the chunk layout over waves changes no
+// bits). HALF: two workgroups per tile, each owning 8 of its 16 columns (its
+// other lanes load zero weights through an invalid buffer offset: no memory
+// traffic), so a 2048-column projection spreads over 256 workgroups instead
+// of 128. The MFMA output of a column does not depend on the other columns'
+// operands, so both forms give the same bits.
+template <typename T, typename TO, int EPI, int RM, bool HALF, int WW>
 __global__ __launch_bounds__(64 * WW) void linear_wide_kernel(
     const T* __restrict__ x, const int32_t* __restrict__ x_rows, int64_t ldx, const T* __restrict__ W,
     TO* __restrict__ y, int64_t ldy, int n, int K, int pair_off, const RopeArgs ra) {
-  extern __shared__ f32x4 red[];  // [P][64 lanes]
+  constexpr int KPW = kSlices * kSubSlices / WW;  // sub-slices per wave
+  static_assert(KPW * WW == kSlices * kSubSlices, "16 or 8 waves");
+  __shared__ f32x4 red[kSlices * kSubSlices][64];  // sub-slice sums [sub-slice][lane]
   constexpr int V = LinTraits<T>::V;
   const int P = K / LinTraits<T>::KC;
+  const int Q = slice_chunks(P);
+  const int R = sub_chunks(P);
   const int g = HALF ? blockIdx.x >> 1 : blockIdx.x;
   const int half = HALF ? (int)(blockIdx.x & 1) : 0;
   const int wave = threadIdx.x >> 6;
@@ -258,51 +318,70 @@ __global__ __launch_bounds__(64 * WW) void linear_wide_kernel(
   const T* const wtile[1] = {W + packed_off<T>(g, 0, P, 0)};
   const __amdgpu_buffer_rsrc_t wrs = buf_rsrc(wtile[0]);
 
-  // Every load is unconditional; a wave past the last chunk re-reads chunk
-  // P-1 and discards it.
-  u32x4 wf[MC][1][kChunkSteps];
-  u32x4 xf[MC][kChunkSteps];
+  // Sub-slice k = 4 q + u covers chunks [c0, c1) of slice q; an empty one
+  // (past the last chunk) sums to +0. Every load is unconditional: a chunk
+  // slot past the sub-slice's end re-reads chunk P-1 and is not added.
+  int c0[KPW], c1[KPW];
 #pragma unroll
-  for (int j = 0; j < MC; ++j) {
-    const int p = wave + WW * j;
-    const int pc = p < P ? p : P - 1;
-    if (HALF) {
-      const bool mine = (col >> 3) == half;
-#pragma unroll
-      for (int s2 = 0; s2 < kChunkSteps; ++s2) {
-        const uint32_t off = (uint32_t)((packed_off<T>(0, pc, P, lane) + (int64_t)s2 * 64 * V) * sizeof(T));
-        wf[j][0][s2] = buf_ld16(wrs, mine ? off : kBufInvalid);
-      }
-    } else {
-      load_w<T, 1>(wf[j], wtile, P, pc, lane);
-    }
-    load_x<T>(xf[j], xrs, xoff, pc);
+  for (int i = 0; i < KPW; ++i) {
+    const int k = wave + WW * i;
+    const int q = k / kSubSlices, u = k % kSubSlices;
+    const int se = (q + 1) * Q < P ? (q + 1) * Q : P;
+    c0[i] = q * Q + u * R;
+    c1[i] = c0[i] + R < se ? c0[i] + R : se;
   }
+  u32x4 wf[KPW][RM][1][kChunkSteps];
+  u32x4 xf[KPW][RM][kChunkSteps];
 #pragma unroll
-  for (int j = 0; j < MC; ++j) {
-    const int p = wave + WW * j;
-    if (p < P) {
-      f32x4 acc[1];
-      chunk_mma<T, 1>(acc, xf[j], wf[j]);
-      red[p * 64 + lane] = acc[0];
+  for (int i = 0; i < KPW; ++i)
+#pragma unroll
+    for (int j = 0; j < RM; ++j) {
+      const int p = c0[i] + j;
+      const int pc = p < c1[i] ? p : P - 1;
+      if (HALF) {
+        const bool mine = (col >> 3) == half;
+#pragma unroll
+        for (int s2 = 0; s2 < kChunkSteps; ++s2) {
+          const uint32_t off = (uint32_t)((packed_off<T>(0, pc, P, lane) + (int64_t)s2 * 64 * V) * sizeof(T));
+          wf[i][j][0][s2] = buf_ld16(wrs, mine ? off : kBufInvalid);
+        }
+      } else {
+        load_w<T, 1>(wf[i][j], wtile, P, pc, lane);
+      }
+      load_x<T>(xf[i][j], xrs, xoff, pc);
     }
+#pragma unroll
+  for (int i = 0; i < KPW; ++i) {
+    f32x4 sub = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < RM; ++j) {
+      if (c0[i] + j < c1[i]) {  // uniform
+        f32x4 acc[1];
+        chunk_mma<T, 1>(acc, xf[i][j], wf[i][j]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sub[r] += acc[0][r];
+      }
+    }
+    red[wave + WW * i][lane] = sub;
   }
   __syncthreads();
 
-  // threads 0..255: one (lane', r) output each; chunk partials summed slice by slice, in order
+  // threads 0..255: one (lane', r) output each, the 16 sub-slice sums added
+  // sub-slice by sub-slice within each slice, then slice by slice
   if (threadIdx.x < 256) {
     const int ln = threadIdx.x >> 2;
     const int r = threadIdx.x & 3;
     const int row = 4 * (ln >> 4) + r;
-    const float* rf = reinterpret_cast<const float*>(red);
-    const int Q = slice_chunks(P);
-    float v = 0.f, sl = 0.f;
-    for (int p = 0; p < P; ++p) {
-      sl += rf[(p * 64 + ln) * 4 + r];
-      if (slice_end(p, P, Q)) {
-        v += sl;
-        sl = 0.f;
-      }
+    float us[kSlices * kSubSlices];
+#pragma unroll
+    for (int k = 0; k < kSlices * kSubSlices; ++k) us[k] = red[k][ln][r];
+    float v = 0.f;
+#pragma unroll
+    for (int q = 0; q < kSlices; ++q) {
+      float sl = 0.f;
+#pragma unroll
+      for (int u = 0; u < kSubSlices; ++u) sl += us[q * kSubSlices + u];
+      v += sl;
     }
     // column ln ^ 1 lives in thread threadIdx.x ^ 4, column ln ^ 8 in threadIdx.x ^ 32
     const float partner = EPI == kEpiRope     ? __shfl_xor(v, 4, 64)
@@ -342,25 +421,11 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ 
 
   // two-stage register pipeline; every load is unconditional (the stage past
   // the last chunk re-reads chunk P-1 and is never used)
-  const int Q = slice_chunks(P);
-  f32x4 tot[NB], sl[NB];
+  SliceWalk walk(P, 0);
+  f32x4 tot[NB], sl[NB], sub[NB];
 #pragma unroll
-  for (int c = 0; c < NB; ++c) tot[c] = sl[c] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // chunk p's partial into its slice; at the slice's end the slice into the total
-  auto add = [&](const f32x4 (&acc)[NB], int p) {
-#pragma unroll
-    for (int c = 0; c < NB; ++c)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sl[c][r] += acc[c][r];
-    if (slice_end(p, P, Q)) {
-#pragma unroll
-      for (int c = 0; c < NB; ++c) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) tot[c][r] += sl[c][r];
-        sl[c] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-    }
-  };
+  for (int c = 0; c < NB; ++c) tot[c] = sl[c] = sub[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto add = [&](const f32x4 (&acc)[NB], int p) { contract_add<NB>(sub, sl, tot, acc, walk.end(p)); };
   u32x4 wa[NB][kChunkSteps], wb[NB][kChunkSteps], xa[kChunkSteps], xb[kChunkSteps];
   load_w<T, NB>(wa, wtile, P, 0, lane);
   load_x<T>(xa, xrs, xoff, 0);
@@ -477,11 +542,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
 #pragma unroll
     for (int i = 0; i < FPW; ++i) wl[b][wave * FPW + i][lane] = wr[i];
   };
-  f32x4 tot[BT], sl[BT];
+  SliceWalk walk(P, pb);
+  f32x4 tot[BT], sl[BT], sub[BT];
 #pragma unroll
-  for (int t = 0; t < BT; ++t) tot[t] = sl[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // chunk p from LDS stage b: its partial into the slice; at the slice's end
-  // (full-K form) the slice into the total
+  for (int t = 0; t < BT; ++t) tot[t] = sl[t] = sub[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // chunk p from LDS stage b: its partial into the contract's running sums
   auto mma = [&](const u32x4 (&xf)[kChunkSteps], int b, int p) {
     f32x4 acc[BT];
 #pragma unroll
@@ -499,18 +564,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
 #pragma unroll
       for (int t = 0; t < BT; ++t) acc[t] = mfma_step<T>(xf[st], wf[st & 1][t], acc[t]);
     }
-#pragma unroll
-    for (int t = 0; t < BT; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sl[t][r] += acc[t][r];
-    if (!PART && slice_end(p, P, Q)) {
-#pragma unroll
-      for (int t = 0; t < BT; ++t) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) tot[t][r] += sl[t][r];
-        sl[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-    }
+    contract_add<BT>(sub, sl, tot, acc, walk.end(p));
   };
 
   // Register rings, statically unrolled by two (no copies, no exit inside
@@ -552,7 +606,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int orow = row0 + 4 * grp + r;
-        if (orow < n) part[((int64_t)blockIdx.y * n + orow) * N + 16 * g + col] = sl[t][r];
+        if (orow < n) part[((int64_t)blockIdx.y * n + orow) * N + 16 * g + col] = tot[t][r];  // == the slice sum
       }
     }
     return;
@@ -670,10 +724,10 @@ __global__ __launch_bounds__(256) void linear_stream_kernel(const T* __restrict_
   for (int u = 0; u < NS - 1; ++u)
     if (u < P) issue(u);
 
-  const int Q = slice_chunks(P);
-  f32x4 tot[BT], sl[BT];
+  SliceWalk walk(P, 0);
+  f32x4 tot[BT], sl[BT], sub[BT];
 #pragma unroll
-  for (int t = 0; t < BT; ++t) tot[t] = sl[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < BT; ++t) tot[t] = sl[t] = sub[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int p = 0; p < P; ++p) {
     // this wave's chunk p is in LDS once at most the later chunks' loads are outstanding
     if (p + NS - 2 < P) {
@@ -694,18 +748,7 @@ __global__ __launch_bounds__(256) void linear_stream_kernel(const T* __restrict_
 #pragma unroll
         for (int t = 0; t < BT; ++t) acc[t] = mfma_step<T>(xf, wst[st][t * kChunkSteps + s][lane], acc[t]);
       }
-#pragma unroll
-      for (int t = 0; t < BT; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sl[t][r] += acc[t][r];
-      if (slice_end(p, P, Q)) {
-#pragma unroll
-        for (int t = 0; t < BT; ++t) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) tot[t][r] += sl[t][r];
-          sl[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-      }
+      contract_add<BT>(sub, sl, tot, acc, walk.end(p));
     }
   }
   if (!rows) return;  // after the last barrier; every load of this wave has completed
@@ -730,37 +773,32 @@ static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const v
                           int N, int K, int pair_off, const RopeArgs& ra, hipStream_t st) {
   const int tiles = N / 16;
   const int P = K / LinTraits<T>::KC;
-  const size_t lds = (size_t)P * 64 * sizeof(f32x4);
-  const int mc = (P + kWideWaves - 1) / kWideWaves;  // chunks per wave
-  const bool wide = n <= kWideMaxRows && mc <= kWideMaxChunksPerWave && lds <= 65536;
+  const int R = sub_chunks(P);  // chunks per sub-slice: one sub-slice per wave (two with 8 waves)
+  const bool wide = n <= kWideMaxRows && R <= kWideMaxChunksPerWave;
   // fewer tiles than half the chip's 256 CUs x 2: split tiles into column halves
   // (not for SwiGLU, whose partner column c ^ 8 lies in the other half)
   const bool half = EPI != kEpiSwiGLU && tiles <= kHalfTileMax;
   // more tiles than two 1024-thread workgroups per CU hold: 8-wave workgroups
   // (four per CU), so the whole launch is resident in one round (gate|up at
-  // 704 tiles: 11.5 -> 10.4 us)
-  const int mc8 = (P + 7) / 8;
-  const bool ww8 = !half && tiles > kResidentWide && mc8 <= kWideMaxChunksPerWave;
-#define WFD_WIDE(MCV)                                                                                             \
+  // 704 tiles: 11.5 -> 10.4 us); each wave then sums two sub-slices, so only
+  // for one chunk per sub-slice (K <= 16 chunks)
+  const bool ww8 = !half && tiles > kResidentWide && R == 1;
+#define WFD_WIDE(RMV)                                                                                             \
   if (half)                                                                                                       \
-    hipLaunchKernelGGL((linear_wide_kernel<T, TO, EPI, MCV, true, kWideWaves>), dim3(2 * tiles),                 \
-                       dim3(64 * kWideWaves), lds, st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K,     \
+    hipLaunchKernelGGL((linear_wide_kernel<T, TO, EPI, RMV, true, kWideWaves>), dim3(2 * tiles),                 \
+                       dim3(64 * kWideWaves), 0, st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K,       \
                        pair_off, ra);                                                                             \
   else                                                                                                            \
-    hipLaunchKernelGGL((linear_wide_kernel<T, TO, EPI, MCV, false, kWideWaves>), dim3(tiles), dim3(64 * kWideWaves), \
-                       lds, st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra);
-#define WFD_WIDE8(MCV)                                                                                          \
-  hipLaunchKernelGGL((linear_wide_kernel<T, TO, EPI, MCV, false, 8>), dim3(tiles), dim3(64 * 8), lds, st,      \
+    hipLaunchKernelGGL((linear_wide_kernel<T, TO, EPI, RMV, false, kWideWaves>), dim3(tiles), dim3(64 * kWideWaves), \
+                       0, st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra);
+#define WFD_WIDE8(RMV)                                                                                          \
+  hipLaunchKernelGGL((linear_wide_kernel<T, TO, EPI, RMV, false, 8>), dim3(tiles), dim3(64 * 8), 0, st,        \
                      (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra);
-  if (wide && ww8 && mc8 == 1) {
+  if (wide && ww8) {
     WFD_WIDE8(1)
-  } else if (wide && ww8 && mc8 == 2) {
-    WFD_WIDE8(2)
-  } else if (wide && ww8) {
-    WFD_WIDE8(3)
-  } else if (wide && mc == 1) {
+  } else if (wide && R == 1) {
     WFD_WIDE(1)
-  } else if (wide && mc == 2) {
+  } else if (wide && R == 2) {
     WFD_WIDE(2)
   } else if (wide) {
     WFD_WIDE(3)
