@@ -515,7 +515,7 @@ def roofline_section(args, dev, res):
     ach = by / (us * 1e-6) / 1e9
     rl = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
           "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-          "kernel": "wfd::linear_wide_kernel<bf16_t, bf16_t, 1, 2, false, 8> (gate|up 11264x2048 + SwiGLU, n=8 rows)",
+          "kernel": "wfd::linear_wide_kernel<bf16_t, bf16_t, 1, 1, false, 8> (gate|up 11264x2048 + SwiGLU, n=8 rows)",
           "bytes_per_launch": int(by), "avg_launch_us": round(us, 2)}
     _attach_traffic(rl, "linear_swiglu_n8_traffic.json")
     res["extra"]["roofline_linear"] = rl
