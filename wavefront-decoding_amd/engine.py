@@ -133,6 +133,13 @@ _SPLIT_ROWS = (17, 512)
 
 
 def _bucket(n: int) -> int:
+    """Padded row count of a pass under graphs (one captured graph per
+    count): powers of two up to 64, then multiples of 64, the many-row
+    linears' row block -- a 150-row union runs 3 row blocks, not the 4 of a
+    256-row bucket (padding rows cost the linears a whole block each; the
+    attention skips them)."""
+    if n > 64:
+        return (n + 63) // 64 * 64
     b = 1
     while b < n:
         b *= 2
