@@ -62,7 +62,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--quick", action="store_true", help="fewer extras (development)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--only", default="", help="comma list of sections: bs1,roofline,attn,bs32,prefill,c5,gqa,cpu")
+    ap.add_argument("--only", default="", help="comma list of sections: bs1,roofline,attn,linrows,bs32,prefill,c5,gqa,cpu")
     ap.add_argument("--eager", action="store_true", help="launch every pass eagerly (no hipGraph capture)")
     return ap.parse_args()
 
@@ -302,6 +302,66 @@ def bs1_section(args, dev, res):
         del m2, b2, pf2
         torch.cuda.empty_cache()
     return w
+
+
+def linrows_section(args, dev, res):
+    """The decode linears of the 2048-d model at the row counts of bs=32
+    passes (17-256 rows): per shape, the launch the engine uses (the split-K
+    slice launch plus its split residual norm for the 2048-column
+    projections; one launch for gate|up + SwiGLU and Wqkv), timed like the
+    n=8 shapes (HIP events around graph replays over rotating weight copies)."""
+    import torch
+    from wavefront_decoding_amd import model as M
+    from wavefront_decoding_amd import ops
+
+    c = M.CONFIGS["looped-2048"]
+    D = c.d_model
+    shapes = [("gate_up_swiglu", 2 * c.ffn, D, True), ("Wqkv", c.qkv_dim, D, False),
+              ("proj", D, c.n_heads * c.head_dim, False), ("mlp_proj", D, c.ffn, False), ("adapter", D, 2 * D, False)]
+    g = torch.Generator(device=dev).manual_seed(2)
+    w1 = (1 + 0.1 * torch.randn(D, device=dev, generator=g)).to(torch.bfloat16)
+    w2 = (1 + 0.1 * torch.randn(D, device=dev, generator=g)).to(torch.bfloat16)
+    rows = (17, 64, 128, 256)
+    part = torch.empty(4 * max(rows) * D, dtype=torch.float32, device=dev)
+    out = {}
+    iters = 12
+    for name, N, K, sw in shapes:
+        copies = max(2, math.ceil(2 * MALL_BYTES / (N * K * 2)) + 1)
+        Ws = [ops.pack_linear((0.02 * torch.randn(N, K, device=dev, generator=g)).to(torch.bfloat16), swiglu=sw)
+              for _ in range(copies)]
+        for n in rows:
+            x = torch.randn(n, K + 32, device=dev, generator=g).to(torch.bfloat16)[:, :K]
+            res_ = torch.randn(n, D, device=dev, generator=g).to(torch.bfloat16)
+            y = torch.empty(n, N // 2 if sw else N, device=dev, dtype=torch.bfloat16)
+            xo, ho = torch.empty(n, D, device=dev, dtype=torch.bfloat16), torch.empty(n, D, device=dev,
+                                                                                      dtype=torch.bfloat16)
+            split = N == D
+
+            def loop(Ws=Ws, x=x, y=y, n=n, sw=sw, split=split, res_=res_, xo=xo, ho=ho):
+                for i in range(iters):
+                    if split:
+                        S = ops.linear_partials(x, Ws[i % copies], part, n=n)
+                        ops.add_rmsnorm_split(part, S, n, w1, 1e-6, dtype=torch.bfloat16, res=res_, w2=w2,
+                                              x_out=xo, h_out=ho)
+                    else:
+                        ops.linear(x, Ws[i % copies], n=n, out=y, swiglu=sw)
+
+            loop()
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                loop()
+            graph.replay()
+            us = timed(lambda i: graph.replay(), 3) / iters * 1e3
+            del graph
+            wb = N * K * 2
+            out[f"{name}_n{n}"] = {"us": round(us, 2), "weight_MB": round(wb / 1e6, 2),
+                                   "GBs": round(wb / (us * 1e-6) / 1e9, 1),
+                                   "form": "split-K slices + split residual norm" if split else "one launch"}
+        del Ws
+    torch.cuda.empty_cache()
+    res["extra"]["linears_bs32_rows"] = out
+    log(f"linrows: {out}")
 
 
 def bs32_section(args, dev, res, w=None):
@@ -703,6 +763,8 @@ def main():
         roofline_section(args, dev, res)
     if want("attn"):
         attn_section(args, dev, res)
+    if want("linrows"):
+        linrows_section(args, dev, res)
     if want("bs32") and not args.quick:
         bs32_section(args, dev, res, w)
     if want("prefill"):
