@@ -160,6 +160,29 @@ def test_bf16_wfd_is_lossless(gpu, cfg):
         assert toks == ar, T_draft
 
 
+def test_rollback_reappend_reproduces_committed_cache_rows(gpu):
+    """Slot-cache append and rollback: greedy WFD on random-init weights
+    rejects almost every draft, so rows of rejected tokens are dropped and
+    rewritten by the gold token at the same positions. Over every committed
+    position that has been through the whole model, every slot's K and V
+    rows then equal those of sequential decode bit for bit (the invariant of
+    reference kv_cache.py:158-165 with reads bounded by the query's position)."""
+    cfg = MINI_BF16
+    model = LoopedModel(cfg, M.init_weights(cfg, 0), gpu, max_seq_len=512, max_batch=1)
+    blocks = LoopedBlocks(model)
+    ids = _prompt(200, 11).to(gpu)
+    N = 40
+    print("[rollback] sequential", flush=True)
+    ar, _ = blocks.ar_generate(ids, N)
+    cache = blocks._cache
+    end = 200 + N - 1  # the last token is committed but not yet run through the model
+    K0, V0 = cache.K[:, 0, :end].clone(), cache.V[:, 0, :end].clone()
+    print("[rollback] WFD", flush=True)
+    toks, tr = generate_wavefront_dynamic(blocks, ids, N, SsdPolicy(cfg.T_total, 2))
+    assert toks == ar and tr.n_rollback_events > 0
+    assert torch.equal(cache.K[:, 0, :end], K0) and torch.equal(cache.V[:, 0, :end], V0)
+
+
 def test_core_tick_row_invariant(gpu):
     """One R tick over a mixed-depth union equals each row ticked alone, bit for bit."""
     cfg = MINI_BF16
