@@ -81,3 +81,36 @@ def test_embed_copy_rows_argmax_reject_short_buffers():
         ops.argmax(_m(4, 100, dtype=torch.float32), n=8)
     with pytest.raises(_lib.WfdError, match="out: int64"):
         ops.argmax(_m(8, 100, dtype=torch.float32), n=8, out=_m(4, dtype=torch.int64))
+
+
+def test_linear_partials_rejects_short_x_and_part(monkeypatch):
+    monkeypatch.setattr(ops, "linear_slices", lambda K, dtype: 4)
+    W = _w(256, 512)
+    part = _m(4 * 8 * 256, dtype=torch.float32)
+    with pytest.raises(_lib.WfdError, match="rows < n"):
+        ops.linear_partials(_m(4, 512), W, part, n=8)
+    with pytest.raises(_lib.WfdError, match="part"):
+        ops.linear_partials(_m(8, 512), W, _m(4 * 8 * 256 - 1, dtype=torch.float32), n=8)
+    with pytest.raises(_lib.WfdError, match="part"):
+        ops.linear_partials(_m(8, 512), W, _m(4 * 8 * 256), n=8)  # bf16, not fp32
+    with pytest.raises(_lib.WfdError, match="x_rows"):
+        ops.linear_partials(_m(8, 512), W, part, n=8, x_rows=_m(4, dtype=torch.int32))
+
+
+def test_add_rmsnorm_split_rejects_short_buffers():
+    D, n = 256, 8
+    w = _m(D)
+    part = _m(4 * n * D, dtype=torch.float32)
+    kw = dict(dtype=torch.bfloat16)
+    with pytest.raises(_lib.WfdError, match="part"):
+        ops.add_rmsnorm_split(_m(4 * n * D - 1, dtype=torch.float32), 4, n, w, 1e-6, **kw)
+    with pytest.raises(_lib.WfdError, match="nslices"):
+        ops.add_rmsnorm_split(part, 5, n, w, 1e-6, **kw)
+    with pytest.raises(_lib.WfdError, match="bad res"):
+        ops.add_rmsnorm_split(part, 4, n, w, 1e-6, res=_m(n - 1, D), **kw)
+    with pytest.raises(_lib.WfdError, match="bad a_out"):
+        ops.add_rmsnorm_split(part, 4, n, w, 1e-6, a_out=_m(n - 1, D), **kw)
+    with pytest.raises(_lib.WfdError, match="x_out"):
+        ops.add_rmsnorm_split(part, 4, n, w, 1e-6, x_out=_m(n - 1, D), **kw)
+    with pytest.raises(_lib.WfdError, match="h_out"):
+        ops.add_rmsnorm_split(part, 4, n, w, 1e-6, w2=w, x_out=_m(n, D), h_out=_m(n - 1, D), **kw)
