@@ -166,29 +166,70 @@ __device__ __forceinline__ int weight_row(int g, int c, int pair_off) {
   return 16 * g + c;
 }
 
+// The table operands of one output (row, col) of the QKV-RoPE-append
+// epilogue: its rotation (cos, sin at the row's position; identity for v
+// heads) and, for k / v heads, the row's slot-cache row. Loaded apart from the
+// stores: a store may alias the tables as far as the compiler knows, so a
+// load placed after one would wait for it -- kernels gather every operand of
+// their outputs first (or at launch), then store.
+struct RopePre {
+  float c, s;
+  int64_t fr;
+};
+
+__device__ __forceinline__ RopePre rope_pre(const RopeArgs& ra, int row, int col) {
+  RopePre o{1.f, 0.f, 0};
+  const int head = col / ra.Dh;  // uniform over a 16-column tile (Dh % 16 == 0)
+  const int d = col - head * ra.Dh;
+  if (head >= ra.H) o.fr = ra.flat_row[row];
+  if (head < ra.H + ra.Hkv) {
+    int p = ra.pos[row];
+    p = p < 0 ? 0 : (p >= ra.tab_rows ? ra.tab_rows - 1 : p);
+    const int half = ra.Dh >> 1;
+    o.c = ra.cos_t[(int64_t)p * half + (d >> 1)];
+    o.s = ra.sin_t[(int64_t)p * half + (d >> 1)];
+  }
+  return o;
+}
+
 // Value v0 of output (row, col) and its RoPE partner v1 = value of column col ^ 1.
 template <typename TO>
-__device__ __forceinline__ void store_rope(const RopeArgs& ra, int row, int col, float v0, float v1) {
+__device__ __forceinline__ void store_rope(const RopeArgs& ra, const RopePre& o, int row, int col, float v0,
+                                           float v1) {
   const int head = col / ra.Dh;
   const int d = col - head * ra.Dh;
   TO* dst;
   float out;
   if (head >= ra.H + ra.Hkv) {
-    dst = (TO*)ra.v_cache + kv_offset(ra.flat_row[row], head - ra.H - ra.Hkv, ra.Hkv, ra.Dh, ra.block_rows) + d;
+    dst = (TO*)ra.v_cache + kv_offset(o.fr, head - ra.H - ra.Hkv, ra.Hkv, ra.Dh, ra.block_rows) + d;
     out = v0;
   } else {
-    int p = ra.pos[row];
-    p = p < 0 ? 0 : (p >= ra.tab_rows ? ra.tab_rows - 1 : p);
-    const int half = ra.Dh >> 1;
-    const float c = ra.cos_t[(int64_t)p * half + (d >> 1)];
-    const float s = ra.sin_t[(int64_t)p * half + (d >> 1)];
     const float xm = Elem<TO>::round(v0);
     const float xp = Elem<TO>::round(v1);
-    out = (d & 1) ? fmaf(xp, s, xm * c) : fmaf(xm, c, -(xp * s));
+    out = (d & 1) ? fmaf(xp, o.s, xm * o.c) : fmaf(xm, o.c, -(xp * o.s));
     dst = head < ra.H ? (TO*)ra.q_out + ((int64_t)row * ra.H + head) * ra.Dh + d
-                      : (TO*)ra.k_cache + kv_offset(ra.flat_row[row], head - ra.H, ra.Hkv, ra.Dh, ra.block_rows) + d;
+                      : (TO*)ra.k_cache + kv_offset(o.fr, head - ra.H, ra.Hkv, ra.Dh, ra.block_rows) + d;
   }
   Elem<TO>::store(dst, out);
+}
+
+// Table operands of a lane's epilogue outputs -- rows row4 .. row4 + 3 (rows
+// past n read row 0's, never stored) of tiles g0 .. g0 + NT - 1 (past the
+// last tile: the last one's) at column col -- all loaded before the first
+// store. A no-op for the other epilogues.
+template <int EPI, int NT>
+__device__ __forceinline__ void gather_rope(RopePre (&rp)[NT][4], const RopeArgs& ra, int row4, int n, int g0,
+                                            int tiles, int col) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      rp[t][r] = RopePre{1.f, 0.f, 0};
+      if constexpr (EPI == kEpiRope) {
+        const int g = g0 + t < tiles ? g0 + t : tiles - 1;
+        rp[t][r] = rope_pre(ra, row4 + r < n ? row4 + r : 0, 16 * g + col);
+      }
+    }
 }
 
 // Store of output (row, column c of tile g); `partner` is the value of column
@@ -196,11 +237,11 @@ __device__ __forceinline__ void store_rope(const RopeArgs& ra, int row, int col,
 // lane fetches its partner before any lane branches here.
 template <typename TO, int EPI>
 __device__ __forceinline__ void store_out(TO* __restrict__ y, int64_t ldy, const RopeArgs& ra, int row, int g, int c,
-                                          float v, float partner) {
+                                          float v, float partner, const RopePre& rp) {
   if (EPI == kEpiSwiGLU) {
     if (c < 8) Elem<TO>::store(y + (int64_t)row * ldy + 8 * g + c, (v / (1.0f + expf(-v))) * partner);
   } else if (EPI == kEpiRope) {
-    store_rope<TO>(ra, row, 16 * g + c, v, partner);
+    store_rope<TO>(ra, rp, row, 16 * g + c, v, partner);
   } else {
     Elem<TO>::store(y + (int64_t)row * ldy + 16 * g + c, v);
   }
@@ -317,6 +358,15 @@ __global__ __launch_bounds__(64 * WW) void linear_wide_kernel(
   const __amdgpu_buffer_rsrc_t xrs = buf_rsrc(x);
   const T* const wtile[1] = {W + packed_off<T>(g, 0, P, 0)};
   const __amdgpu_buffer_rsrc_t wrs = buf_rsrc(wtile[0]);
+  // the RoPE epilogue's table operands of this thread's output, fetched at
+  // launch so the epilogue waits on no load
+  RopePre rp{1.f, 0.f, 0};
+  if constexpr (EPI == kEpiRope) {
+    if (threadIdx.x < 256) {
+      const int orow = 4 * ((threadIdx.x >> 2) >> 4) + (threadIdx.x & 3);
+      rp = rope_pre(ra, orow < n ? orow : 0, 16 * g + ((threadIdx.x >> 2) & 15));
+    }
+  }
 
   // Sub-slice k = 4 q + u covers chunks [c0, c1) of slice q; an empty one
   // (past the last chunk) sums to +0. Every load is unconditional: a chunk
@@ -387,7 +437,8 @@ __global__ __launch_bounds__(64 * WW) void linear_wide_kernel(
     const float partner = EPI == kEpiRope     ? __shfl_xor(v, 4, 64)
                           : EPI == kEpiSwiGLU ? __shfl_xor(v, 32, 64)
                                               : 0.f;
-    if (row < n && (!HALF || ((ln & 15) >> 3) == half)) store_out<TO, EPI>(y, ldy, ra, row, g, ln & 15, v, partner);
+    if (row < n && (!HALF || ((ln & 15) >> 3) == half))
+      store_out<TO, EPI>(y, ldy, ra, row, g, ln & 15, v, partner, rp);
   }
 }
 
@@ -443,6 +494,8 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ 
     chunk_mma<T, NB>(acc, xb, wb);
     add(acc, p + 1);
   }
+  RopePre rp[NB][4];
+  gather_rope<EPI, NB>(rp, ra, row0 + 4 * grp, n, blockIdx.y * NB, tiles, col);
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
     if (!gok[b]) continue;  // uniform over the workgroup
@@ -454,7 +507,7 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ 
       const float partner = EPI == kEpiRope     ? __shfl_xor(tot[b][r], 1, 64)
                             : EPI == kEpiSwiGLU ? __shfl_xor(tot[b][r], 8, 64)
                                                 : 0.f;
-      if (orow < n) store_out<TO, EPI>(y, ldy, ra, orow, g, col, tot[b][r], partner);
+      if (orow < n) store_out<TO, EPI>(y, ldy, ra, orow, g, col, tot[b][r], partner, rp[b][r]);
     }
   }
 }
@@ -611,6 +664,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
     }
     return;
   }
+  RopePre rp[BT][4];
+  gather_rope<EPI, BT>(rp, ra, row0 + 4 * grp, n, tg * BT, tiles, col);
 #pragma unroll
   for (int t = 0; t < BT; ++t) {
     const int g = tg * BT + t;
@@ -622,7 +677,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
       const float partner = EPI == kEpiRope     ? __shfl_xor(tot[t][r], 1, 64)
                             : EPI == kEpiSwiGLU ? __shfl_xor(tot[t][r], 8, 64)
                                                 : 0.f;
-      if (orow < n) store_out<TO, EPI>(y, ldy, ra, orow, g, col, tot[t][r], partner);
+      if (orow < n) store_out<TO, EPI>(y, ldy, ra, orow, g, col, tot[t][r], partner, rp[t][r]);
     }
   }
 }
@@ -752,6 +807,8 @@ __global__ __launch_bounds__(256) void linear_stream_kernel(const T* __restrict_
     }
   }
   if (!rows) return;  // after the last barrier; every load of this wave has completed
+  RopePre rp[BT][4];
+  gather_rope<EPI, BT>(rp, ra, row0 + 4 * grp, n, blockIdx.y * BT, tiles, col);
 #pragma unroll
   for (int t = 0; t < BT; ++t) {
     const int g = blockIdx.y * BT + t;
@@ -763,7 +820,7 @@ __global__ __launch_bounds__(256) void linear_stream_kernel(const T* __restrict_
       const float partner = EPI == kEpiRope     ? __shfl_xor(tot[t][r], 1, 64)
                             : EPI == kEpiSwiGLU ? __shfl_xor(tot[t][r], 8, 64)
                                                 : 0.f;
-      if (orow < n) store_out<TO, EPI>(y, ldy, ra, orow, g, col, tot[t][r], partner);
+      if (orow < n) store_out<TO, EPI>(y, ldy, ra, orow, g, col, tot[t][r], partner, rp[t][r]);
     }
   }
 }
