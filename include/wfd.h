@@ -290,6 +290,24 @@ int wfd_embed(const int64_t* ids, const int64_t* ring, int64_t ring_len, const v
               int64_t ldo, int n, int vocab, int D, int dtype, wfd_stream_t stream);
 
 /*
+ * The opening of a prelude pass in one launch: x_out[i] = wfd_embed's row i
+ * (table[id_i] * scale, ids / ring handles as there) if x_out is given,
+ * h_out[i] = rmsnorm(that row) * w1 (wfd_add_rmsnorm's math), and, with
+ * cp_src, the side copy cp_dst[cp_dst_rows[i], :cp_width] =
+ * cp_src[cp_src_rows[i], :cp_width] (the token's initial loop state into its
+ * wave-state row). Same bits as wfd_embed + wfd_add_rmsnorm + wfd_copy_rows.
+ * D and the row pitches as for wfd_add_rmsnorm; cp_width a multiple of 16 bytes.
+ * Replaces: wte(ids) * emb_scale, the first prelude block's norm_1 and the s0
+ *   table lookup (src/decoding/huginn_blocks.py:95,184-186,190;
+ *   huginn_blocks_batch.py:215-217; parcae_blocks.py:137-146).
+ */
+int wfd_embed_rmsnorm(const int64_t* ids, const int64_t* ring, int64_t ring_len, const void* table, float scale,
+                      int vocab, const void* w1, void* x_out, int64_t ldx, void* h_out, int64_t ldh,
+                      const void* cp_src, const int32_t* cp_src_rows, int64_t cp_lds, void* cp_dst,
+                      const int32_t* cp_dst_rows, int64_t cp_ldd, int cp_width, int n, int D, float eps, int dtype,
+                      wfd_stream_t stream);
+
+/*
  * dst[dst_rows ? dst_rows[i] : i, :width] = src[src_rows ? src_rows[i] : i, :width].
  * Replaces: the per-token torch.stack of hidden/static rows and the s0 table
  *   lookup (src/decoding/huginn_blocks.py:190,205-209; parcae_blocks.py:137-146).

@@ -481,6 +481,37 @@ def test_embed_copy_argmax(gpu):
     assert am[2].item() == 17
 
 
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 2048), (torch.bfloat16, 256), (torch.float32, 256)])
+def test_embed_rmsnorm_same_bits_as_three_launches(gpu, dtype, D):
+    """The prelude's opening launch -- embed (ids and ring handles), the first
+    norm, and the initial-loop-state copy into the wave-state rows -- equals
+    embed + rmsnorm + copy_rows bit for bit."""
+    g = torch.Generator().manual_seed(D)
+    V, n = 300, 6
+    table = torch.randn(V, D, generator=g).to(dtype).to(gpu)
+    w = (1 + 0.1 * torch.randn(D, generator=g)).to(dtype).to(gpu)
+    ring = torch.tensor([7, 250, 3], dtype=torch.int64, device=gpu)
+    ids = torch.tensor([5, -2, 299, -1, 0, 7], dtype=torch.int64, device=gpu)  # -2, -1: ring handles
+    s0 = torch.randn(40, D, generator=g).to(dtype).to(gpu)
+    pos = torch.tensor([3, 9, 0, 39, 12, 5], dtype=torch.int32, device=gpu)
+    rows = torch.tensor([4, 0, 9, 2, 7, 5], dtype=torch.int32, device=gpu)
+    pad = 64 // table.element_size()
+    for scale in (1.0, 45.25):
+        print(f"[embed_rmsnorm] dtype={dtype} D={D} scale={scale}", flush=True)
+        x0 = ops.embed(ids, table, scale, ring=ring)
+        h0 = ops.rmsnorm(x0, w, 1e-6)
+        pool0 = torch.zeros(10, 2 * D + pad, dtype=dtype, device=gpu)[:, :2 * D]
+        ops.copy_rows(s0, pool0, n=n, width=D, src_rows=pos, dst_rows=rows)
+        x1 = torch.empty(n, D, dtype=dtype, device=gpu)
+        h1 = torch.empty(n, D + pad, dtype=dtype, device=gpu)[:, :D]
+        pool1 = torch.zeros(10, 2 * D + pad, dtype=dtype, device=gpu)[:, :2 * D]
+        ops.embed_rmsnorm(ids, table, scale, w, 1e-6, h_out=h1, x_out=x1, ring=ring, copy=(s0, pos, pool1, rows, D))
+        assert torch.equal(x1, x0) and torch.equal(h1, h0) and torch.equal(pool1, pool0)
+        h2 = torch.empty(n, D, dtype=dtype, device=gpu)
+        ops.embed_rmsnorm(ids, table, scale, w, 1e-6, h_out=h2, ring=ring)  # no x_out, no copy
+        assert torch.equal(h2, h0)
+
+
 def test_token_ring_round_trip(gpu):
     """argmax drops ids into ring slots (padding rows aimed at a trash slot);
     embed takes a handle -(slot + 1) from the ring, and plain ids as before."""

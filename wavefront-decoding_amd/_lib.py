@@ -57,6 +57,8 @@ SIGNATURES: dict[str, tuple] = {
     "wfd_add_rmsnorm_split": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _i64,
                                      _i32, _i32, _f32, _i32, _vp]),
     "wfd_embed": (_i32, [_vp, _vp, _i64, _vp, _f32, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
+    "wfd_embed_rmsnorm": (_i32, [_vp, _vp, _i64, _vp, _f32, _i32, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp,
+                                 _vp, _i64, _i32, _i32, _i32, _f32, _i32, _vp]),
     "wfd_copy_rows": (_i32, [_vp, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _i32, _vp]),
     "wfd_argmax": (_i32, [_vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i32, _i32, _vp]),
 }

@@ -55,27 +55,52 @@ constexpr int kNormRowsPerCuLaunch = 1024;  // rows from which the norm packs 4 
 // unconditional, and the residual / second-norm variants are compile-time, so
 // no load sits behind a data-dependent branch (whose join would wait for it).
 //
-// SPLIT: `a` is not a row but the fp32 slice partials of a split-K linear
-// (wfd_linear_partials: slice q of row i at part + q * slice_stride + i * D);
-// the kernel adds them in slice order from zero -- the linear's arithmetic
-// contract -- and rounds to T as the linear's store would, optionally keeps
-// that row (a_out), and continues as the plain kernel from the same values.
+// Where the row `a` comes from (SRC):
+//  * kSrcRows: rows of `a` (a_rows[i] or i).
+//  * kSrcSplit: the fp32 slice partials of a split-K linear
+//    (wfd_linear_partials: slice q of row i at part + q * slice_stride + i * D),
+//    added in slice order from zero -- the linear's arithmetic contract -- and
+//    rounded to T as the linear's store would.
+//  * kSrcEmbed: the embedding row table[id_i] * scale rounded to T, id_i =
+//    ids[i] or, for a negative id with a ring, the device token ring's entry
+//    -(id + 1) (wfd_embed's arithmetic); each row's wave also copies row
+//    cp_src_rows[i] of cp_src to row cp_dst_rows[i] of cp_dst (cp_width
+//    elements; the prelude's initial loop state).
+// With a_out the resolved row is stored there (the adapter's output and the
+// embedding are their block's residual stream); the rest is the plain
+// kernel's math on the same values.
+enum : int { kSrcRows = 0, kSrcSplit = 1, kSrcEmbed = 2 };
 constexpr int kSplitMaxSlices = 4;  // the linear's K slices (at most 4)
 
-struct SplitArgs {
-  const float* part;
+struct SrcArgs {
+  const float* part;  // kSrcSplit
   int64_t slice_stride;
   int nslices;
-  void* a_out;
+  const int64_t* ids;  // kSrcEmbed
+  const int64_t* ring;
+  int64_t ring_len;
+  const void* table;
+  float scale;
+  int vocab;
+  const void* cp_src;
+  const int32_t* cp_src_rows;
+  int64_t cp_lds;
+  void* cp_dst;
+  const int32_t* cp_dst_rows;
+  int64_t cp_ldd;
+  int cp_width;
+  void* a_out;  // kSrcSplit, kSrcEmbed
   int64_t lda_out;
 };
 
-template <typename T, bool RES, bool TWO, int MAXR, bool SPLIT>
+template <typename T, bool RES, bool TWO, int MAXR, int SRC>
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
     const T* __restrict__ a, const int32_t* __restrict__ a_rows, int64_t lda, const T* __restrict__ res,
     int64_t ldr, const T* __restrict__ w1, const T* __restrict__ w2, T* __restrict__ x_out,
     const int32_t* __restrict__ out_rows, int64_t ldo, T* __restrict__ h_out, int64_t ldh, int n, int D, float eps,
-    const SplitArgs sp) {
+    const SrcArgs sp) {
+  constexpr bool SPLIT = SRC == kSrcSplit;
+  constexpr bool KEEP = SRC != kSrcRows;  // a row resolved here, storable to a_out
   constexpr int V = Chunk<T>::V;
   constexpr int KSTEP = Chunk<T>::KSTEP;
   constexpr int KC = Chunk<T>::KC;
@@ -85,12 +110,28 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
   const int j = lane >> 4;
   if (i >= n) return;  // no barriers below
   const int P = D / KC;
-  const int64_t ar = a_rows ? a_rows[i] : i;
+  const int64_t ar = SRC == kSrcRows && a_rows ? a_rows[i] : i;
+  [[maybe_unused]] const T* erow = nullptr;  // kSrcEmbed: the table row
+  if constexpr (SRC == kSrcEmbed) {
+    int64_t id = sp.ids[i];
+    if (id < 0 && sp.ring) {  // a token handle: the id sits in the device token ring
+      const int64_t slot = -id - 1;
+      id = slot < sp.ring_len ? sp.ring[slot] : 0;
+    }
+    id = id < 0 ? 0 : (id >= sp.vocab ? sp.vocab - 1 : id);
+    erow = (const T*)sp.table + id * D;
+    if (sp.cp_src) {  // the side copy, independent of the row's math
+      const int64_t sr = sp.cp_src_rows ? sp.cp_src_rows[i] : i;
+      const int64_t dr = sp.cp_dst_rows ? sp.cp_dst_rows[i] : i;
+      for (int e = lane * V; e < sp.cp_width; e += 64 * V)
+        *reinterpret_cast<u32x4*>((T*)sp.cp_dst + dr * sp.cp_ldd + e) = ld16((const T*)sp.cp_src + sr * sp.cp_lds + e);
+    }
+  }
   // every load is unconditional: a lane past the last chunk re-reads chunk
   // P-1 (its sum is never used, nothing is stored for it)
   float v[MAXR][kChunkSteps][V];
   u32x4 wa[MAXR][kChunkSteps], wb[MAXR][kChunkSteps];
-  [[maybe_unused]] u32x4 wr[SPLIT ? MAXR : 1][SPLIT ? kChunkSteps : 1];
+  [[maybe_unused]] u32x4 wr[KEEP ? MAXR : 1][KEEP ? kChunkSteps : 1];
 #pragma unroll
   for (int r = 0; r < MAXR; ++r) {
     const int p = r * 16 + c < P ? r * 16 + c : P - 1;
@@ -117,12 +158,16 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
         }
 #pragma unroll
         for (int e = 0; e < V; ++e) v[r][s][e] = Elem<T>::round(sum[e]);
+      } else if constexpr (SRC == kSrcEmbed) {
+        Elem<T>::unpack(ld16(erow + off), v[r][s]);
+#pragma unroll
+        for (int e = 0; e < V; ++e) v[r][s][e] = Elem<T>::round(v[r][s][e] * sp.scale);
       } else {
         Elem<T>::unpack(ld16(a + ar * lda + off), v[r][s]);
       }
       wa[r][s] = ld16(w1 + off);
       if constexpr (TWO) wb[r][s] = ld16(w2 + off);
-      if constexpr (RES && SPLIT) {
+      if constexpr (RES && KEEP) {
         wr[r][s] = ld16(res + (int64_t)i * ldr + off);  // added after a_out is stored
       } else if constexpr (RES) {
         float q[V];
@@ -132,8 +177,8 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
       }
     }
   }
-  if constexpr (SPLIT) {
-    if (sp.a_out) {  // the linear's output rows, when the caller keeps them
+  if constexpr (KEEP) {
+    if (sp.a_out) {  // the resolved rows, when the caller keeps them
 #pragma unroll
       for (int r = 0; r < MAXR; ++r)
 #pragma unroll
@@ -205,10 +250,10 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
   }
 }
 
-template <typename T, int MAXR, bool SPLIT>
+template <typename T, int MAXR, int SRC>
 static void launch_norm_r(const void* a, const int32_t* a_rows, int64_t lda, const void* res, int64_t ldr,
                           const void* w1, const void* w2, void* x_out, const int32_t* out_rows, int64_t ldo,
-                          void* h_out, int64_t ldh, int n, int D, float eps, const SplitArgs& sp,
+                          void* h_out, int64_t ldh, int n, int D, float eps, const SrcArgs& sp,
                           hipStream_t stream) {
   // one row (wave) per workgroup unless there are rows enough to fill every
   // CU four times over: a CU streams its waves' rows at a bounded rate, so a
@@ -218,49 +263,44 @@ static void launch_norm_r(const void* a, const int32_t* a_rows, int64_t lda, con
   const T *at = (const T*)a, *rt = (const T*)res, *w1t = (const T*)w1, *w2t = (const T*)w2;
   T *xo = (T*)x_out, *ho = (T*)h_out;
   if (res && w2)
-    hipLaunchKernelGGL((add_rmsnorm_kernel<T, true, true, MAXR, SPLIT>), grid, block, 0, stream, at, a_rows, lda, rt,
+    hipLaunchKernelGGL((add_rmsnorm_kernel<T, true, true, MAXR, SRC>), grid, block, 0, stream, at, a_rows, lda, rt,
                        ldr, w1t, w2t, xo, out_rows, ldo, ho, ldh, n, D, eps, sp);
   else if (res)
-    hipLaunchKernelGGL((add_rmsnorm_kernel<T, true, false, MAXR, SPLIT>), grid, block, 0, stream, at, a_rows, lda, rt,
+    hipLaunchKernelGGL((add_rmsnorm_kernel<T, true, false, MAXR, SRC>), grid, block, 0, stream, at, a_rows, lda, rt,
                        ldr, w1t, w2t, xo, out_rows, ldo, ho, ldh, n, D, eps, sp);
   else if (w2)
-    hipLaunchKernelGGL((add_rmsnorm_kernel<T, false, true, MAXR, SPLIT>), grid, block, 0, stream, at, a_rows, lda, rt,
+    hipLaunchKernelGGL((add_rmsnorm_kernel<T, false, true, MAXR, SRC>), grid, block, 0, stream, at, a_rows, lda, rt,
                        ldr, w1t, w2t, xo, out_rows, ldo, ho, ldh, n, D, eps, sp);
   else
-    hipLaunchKernelGGL((add_rmsnorm_kernel<T, false, false, MAXR, SPLIT>), grid, block, 0, stream, at, a_rows, lda, rt,
+    hipLaunchKernelGGL((add_rmsnorm_kernel<T, false, false, MAXR, SRC>), grid, block, 0, stream, at, a_rows, lda, rt,
                        ldr, w1t, w2t, xo, out_rows, ldo, ho, ldh, n, D, eps, sp);
 }
 
 // Rounds of 16 chunks per lane: a row of up to 16 chunks needs one (the usual
 // d_model), wider rows up to kNormMaxD take the general form.
-template <typename T, bool SPLIT>
+template <typename T, int SRC>
 static void launch_norm_t(const void* a, const int32_t* a_rows, int64_t lda, const void* res, int64_t ldr,
                           const void* w1, const void* w2, void* x_out, const int32_t* out_rows, int64_t ldo,
-                          void* h_out, int64_t ldh, int n, int D, float eps, const SplitArgs& sp, hipStream_t stream) {
+                          void* h_out, int64_t ldh, int n, int D, float eps, const SrcArgs& sp, hipStream_t stream) {
   if (D <= 16 * Chunk<T>::KC)
-    launch_norm_r<T, 1, SPLIT>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, sp,
-                               stream);
+    launch_norm_r<T, 1, SRC>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, sp,
+                             stream);
   else
-    launch_norm_r<T, kNormMaxD / (16 * Chunk<T>::KC), SPLIT>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo,
-                                                              h_out, ldh, n, D, eps, sp, stream);
+    launch_norm_r<T, kNormMaxD / (16 * Chunk<T>::KC), SRC>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo,
+                                                            h_out, ldh, n, D, eps, sp, stream);
 }
 
-static void launch_add_rmsnorm(int dtype, const void* a, const int32_t* a_rows, int64_t lda, const void* res, int64_t ldr,
-                        const void* w1, const void* w2, void* x_out, const int32_t* out_rows, int64_t ldo,
-                        void* h_out, int64_t ldh, int n, int D, float eps, const SplitArgs* sp, hipStream_t stream) {
-  const SplitArgs none{};
-  if (dtype == kBF16 && sp)
-    launch_norm_t<bf16_t, true>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, *sp,
-                                stream);
-  else if (dtype == kBF16)
-    launch_norm_t<bf16_t, false>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, none,
-                                 stream);
-  else if (sp)
-    launch_norm_t<float, true>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, *sp,
+template <int SRC>
+static void launch_add_rmsnorm(int dtype, const void* a, const int32_t* a_rows, int64_t lda, const void* res,
+                               int64_t ldr, const void* w1, const void* w2, void* x_out, const int32_t* out_rows,
+                               int64_t ldo, void* h_out, int64_t ldh, int n, int D, float eps, const SrcArgs& sp,
+                               hipStream_t stream) {
+  if (dtype == kBF16)
+    launch_norm_t<bf16_t, SRC>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, sp,
                                stream);
   else
-    launch_norm_t<float, false>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, none,
-                                stream);
+    launch_norm_t<float, SRC>(a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, sp,
+                              stream);
 }
 
 template <typename T>
@@ -462,8 +502,8 @@ int wfd_add_rmsnorm(const void* a, const int32_t* a_rows, int64_t lda, const voi
     set_error("wfd_add_rmsnorm: null pointer argument");
     return kBadArg;
   }
-  launch_add_rmsnorm(dtype, a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, nullptr,
-                     stream);
+  launch_add_rmsnorm<kSrcRows>(dtype, a, a_rows, lda, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps,
+                               SrcArgs{}, stream);
   return launch_status("wfd_add_rmsnorm");
 }
 
@@ -495,10 +535,66 @@ int wfd_add_rmsnorm_split(const float* part, int64_t slice_stride, int nslices, 
     set_error("wfd_add_rmsnorm_split: null pointer argument");
     return kBadArg;
   }
-  const SplitArgs sp{part, slice_stride, nslices, a_out, lda_out};
-  launch_add_rmsnorm(dtype, nullptr, nullptr, 0, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D, eps, &sp,
-                     stream);
+  SrcArgs sp{};
+  sp.part = part;
+  sp.slice_stride = slice_stride;
+  sp.nslices = nslices;
+  sp.a_out = a_out;
+  sp.lda_out = lda_out;
+  launch_add_rmsnorm<kSrcSplit>(dtype, nullptr, nullptr, 0, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D,
+                                eps, sp, stream);
   return launch_status("wfd_add_rmsnorm_split");
+}
+
+int wfd_embed_rmsnorm(const int64_t* ids, const int64_t* ring, int64_t ring_len, const void* table, float scale,
+                      int vocab, const void* w1, void* x_out, int64_t ldx, void* h_out, int64_t ldh,
+                      const void* cp_src, const int32_t* cp_src_rows, int64_t cp_lds, void* cp_dst,
+                      const int32_t* cp_dst_rows, int64_t cp_ldd, int cp_width, int n, int D, float eps, int dtype,
+                      hipStream_t stream) {
+  using namespace wfd;
+  if (dtype != kBF16 && dtype != kF32) {
+    set_error("wfd_embed_rmsnorm: unsupported dtype %d", dtype);
+    return kUnsupported;
+  }
+  const int kc = dtype == kBF16 ? Chunk<bf16_t>::KC : Chunk<float>::KC;
+  const int esz = dtype == kBF16 ? 2 : 4;
+  const int vec = 16 / esz;
+  if (n < 0 || D <= 0 || D > kNormMaxD || D % kc != 0 || vocab <= 0 || ring_len < 0 ||
+      (cp_src && (cp_width <= 0 || cp_width % vec || cp_lds < cp_width || cp_ldd < cp_width))) {
+    set_error("wfd_embed_rmsnorm: bad shape n=%d D=%d vocab=%d cp_width=%d", n, D, vocab, cp_width);
+    return kBadArg;
+  }
+  if ((((uintptr_t)table | (uintptr_t)w1 | (uintptr_t)x_out | (uintptr_t)h_out | (uintptr_t)cp_src |
+        (uintptr_t)cp_dst) & 15) || (x_out && ((ldx * esz) & 15)) || ((ldh * esz) & 15) ||
+      (cp_src && (((cp_lds * esz) & 15) || ((cp_ldd * esz) & 15)))) {
+    set_error("wfd_embed_rmsnorm: rows must be 16-byte aligned");
+    return kBadArg;
+  }
+  if (n == 0) return kOk;
+  if (!ids || !table || !w1 || !h_out || (cp_src && !cp_dst)) {
+    set_error("wfd_embed_rmsnorm: null pointer argument");
+    return kBadArg;
+  }
+  SrcArgs sp{};
+  sp.ids = ids;
+  sp.ring = ring;
+  sp.ring_len = ring_len;
+  sp.table = table;
+  sp.scale = scale;
+  sp.vocab = vocab;
+  sp.cp_src = cp_src;
+  sp.cp_src_rows = cp_src_rows;
+  sp.cp_lds = cp_lds;
+  sp.cp_dst = cp_dst;
+  sp.cp_dst_rows = cp_dst_rows;
+  sp.cp_ldd = cp_ldd;
+  sp.cp_width = cp_width;
+  sp.a_out = x_out;
+  sp.lda_out = ldx;
+  // the norm's output is h; the embedded row is kept through a_out
+  launch_add_rmsnorm<kSrcEmbed>(dtype, nullptr, nullptr, 0, nullptr, 0, w1, nullptr, h_out, nullptr, ldh, nullptr, 0,
+                                n, D, eps, sp, stream);
+  return launch_status("wfd_embed_rmsnorm");
 }
 
 int wfd_qkv_rope_append(const void* qkv, int64_t ldq, const int32_t* pos, const float* rope_cos,

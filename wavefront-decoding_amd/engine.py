@@ -423,14 +423,17 @@ class LoopedModel:
         rb = lambda l: t64[off + l * nb: off + (l + 1) * nb]  # noqa: E731
         fr = lambda l: t64[off + (L + l) * nb: off + (L + l + 1) * nb]  # noqa: E731
         if kind == "P":
-            ops.embed(t64[:nb], W["wte"], c.emb_scale, out=sc["x"], ring=self.tok_ring)
-            ops.rmsnorm(sc["x"], W["prelude.0.norm_1"], c.norm_eps, n=nb, x_out=sc["h"])
+            # embed -> x, prelude.0.norm_1 -> h, and each token's initial loop
+            # state s0[pos] into its wave-state row (the prelude below writes
+            # only the row's static half)
+            ops.embed_rmsnorm(t64[:nb], W["wte"], c.emb_scale, W["prelude.0.norm_1"], c.norm_eps, h_out=sc["h"],
+                              x_out=sc["x"], ring=self.tok_ring, n=nb,
+                              copy=(self.s0, pos_d, self.pool, rows_d, c.d_model))
             static_half = self.pool[:, c.d_model:]
             for i in range(L):
                 nxt = W[f"prelude.{i + 1}.norm_1"] if i + 1 < L else None
                 self._block(f"prelude.{i}.", nb, sc, pos_d, kvlen_d, rb(i), fr(i), kv_max, ws, cache, nxt,
                             final_out=static_half, final_rows=rows_d, group_first=gf)
-            ops.copy_rows(self.s0, self.pool, n=nb, width=c.d_model, src_rows=pos_d, dst_rows=rows_d)
         elif kind == "R":
             # adapter -> x (the first core block's residual), core.0.norm_1 -> h
             self._linear_norm(self.pool, W["adapter"], nb, sc, "x", W["core.0.norm_1"], x_rows=rows_d,

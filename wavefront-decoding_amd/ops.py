@@ -473,6 +473,42 @@ def embed(ids: torch.Tensor, table: torch.Tensor, scale: float = 1.0, *, out: to
     return out
 
 
+def embed_rmsnorm(ids: torch.Tensor, table: torch.Tensor, scale: float, w1: torch.Tensor, eps: float, *,
+                  h_out: torch.Tensor, x_out: torch.Tensor | None = None, ring: torch.Tensor | None = None,
+                  n: int | None = None, copy: tuple | None = None) -> None:
+    """One launch for embed(ids) -> x_out (optional) and rmsnorm(x) * w1 ->
+    h_out, the bits of embed + rmsnorm; `copy` = (src, src_rows, dst,
+    dst_rows, width) adds copy_rows(src, dst, ...) for the same n rows."""
+    _need_cuda(ids, table, w1, h_out, x_out, ring)
+    _need(ids.dtype == torch.int64 and ids.is_contiguous(), "ids: int64")
+    if ring is not None:
+        _need(ring.dtype == torch.int64 and ring.is_contiguous(), "ring: int64 contiguous")
+    n = ids.numel() if n is None else n
+    _need(0 <= n <= ids.numel(), f"ids hold {ids.numel()} < n={n}")
+    Vocab, D = table.shape
+    _need(table.dim() == 2 and table.is_contiguous() and w1.numel() == D, "table: contiguous (vocab, D); w1: (D,)")
+    for name, t in (("h_out", h_out), ("x_out", x_out)):
+        if t is not None:
+            _need(t.dim() == 2 and t.stride(1) == 1 and t.shape[0] >= n and t.shape[1] >= D and t.dtype == table.dtype,
+                  f"{name}: (>= n rows, D+) of the table's dtype")
+    cp = (None, None, 0, None, None, 0, 0)
+    if copy is not None:
+        src, src_rows, dst, dst_rows, width = copy
+        _need_cuda(src, src_rows, dst, dst_rows)
+        _rows(src_rows, n, "src_rows")
+        _rows(dst_rows, n, "dst_rows")
+        _need(src.dtype == dst.dtype == table.dtype and src.dim() == 2 and dst.dim() == 2 and src.stride(1) == 1
+              and dst.stride(1) == 1 and 0 < width <= min(src.shape[1], dst.shape[1]), "copy: 2-D src/dst, width")
+        _need(src_rows is not None or src.shape[0] >= n, f"src holds {src.shape[0]} rows < n={n}")
+        _need(dst_rows is not None or dst.shape[0] >= n, f"dst holds {dst.shape[0]} rows < n={n}")
+        cp = (src.data_ptr(), _p(src_rows), src.stride(0), dst.data_ptr(), _p(dst_rows), dst.stride(0), width)
+    rc = _lib.load().wfd_embed_rmsnorm(
+        ids.data_ptr(), _p(ring), ring.numel() if ring is not None else 0, table.data_ptr(), float(scale), Vocab,
+        w1.data_ptr(), _p(x_out), x_out.stride(0) if x_out is not None else 0, h_out.data_ptr(), h_out.stride(0),
+        *cp, n, D, float(eps), _dt(table), _stream())
+    _lib.check(rc, "wfd_embed_rmsnorm")
+
+
 def copy_rows(src: torch.Tensor, dst: torch.Tensor, *, n: int, width: int, src_rows: torch.Tensor | None = None,
               dst_rows: torch.Tensor | None = None) -> None:
     _need_cuda(src, dst, src_rows, dst_rows)
