@@ -89,6 +89,19 @@ def load() -> ctypes.CDLL:
     return lib
 
 
+def load_tick():
+    """The _tick extension (csrc/tick.cpp: a decode tick's row tables, upload
+    and graph launch). Imported after torch for the same reason as libwfd.so;
+    raises if it is not built."""
+    import importlib
+
+    try:
+        return importlib.import_module(__name__.rsplit(".", 1)[0] + "._tick")
+    except ImportError as e:
+        raise WfdError(f"the _tick extension is not built ({e}); build it with "
+                       "`python wavefront-decoding_amd/build.py`") from e
+
+
 def check(rc: int, what: str) -> None:
     if rc != 0:
         msg = load().wfd_last_error().decode(errors="replace")

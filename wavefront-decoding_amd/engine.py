@@ -38,7 +38,7 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-from . import ops
+from . import _lib, ops
 from .kv_cache import BatchStaticKVCache
 from .model import LoopedLMConfig, initial_state_prefill, initial_state_tokens, rope_tables
 
@@ -81,40 +81,48 @@ class _Staging:
 
 
 class _Captured:
-    """One captured pass: fixed device tables, a ring of pinned host copies, the graph.
+    """One captured pass sequence: fixed device tables, a ring of pinned host
+    copies, the graph.
 
     The device table buffer is baked into the graph; each replay is preceded by
     one host->device copy into it (stream-ordered behind the previous replay).
-    The pinned source buffers rotate through a ring, so the host can enqueue
-    several replays ahead of the GPU and only waits when it laps the ring."""
+    The pinned source buffers rotate through a ring, each with an event recorded
+    behind its copy, so the host can enqueue several replays ahead of the GPU
+    and only waits when it laps the ring. Upload and launch are one native call
+    (_tick.launch: event wait, pack, copy, event record, hipGraphLaunch)."""
 
     DEPTH = 8
 
-    def __init__(self, kind: str, nb: int, cache, n32: int, n64: int, device):
-        self.kind, self.nb, self.cache = kind, nb, cache
+    def __init__(self, kind: str, nb: int, cache, n32: int, n64: int, device, tick):
+        self.kind, self.nb, self.cache, self.tick = kind, nb, cache, tick
         # one buffer [int64 tables | int32 tables] so a replay needs one host->device copy
         words = n64 + (n32 + 1) // 2
         self.host = [torch.empty(words, dtype=torch.int64).pin_memory() for _ in range(self.DEPTH)]
-        self.events: list[torch.cuda.Event | None] = [None] * self.DEPTH
+        self.host_ptr = [h.data_ptr() for h in self.host]
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        self.events = [tick.event_create(index) for _ in range(self.DEPTH)]
         self.i = 0
         self.dev = torch.empty(words, dtype=torch.int64, device=device)
         self.n32, self.n64 = n32, n64
         self.d64 = self.dev[:n64]
         self.d32 = self.dev[n64:].view(torch.int32)[:n32]
         self.graph: torch.cuda.CUDAGraph | None = None
+        self.exec = 0  # the graph's executable (raw handle) once captured
 
-    def load(self, i32: np.ndarray, i64: np.ndarray) -> None:
+    def launch(self, t64: np.ndarray, t32: np.ndarray, stream: int, replay: bool = True) -> None:
+        """Upload the first n64 / n32 words of the host tables and replay the
+        graph (replay=False: the upload only)."""
         j = self.i
         self.i = (j + 1) % self.DEPTH
-        if self.events[j] is not None:
-            self.events[j].synchronize()      # the copy out of this pinned buffer DEPTH loads ago is done
-        h = self.host[j].numpy()
-        h[: self.n64] = i64
-        h[self.n64:].view(np.int32)[: self.n32] = i32
-        self.dev.copy_(self.host[j], non_blocking=True)
-        ev = torch.cuda.Event()
-        ev.record()
-        self.events[j] = ev
+        self.tick.launch(self.exec if replay else 0, stream, self.events[j], self.host_ptr[j], self.dev.data_ptr(),
+                         t64, self.n64, t32, self.n32)
+
+    def __del__(self):
+        for e in getattr(self, "events", ()):
+            try:
+                self.tick.event_destroy(e)
+            except Exception:  # interpreter shutdown: the runtime may be gone
+                pass
 
 
 # weights read by the linear kernels (the rest -- embedding, norms -- stay plain)
@@ -207,6 +215,12 @@ class LoopedModel:
                                    dtype=torch.uint8, device=self.device)
         self.staging = _Staging(self.device)
         self._graphs: dict[tuple, _Captured] = {}
+        # the native host side of a tick (row tables, upload, graph launch)
+        self._tick = _lib.load_tick()
+        self._params: dict[tuple, tuple] = {}
+        self._bytes_coef: dict[str, tuple[int, int, int]] = {}
+        self._t_passes = 0
+        self._t32 = self._t64 = None
         # device token ring: every C pass drops its argmax ids at host-allocated
         # slots; a token is then a handle -(slot + 1) until read back, and the P
         # pass embeds handles straight from the ring (no host round trip per
@@ -238,6 +252,7 @@ class LoopedModel:
                                   self.max_seq_len, self.dtype, self.device)
 
     def clear_graphs(self) -> None:
+        torch.cuda.synchronize()  # no upload may still read a pinned buffer about to be freed
         self._graphs.clear()
 
     # -- scratch -----------------------------------------------------------------
@@ -340,77 +355,6 @@ class LoopedModel:
         c = self.cfg
         return {"P": c.n_prelude, "R": c.n_core, "C": c.n_coda}[kind]
 
-    def _groups(self, kind: str, seqs, steps, nb: int) -> np.ndarray | None:
-        """group_first for the attention of a pass (nb + 1 entries): adjacent
-        rows that read the same slots -- same sequence, and for R the same
-        depth (draft-then-verify sources, a coda's verifies and draft) -- form
-        one group of at most attn_group_max_rows rows; padding rows are groups
-        of one. None when every group would hold one row, or when the groups
-        would leave fewer than group_min_workgroups (group, kv head) workgroups:
-        below that, the chip's parallelism is worth more than the re-reads
-        (bs=1 draft-then-verify ran 7 % slower grouped, bs=32 16 % faster)."""
-        n = len(seqs)
-        key = seqs if kind != "R" else seqs * (self.cfg.T_total + 1) + steps
-        if n < 2 or not np.any(key[1:] == key[:-1]):
-            return None
-        gmax = ops.attn_group_max_rows(self.cfg.n_heads, self.cfg.n_kv_heads)
-        first = [0]
-        for i in range(1, n):
-            if key[i] != key[i - 1] or i - first[-1] >= gmax:
-                first.append(i)
-        if len(first) * self.cfg.n_kv_heads < self.group_min_workgroups:
-            return None
-        first += list(range(n, nb + 1))  # padding rows one by one, then the end
-        gf = np.full(nb + 1, nb, dtype=np.int32)
-        gf[:len(first)] = first
-        return gf
-
-    def _tables(self, kind: str, cache, seqs, pos, steps, ids, nb: int, ring_base: int | None = None,
-                groups: np.ndarray | None = None):
-        """int32 [pos | kv_len | pool_row | ring_slot (C only) | group_first
-        (grouped passes, nb + 1)] and int64 [ids (P only) | row_base x L |
-        flat_row x L | expected token (C only)], each block nb wide; rows
-        n..nb-1 are padding aimed at the trash rows / trash ring slot. For C,
-        `ids` carries the expected tokens of a device-side greedy verify
-        (NO_EXPECT: no comparison)."""
-        c = self.cfg
-        n = len(pos)
-        L = self._layers(kind)
-        if kind == "P":
-            slots = np.repeat(np.arange(L, dtype=np.int64)[:, None], n, axis=1)
-        elif kind == "R":
-            slots = c.n_prelude + steps[None, :] * c.n_core + np.arange(L, dtype=np.int64)[:, None]
-        else:
-            slots = self.coda_base + np.repeat(np.arange(L, dtype=np.int64)[:, None], n, axis=1)
-        rb = np.full((L, nb), cache.trash_row, dtype=np.int64)
-        rb[:, :n] = (slots * cache.B + seqs[None, :]) * cache.S
-        fr = rb.copy()
-        fr[:, :n] += pos[None, :]
-        nblk = 4 if kind == "C" else 3
-        i32 = np.zeros(nblk * nb + (nb + 1 if groups is not None else 0), dtype=np.int32)
-        if groups is not None:
-            i32[nblk * nb:] = groups
-        i32[:n] = pos
-        i32[nb: nb + n] = pos + 1
-        i32[nb + n: 2 * nb] = 1
-        i32[2 * nb: 2 * nb + n] = seqs * self.R + pos % self.R
-        i32[2 * nb + n: 3 * nb] = self.trash_pool_row
-        if kind == "C":
-            i32[3 * nb: 4 * nb] = self.ring_len
-            if ring_base is not None:
-                i32[3 * nb: 3 * nb + n] = np.arange(ring_base, ring_base + n, dtype=np.int32)
-        parts = [rb.reshape(-1), fr.reshape(-1)]
-        if kind == "P":
-            idp = np.zeros(nb, dtype=np.int64)
-            idp[:n] = ids
-            parts.insert(0, idp)
-        elif kind == "C":
-            exp = np.full(nb, NO_EXPECT, dtype=np.int64)
-            if ids is not None and len(ids):
-                exp[:n] = ids
-            parts.append(exp)
-        return i32, np.concatenate(parts)
-
     def _launch(self, kind: str, cache, nb: int, t32: torch.Tensor, t64: torch.Tensor, kv_max: int,
                 grouped: bool = False) -> None:
         """The launch sequence of one pass over nb rows (eager or under capture)."""
@@ -453,26 +397,39 @@ class LoopedModel:
             ops.argmax(sc["logits"], n=nb, out=sc["ids"], ring=self.tok_ring, ring_rows=t32[3 * nb: 4 * nb],
                        expect=t64[2 * L * nb: 2 * L * nb + nb], accept=sc["accept"])
 
-    def _plan(self, kind: str, cache, seqs, pos, steps=None, ids=None, ring_base=None) -> dict:
-        # ids: token ids / handles (P) or expected tokens (C)
-        """Tables and launch shape of one pass (padded to its row bucket under graphs)."""
-        n = len(pos)
-        nb = _bucket(n) if self.use_graphs else n
-        if nb > self.max_rows:
-            raise ValueError(f"union of {n} rows exceeds max_rows={self.max_rows}")
-        groups = self._groups(kind, seqs, steps, nb) if self.group_attention else None
-        i32, i64 = self._tables(kind, cache, seqs, pos, steps, ids, nb, ring_base, groups)
-        return dict(kind=kind, nb=nb, grouped=groups is not None, i32=i32, i64=i64, kv_max=int(pos.max()) + 1)
+    # -- a tick: row tables, upload, launch -------------------------------------------
+    def _tick_params(self, cache) -> tuple:
+        """The constants _tick.plan_pass reads (one tuple per cache shape)."""
+        key = (cache.B, cache.S, cache.trash_row)
+        prm = self._params.get(key)
+        if prm is None:
+            c = self.cfg
+            prm = (cache.B, cache.S, cache.trash_row, self.R, self.trash_pool_row, c.n_prelude, c.n_core, c.n_coda,
+                   c.T_total, self.coda_base, self.ring_len, self.max_batch, self.max_seq_len, self.max_rows,
+                   int(self.use_graphs), int(self.group_attention),
+                   ops.attn_group_max_rows(c.n_heads, c.n_kv_heads), self.group_min_workgroups, c.n_kv_heads)
+            assert len(prm) == self._tick.NUM_PARAMS
+            self._params[key] = prm
+        return prm
+
+    def _table_scratch(self, passes: int) -> tuple[np.ndarray, np.ndarray]:
+        """Host scratch for the tables of `passes` passes (int32, int64), grown on demand."""
+        if passes > self._t_passes:
+            c, nb = self.cfg, self.max_rows
+            lmax = max(c.n_prelude, c.n_core, c.n_coda)
+            self._t32 = np.zeros(passes * (5 * nb + 1), dtype=np.int32)
+            self._t64 = np.zeros(passes * (2 + 2 * lmax) * nb, dtype=np.int64)
+            self._t_passes = passes
+        return self._t32, self._t64
 
     def _launch_plans(self, cache, plans, t32: torch.Tensor, t64: torch.Tensor, kv_max: int | None = None) -> None:
         """Launch the passes in order, each on its slice of the joint tables."""
         o32 = o64 = 0
         for p in plans:
-            n32, n64 = len(p["i32"]), len(p["i64"])
-            self._launch(p["kind"], cache, p["nb"], t32[o32: o32 + n32], t64[o64: o64 + n64],
+            self._launch(p["kind"], cache, p["nb"], t32[o32: o32 + p["n32"]], t64[o64: o64 + p["n64"]],
                          kv_max if kv_max is not None else p["kv_max"], p["grouped"])
-            o32 += n32
-            o64 += n64
+            o32 += p["n32"]
+            o64 += p["n64"]
 
     def _captured(self, cache, plans) -> _Captured:
         """The graph of a pass sequence: one per (cache, [(kind, bucket, grouped)])."""
@@ -480,49 +437,57 @@ class LoopedModel:
         g = self._graphs.get(key)
         if g is not None and g.cache is cache:
             return g
-        empty = np.zeros(0, dtype=np.int64)
-        pad = []  # the same shapes with every row a padding row
-        for p in plans:
-            solo = np.arange(p["nb"] + 1, dtype=np.int32) if p["grouped"] else None
-            i32, i64 = self._tables(p["kind"], cache, empty, empty, empty, empty, p["nb"], groups=solo)
-            pad.append(dict(p, i32=i32, i64=i64))
-        g = _Captured("+".join(p["kind"] for p in plans), plans[0]["nb"], cache, sum(len(p["i32"]) for p in pad),
-                      sum(len(p["i64"]) for p in pad), self.device)
-        g.load(np.concatenate([p["i32"] for p in pad]), np.concatenate([p["i64"] for p in pad]))
+        prm = self._tick_params(cache)
+        n32 = sum(p["n32"] for p in plans)
+        n64 = sum(p["n64"] for p in plans)
+        pad32, pad64 = np.zeros(n32, dtype=np.int32), np.zeros(n64, dtype=np.int64)
+        o32 = o64 = 0
+        for p in plans:  # the same shapes with every row a padding row (and every grouped row its own group)
+            _, m32, m64, _, _, _ = self._tick.plan_pass(pad32, o32, pad64, o64, prm, p["kind"], [], [],
+                                                        None if p["kind"] == "C" else [], p["nb"],
+                                                        int(p["grouped"]), -1)
+            o32 += m32
+            o64 += m64
+        g = _Captured("+".join(p["kind"] for p in plans), plans[0]["nb"], cache, n32, n64, self.device, self._tick)
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        g.launch(pad64, pad32, stream, replay=False)
         torch.cuda.synchronize()
-        self._launch_plans(cache, pad, g.d32, g.d64, cache.S)                   # warm-up, then capture
+        self._launch_plans(cache, plans, g.d32, g.d64, cache.S)                   # warm-up, then capture
         torch.cuda.synchronize()
         g.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g.graph):
-            self._launch_plans(cache, pad, g.d32, g.d64, cache.S)
+            self._launch_plans(cache, plans, g.d32, g.d64, cache.S)
         torch.cuda.synchronize()
+        g.exec = g.graph.raw_cuda_graph_exec()
         self._graphs[key] = g
         return g
 
-    def _run_plans(self, cache, plans) -> None:
-        """One replay (graphs) or one table upload + launches (eager) for the whole sequence."""
-        i32 = np.concatenate([p["i32"] for p in plans])
-        i64 = np.concatenate([p["i64"] for p in plans])
-        if self.use_graphs:
-            g = self._captured(cache, plans)
-            g.load(i32, i64)
-            g.graph.replay()
-        else:
-            t32, t64 = self.staging.upload([i32, i64])
-            self._launch_plans(cache, plans, t32, t64)
-
-    def _run(self, kind: str, cache, seqs, pos, steps=None, ids=None, ring_base=None) -> None:
-        self._run_plans(cache, [self._plan(kind, cache, seqs, pos, steps, ids, ring_base)])
-
-    def _check(self, cache, seqs, pos):
-        if len(pos) and (pos.min() < 0 or pos.max() >= cache.S):
-            raise IndexError(f"position out of range [0, {cache.S})")
-        if len(seqs) and (seqs.min() < 0 or seqs.max() >= cache.B or seqs.max() >= self.max_batch):
-            raise IndexError("sequence index out of range")
-        if cache.S > self.max_seq_len:
-            raise ValueError("cache longer than the engine's tables (max_seq_len)")
-
     # -- traffic accounting ------------------------------------------------------------
+    def _bytes_terms(self, kind: str) -> tuple[int, int, int]:
+        """pass_bytes = fixed + per_row * n + per_key * (keys read), keys read =
+        sum over rows of position + 1."""
+        t = self._bytes_coef.get(kind)
+        if t is None:
+            c = self.cfg
+            el = torch.empty(0, dtype=self.dtype).element_size()
+            D, F, Hd, Kd = c.d_model, c.ffn, c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
+            L = self._layers(kind)
+            fixed = L * (c.qkv_dim * D + D * Hd + 2 * F * D + D * F + 4 * D) * el
+            # per row: its K/V append; Wqkv x -> q; attention q -> o; proj o -> a;
+            # norm (a, x) -> (x, h); fc h -> u; mlp_proj u -> m; norm (m, x) -> (x, h)
+            per_row = L * (2 * Kd + 12 * D + 4 * Hd + 2 * F) * el
+            per_key = L * 2 * Kd * el
+            if kind == "P":
+                per_row += 4 * D * el  # embedding row, pool row written (2 D), s0 row
+            elif kind == "R":
+                fixed += 2 * D * D * el  # adapter weights
+                per_row += 3 * D * el    # its x rows and output
+            else:
+                fixed += (c.vocab_size * D + D) * el  # lm_head, ln_f
+                per_row += D * el + c.vocab_size * 4 + 8  # the final norm's row, logits, ids
+            t = self._bytes_coef[kind] = (fixed, per_row, per_key)
+        return t
+
     def pass_bytes(self, kind: str, positions) -> int:
         """Algorithmic HBM bytes of one pass over rows at `positions`: every
         weight byte of its layers once (plus the embedding rows for P, the
@@ -531,56 +496,22 @@ class LoopedModel:
         rows the layers read and write (x into each linear, its output, the
         norms' inputs and outputs). Padding rows of a captured launch are not
         counted: they are not part of the work."""
-        c = self.cfg
-        el = torch.empty(0, dtype=self.dtype).element_size()
-        D, F, Hd, Kd = c.d_model, c.ffn, c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
-        layer_w = (c.qkv_dim * D + D * Hd + 2 * F * D + D * F + 4 * D) * el
+        fixed, per_row, per_key = self._bytes_terms(kind)
         n = len(positions)
-        kv_keys = sum(int(p) + 1 for p in positions)
-        layer_kv = (kv_keys * 2 * Kd + n * 2 * Kd) * el
-        # per row: Wqkv x -> q; attention q -> o; proj o -> a; norm (a, x) -> (x, h);
-        # fc h -> u; mlp_proj u -> m; norm (m, x) -> (x, h)
-        layer_act = n * (12 * D + 4 * Hd + 2 * F) * el
-        L = self._layers(kind)
-        total = L * (layer_w + layer_kv + layer_act)
-        if kind == "P":
-            total += n * D * el + n * 2 * D * el + n * D * el  # embedding rows, pool rows written, s0 rows
-        elif kind == "R":
-            total += 2 * D * D * el + n * (2 * D + D) * el  # adapter weights, its x rows and output
-        else:
-            total += (c.vocab_size * D + D) * el + n * (D + c.vocab_size * 4 + 8)  # lm_head, ln_f, logits, ids
-        return int(total)
+        return int(fixed + per_row * n + per_key * sum(int(p) + 1 for p in positions))
 
     # -- P / R / C ---------------------------------------------------------------------
-    def _prepare(self, cache, kind: str, seqs, positions, extra=None):
-        """Validated plan + bookkeeping closure of one pass. extra: token ids (P),
-        steps (R). A C pass takes its token-ring slots here."""
+    def _note_writes(self, cache, kind: str, seqs, pos, extra) -> None:
+        """The slot lengths the pass's appends extend (the cache's note_write
+        per (slot, row), positions already validated)."""
         c = self.cfg
-        seqs = np.asarray(seqs, dtype=np.int64)
-        pos = np.asarray(positions, dtype=np.int64)
-        self._check(cache, seqs, pos)
-        if kind == "P":
-            plan = self._plan("P", cache, seqs, pos, ids=np.asarray(extra, dtype=np.int64))
-            writes = [(self.slot_prelude(i), b, p) for b, p in zip(seqs.tolist(), pos.tolist())
-                      for i in range(c.n_prelude)]
-            return plan, writes, None
         if kind == "R":
-            st = np.asarray(extra, dtype=np.int64)
-            if st.min() < 0 or st.max() >= c.T_total:
-                raise ValueError(f"core step out of range [0, {c.T_total})")
-            plan = self._plan("R", cache, seqs, pos, steps=st)
-            writes = [(self.slot_core(s_, l), b, p) for b, p, s_ in zip(seqs.tolist(), pos.tolist(), st.tolist())
-                      for l in range(c.n_core)]
-            return plan, writes, None
-        n = len(pos)
-        base = None
-        if self._ring_next + n <= self.ring_len:
-            base = self._ring_next
-            self._ring_next += n
-        expect = None if extra is None else np.asarray(extra, dtype=np.int64)
-        plan = self._plan("C", cache, seqs, pos, ids=expect, ring_base=base)
-        writes = [(self.slot_coda(i), b, p) for b, p in zip(seqs.tolist(), pos.tolist()) for i in range(c.n_coda)]
-        return plan, writes, (None if base is None else [-(base + i) - 1 for i in range(n)])
+            first = [c.n_prelude + int(s) * c.n_core for s in extra]
+            cache.note_writes(first, c.n_core, seqs, pos)
+        elif kind == "P":
+            cache.note_writes(self.slot_prelude(0), c.n_prelude, seqs, pos)
+        else:
+            cache.note_writes(self.slot_coda(0), c.n_coda, seqs, pos)
 
     def run_passes(self, cache, passes) -> tuple[torch.Tensor, torch.Tensor] | None:
         """Several passes as one launch sequence -- one graph replay and one
@@ -590,26 +521,46 @@ class LoopedModel:
         plain id, a ring handle, or NO_EXPECT -- for a device-side greedy
         verify whose flags land in `last_accept`; at most one C, last). A
         scheduler tick (P, R, C) or a whole sequential token (P, T_total x R,
-        C) then costs one replay. Returns what coda_union returns for the C
-        pass, else None."""
-        plans, writes, handles, n_c = [], [], None, 0
+        C) then costs one replay. Every pass is validated and tabled (natively,
+        _tick.plan_pass) before anything launches; the slot-length bookkeeping
+        and the traffic count run after the launch, while the GPU works.
+        Returns what coda_union returns for the C pass, else None."""
+        tick = self._tick
+        prm = self._tick_params(cache)
+        t32, t64 = self._table_scratch(len(passes))
+        plans, live, n_c, c_base = [], [], 0, -1
+        o32 = o64 = 0
+        last = passes[-1][0] if passes else None
         for kind, seqs, positions, extra in passes:
-            if len(positions) == 0:
+            n = len(positions)
+            if n == 0:
                 continue
-            if kind == "C" and passes[-1][0] != "C":
-                raise ValueError("the C pass must come last")
-            plan, w, h = self._prepare(cache, kind, seqs, positions, extra)
-            plans.append(plan)
-            self.bytes_moved += self.pass_bytes(kind, positions)
-            writes += w
             if kind == "C":
-                handles, n_c = h, len(positions)
+                if last != "C":
+                    raise ValueError("the C pass must come last")
+                c_base = self._ring_next if self._ring_next + n <= self.ring_len else -1
+            nb, n32, n64, grouped, kv_max, psum = tick.plan_pass(t32, o32, t64, o64, prm, kind, seqs, positions,
+                                                                 extra, -1, -1, c_base if kind == "C" else -1)
+            plans.append(dict(kind=kind, nb=nb, grouped=grouped, kv_max=kv_max, n32=n32, n64=n64))
+            live.append((kind, seqs, positions, extra, n, psum))
+            o32 += n32
+            o64 += n64
+            if kind == "C":
+                n_c = n
         if plans:
-            self._run_plans(cache, plans)
-        for slot, b, p in writes:
-            cache.note_write(slot, b, p)
+            if self.use_graphs:
+                self._captured(cache, plans).launch(t64, t32, torch.cuda.current_stream(self.device).cuda_stream)
+            else:
+                d32, d64 = self.staging.upload([t32[:o32], t64[:o64]])
+                self._launch_plans(cache, plans, d32, d64)
+        if n_c and c_base >= 0:
+            self._ring_next = c_base + n_c
+        for kind, seqs, positions, extra, n, psum in live:
+            fixed, per_row, per_key = self._bytes_terms(kind)
+            self.bytes_moved += fixed + per_row * n + per_key * (psum + n)
+            self._note_writes(cache, kind, seqs, positions, extra)
         if n_c:
-            self.last_c_handles = handles
+            self.last_c_handles = None if c_base < 0 else [-(c_base + i) - 1 for i in range(n_c)]
             self.last_accept = self.sc["accept"][:n_c]
             return self.sc["logits"][:n_c], self.sc["ids"][:n_c]
         return None

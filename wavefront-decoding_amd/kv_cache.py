@@ -86,6 +86,17 @@ class BatchStaticKVCache:
         if pos + 1 > self.seqlen[slot][b]:
             self.seqlen[slot][b] = pos + 1
 
+    def note_writes(self, first_slot, n_slots: int, seq_ids, positions) -> None:
+        """note_write for slots first_slot .. first_slot + n_slots - 1 of every
+        row (first_slot: one int, or one per row), positions already checked."""
+        seqlen = self.seqlen
+        firsts = [first_slot] * len(positions) if isinstance(first_slot, int) else first_slot
+        for s0, b, p in zip(firsts, seq_ids, positions):
+            v = int(p) + 1
+            for row in seqlen[s0: s0 + n_slots]:
+                if row[b] < v:
+                    row[b] = v
+
     # -- reference API --------------------------------------------------------
     def write_prefill(self, slot: int, k: torch.Tensor, v: torch.Tensor, seq_ids=None) -> None:
         """k, v: (B', L, Hkv, Dh) prompt K/V at positions [0, L) of `slot` for
