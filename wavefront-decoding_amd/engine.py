@@ -217,6 +217,7 @@ class LoopedModel:
         self._graphs: dict[tuple, _Captured] = {}
         # the native host side of a tick (row tables, upload, graph launch)
         self._tick = _lib.load_tick()
+        self._dev_index = self.device.index if self.device.index is not None else torch.cuda.current_device()
         self._params: dict[tuple, tuple] = {}
         self._bytes_coef: dict[str, tuple[int, int, int]] = {}
         self._t_passes = 0
@@ -449,8 +450,7 @@ class LoopedModel:
             o32 += m32
             o64 += m64
         g = _Captured("+".join(p["kind"] for p in plans), plans[0]["nb"], cache, n32, n64, self.device, self._tick)
-        stream = torch.cuda.current_stream(self.device).cuda_stream
-        g.launch(pad64, pad32, stream, replay=False)
+        g.launch(pad64, pad32, self._raw_stream(), replay=False)
         torch.cuda.synchronize()
         self._launch_plans(cache, plans, g.d32, g.d64, cache.S)                   # warm-up, then capture
         torch.cuda.synchronize()
@@ -463,6 +463,11 @@ class LoopedModel:
         return g
 
     # -- traffic accounting ------------------------------------------------------------
+    def _raw_stream(self) -> int:
+        """Handle of torch's current stream on the engine's device (the stream
+        every launch of the engine is ordered on)."""
+        return torch._C._cuda_getCurrentRawStream(self._dev_index)
+
     def _bytes_terms(self, kind: str) -> tuple[int, int, int]:
         """pass_bytes = fixed + per_row * n + per_key * (keys read), keys read =
         sum over rows of position + 1."""
@@ -549,7 +554,7 @@ class LoopedModel:
                 n_c = n
         if plans:
             if self.use_graphs:
-                self._captured(cache, plans).launch(t64, t32, torch.cuda.current_stream(self.device).cuda_stream)
+                self._captured(cache, plans).launch(t64, t32, self._raw_stream())
             else:
                 d32, d64 = self.staging.upload([t32[:o32], t64[:o64]])
                 self._launch_plans(cache, plans, d32, d64)
