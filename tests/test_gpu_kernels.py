@@ -84,22 +84,27 @@ def test_attn_decode_long_prefix(gpu, L):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_attn_decode_row_invariant(gpu, dtype):
+@pytest.mark.parametrize("H,Hkv,Dh", [(16, 16, 128), (16, 4, 128), (4, 4, 64)])
+def test_attn_decode_row_invariant(gpu, dtype, H, Hkv, Dh):
     """A query's output bits do not depend on the other queries, the batch
-    size, or kv_len_max (the grid bound): alone, among 8 rows (256
-    workgroups) and among 64 rows (2048 workgroups)."""
+    size, or kv_len_max (the grid bound): alone (each (split, head, row)
+    split over two workgroups by output columns), among 8 rows and among 64
+    rows (one workgroup each at 16 kv heads)."""
     lens = [700, 33, 1500, 256, 1, 900, 511, 1024]
-    q, K, V, rb, kl = _attn_case(gpu, dtype, 8, 16, 16, 128, lens, S=1803, seed=7)
+    q, K, V, rb, kl = _attn_case(gpu, dtype, 8, H, Hkv, Dh, lens, S=1803, seed=7 + Hkv + Dh)
     K, V = _blocks(K, 1803), _blocks(V, 1803)
     q, K, V, rb, kl = (t.to(gpu) for t in (q, K, V, rb, kl))
-    full = ops.attn_decode(q, K, V, rb, kl, kv_len_max=1500)  # 2 x 16 x 8 = 256 workgroups
+    print(f"[attn row-invariant] dtype={dtype} H={H} Hkv={Hkv} Dh={Dh}", flush=True)
+    full = ops.attn_decode(q, K, V, rb, kl, kv_len_max=1500)  # 2 x Hkv x 8 workgroups (x2 column parts at Hkv 4)
     for i in range(8):
         one = ops.attn_decode(q[i:i + 1].contiguous(), K, V, rb[i:i + 1], kl[i:i + 1], kv_len_max=lens[i] + 300)
         assert torch.equal(one[0], full[i]), i
-    # the same 8 queries repeated over 64 rows: 2 x 16 x 64 = 2048 workgroups
+    # the same 8 queries repeated over 64 rows: 2 x Hkv x 64 workgroups
     big = ops.attn_decode(q.repeat(8, 1, 1), K, V, rb.repeat(8), kl.repeat(8), kv_len_max=1500)
     for r in range(64):
         assert torch.equal(big[r], full[r % 8]), r
+    ref = ok.attention_rows(_np(q), _np(_rows(K)), _np(_rows(V)), rb.cpu().numpy(), kl.cpu().numpy())
+    assert rel_err(_np(full), ref) <= TOL[dtype]
 
 
 @pytest.mark.parametrize("blocks", [False, True])

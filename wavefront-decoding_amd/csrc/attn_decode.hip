@@ -31,6 +31,9 @@
 // merge through LDS in fixed order. A query whose keys fit one split (every
 // decode query up to 1024 keys) is finished in its workgroup; longer ones
 // leave per-split partials that a second kernel merges in fixed split order.
+// A launch of fewer than 256 such workgroups splits each in two by output
+// columns (both read all of K, each half of V; see attn_vsplit): the same
+// arithmetic per column, so the same bits.
 // 1024 rather than 2048 keys per split: with ragged lengths (the batched
 // decode) the longest workgroups set the launch's tail, and halving them made
 // the B=32 decode 13 % faster; uniform long prefixes lose ~2-3 %.
@@ -59,7 +62,7 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict
                                                              const int32_t* __restrict__ group_first,
                                                              float* __restrict__ part_o, float* __restrict__ part_ml,
                                                              T* __restrict__ out, int H, int Hkv, int max_splits,
-                                                             float scale_log2, int64_t block_rows) {
+                                                             float scale_log2, int64_t block_rows, int vsplit) {
   constexpr int V = Elem<T>::kVec;
   constexpr int KSTEP = 4 * V;
   constexpr int NDS = DH / KSTEP;  // MFMA k-steps per 16-key block
@@ -77,8 +80,15 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict
 
   const int split = blockIdx.x;
   const int g = blockIdx.y;
-  const int q0 = group_first ? group_first[blockIdx.z] : (int)blockIdx.z;
-  const int qn = group_first ? min(group_first[blockIdx.z + 1] - q0, QG) : 1;
+  // V split: grid z = vsplit x (rows or groups); part vp owns output columns
+  // [vp * DV, vp * DV + DV) and loads only their V fragments (K whole)
+  const int nz = gridDim.z / vsplit;
+  const int vp = blockIdx.z / nz;
+  const int zi = blockIdx.z - vp * nz;
+  const int DV = DH / vsplit;
+  const int d0 = vp * DV;
+  const int q0 = group_first ? group_first[zi] : zi;
+  const int qn = group_first ? min(group_first[zi + 1] - q0, QG) : 1;
   if (qn <= 0) return;  // empty group slot (uniform)
   int lenq[QG];
   int maxlen = 0;
@@ -92,8 +102,8 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict
     // writes their zero rows (the flash-attention convention for a query that
     // attends nothing)
     if (split == 0)
-      for (int idx = threadIdx.x; idx < qn * G * DH; idx += 64 * NW)
-        Elem<T>::store(out + ((int64_t)(q0 + idx / (G * DH)) * H + g * G + (idx / DH) % G) * DH + idx % DH, 0.f);
+      for (int idx = threadIdx.x; idx < qn * G * DV; idx += 64 * NW)
+        Elem<T>::store(out + ((int64_t)(q0 + idx / (G * DV)) * H + g * G + (idx / DV) % G) * DH + d0 + idx % DV, 0.f);
     return;
   }
   const int kend_max = min(maxlen, (split + 1) * kAttnSplit);
@@ -105,6 +115,9 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict
   const int grp = lane >> 4;
   const int vg = lane / LPR;
   const int dseg = lane % LPR;
+  // this lane's V columns belong to the part (the others load nothing and
+  // accumulate zeros: the part's columns get exactly the unsplit arithmetic)
+  const bool vmine = dseg * V >= d0 && dseg * V < d0 + DV;
   const int64_t hb = kv_offset(row_base[q0], g, Hkv, DH, block_rows);  // position 0, kv head g
   const int64_t rs = block_rows > 1 ? (int64_t)DH : (int64_t)Hkv * DH;  // key stride
   const T* kb = kc + hb;
@@ -158,7 +171,7 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict
 #pragma unroll
     for (int k = 0; k < KPL; ++k) {
       const int key = min(t0 + RG * k + vg, maxlen - 1);
-      vf[k] = ld16(vb + (int64_t)key * rs + dseg * V);
+      vf[k] = vmine ? ld16(vb + (int64_t)key * rs + dseg * V) : zero16();
     }
 
     // scores: lane (grp, col) holds S[row 4*grp + r][key 16j + col] in acc[j][r]
@@ -277,9 +290,9 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict
   // finished here (the split merge over one split, exactly as
   // attn_combine_kernel computes it); otherwise it leaves this split's
   // unnormalised partial. Rows with no keys in this split write nothing.
-  for (int idx = threadIdx.x; idx < NR * DH; idx += 64 * NW) {
-    const int m = idx / DH;
-    const int d = idx - m * DH;
+  for (int idx = threadIdx.x; idx < NR * DV; idx += 64 * NW) {
+    const int m = idx / DV;
+    const int d = d0 + (idx - m * DV);
     const int j = m / G;
     int len = 0;
 #pragma unroll
@@ -414,6 +427,25 @@ static size_t attn_ws_bytes(int n, int H, int Dh, int kv_len_max) {
 constexpr int kAttnGroupRows = 8;
 constexpr int group_max_rows(int G) { return G >= kAttnGroupRows ? 1 : kAttnGroupRows / G; }
 
+// V split of a launch: a workgroup per (split, kv head, row) streams from one
+// CU at ~35-40 GB/s, so a launch of fewer workgroups than the chip has CUs is
+// bound by its longest workgroups, not by HBM (one bs=1 layer tick: 8 rows x
+// 16 heads = 128). Splitting each in two by output columns cuts the bytes one
+// workgroup streams to its whole K plus half its V (K is then read twice).
+// Measured on the 2048-d model's layer tick (8 rows, 512-778 keys): 15.2 ->
+// 13.7 us; 2 rows 12.3 -> 10.7 us; 4 and 8 parts are slower (21 / 35 us),
+// since the repeated K reads reach HBM again whatever the dispatch order.
+// Every column keeps the unsplit arithmetic, so the split changes no bits.
+constexpr int kAttnFillWorkgroups = 256;
+constexpr int kAttnMaxVSplit = 2;
+
+static int attn_vsplit(int ms, int Hkv, int n, int DH) {
+  const int64_t base = (int64_t)ms * Hkv * n;
+  int vs = 1;
+  while (vs < kAttnMaxVSplit && base * vs < kAttnFillWorkgroups && DH % (16 * vs) == 0) vs *= 2;
+  return vs;
+}
+
 template <typename T, int DH, int G>
 static void launch_attn(const void* q, const void* kc, const void* vc, const int64_t* rb, const int32_t* kl,
                         const int32_t* gf, void* out, int n, int H, int Hkv, int ms, float scale, int64_t br,
@@ -422,14 +454,15 @@ static void launch_attn(const void* q, const void* kc, const void* vc, const int
   constexpr int TK = DH == 64 ? 64 : 32;  // key tile that fits the registers
   constexpr int NW = 8;  // waves per workgroup: 8 beat 4 and 16 on every measured shape
   constexpr int QG = group_max_rows(G);
+  const int vs = attn_vsplit(ms, Hkv, n, DH);
   if (gf)
-    hipLaunchKernelGGL((attn_split_kernel<T, DH, G, QG, NW, TK>), dim3(ms, Hkv, n), dim3(64 * NW), 0, st,
+    hipLaunchKernelGGL((attn_split_kernel<T, DH, G, QG, NW, TK>), dim3(ms, Hkv, n * vs), dim3(64 * NW), 0, st,
                        (const T*)q, (const T*)kc, (const T*)vc, rb, kl, gf, po, pml, (T*)out, H, Hkv, ms, scale_log2,
-                       br);
+                       br, vs);
   else
-    hipLaunchKernelGGL((attn_split_kernel<T, DH, G, 1, NW, TK>), dim3(ms, Hkv, n), dim3(64 * NW), 0, st,
+    hipLaunchKernelGGL((attn_split_kernel<T, DH, G, 1, NW, TK>), dim3(ms, Hkv, n * vs), dim3(64 * NW), 0, st,
                        (const T*)q, (const T*)kc, (const T*)vc, rb, kl, gf, po, pml, (T*)out, H, Hkv, ms, scale_log2,
-                       br);
+                       br, vs);
   if (ms > 1)  // some query may span several splits
     hipLaunchKernelGGL((attn_combine_kernel<T, DH>), dim3(H, n), dim3(DH), 0, st, po, pml, kl, (T*)out, H, ms);
 }
