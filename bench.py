@@ -437,7 +437,8 @@ def attn_section(args, dev, res):
     res["roofline"] = {
         "bound": "hbm", "achieved": t["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": t["frac"],
         "traffic": None, "kernel": "wfd::attn_split_kernel<bf16_t, 128, 1, 1, 8, 32> (2048-d model, one bs=1 "
-                                   "layer tick: 8 rows x 16 heads x Dh 128, prefixes 512..778 keys, one split each)",
+                                   "layer tick: 8 rows x 16 heads x Dh 128, prefixes 512..778 keys, one key split "
+                                   "and two column halves each: 256 workgroups)",
         "bytes_per_launch": int(t["MB"] * 1e6), "avg_launch_us": t["us"]}
     _attach_traffic(res["roofline"], "wavefront_attention_c3_tick_traffic.json")
     log(f"attn: {out}")
