@@ -322,6 +322,9 @@ int wfd_copy_rows(const void* src, const int32_t* src_rows, int64_t lds, void* d
  * accept[i] = 1 if out[i] equals the expected token -- expect[i] >= 0 a plain
  * id, -ring_len <= expect[i] < 0 a ring handle -(slot + 1) whose id an
  * earlier pass wrote -- else 0 (also for any other expect[i]: no comparison).
+ * `accept` may be device memory or the device address of mapped, coherent
+ * pinned host memory, which the host can then poll for the flags (each flag
+ * is one 4-byte store of row i's workgroup) instead of copying them back.
  * Replaces: greedy_sample's argmax and its .item() (src/decoding/acceptance.py:40-44),
  *   greedy_accept's draft == argmax comparison (acceptance.py:47-58), and
  *   coda_argmax_union's argmax + .tolist() (src/decoding/huginn_blocks_batch.py:345-346):

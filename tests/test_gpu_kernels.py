@@ -536,6 +536,39 @@ def test_token_ring_round_trip(gpu):
     assert torch.equal(e, table[want])
 
 
+def test_argmax_accept_flags_into_mapped_host_memory(gpu):
+    """The greedy verify flags stored straight into mapped, coherent pinned
+    host memory (what the engine polls): the same flags as into a device
+    tensor, each written over the -1 the host cleared it to."""
+    from wavefront_decoding_amd import _lib
+
+    tick = _lib.load_tick()
+    g = torch.Generator().manual_seed(11)
+    logits = torch.randn(6, 700, generator=g).to(gpu)
+    ref = logits.argmax(dim=-1)
+    ring = torch.full((9,), -7, dtype=torch.int64, device=gpu)
+    ring[3] = ref[1]
+    # expected tokens: a match, a ring handle that matches, a mismatch, "no comparison", a match, a mismatch
+    expect = torch.tensor([ref[0].item(), -4, (ref[2].item() + 1) % 700, -(1 << 62), ref[4].item(),
+                           (ref[5].item() + 3) % 700], dtype=torch.int64, device=gpu)
+    dev_flags = torch.full((6,), -5, dtype=torch.int32, device=gpu)
+    ops.argmax(logits, ring=ring, ring_rows=torch.full((6,), 8, dtype=torch.int32, device=gpu), expect=expect,
+               accept=dev_flags)
+    host, devp = tick.host_alloc(4 * 8)
+    try:
+        tick.clear_flags(host, 8)
+        ops.argmax(logits, ring=ring, ring_rows=torch.full((6,), 8, dtype=torch.int32, device=gpu), expect=expect,
+                   accept_mapped=(devp, 8))
+        flags = tick.wait_flags(host, 6, 10.0)
+        torch.cuda.synchronize()
+        assert flags == [True, True, False, False, True, False]
+        assert flags == [bool(v) for v in dev_flags.tolist()]
+        assert tick.wait_flags(host, 8, 0.0) is None  # flags 6, 7: no row of this launch, still -1
+    finally:
+        torch.cuda.synchronize()
+        tick.host_free(host)
+
+
 def test_bad_arguments_raise(gpu):
     from wavefront_decoding_amd import _lib
 

@@ -252,6 +252,30 @@ def test_rejects_bad_rows(tick):
 def test_launch_checks_its_arguments_before_any_runtime_call(tick):
     t64, t32 = np.zeros(8, np.int64), np.zeros(8, np.int32)
     with pytest.raises(ValueError, match="null"):
-        tick.launch(0, 0, 0, 1, 1, t64, 4, t32, 4)
+        tick.launch(0, 0, 0, 1, 1, t64, 4, t32, 4, 0, 0)
     with pytest.raises(ValueError, match="beyond the scratch"):
-        tick.launch(0, 0, 1, 1, 1, t64, 9, t32, 4)
+        tick.launch(0, 0, 1, 1, 1, t64, 9, t32, 4, 0, 0)
+    with pytest.raises(ValueError, match="accept flag"):
+        tick.launch(0, 0, 1, 1, 1, t64, 4, t32, 4, 0, 3)
+    with pytest.raises(TypeError):
+        tick.launch(0, 0, 1, 1, 1, t64, 4, t32, 4)
+
+
+def test_accept_flag_polling(tick):
+    """clear_flags / wait_flags on ordinary host memory (the engine points
+    them at mapped pinned memory the argmax kernel stores into): a flag reads
+    -1 until written; the poll returns the flags once all n are written, None
+    on timeout."""
+    f = np.array([5, 0, 1, 7, 9], dtype=np.int32)
+    tick.clear_flags(f.ctypes.data, 4)
+    assert f.tolist() == [-1, -1, -1, -1, 9]
+    assert tick.wait_flags(f.ctypes.data, 4, 0.01) is None
+    f[:3] = [1, 0, 1]
+    assert tick.wait_flags(f.ctypes.data, 4, 0.01) is None  # one still unwritten
+    f[3] = 0
+    assert tick.wait_flags(f.ctypes.data, 4, 0.01) == [True, False, True, False]
+    assert tick.wait_flags(f.ctypes.data, 0, 0.0) == []
+    with pytest.raises(ValueError):
+        tick.wait_flags(0, 2, 0.0)
+    with pytest.raises(ValueError):
+        tick.clear_flags(f.ctypes.data, -1)

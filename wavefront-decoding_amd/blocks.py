@@ -336,7 +336,7 @@ class LoopedBlocksBatch:
         if out is None:
             return None
         if expect is not None:
-            self.last_accept = [bool(f) for f in self.model.last_accept.tolist()]
+            self.last_accept = self.model.accept_flags()
         if lazy and self.model.last_c_handles is not None:
             return list(self.model.last_c_handles)
         return out[1].tolist()

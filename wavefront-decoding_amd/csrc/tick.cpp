@@ -8,6 +8,9 @@
 // validates the rows, forms the attention groups and writes the tables in
 // place, and the upload + graph launch is a second call that makes three HIP
 // runtime calls (copy, event record, graph launch) with no Python in between.
+// A greedy tick's accept flags come back through mapped, coherent pinned host
+// memory that the argmax kernel stores into and the host polls (host_alloc,
+// clear_flags, wait_flags), with no device->host copy behind the graph.
 //
 // Table layout of one pass over nb rows (rows n..nb-1 are padding aimed at the
 // trash rows / trash ring slot; L = the pass's layer count):
@@ -21,6 +24,8 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <atomic>
+#include <chrono>
 #include <cstdint>
 #include <cstring>
 #include <vector>
@@ -294,14 +299,25 @@ bool hip_ok(hipError_t e, const char* what) {
 
 void* as_ptr(PyObject* o) { return PyLong_AsVoidPtr(o); }
 
-// launch(graph_exec, stream, event, pinned, dev, out64, n64, out32, n32)
+// Accept flags in mapped, coherent pinned host memory: the argmax kernel
+// stores each C row's flag (0 / 1) straight into it, and the host polls for
+// the tick's flags instead of copying them back behind the graph. A flag
+// reads -1 until the tick's kernel has written it.
+void clear_flags(void* flags, long long n) {
+  volatile int32_t* f = static_cast<volatile int32_t*>(flags);
+  for (long long i = 0; i < n; ++i) f[i] = -1;
+  std::atomic_thread_fence(std::memory_order_seq_cst);  // cleared before the launch that rewrites them
+}
+
+// launch(graph_exec, stream, event, pinned, dev, out64, n64, out32, n32, flags, nflags)
 // Waits for `event` (the last upload out of `pinned`), packs the first n64
 // words of out64 and n32 of out32 into `pinned` ([int64 | int32]), copies them
-// to `dev` on `stream`, records `event` behind the copy and launches the
+// to `dev` on `stream`, records `event` behind the copy, clears the first
+// nflags accept flags at `flags` (host address; 0: none) and launches the
 // graph (graph_exec 0: the copy only).
 PyObject* launch(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
-  if (nargs != 9) {
-    PyErr_SetString(PyExc_TypeError, "launch takes 9 arguments");
+  if (nargs != 11) {
+    PyErr_SetString(PyExc_TypeError, "launch takes 11 arguments");
     return nullptr;
   }
   auto exec = static_cast<hipGraphExec_t>(as_ptr(args[0]));
@@ -310,7 +326,13 @@ PyObject* launch(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
   auto* pinned = static_cast<char*>(as_ptr(args[3]));
   void* dev = as_ptr(args[4]);
   const long long n64 = PyLong_AsLongLong(args[6]), n32 = PyLong_AsLongLong(args[8]);
+  void* flags = as_ptr(args[9]);
+  const long long nflags = PyLong_AsLongLong(args[10]);
   if (PyErr_Occurred()) return nullptr;
+  if (nflags < 0 || (nflags > 0 && flags == nullptr)) {
+    PyErr_SetString(PyExc_ValueError, "launch: bad accept flag buffer");
+    return nullptr;
+  }
   if (event == nullptr || pinned == nullptr || dev == nullptr) {
     PyErr_SetString(PyExc_ValueError, "launch: null event / pinned / device buffer");
     return nullptr;
@@ -327,8 +349,94 @@ PyObject* launch(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
   const size_t bytes = size_t(n64) * 8 + size_t(n32) * 4;
   if (!hip_ok(hipMemcpyAsync(dev, pinned, bytes, hipMemcpyHostToDevice, stream), "hipMemcpyAsync")) return nullptr;
   if (!hip_ok(hipEventRecord(event, stream), "hipEventRecord")) return nullptr;
+  if (nflags > 0) clear_flags(flags, nflags);
   if (exec != nullptr && !hip_ok(hipGraphLaunch(exec, stream), "hipGraphLaunch")) return nullptr;
   Py_RETURN_NONE;
+}
+
+// host_alloc(nbytes) -> (host address, device address) of mapped, coherent
+// pinned memory, every byte 0xff (flags read -1)
+PyObject* host_alloc(PyObject*, PyObject* arg) {
+  const size_t n = PyLong_AsSize_t(arg);
+  if (PyErr_Occurred()) return nullptr;
+  void* h = nullptr;
+  if (!hip_ok(hipHostMalloc(&h, n ? n : 1, hipHostMallocMapped | hipHostMallocCoherent), "hipHostMalloc"))
+    return nullptr;
+  void* d = nullptr;
+  if (!hip_ok(hipHostGetDevicePointer(&d, h, 0), "hipHostGetDevicePointer")) {
+    (void)hipHostFree(h);
+    return nullptr;
+  }
+  std::memset(h, 0xff, n);
+  return Py_BuildValue("(NN)", PyLong_FromVoidPtr(h), PyLong_FromVoidPtr(d));
+}
+
+PyObject* host_free(PyObject*, PyObject* arg) {
+  void* h = as_ptr(arg);
+  if (PyErr_Occurred()) return nullptr;
+  if (h != nullptr && !hip_ok(hipHostFree(h), "hipHostFree")) return nullptr;
+  Py_RETURN_NONE;
+}
+
+// clear_flags(host address, n): every flag -1 (for launches made without `launch`)
+PyObject* clear_flags_py(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
+  if (nargs != 2) {
+    PyErr_SetString(PyExc_TypeError, "clear_flags takes 2 arguments");
+    return nullptr;
+  }
+  void* f = as_ptr(args[0]);
+  const long long n = PyLong_AsLongLong(args[1]);
+  if (PyErr_Occurred()) return nullptr;
+  if (f == nullptr || n < 0) {
+    PyErr_SetString(PyExc_ValueError, "clear_flags: bad flag buffer");
+    return nullptr;
+  }
+  clear_flags(f, n);
+  Py_RETURN_NONE;
+}
+
+// wait_flags(host address, n, timeout_s) -> [bool] * n once every flag is
+// written (>= 0), or None after timeout_s seconds (the GIL is released while
+// polling)
+PyObject* wait_flags(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
+  if (nargs != 3) {
+    PyErr_SetString(PyExc_TypeError, "wait_flags takes 3 arguments");
+    return nullptr;
+  }
+  const volatile int32_t* f = static_cast<const volatile int32_t*>(as_ptr(args[0]));
+  const long long n = PyLong_AsLongLong(args[1]);
+  const double timeout = PyFloat_AsDouble(args[2]);
+  if (PyErr_Occurred()) return nullptr;
+  if (f == nullptr || n < 0) {
+    PyErr_SetString(PyExc_ValueError, "wait_flags: bad flag buffer");
+    return nullptr;
+  }
+  bool done = false;
+  Py_BEGIN_ALLOW_THREADS
+  const auto t0 = std::chrono::steady_clock::now();
+  for (long long spin = 0;; ++spin) {
+    long long i = 0;
+    while (i < n && f[i] >= 0) ++i;
+    if (i == n) {
+      done = true;
+      break;
+    }
+    if ((spin & 255) == 0 &&
+        std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() >= timeout)
+      break;
+    __builtin_ia32_pause();
+  }
+  Py_END_ALLOW_THREADS
+  std::atomic_thread_fence(std::memory_order_acquire);
+  if (!done) Py_RETURN_NONE;
+  PyObject* out = PyList_New(n);
+  if (out == nullptr) return nullptr;
+  for (long long i = 0; i < n; ++i) {
+    PyObject* b = f[i] ? Py_True : Py_False;
+    Py_INCREF(b);
+    PyList_SET_ITEM(out, i, b);
+  }
+  return out;
 }
 
 // event_create(device) -> handle of a timing-free event on that device
@@ -361,6 +469,12 @@ PyMethodDef kMethods[] = {
      "Validate one pass's rows and write its row tables; returns (nb, n32, n64, grouped, kv_max, position_sum)."},
     {"launch", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(launch)), METH_FASTCALL,
      "Upload a tick's tables through a pinned buffer and launch its graph."},
+    {"host_alloc", host_alloc, METH_O, "Mapped, coherent pinned host memory: (host address, device address)."},
+    {"host_free", host_free, METH_O, "Free memory from host_alloc."},
+    {"clear_flags", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(clear_flags_py)), METH_FASTCALL,
+     "Set n int32 accept flags to -1."},
+    {"wait_flags", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(wait_flags)), METH_FASTCALL,
+     "Poll n int32 accept flags until all are written; [bool] or None on timeout."},
     {"event_create", event_create, METH_O, "A timing-free HIP event on the given device."},
     {"event_destroy", event_destroy, METH_O, "Wait for and destroy an event made by event_create."},
     {nullptr, nullptr, 0, nullptr}};

@@ -109,13 +109,15 @@ class _Captured:
         self.graph: torch.cuda.CUDAGraph | None = None
         self.exec = 0  # the graph's executable (raw handle) once captured
 
-    def launch(self, t64: np.ndarray, t32: np.ndarray, stream: int, replay: bool = True) -> None:
+    def launch(self, t64: np.ndarray, t32: np.ndarray, stream: int, replay: bool = True,
+               flags: tuple[int, int] = (0, 0)) -> None:
         """Upload the first n64 / n32 words of the host tables and replay the
-        graph (replay=False: the upload only)."""
+        graph (replay=False: the upload only); flags = (host address, count)
+        of accept flags to clear before the replay."""
         j = self.i
         self.i = (j + 1) % self.DEPTH
         self.tick.launch(self.exec if replay else 0, stream, self.events[j], self.host_ptr[j], self.dev.data_ptr(),
-                         t64, self.n64, t32, self.n32)
+                         t64, self.n64, t32, self.n32, flags[0], flags[1])
 
     def __del__(self):
         for e in getattr(self, "events", ()):
@@ -210,13 +212,13 @@ class LoopedModel:
         self.sc = self._scratch(self.max_rows)
         self.sc["logits"] = torch.empty(self.max_rows, cfg.vocab_size, dtype=torch.float32, device=self.device)
         self.sc["ids"] = torch.empty(self.max_rows, dtype=torch.int64, device=self.device)
-        self.sc["accept"] = torch.zeros(self.max_rows, dtype=torch.int32, device=self.device)
         self.attn_ws = torch.zeros(ops.attn_workspace_bytes(self.max_rows, cfg.n_heads, cfg.head_dim, max_seq_len),
                                    dtype=torch.uint8, device=self.device)
         self.staging = _Staging(self.device)
         self._graphs: dict[tuple, _Captured] = {}
         # the native host side of a tick (row tables, upload, graph launch)
         self._tick = _lib.load_tick()
+        self._flags_host, self._flags_dev = self._tick.host_alloc(4 * self.max_rows)
         self._dev_index = self.device.index if self.device.index is not None else torch.cuda.current_device()
         self._params: dict[tuple, tuple] = {}
         self._bytes_coef: dict[str, tuple[int, int, int]] = {}
@@ -230,7 +232,14 @@ class LoopedModel:
         self.tok_ring = torch.zeros(ring_len + 1, dtype=torch.int64, device=self.device)
         self._ring_next = 0
         self.last_c_handles: list[int] | None = None
-        self.last_accept: torch.Tensor | None = None
+        # greedy verify flags of the last C pass: the argmax kernel stores them
+        # into mapped, coherent pinned host memory, which accept_flags() polls
+        # (no device->host copy behind the graph); -1 until written. Every C
+        # pass's argmax writes them; _flags_pending marks a C launch whose
+        # writes may still be in flight (cleared by a read or a stream wait)
+        self._accept_n = self._accept_nb = 0
+        self._accept_unread = False
+        self._flags_pending = False
         # algorithmic HBM bytes of every pass launched (see pass_bytes)
         self.bytes_moved = 0
 
@@ -396,7 +405,7 @@ class LoopedModel:
                             group_first=gf)
             ops.linear(sc["h"], W["lm_head"], n=nb, out=sc["logits"], out_dtype=torch.float32)
             ops.argmax(sc["logits"], n=nb, out=sc["ids"], ring=self.tok_ring, ring_rows=t32[3 * nb: 4 * nb],
-                       expect=t64[2 * L * nb: 2 * L * nb + nb], accept=sc["accept"])
+                       expect=t64[2 * L * nb: 2 * L * nb + nb], accept_mapped=(self._flags_dev, self.max_rows))
 
     # -- a tick: row tables, upload, launch -------------------------------------------
     def _tick_params(self, cache) -> tuple:
@@ -524,7 +533,7 @@ class LoopedModel:
         kind "P" (extra = token ids or ring handles), "R" (extra = steps) or
         "C" (extra = None, or per row the token expected from its argmax -- a
         plain id, a ring handle, or NO_EXPECT -- for a device-side greedy
-        verify whose flags land in `last_accept`; at most one C, last). A
+        verify whose flags `accept_flags()` returns; at most one C, last). A
         scheduler tick (P, R, C) or a whole sequential token (P, T_total x R,
         C) then costs one replay. Every pass is validated and tabled (natively,
         _tick.plan_pass) before anything launches; the slot-length bookkeeping
@@ -533,7 +542,7 @@ class LoopedModel:
         tick = self._tick
         prm = self._tick_params(cache)
         t32, t64 = self._table_scratch(len(passes))
-        plans, live, n_c, c_base = [], [], 0, -1
+        plans, live, n_c, c_base, c_expect = [], [], 0, -1, False
         o32 = o64 = 0
         last = passes[-1][0] if passes else None
         for kind, seqs, positions, extra in passes:
@@ -552,10 +561,20 @@ class LoopedModel:
             o64 += n64
             if kind == "C":
                 n_c = n
+                c_expect = extra is not None and len(extra) > 0
+        # a C pass with expected tokens clears the flags its argmax will write
+        # (one per row, padding included); if an earlier C launch may still be
+        # writing them (its flags were never read), wait for it first
+        nflags = plans[-1]["nb"] if n_c and c_expect else 0
+        if nflags and self._flags_pending:
+            torch.cuda.current_stream(self.device).synchronize()
+            self._flags_pending = False
         if plans:
             if self.use_graphs:
-                self._captured(cache, plans).launch(t64, t32, self._raw_stream())
+                self._captured(cache, plans).launch(t64, t32, self._raw_stream(), flags=(self._flags_host, nflags))
             else:
+                if nflags:
+                    self._tick.clear_flags(self._flags_host, nflags)
                 d32, d64 = self.staging.upload([t32[:o32], t64[:o64]])
                 self._launch_plans(cache, plans, d32, d64)
         if n_c and c_base >= 0:
@@ -566,9 +585,38 @@ class LoopedModel:
             self._note_writes(cache, kind, seqs, positions, extra)
         if n_c:
             self.last_c_handles = None if c_base < 0 else [-(c_base + i) - 1 for i in range(n_c)]
-            self.last_accept = self.sc["accept"][:n_c]
+            self._accept_n, self._accept_nb = n_c, plans[-1]["nb"]
+            self._accept_unread, self._flags_pending = c_expect, True
             return self.sc["logits"][:n_c], self.sc["ids"][:n_c]
         return None
+
+    def accept_flags(self, timeout_s: float = 30.0) -> list[bool]:
+        """The greedy verify flags of the last C pass (one per C row; False
+        for rows that asked for no comparison): polls the mapped flag buffer
+        until the pass's argmax has written every flag. Only after a C pass
+        that carried expected tokens, once."""
+        if not self._accept_unread:
+            raise RuntimeError("the last C pass carried no expected tokens, or its flags were already read")
+        # every row's flag, padding rows' included: then no workgroup of this
+        # argmax is left to store one after the next pass clears them
+        flags = self._tick.wait_flags(self._flags_host, self._accept_nb, timeout_s)
+        if flags is None:  # still unwritten: wait for the stream, then read once more
+            torch.cuda.current_stream(self.device).synchronize()
+            flags = self._tick.wait_flags(self._flags_host, self._accept_nb, 0.0)
+            if flags is None:
+                raise RuntimeError("the C pass finished without writing its accept flags")
+        self._accept_unread = self._flags_pending = False
+        return flags[: self._accept_n]
+
+    def __del__(self):
+        host = getattr(self, "_flags_host", 0)
+        if host:
+            try:  # no kernel may still write the flags when they are freed
+                torch.cuda.synchronize(self.device)
+                self._tick.host_free(host)
+            except Exception:  # interpreter shutdown: the runtime may be gone
+                pass
+            self._flags_host = 0
 
     def prelude_union(self, cache, seqs, positions, token_ids) -> np.ndarray:
         """Embed + prelude blocks for n new tokens; fills pool[row] = [s0(pos) | e].

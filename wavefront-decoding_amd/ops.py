@@ -526,11 +526,14 @@ def copy_rows(src: torch.Tensor, dst: torch.Tensor, *, n: int, width: int, src_r
 
 def argmax(logits: torch.Tensor, *, n: int | None = None, out: torch.Tensor | None = None,
            ring: torch.Tensor | None = None, ring_rows: torch.Tensor | None = None,
-           expect: torch.Tensor | None = None, accept: torch.Tensor | None = None) -> torch.Tensor:
+           expect: torch.Tensor | None = None, accept: torch.Tensor | None = None,
+           accept_mapped: tuple[int, int] | None = None) -> torch.Tensor:
     """out[i] = argmax logits[i] (first index on ties); with `ring`, also
     ring[ring_rows[i]] = out[i]; with `expect` (int64: a plain id, a ring
     handle, or anything below -len(ring) for no comparison) also
-    accept[i] = int32(out[i] == expected token)."""
+    accept[i] = int32(out[i] == expected token). The flags go to `accept` (a
+    device tensor) or to `accept_mapped` = (device address, capacity in
+    flags) of mapped pinned host memory, which the host polls without a copy."""
     _need_cuda(logits, out, ring, ring_rows, expect, accept)
     _need(logits.dtype == torch.float32 and logits.dim() == 2 and logits.stride(1) == 1, "logits: float32 (n, V)")
     n = logits.shape[0] if n is None else n
@@ -542,12 +545,19 @@ def argmax(logits: torch.Tensor, *, n: int | None = None, out: torch.Tensor | No
     if out is None:
         out = torch.empty(n, dtype=torch.int64, device=logits.device)
     _need(out.dtype == torch.int64 and out.is_contiguous() and out.numel() >= n, "out: int64 (>= n,)")
-    _need((expect is None) == (accept is None), "expect and accept go together")
+    _need(accept is None or accept_mapped is None, "accept or accept_mapped, not both")
+    _need((expect is None) == (accept is None and accept_mapped is None), "expect and accept go together")
     if expect is not None:
         _need(expect.dtype == torch.int64 and expect.is_contiguous() and expect.numel() >= n, "expect: int64 (>= n,)")
-        _need(accept.dtype == torch.int32 and accept.is_contiguous() and accept.numel() >= n, "accept: int32 (>= n,)")
+        if accept is not None:
+            _need(accept.dtype == torch.int32 and accept.is_contiguous() and accept.numel() >= n,
+                  "accept: int32 (>= n,)")
+        else:
+            _need(accept_mapped[0] != 0 and accept_mapped[0] % 4 == 0 and accept_mapped[1] >= n,
+                  "accept_mapped: (aligned device address, capacity >= n)")
+    acc = _p(accept) if accept is not None else (accept_mapped[0] if accept_mapped is not None else None)
     rc = _lib.load().wfd_argmax(logits.data_ptr(), logits.stride(0), out.data_ptr(), _p(ring), _p(ring_rows),
-                                ring.numel() if ring is not None else 0, _p(expect), _p(accept), n, logits.shape[1],
+                                ring.numel() if ring is not None else 0, _p(expect), acc, n, logits.shape[1],
                                 _stream())
     _lib.check(rc, "wfd_argmax")
     return out
