@@ -313,7 +313,7 @@ class LoopedBlocksBatch:
         coda_argmax_union would do. Returns the C pass's ids (or handles).
         `expect` (C rows, each a plain id, a ring handle or None): the C pass
         also compares every row's argmax with it on the device, and
-        `last_accept` receives the flags (one device->host read for the tick)."""
+        `last_accept` receives the flags (polled from mapped host memory, no copy)."""
         eng, R = [], self.model.R
         for kind, seq_ids, toks in passes:
             if not toks:
