@@ -409,8 +409,9 @@ class LoopedModel:
 
     # -- a tick: row tables, upload, launch -------------------------------------------
     def _tick_params(self, cache) -> tuple:
-        """The constants _tick.plan_pass reads (one tuple per cache shape)."""
-        key = (cache.B, cache.S, cache.trash_row)
+        """The constants _tick.plan_pass reads (one tuple per cache shape and
+        grouping setting)."""
+        key = (cache.B, cache.S, cache.trash_row, self.use_graphs, self.group_attention, self.group_min_workgroups)
         prm = self._params.get(key)
         if prm is None:
             c = self.cfg
