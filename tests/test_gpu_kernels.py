@@ -231,9 +231,9 @@ def test_linear_row_invariant(gpu, dtype, N):
     """Row m of y is bit-identical for every batch size and position in the
     batch, whichever kernel a row count selects. N = 24, 256, 257 and 705
     column tiles: at 300 rows, the LDS-pipelined stream kernel with 1 and 2
-    tiles per workgroup, then weights shared through LDS 4 tiles per
-    workgroup (2 at 33-65 rows; both with a ragged tail); gathered rows at 3
-    and 40 rows; x
+    tiles per workgroup, then weights shared through LDS 2 or 4 tiles per
+    workgroup (2 at 33-64 rows for 257 tiles; both with a ragged tail);
+    gathered rows at 3 and 40 rows; x
     read at a row pitch of K + 64 bytes (the engine's activation buffers)."""
     g = torch.Generator().manual_seed(5)
     K = 2048
@@ -266,7 +266,8 @@ def test_linear_row_invariant(gpu, dtype, N):
 def test_linear_split_k_same_bits(gpu, dtype, N, K):
     """Split-K projections: the slice sums of linear_partials, added in slice
     order in fp32 and rounded, equal the one-launch linear bit for bit (1 to 4
-    slices: K = 128 .. 5632), over contiguous and gathered rows; the norm that
+    slices: K = 128 .. 5632; 2, 4 and 8 tiles per workgroup: 8 at 200 rows of
+    2048 columns), over contiguous and gathered rows; the norm that
     reduces them (add_rmsnorm_split) equals linear + add_rmsnorm, including
     the kept linear rows (a_out), and matches the oracle."""
     if K % ops.linear_k_multiple(dtype):
@@ -284,7 +285,7 @@ def test_linear_split_k_same_bits(gpu, dtype, N, K):
     P = K // ops.linear_k_multiple(dtype)
     assert S == -(-P // -(-P // 4))  # ceil(P / Q) slices of Q = ceil(P / 4) chunks
     norm_ok = N % ops.linear_k_multiple(dtype) == 0
-    for n, rows in ((1, None), (17, None), (64, None), (113, None), (300, None),
+    for n, rows in ((1, None), (17, None), (64, None), (113, None), (200, None), (300, None),
                     (40, torch.randperm(300, generator=g)[:40].to(torch.int32).to(gpu))):
         y = ops.linear(X, W, n=n, x_rows=rows)
         assert ops.linear_partials(X, W, part, n=n, x_rows=rows) == S

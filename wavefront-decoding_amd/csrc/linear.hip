@@ -527,6 +527,31 @@ __host__ __device__ constexpr int xcd_grid(int rb, int groups) {
   return rb * ((groups + kXcds - 1) / kXcds) * kXcds;
 }
 
+// Tiles per workgroup of a slice launch (2, 4 or 8; S = K slices in grid y).
+// Each workgroup moves 64 rows x 128 K of x (16 KB) and BT x 4 KB of weights
+// per chunk, and the XCD-aware grid spreads the workgroups evenly over the 8
+// XCDs of 32 CUs, so the busiest CU streams ceil(workgroups / 256) of them:
+// the choice minimizes that product (ties: fewer tiles); 8 tiles only above
+// 32 rows, where at least three of the four waves carry rows. The 2048-column
+// projections' slice launches at 192-512 rows: 5-12 % faster than with at
+// most 4 tiles (in the bs=32 decode, 15.0 -> 14.3 us at 192 rows).
+constexpr int kCusPerXcd = 32;
+
+static int gemm_tiles_per_workgroup(int n, int rb, int tiles, int S) {
+  int best = 2;
+  long best_cost = -1;
+  for (int bt = 2; bt <= (n > 32 ? 8 : 4); bt *= 2) {
+    const long wgs = (long)xcd_grid(rb, (tiles + bt - 1) / bt) * S;
+    const long per_cu = ((wgs + kXcds - 1) / kXcds + kCusPerXcd - 1) / kCusPerXcd;
+    const long cost = per_cu * (16 + 4 * bt);
+    if (best_cost < 0 || cost < best_cost) {
+      best_cost = cost;
+      best = bt;
+    }
+  }
+  return best;
+}
+
 template <int BT>
 __device__ __forceinline__ bool xcd_block(int n, int tiles, int& rbk, int& tg) {
   const int R = (n + 63) / 64;
@@ -885,9 +910,15 @@ static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const v
       return;
     }
     // weights through LDS, shared by the 4 waves: 4 tiles per workgroup
-    // while that still leaves >= 256 workgroups, else 2 (lm_head at 64 rows:
-    // 500 four-tile workgroups 34 us, 1000 two-tile ones 42 us)
-    if (rb * ((tiles + 3) / 4) >= 256)
+    // while that still leaves >= 256 workgroups (128 for the epilogues
+    // without the RoPE operand tables), else 2. lm_head at 64 rows: 500
+    // four-tile workgroups 34 us, 1000 two-tile ones 42 us; gate|up at 64
+    // rows: 176 four-tile ones 16.4 us, 352 two-tile ones 17.8 us (in the
+    // bs=32 decode); Wqkv + RoPE at 128 rows keeps 2 (192 four-tile
+    // workgroups: 21.1 -> 24.5 us, the epilogue's tables cost registers per
+    // tile). Eight tiles per workgroup were slower in the decode for every
+    // one-launch shape (Wqkv + RoPE at 192 rows 28 -> 48 us).
+    if (rb * ((tiles + 3) / 4) >= (EPI == kEpiRope ? 256 : 128))
       hipLaunchKernelGGL((linear_gemm_kernel<T, TO, EPI, 4, false>), dim3(xcd_grid(rb, (tiles + 3) / 4)), dim3(256), 0,
                          st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra, nullptr);
     else
@@ -896,11 +927,10 @@ static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const v
   }
 }
 
-// The slice form: grid (xcd-mapped row blocks x tile groups, slices). Four
-// tiles per workgroup while that leaves >= 256 workgroups, else two: each
-// workgroup then reads its 64 rows of x once for 64 (or 32) output columns
-// and only its slice of K, where the stream kernel reads them for 16 columns
-// and all of K.
+// The slice form: grid (xcd-mapped row blocks x tile groups, slices), 2, 4
+// or 8 tiles per workgroup as for the one-launch gemm: each workgroup reads
+// its 64 rows of x once for 32-128 output columns and only its slice of K,
+// where the stream kernel reads them for 16 columns and all of K.
 template <typename T>
 static void launch_linear_partials(const void* x, const int32_t* xr, int64_t ldx, const void* W, float* part, int n,
                                    int N, int K, hipStream_t st) {
@@ -909,12 +939,17 @@ static void launch_linear_partials(const void* x, const int32_t* xr, int64_t ldx
   const int S = slice_count(P);
   const int rb = (n + 63) / 64;
   const RopeArgs ra{};
-  if (rb * ((tiles + 3) / 4) * S >= 256)
-    hipLaunchKernelGGL((linear_gemm_kernel<T, T, kEpiPlain, 4, true>), dim3(xcd_grid(rb, (tiles + 3) / 4), S),
-                       dim3(256), 0, st, (const T*)x, xr, ldx, (const T*)W, (T*)nullptr, 0, n, K, 0, tiles, ra, part);
+  const int bt = gemm_tiles_per_workgroup(n, rb, tiles, S);
+#define WFD_GEMM_PART(BTV)                                                                                          \
+  hipLaunchKernelGGL((linear_gemm_kernel<T, T, kEpiPlain, BTV, true>), dim3(xcd_grid(rb, (tiles + BTV - 1) / BTV), S), \
+                     dim3(256), 0, st, (const T*)x, xr, ldx, (const T*)W, (T*)nullptr, 0, n, K, 0, tiles, ra, part)
+  if (bt == 8)
+    WFD_GEMM_PART(8);
+  else if (bt == 4)
+    WFD_GEMM_PART(4);
   else
-    hipLaunchKernelGGL((linear_gemm_kernel<T, T, kEpiPlain, 2, true>), dim3(xcd_grid(rb, (tiles + 1) / 2), S),
-                       dim3(256), 0, st, (const T*)x, xr, ldx, (const T*)W, (T*)nullptr, 0, n, K, 0, tiles, ra, part);
+    WFD_GEMM_PART(2);
+#undef WFD_GEMM_PART
 }
 
 }  // namespace wfd
