@@ -160,6 +160,34 @@ def test_bf16_wfd_is_lossless(gpu, cfg):
         assert toks == ar, T_draft
 
 
+@pytest.mark.parametrize("graphs", [True, False])
+def test_greedy_flags_after_runs_that_never_read_them(gpu, graphs):
+    """The C passes' accept flags land in mapped host memory that every C
+    launch rewrites. Runs that never read them (emulated acceptance,
+    sequential decode) leave launches in flight; a greedy run on the same
+    engine right after must still see its own flags: its tokens equal
+    sequential decode's, and equal a greedy run on a fresh engine, with the
+    same counters."""
+    cfg = MINI_BF16
+    w = M.init_weights(cfg, 0)
+    P = [_prompt(60, 11, V=cfg.vocab_size), _prompt(45, 12, V=cfg.vocab_size)]
+    pol = SsdPolicy(cfg.T_total, 2)
+
+    def greedy(bb):
+        bt = generate_wavefront_batch(bb, [p.to(gpu) for p in P], [20, 16], pol)
+        return [t.tokens for t in bt.per_seq], [t.counters() for t in bt.per_seq]
+
+    print(f"[flags after unread runs] graphs={graphs}", flush=True)
+    fresh = greedy(LoopedBlocksBatch(LoopedModel(cfg, w, gpu, max_seq_len=128, max_batch=2, use_graphs=graphs), 2))
+    bb = LoopedBlocksBatch(LoopedModel(cfg, w, gpu, max_seq_len=128, max_batch=2, use_graphs=graphs), 2)
+    emus = [EmulatedAcceptance(0.8, 7000 + b) for b in range(2)]
+    generate_wavefront_batch(bb, [p.to(gpu) for p in P], [20, 16], pol, emus)  # flags written, never read
+    seq = ar_generate_batch(bb, [p.to(gpu) for p in P], [20, 16])           # and again
+    after = greedy(bb)
+    assert after == fresh
+    assert after[0] == [t.tokens for t in seq.per_seq]
+
+
 def test_rollback_reappend_reproduces_committed_cache_rows(gpu):
     """Slot-cache append and rollback: greedy WFD on random-init weights
     rejects almost every draft, so rows of rejected tokens are dropped and

@@ -279,3 +279,34 @@ def test_accept_flag_polling(tick):
         tick.wait_flags(0, 2, 0.0)
     with pytest.raises(ValueError):
         tick.clear_flags(f.ctypes.data, -1)
+
+
+def test_note_writes_matches_note_write():
+    """The slot-length bookkeeping of a pass (BatchStaticKVCache.note_writes)
+    extends exactly the lengths a note_write per (slot, row) would."""
+    import torch
+
+    from wavefront_decoding_amd.kv_cache import BatchStaticKVCache
+
+    rng = np.random.default_rng(4)
+    a = BatchStaticKVCache(20, 3, 1, 8, 64, torch.float32, "cpu")
+    b = BatchStaticKVCache(20, 3, 1, 8, 64, torch.float32, "cpu")
+    for _ in range(200):
+        n = int(rng.integers(1, 6))
+        seqs, pos = rng.integers(0, 3, n), rng.integers(0, 64, n)
+        nsl = int(rng.integers(1, 5))
+        if rng.random() < 0.5:
+            first = int(rng.integers(0, 20 - nsl + 1))
+            a.note_writes(first, nsl, seqs, pos)
+            firsts = [first] * n
+        else:
+            firsts = [int(f) for f in rng.integers(0, 20 - nsl + 1, n)]
+            a.note_writes(firsts, nsl, seqs.tolist(), pos.tolist())
+        for f, sq, p in zip(firsts, seqs, pos):
+            for sl in range(f, f + nsl):
+                b.note_write(sl, int(sq), int(p))
+        if rng.random() < 0.1:
+            bq, at = int(rng.integers(0, 3)), int(rng.integers(0, 64))
+            a.drop_positions_at_and_after(bq, at)
+            b.drop_positions_at_and_after(bq, at)
+        assert a.seqlen == b.seqlen
