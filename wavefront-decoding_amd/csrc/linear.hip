@@ -470,6 +470,11 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ 
     wtile[b] = W + packed_off<T>(gok[b] ? g : 0, 0, P, 0);
   }
 
+  // the RoPE epilogue's table operands are fetched at launch, so the tail
+  // after the last MFMA waits on no dependent loads
+  RopePre rp[NB][4];
+  gather_rope<EPI, NB>(rp, ra, row0 + 4 * grp, n, blockIdx.y * NB, tiles, col);
+
   // two-stage register pipeline; every load is unconditional (the stage past
   // the last chunk re-reads chunk P-1 and is never used)
   SliceWalk walk(P, 0);
@@ -494,8 +499,6 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ 
     chunk_mma<T, NB>(acc, xb, wb);
     add(acc, p + 1);
   }
-  RopePre rp[NB][4];
-  gather_rope<EPI, NB>(rp, ra, row0 + 4 * grp, n, blockIdx.y * NB, tiles, col);
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
     if (!gok[b]) continue;  // uniform over the workgroup
@@ -620,6 +623,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
 #pragma unroll
     for (int i = 0; i < FPW; ++i) wl[b][wave * FPW + i][lane] = wr[i];
   };
+  // with at most 2 tiles the RoPE epilogue's table operands are fetched at
+  // launch (the tail then waits on no dependent loads); with 4 their registers
+  // would cost the main loop occupancy, so they are fetched after it
+  constexpr bool kRopeEarly = BT <= 2;
+  RopePre rp[BT][4];
+  if constexpr (kRopeEarly) gather_rope<EPI, BT>(rp, ra, row0 + 4 * grp, n, tg * BT, tiles, col);
   SliceWalk walk(P, pb);
   f32x4 tot[BT], sl[BT], sub[BT];
 #pragma unroll
@@ -689,8 +698,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
     }
     return;
   }
-  RopePre rp[BT][4];
-  gather_rope<EPI, BT>(rp, ra, row0 + 4 * grp, n, tg * BT, tiles, col);
+  if constexpr (!kRopeEarly) gather_rope<EPI, BT>(rp, ra, row0 + 4 * grp, n, tg * BT, tiles, col);
 #pragma unroll
   for (int t = 0; t < BT; ++t) {
     const int g = tg * BT + t;
