@@ -305,7 +305,9 @@ class LoopedBlocksBatch:
     # the next position on the device (wfd_argmax's accept flags)
     device_accept = True
 
-    @torch.no_grad()
+    # no torch.no_grad() wrapper here: it costs ~5 us per call, once per tick,
+    # and the engine creates no autograd state (weights and tables never
+    # require grad); the schedulers run inside their own no-grad context
     def run_passes(self, passes, cache, lazy: bool = False, expect=None) -> list[int] | None:
         """A tick's passes -- [(kind, seq_ids, toks)] with kind "P", "R" or "C"
         (C last) -- as one launch sequence (one graph replay, one table upload),
