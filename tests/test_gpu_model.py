@@ -188,6 +188,37 @@ def test_greedy_flags_after_runs_that_never_read_them(gpu, graphs):
     assert after[0] == [t.tokens for t in seq.per_seq]
 
 
+@pytest.mark.parametrize("graphs", [True, False])
+def test_token_ring_exhaustion_falls_back_to_ids(gpu, graphs):
+    """A token ring too small for a generation: once it is full, C passes
+    return plain ids (their argmax lands in the trash slot) and the greedy
+    verify compares against a mix of handles and ids; tokens and counters
+    equal those of a run whose ring never fills."""
+    cfg = MINI_BF16
+    w = M.init_weights(cfg, 0)
+    P = [_prompt(50, 21, V=cfg.vocab_size), _prompt(37, 22, V=cfg.vocab_size)]
+    pol = SsdPolicy(cfg.T_total, 2)
+    out = []
+    for ring_len in (1 << 20, 9):
+        print(f"[token ring] graphs={graphs} ring_len={ring_len}", flush=True)
+        m = LoopedModel(cfg, w, gpu, max_seq_len=128, max_batch=2, use_graphs=graphs, ring_len=ring_len)
+        full = []
+        run = m.run_passes
+
+        def counted(cache, passes):
+            res = run(cache, passes)
+            if any(k == "C" and len(pos) for k, _, pos, _ in passes):
+                full.append(m.last_c_handles is None)
+            return res
+
+        m.run_passes = counted
+        bt = generate_wavefront_batch(LoopedBlocksBatch(m, 2), [p.to(gpu) for p in P], [18, 14], pol)
+        out.append(([t.tokens for t in bt.per_seq], [t.counters() for t in bt.per_seq], bt.n_r_calls))
+        # the large ring never fills; the small one fills and C passes fall back to ids
+        assert any(full) == (ring_len == 9) and not all(full)
+    assert out[0] == out[1]
+
+
 def test_rollback_reappend_reproduces_committed_cache_rows(gpu):
     """Slot-cache append and rollback: greedy WFD on random-init weights
     rejects almost every draft, so rows of rejected tokens are dropped and
