@@ -22,9 +22,9 @@ lossless here.
 
 hipGraph mode (use_graphs=True): each (pass, row bucket, cache) gets one
 captured launch sequence over fixed scratch and fixed table buffers; a call
-pads its rows to the bucket (power of two) with rows that point at the
-cache's trash row and the pool's trash row, refreshes the tables with one
-host->device copy, and replays. The grid bound for attention is the cache
+pads its rows to the bucket (a power of two up to 64, then a multiple of 64)
+with rows that point at the cache's trash row and the pool's trash row,
+refreshes the tables with one host->device copy, and replays. The grid bound for attention is the cache
 length, so one graph serves every position, depth mix and rollback.
 
 Wave-state pool: row of (seq b, position p) = b*R + p % R with
