@@ -48,6 +48,11 @@
 // So y[m] is bit-identical whatever n is and wherever row m sits -- the
 // property that keeps wavefront decode token-identical to sequential decode.
 //
+// x operand: every kernel but the 8-tile slice form reads a 16-row block's
+// chunk with coalesced loads of whole 256-byte row segments and turns them
+// into MFMA fragments through the wave's LDS (xc_offsets below): a fragment
+// load would touch 16 rows x 64 bytes per instruction.
+//
 // Weight layout ("packed", made once by wfd_linear_pack): W is stored in MFMA
 // fragment order, tile by tile -- for tile g, chunk p, step s the 64 lanes'
 // 16-byte B fragments sit back to back, so every weight load instruction of a
@@ -313,6 +318,74 @@ __device__ __forceinline__ uint32_t x_offset(const int32_t* __restrict__ x_rows,
   return col < m ? (uint32_t)(((int64_t)r * ldx + grp * Chunk<T>::V) * sizeof(T)) : kBufInvalid;
 }
 
+// Coalesced x operand. An MFMA A fragment gives lane l row l % 16 and the
+// 16-byte piece 4 s + l / 16 of that row's 256-byte chunk segment at step s,
+// so a fragment load touches 16 rows x 64 bytes per instruction, which the
+// memory pipeline serves at less than half the rate of whole segments (an
+// L2-resident probe: ~55 against ~125 GB/s per CU). Instead a 16-row block's
+// chunk is read as 4 loads of 4 whole segments -- load s: row r = 4 s + l / 16,
+// piece (l % 16) ^ r -- stored to the wave's 4 KB of LDS as loaded (unit
+// 64 s + l), and read back as fragments: lane l at step s reads unit
+// 16 r' + ((4 s + l / 16) ^ r'), r' = l % 16, which holds row r', piece
+// 4 s + l / 16. The XOR spreads both the stores and the fragment reads over
+// all LDS banks. The fragments carry the same values in the same lanes as a
+// direct fragment load, so the MFMAs and every bit of the result are the same.
+constexpr int kXcUnits = 16 * 16;  // 16-byte units of a wave's LDS block: 16 rows x 16 pieces
+
+// Byte offsets (chunk 0) of lane `lane`'s 4 coalesced loads for the 16-row
+// block at `base` (kBufInvalid for rows at or past n: zeros, no traffic).
+// Rows come from x_rows[base + r] when given, read with uniform scalar loads.
+template <typename T>
+__device__ __forceinline__ void xc_offsets(uint32_t (&off)[kChunkSteps], const int32_t* __restrict__ x_rows,
+                                           int64_t ldx, int base, int lane, int n) {
+  const int m = n - base < 16 ? n - base : 16;
+  int rv[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) rv[j] = base + j;
+  if (x_rows && m > 0) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) rv[j] = x_rows[base + (j < m ? j : 0)];
+  }
+#pragma unroll
+  for (int s = 0; s < kChunkSteps; ++s) {
+    const int r = 4 * s + (lane >> 4);
+    int row = rv[0];
+#pragma unroll
+    for (int j = 1; j < 16; ++j) row = r == j ? rv[j] : row;
+    const int q = (lane & 15) ^ r;
+    off[s] = r < m ? (uint32_t)(((int64_t)row * ldx + q * Chunk<T>::V) * sizeof(T)) : kBufInvalid;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void load_xc(u32x4 (&xc)[kChunkSteps], __amdgpu_buffer_rsrc_t xr,
+                                        const uint32_t (&off)[kChunkSteps], int p) {
+  const uint32_t co = (uint32_t)(p * Chunk<T>::KC * sizeof(T));  // kBufInvalid + co stays out of range
+#pragma unroll
+  for (int s = 0; s < kChunkSteps; ++s) xc[s] = buf_ld16(xr, off[s] + co);
+}
+
+// Other lanes read what a lane stored: keep the compiler from moving LDS
+// accesses across this point (the LDS executes one wave's accesses in order).
+__device__ __forceinline__ void lds_order() { asm volatile("" ::: "memory"); }
+
+__device__ __forceinline__ void xc_store(u32x4* __restrict__ xl, const u32x4 (&xc)[kChunkSteps], int lane) {
+  lds_order();  // after the previous chunk's fragment reads
+#pragma unroll
+  for (int s = 0; s < kChunkSteps; ++s) xl[64 * s + lane] = xc[s];
+  lds_order();  // before this chunk's fragment reads
+}
+
+__device__ __forceinline__ u32x4 xc_frag(const u32x4* __restrict__ xl, int st, int lane) {
+  const int r = lane & 15;
+  return xl[16 * r + ((4 * st + (lane >> 4)) ^ r)];
+}
+
+__device__ __forceinline__ void xc_frags(u32x4 (&xf)[kChunkSteps], const u32x4* __restrict__ xl, int lane) {
+#pragma unroll
+  for (int st = 0; st < kChunkSteps; ++st) xf[st] = xc_frag(xl, st, lane);
+}
+
 template <typename T, int NT>
 __device__ __forceinline__ void chunk_mma(f32x4 (&acc)[NT], const u32x4 (&xf)[kChunkSteps],
                                           const u32x4 (&wf)[NT][kChunkSteps]) {
@@ -343,6 +416,7 @@ __global__ __launch_bounds__(64 * WW) void linear_wide_kernel(
   constexpr int KPW = kSlices * kSubSlices / WW;  // sub-slices per wave
   static_assert(KPW * WW == kSlices * kSubSlices, "16 or 8 waves");
   __shared__ f32x4 red[kSlices * kSubSlices][64];  // sub-slice sums [sub-slice][lane]
+  __shared__ __align__(16) u32x4 xl[WW][kXcUnits];  // each wave's x chunk (coalesced load -> fragments)
   constexpr int V = LinTraits<T>::V;
   const int P = K / LinTraits<T>::KC;
   const int Q = slice_chunks(P);
@@ -352,9 +426,9 @@ __global__ __launch_bounds__(64 * WW) void linear_wide_kernel(
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int col = lane & 15;
-  const int grp = lane >> 4;
 
-  const uint32_t xoff = x_offset<T>(x_rows, ldx, 0, col, grp, n);
+  uint32_t xoff[kChunkSteps];
+  xc_offsets<T>(xoff, x_rows, ldx, 0, lane, n);
   const __amdgpu_buffer_rsrc_t xrs = buf_rsrc(x);
   const T* const wtile[1] = {W + packed_off<T>(g, 0, P, 0)};
   const __amdgpu_buffer_rsrc_t wrs = buf_rsrc(wtile[0]);
@@ -398,7 +472,7 @@ __global__ __launch_bounds__(64 * WW) void linear_wide_kernel(
       } else {
         load_w<T, 1>(wf[i][j], wtile, P, pc, lane);
       }
-      load_x<T>(xf[i][j], xrs, xoff, pc);
+      load_xc<T>(xf[i][j], xrs, xoff, pc);
     }
 #pragma unroll
   for (int i = 0; i < KPW; ++i) {
@@ -406,8 +480,12 @@ __global__ __launch_bounds__(64 * WW) void linear_wide_kernel(
 #pragma unroll
     for (int j = 0; j < RM; ++j) {
       if (c0[i] + j < c1[i]) {  // uniform
+        // the chunk's x fragments through the wave's LDS block
+        u32x4 xa[kChunkSteps];
+        xc_store(xl[wave], xf[i][j], lane);
+        xc_frags(xa, xl[wave], lane);
         f32x4 acc[1];
-        chunk_mma<T, 1>(acc, xf[i][j], wf[i][j]);
+        chunk_mma<T, 1>(acc, xa, wf[i][j]);
 #pragma unroll
         for (int r = 0; r < 4; ++r) sub[r] += acc[0][r];
       }
@@ -450,7 +528,6 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ 
                                                           int64_t ldx, const T* __restrict__ W, TO* __restrict__ y,
                                                           int64_t ldy, int n, int K, int pair_off, int tiles,
                                                           const RopeArgs ra) {
-  constexpr int V = LinTraits<T>::V;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int col = lane & 15;
@@ -458,7 +535,9 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ 
   const int row0 = (blockIdx.x * 4 + wave) * 16;
   if (row0 >= n) return;  // no barriers in this kernel
   const int P = K / LinTraits<T>::KC;
-  const uint32_t xoff = x_offset<T>(x_rows, ldx, row0, col, grp, n);
+  __shared__ __align__(16) u32x4 xl[4][kXcUnits];  // each wave's x chunk (coalesced load -> fragments)
+  uint32_t xoff[kChunkSteps];
+  xc_offsets<T>(xoff, x_rows, ldx, row0, lane, n);
   const __amdgpu_buffer_rsrc_t xrs = buf_rsrc(x);
 
   const T* wtile[NB];
@@ -483,20 +562,27 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ 
   for (int c = 0; c < NB; ++c) tot[c] = sl[c] = sub[c] = f32x4{0.f, 0.f, 0.f, 0.f};
   auto add = [&](const f32x4 (&acc)[NB], int p) { contract_add<NB>(sub, sl, tot, acc, walk.end(p)); };
   u32x4 wa[NB][kChunkSteps], wb[NB][kChunkSteps], xa[kChunkSteps], xb[kChunkSteps];
+  // chunk partials from coalesced x (through the wave's LDS block)
+  auto mma = [&](f32x4 (&acc)[NB], const u32x4 (&xc)[kChunkSteps], const u32x4 (&wr)[NB][kChunkSteps]) {
+    u32x4 xf[kChunkSteps];
+    xc_store(xl[wave], xc, lane);
+    xc_frags(xf, xl[wave], lane);
+    chunk_mma<T, NB>(acc, xf, wr);
+  };
   load_w<T, NB>(wa, wtile, P, 0, lane);
-  load_x<T>(xa, xrs, xoff, 0);
+  load_xc<T>(xa, xrs, xoff, 0);
   for (int p = 0; p < P; p += 2) {
     const int p1 = p + 1 < P ? p + 1 : P - 1;
     load_w<T, NB>(wb, wtile, P, p1, lane);
-    load_x<T>(xb, xrs, xoff, p1);
+    load_xc<T>(xb, xrs, xoff, p1);
     f32x4 acc[NB];
-    chunk_mma<T, NB>(acc, xa, wa);
+    mma(acc, xa, wa);
     add(acc, p);
     if (p + 1 >= P) break;
     const int p2 = p + 2 < P ? p + 2 : P - 1;
     load_w<T, NB>(wa, wtile, P, p2, lane);
-    load_x<T>(xa, xrs, xoff, p2);
-    chunk_mma<T, NB>(acc, xb, wb);
+    load_xc<T>(xa, xrs, xoff, p2);
+    mma(acc, xb, wb);
     add(acc, p + 1);
   }
 #pragma unroll
@@ -586,7 +672,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
   constexpr int V = LinTraits<T>::V;
   constexpr int FR = BT * kChunkSteps;  // 1 KB fragments per chunk: (tile, step)
   constexpr int FPW = FR / 4;           // fragments each wave stages per chunk
+  // x through LDS (coalesced loads) for up to 4 tiles; the 8-tile form runs
+  // one workgroup per CU, which cannot hide the extra LDS round trip, and
+  // loads fragments directly
+  constexpr bool XC = BT <= 4;
   __shared__ __align__(16) u32x4 wl[2][FR][64];
+  __shared__ __align__(16) u32x4 xl[XC ? 4 : 1][XC ? kXcUnits : 1];  // each wave's x chunk
   int rbk, tg;
   if (!xcd_block<BT>(n, tiles, rbk, tg)) return;  // padding workgroup (uniform, before any barrier)
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -601,8 +692,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
   const int pe = PART ? min(P, pb + Q) : P;
   // a wave past the last row still stages weights and meets every barrier;
   // its x loads read zeros and it stores nothing
-  const uint32_t xoff = row0 < n ? x_offset<T>(x_rows, ldx, row0, col, grp, n) : kBufInvalid;
+  uint32_t xoff[kChunkSteps];
+#pragma unroll
+  for (int s = 0; s < kChunkSteps; ++s) xoff[s] = kBufInvalid;
+  if (row0 < n) {
+    if constexpr (XC)
+      xc_offsets<T>(xoff, x_rows, ldx, row0, lane, n);
+    else
+      xoff[0] = x_offset<T>(x_rows, ldx, row0, col, grp, n);
+  }
   const __amdgpu_buffer_rsrc_t xrs = buf_rsrc(x);
+  auto load_xs = [&](u32x4 (&xr)[kChunkSteps], int p) {
+    if constexpr (XC)
+      load_xc<T>(xr, xrs, xoff, p);
+    else
+      load_x<T>(xr, xrs, xoff[0], p);
+  };
 
   // the fragments this wave stages: f = wave * FPW + i -> (tile f / 4, step f % 4)
   const T* wsrc[FPW];
@@ -633,23 +738,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
   f32x4 tot[BT], sl[BT], sub[BT];
 #pragma unroll
   for (int t = 0; t < BT; ++t) tot[t] = sl[t] = sub[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // chunk p from LDS stage b: its partial into the contract's running sums
-  auto mma = [&](const u32x4 (&xf)[kChunkSteps], int b, int p) {
+  // chunk p (coalesced x in xr, through the wave's LDS block; for the 8-tile
+  // form, fragments in xr; weights in LDS stage b): its partial into the
+  // contract's running sums
+  auto mma = [&](const u32x4 (&xr)[kChunkSteps], int b, int p) {
+    if constexpr (XC) xc_store(xl[wave], xr, lane);
+    auto xfrag = [&](int st) { return XC ? xc_frag(xl[wave], st, lane) : xr[st]; };
     f32x4 acc[BT];
 #pragma unroll
     for (int t = 0; t < BT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // step st's BT weight fragments are read from LDS while step st - 1's MFMAs run
-    u32x4 wf[2][BT];
+    // step st's x and weight fragments are read from LDS while step st - 1's MFMAs run
+    u32x4 wf[2][BT], xf[2];
+    xf[0] = xfrag(0);
 #pragma unroll
     for (int t = 0; t < BT; ++t) wf[0][t] = wl[b][t * kChunkSteps][lane];
 #pragma unroll
     for (int st = 0; st < kChunkSteps; ++st) {
       if (st + 1 < kChunkSteps) {
+        xf[(st + 1) & 1] = xfrag(st + 1);
 #pragma unroll
         for (int t = 0; t < BT; ++t) wf[(st + 1) & 1][t] = wl[b][t * kChunkSteps + st + 1][lane];
       }
 #pragma unroll
-      for (int t = 0; t < BT; ++t) acc[t] = mfma_step<T>(xf[st], wf[st & 1][t], acc[t]);
+      for (int t = 0; t < BT; ++t) acc[t] = mfma_step<T>(xf[st & 1], wf[st & 1][t], acc[t]);
     }
     contract_add<BT>(sub, sl, tot, acc, walk.end(p));
   };
@@ -662,22 +773,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
   // the same order so the compiler's wait counts are the steady-state ones.
   u32x4 w0[FPW], w1[FPW], x0[kChunkSteps], x1[kChunkSteps];
   fetch_w(w0, pb);
-  load_x<T>(x0, xrs, xoff, pb);
+  load_xs(x0, pb);
   fetch_w(w1, pb + 1);
-  load_x<T>(x1, xrs, xoff, cl(pb + 1));
+  load_xs(x1, cl(pb + 1));
   stage_w(w0, 0);
   __syncthreads();
   fetch_w(w0, pb + 2);
   for (int p = pb; p + 1 < pe; p += 2) {
     // chunk p: LDS stage 0, x0
     mma(x0, 0, p);
-    load_x<T>(x0, xrs, xoff, cl(p + 2));
+    load_xs(x0, cl(p + 2));
     stage_w(w1, 1);  // chunk p + 1; stage 1 was last read by chunk p - 1, before the previous barrier
     __syncthreads();
     fetch_w(w1, p + 3);
     // chunk p + 1: LDS stage 1, x1
     mma(x1, 1, p + 1);
-    load_x<T>(x1, xrs, xoff, cl(p + 3));
+    load_xs(x1, cl(p + 3));
     stage_w(w0, 0);  // chunk p + 2; stage 0 was last read by chunk p, before the barrier above
     __syncthreads();
     fetch_w(w0, p + 4);
@@ -769,13 +880,34 @@ __device__ __forceinline__ const T* x_row_ptr(const T* __restrict__ x, const int
   return x + (int64_t)r * ldx + grp * Chunk<T>::V;
 }
 
+// The stream kernel's coalesced x sources: a direct-to-LDS load puts lane l's
+// 16 bytes at unit 64 s + l of the wave's block, so load s of lane l reads
+// row r = 4 s + l / 16, piece (l % 16) ^ r -- the layout xc_frag reads.
+// Rows at or past n read the block's first row: they fill fragment rows whose
+// results are never stored.
+template <typename T>
+__device__ __forceinline__ void xc_ptrs(const T* (&src)[kChunkSteps], const T* __restrict__ x,
+                                        const int32_t* __restrict__ x_rows, int64_t ldx, int base, int lane, int n) {
+  const int m = n - base < 16 ? n - base : 16;  // >= 1: the wave has rows
+  int rv[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) rv[j] = x_rows ? x_rows[base + (j < m ? j : 0)] : base + (j < m ? j : 0);
+#pragma unroll
+  for (int s = 0; s < kChunkSteps; ++s) {
+    const int r = 4 * s + (lane >> 4);
+    int row = rv[0];
+#pragma unroll
+    for (int j = 1; j < 16; ++j) row = r == j ? rv[j] : row;
+    src[s] = x + (int64_t)row * ldx + ((lane & 15) ^ r) * Chunk<T>::V;
+  }
+}
+
 template <typename T, typename TO, int EPI, int BT, int NS>
 __global__ __launch_bounds__(256) void linear_stream_kernel(const T* __restrict__ x, const int32_t* __restrict__ x_rows,
                                                             int64_t ldx, const T* __restrict__ W, TO* __restrict__ y,
                                                             int64_t ldy, int n, int K, int pair_off, int tiles,
                                                             const RopeArgs ra) {
   constexpr int V = LinTraits<T>::V;
-  constexpr int KSTEP = LinTraits<T>::KSTEP;
   constexpr int KC = LinTraits<T>::KC;
   constexpr int FR = BT * kChunkSteps;   // weight fragments (tile, step) per chunk, 1 KB each
   constexpr int FPW = BT;                // of which each wave loads FR / 4
@@ -790,7 +922,8 @@ __global__ __launch_bounds__(256) void linear_stream_kernel(const T* __restrict_
   const int row0 = (blockIdx.x * 4 + wave) * 16;
   const bool rows = row0 < n;  // uniform over the wave
   const int P = K / KC;
-  const T* xsrc = rows ? x_row_ptr<T>(x, x_rows, ldx, row0, col, grp, n) : x;
+  const T* xsrc[kChunkSteps] = {x, x, x, x};
+  if (rows) xc_ptrs<T>(xsrc, x, x_rows, ldx, row0, lane, n);
   const T* wsrc[FPW];
 #pragma unroll
   for (int i = 0; i < FPW; ++i) {
@@ -805,7 +938,7 @@ __global__ __launch_bounds__(256) void linear_stream_kernel(const T* __restrict_
     for (int i = 0; i < FPW; ++i) load16_lds(wsrc[i] + p * pstride, &wst[st][wave * FPW + i][0]);
     if (rows) {
 #pragma unroll
-      for (int s = 0; s < kChunkSteps; ++s) load16_lds(xsrc + (int64_t)p * KC + s * KSTEP, &xst[st][wave][s][0]);
+      for (int s = 0; s < kChunkSteps; ++s) load16_lds(xsrc[s] + (int64_t)p * KC, &xst[st][wave][s][0]);
     }
   };
 #pragma unroll
@@ -832,7 +965,7 @@ __global__ __launch_bounds__(256) void linear_stream_kernel(const T* __restrict_
       for (int t = 0; t < BT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < kChunkSteps; ++s) {
-        const u32x4 xf = xst[st][wave][s][lane];
+        const u32x4 xf = xc_frag(&xst[st][wave][0][0], s, lane);
 #pragma unroll
         for (int t = 0; t < BT; ++t) acc[t] = mfma_step<T>(xf, wst[st][t * kChunkSteps + s][lane], acc[t]);
       }
