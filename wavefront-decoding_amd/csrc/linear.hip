@@ -48,10 +48,10 @@
 // So y[m] is bit-identical whatever n is and wherever row m sits -- the
 // property that keeps wavefront decode token-identical to sequential decode.
 //
-// x operand: every kernel but the 8-tile slice form reads a 16-row block's
-// chunk with coalesced loads of whole 256-byte row segments and turns them
-// into MFMA fragments through the wave's LDS (xc_offsets below): a fragment
-// load would touch 16 rows x 64 bytes per instruction.
+// x operand: every kernel reads a 16-row block's chunk with coalesced loads
+// of whole 256-byte row segments and turns them into MFMA fragments through
+// the wave's LDS (xc_offsets below): a fragment load would touch 16 rows x 64
+// bytes per instruction.
 //
 // Weight layout ("packed", made once by wfd_linear_pack): W is stored in MFMA
 // fragment order, tile by tile -- for tile g, chunk p, step s the 64 lanes'
@@ -285,37 +285,6 @@ __global__ __launch_bounds__(256) void linear_pack_kernel(const T* __restrict__ 
   const int row = weight_row<EPI>(g, lane & 15, pair_off);
   const int64_t k = (int64_t)p * Chunk<T>::KC + s * Chunk<T>::KSTEP + (lane >> 4) * V;
   *reinterpret_cast<u32x4*>(Wp + f * V) = ld16(W + (int64_t)row * K + k);
-}
-
-// x fragments of chunk p for the lane whose row starts at byte offset xoff in
-// the x buffer (kBufInvalid for a padding row: zeros, no memory traffic).
-template <typename T>
-__device__ __forceinline__ void load_x(u32x4 (&xf)[kChunkSteps], __amdgpu_buffer_rsrc_t xr, uint32_t xoff, int p) {
-  constexpr int KSTEP = LinTraits<T>::KSTEP;
-#pragma unroll
-  for (int s = 0; s < kChunkSteps; ++s) xf[s] = buf_ld16(xr, xoff + (uint32_t)((p * kChunkSteps + s) * KSTEP * sizeof(T)));
-}
-
-// Byte offset of lane `col`'s operand row in the 16-row block starting at
-// `base` (uniform over the wave): row x_rows[base + col], read with uniform
-// scalar loads, so the vector-memory counter tracks operand data only and no
-// weight load waits for an index. Lanes at or past n get kBufInvalid: their x
-// loads return zeros without touching memory, nothing is stored for them, and
-// MFMA rows never mix.
-template <typename T>
-__device__ __forceinline__ uint32_t x_offset(const int32_t* __restrict__ x_rows, int64_t ldx, int base, int col, int grp,
-                                             int n) {
-  const int m = n - base < 16 ? n - base : 16;
-  int r = base + col;
-  if (x_rows) {
-    r = 0;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int v = x_rows[base + (j < m ? j : 0)];
-      r = col == j ? v : r;
-    }
-  }
-  return col < m ? (uint32_t)(((int64_t)r * ldx + grp * Chunk<T>::V) * sizeof(T)) : kBufInvalid;
 }
 
 // Coalesced x operand. An MFMA A fragment gives lane l row l % 16 and the
@@ -616,20 +585,21 @@ __host__ __device__ constexpr int xcd_grid(int rb, int groups) {
   return rb * ((groups + kXcds - 1) / kXcds) * kXcds;
 }
 
-// Tiles per workgroup of a slice launch (2, 4 or 8; S = K slices in grid y).
+// Tiles per workgroup of a slice launch (2 or 4; S = K slices in grid y).
 // Each workgroup moves 64 rows x 128 K of x (16 KB) and BT x 4 KB of weights
 // per chunk, and the XCD-aware grid spreads the workgroups evenly over the 8
 // XCDs of 32 CUs, so the busiest CU streams ceil(workgroups / 256) of them:
-// the choice minimizes that product (ties: fewer tiles); 8 tiles only above
-// 32 rows, where at least three of the four waves carry rows. The 2048-column
-// projections' slice launches at 192-512 rows: 5-12 % faster than with at
-// most 4 tiles (in the bs=32 decode, 15.0 -> 14.3 us at 192 rows).
+// the choice minimizes that product (ties: fewer tiles). Eight tiles per
+// workgroup (one workgroup per CU by registers) were faster at 192-512 rows
+// with fragment loads of x, and slower than four once x is coalesced
+// (proj / mlp_proj / adapter at 512 rows: 18.0 / 28.8 / 24.4 -> 14.4 / 25.2 /
+// 21.0 us).
 constexpr int kCusPerXcd = 32;
 
-static int gemm_tiles_per_workgroup(int n, int rb, int tiles, int S) {
+static int gemm_tiles_per_workgroup(int rb, int tiles, int S) {
   int best = 2;
   long best_cost = -1;
-  for (int bt = 2; bt <= (n > 32 ? 8 : 4); bt *= 2) {
+  for (int bt = 2; bt <= 4; bt *= 2) {
     const long wgs = (long)xcd_grid(rb, (tiles + bt - 1) / bt) * S;
     const long per_cu = ((wgs + kXcds - 1) / kXcds + kCusPerXcd - 1) / kCusPerXcd;
     const long cost = per_cu * (16 + 4 * bt);
@@ -672,12 +642,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
   constexpr int V = LinTraits<T>::V;
   constexpr int FR = BT * kChunkSteps;  // 1 KB fragments per chunk: (tile, step)
   constexpr int FPW = FR / 4;           // fragments each wave stages per chunk
-  // x through LDS (coalesced loads) for up to 4 tiles; the 8-tile form runs
-  // one workgroup per CU, which cannot hide the extra LDS round trip, and
-  // loads fragments directly
-  constexpr bool XC = BT <= 4;
   __shared__ __align__(16) u32x4 wl[2][FR][64];
-  __shared__ __align__(16) u32x4 xl[XC ? 4 : 1][XC ? kXcUnits : 1];  // each wave's x chunk
+  __shared__ __align__(16) u32x4 xl[4][kXcUnits];  // each wave's x chunk (coalesced load -> fragments)
   int rbk, tg;
   if (!xcd_block<BT>(n, tiles, rbk, tg)) return;  // padding workgroup (uniform, before any barrier)
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -693,21 +659,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
   // a wave past the last row still stages weights and meets every barrier;
   // its x loads read zeros and it stores nothing
   uint32_t xoff[kChunkSteps];
-#pragma unroll
-  for (int s = 0; s < kChunkSteps; ++s) xoff[s] = kBufInvalid;
   if (row0 < n) {
-    if constexpr (XC)
-      xc_offsets<T>(xoff, x_rows, ldx, row0, lane, n);
-    else
-      xoff[0] = x_offset<T>(x_rows, ldx, row0, col, grp, n);
+    xc_offsets<T>(xoff, x_rows, ldx, row0, lane, n);
+  } else {
+#pragma unroll
+    for (int s = 0; s < kChunkSteps; ++s) xoff[s] = kBufInvalid;
   }
   const __amdgpu_buffer_rsrc_t xrs = buf_rsrc(x);
-  auto load_xs = [&](u32x4 (&xr)[kChunkSteps], int p) {
-    if constexpr (XC)
-      load_xc<T>(xr, xrs, xoff, p);
-    else
-      load_x<T>(xr, xrs, xoff[0], p);
-  };
+  auto load_xs = [&](u32x4 (&xr)[kChunkSteps], int p) { load_xc<T>(xr, xrs, xoff, p); };
 
   // the fragments this wave stages: f = wave * FPW + i -> (tile f / 4, step f % 4)
   const T* wsrc[FPW];
@@ -738,12 +697,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
   f32x4 tot[BT], sl[BT], sub[BT];
 #pragma unroll
   for (int t = 0; t < BT; ++t) tot[t] = sl[t] = sub[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // chunk p (coalesced x in xr, through the wave's LDS block; for the 8-tile
-  // form, fragments in xr; weights in LDS stage b): its partial into the
-  // contract's running sums
+  // chunk p (coalesced x in xr, through the wave's LDS block; weights in LDS
+  // stage b): its partial into the contract's running sums
   auto mma = [&](const u32x4 (&xr)[kChunkSteps], int b, int p) {
-    if constexpr (XC) xc_store(xl[wave], xr, lane);
-    auto xfrag = [&](int st) { return XC ? xc_frag(xl[wave], st, lane) : xr[st]; };
+    xc_store(xl[wave], xr, lane);
+    auto xfrag = [&](int st) { return xc_frag(xl[wave], st, lane); };
     f32x4 acc[BT];
 #pragma unroll
     for (int t = 0; t < BT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -858,26 +816,6 @@ template <int N>
 __device__ __forceinline__ void wait_vmem_barrier() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
-}
-
-// Row pointer of lane `col` in the 16-row block at `base` (lane group grp's
-// first element); padding lanes (col >= rows left) take the block's first
-// row: their MFMA rows are never stored and never mix with real rows.
-template <typename T>
-__device__ __forceinline__ const T* x_row_ptr(const T* __restrict__ x, const int32_t* __restrict__ x_rows,
-                                              int64_t ldx, int base, int col, int grp, int n) {
-  const int m = n - base < 16 ? n - base : 16;
-  int r = base + (col < m ? col : 0);
-  if (x_rows) {
-    int v0 = 0;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int v = x_rows[base + (j < m ? j : 0)];
-      v0 = (col < m ? col : 0) == j ? v : v0;
-    }
-    r = v0;
-  }
-  return x + (int64_t)r * ldx + grp * Chunk<T>::V;
 }
 
 // The stream kernel's coalesced x sources: a direct-to-LDS load puts lane l's
@@ -1068,9 +1006,9 @@ static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const v
   }
 }
 
-// The slice form: grid (xcd-mapped row blocks x tile groups, slices), 2, 4
-// or 8 tiles per workgroup as for the one-launch gemm: each workgroup reads
-// its 64 rows of x once for 32-128 output columns and only its slice of K,
+// The slice form: grid (xcd-mapped row blocks x tile groups, slices), 2 or 4
+// tiles per workgroup as for the one-launch gemm: each workgroup reads its 64
+// rows of x once for 32 or 64 output columns and only its slice of K,
 // where the stream kernel reads them for 16 columns and all of K.
 template <typename T>
 static void launch_linear_partials(const void* x, const int32_t* xr, int64_t ldx, const void* W, float* part, int n,
@@ -1080,13 +1018,11 @@ static void launch_linear_partials(const void* x, const int32_t* xr, int64_t ldx
   const int S = slice_count(P);
   const int rb = (n + 63) / 64;
   const RopeArgs ra{};
-  const int bt = gemm_tiles_per_workgroup(n, rb, tiles, S);
+  const int bt = gemm_tiles_per_workgroup(rb, tiles, S);
 #define WFD_GEMM_PART(BTV)                                                                                          \
   hipLaunchKernelGGL((linear_gemm_kernel<T, T, kEpiPlain, BTV, true>), dim3(xcd_grid(rb, (tiles + BTV - 1) / BTV), S), \
                      dim3(256), 0, st, (const T*)x, xr, ldx, (const T*)W, (T*)nullptr, 0, n, K, 0, tiles, ra, part)
-  if (bt == 8)
-    WFD_GEMM_PART(8);
-  else if (bt == 4)
+  if (bt == 4)
     WFD_GEMM_PART(4);
   else
     WFD_GEMM_PART(2);
