@@ -981,8 +981,11 @@ static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const v
                            (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra);
       return;
     }
-    if (rb * tiles <= kGemmMinBlockTiles) {
-      // few (row block, tile) pairs: every wave streams its own weights, no barriers
+    // few (row block, tile) pairs, or at most 32 rows where four-tile gemm
+    // workgroups would not cover the CUs: every wave streams its own weights,
+    // no barriers (gate|up at 17-32 rows: 16.1-17.1 -> 14.0-14.9 us; lm_head,
+    // with 500 gemm workgroups, stays on the gemm)
+    if (rb * tiles <= kGemmMinBlockTiles || (n <= 32 && (tiles + 3) / 4 < 256)) {
       constexpr int NB = 2;
       hipLaunchKernelGGL((linear_tile_kernel<T, TO, EPI, NB>), dim3(rb, (tiles + NB - 1) / NB), dim3(256), 0, st,
                          (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra);
