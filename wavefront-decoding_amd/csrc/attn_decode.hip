@@ -25,8 +25,9 @@
 // of 8 waves owns one (split, kv head, query), and its waves take the split's
 // key tiles round-robin (TK keys per tile: 64 for Dh 64, 32 for Dh 128, 64
 // VGPRs of K and V fragments per lane), each keeping an online softmax. QK^T runs on MFMA (q rows = the G query heads of the kv
-// head, padded to 16; K tile as the B operand loaded straight from HBM in
-// 16-byte fragments); P.V runs on the VALU in fp32 with one 16-byte V
+// head, padded to 16; K tile as the B operand: 16-byte fragments straight
+// from HBM, or, for one query row per workgroup, whole key rows turned into
+// fragments through the wave's LDS); P.V runs on the VALU in fp32 with one 16-byte V
 // fragment per lane per key, so K and V are each read exactly once. The waves
 // merge through LDS in fixed order. A query whose keys fit one split (every
 // decode query up to 1024 keys) is finished in its workgroup; longer ones
@@ -73,6 +74,19 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict
   constexpr int NR = QG * G;       // real MFMA rows
   static_assert(DH % KSTEP == 0 && 64 % LPR == 0 && TK % 16 == 0 && TK % RG == 0 && NR <= 16, "unsupported tile");
 
+  // K through LDS (KCO): one query row per workgroup in bf16, whose LDS is
+  // otherwise a few KB. A K fragment load (16 keys x 64 bytes per
+  // instruction) streams at about half the rate of whole key rows per
+  // instruction; each wave instead loads its tile's key rows whole (KPI rows
+  // per instruction, lane l: key KPI s + l / LPK, 16-byte piece
+  // (l % LPK) ^ key), stores them to its LDS block as loaded, and reads the
+  // MFMA B fragments back (lane l, step st: key l % 16, piece 4 st + l / 16).
+  // The same values reach the same lanes, so the bits are the same.
+  constexpr bool KCO = NR == 1 && sizeof(T) == 2;
+  constexpr int LPK = DH / V;    // 16-byte pieces (lanes) per key row
+  constexpr int KPI = 64 / LPK;  // key rows per load instruction
+  static_assert(!KCO || (64 % LPK == 0 && NDS * 64 == 16 * LPK), "key row layout");
+  __shared__ __align__(16) u32x4 k_lds[KCO ? NW : 1][KCO ? NJ * NDS * 64 : 1];
   __shared__ float p_lds[NW][NR][TK];
   __shared__ float o_lds[NW][NR][DH];
   __shared__ float m_lds[NW][NR];
@@ -160,12 +174,23 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict
     const int t0 = split * kAttnSplit + t * TK;
     // every load of the tile first: K (MFMA B fragments), V
     u32x4 kf[NJ][NDS];
+    if constexpr (KCO) {  // whole key rows, turned into fragments through LDS below
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int key = min(t0 + 16 * j + col, maxlen - 1);
-      const T* p = kb + (int64_t)key * rs + grp * V;
+      for (int j = 0; j < NJ; ++j)
 #pragma unroll
-      for (int s = 0; s < NDS; ++s) kf[j][s] = ld16(p + s * KSTEP);
+        for (int s = 0; s < NDS; ++s) {
+          const int r = KPI * s + lane / LPK;  // key within the 16-key block
+          const int key = min(t0 + 16 * j + r, maxlen - 1);
+          kf[j][s] = ld16(kb + (int64_t)key * rs + ((lane % LPK) ^ (r % LPK)) * V);
+        }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int key = min(t0 + 16 * j + col, maxlen - 1);
+        const T* p = kb + (int64_t)key * rs + grp * V;
+#pragma unroll
+        for (int s = 0; s < NDS; ++s) kf[j][s] = ld16(p + s * KSTEP);
+      }
     }
     u32x4 vf[KPL];
 #pragma unroll
@@ -174,6 +199,21 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict
       vf[k] = vmine ? ld16(vb + (int64_t)key * rs + dseg * V) : zero16();
     }
 
+    if constexpr (KCO) {
+      // the LDS executes one wave's accesses in order: the previous tile's
+      // fragment reads come before these stores, the stores before the reads
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int s = 0; s < NDS; ++s) k_lds[wave][(j * NDS + s) * 64 + lane] = kf[j][s];
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int s = 0; s < NDS; ++s)
+          kf[j][s] = k_lds[wave][j * NDS * 64 + col * LPK + ((4 * s + grp) ^ (col % LPK))];
+    }
     // scores: lane (grp, col) holds S[row 4*grp + r][key 16j + col] in acc[j][r]
     f32x4 acc[NJ];
 #pragma unroll
