@@ -657,7 +657,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
   const int pb = PART ? (int)blockIdx.y * Q : 0;
   const int pe = PART ? min(P, pb + Q) : P;
   // a wave past the last row still stages weights and meets every barrier;
-  // its x loads read zeros and it stores nothing
+  // its x loads read zeros (no memory traffic), it runs no MFMA and stores
+  // nothing
   uint32_t xoff[kChunkSteps];
   if (row0 < n) {
     xc_offsets<T>(xoff, x_rows, ldx, row0, lane, n);
@@ -700,6 +701,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
   // chunk p (coalesced x in xr, through the wave's LDS block; weights in LDS
   // stage b): its partial into the contract's running sums
   auto mma = [&](const u32x4 (&xr)[kChunkSteps], int b, int p) {
+    if (row0 >= n) return;  // a wave without rows only stages weights (uniform over the wave)
     xc_store(xl[wave], xr, lane);
     auto xfrag = [&](int st) { return xc_frag(xl[wave], st, lane); };
     f32x4 acc[BT];
