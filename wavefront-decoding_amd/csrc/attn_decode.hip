@@ -25,9 +25,9 @@
 // of 8 waves owns one (split, kv head, query), and its waves take the split's
 // key tiles round-robin (TK keys per tile: 64 for Dh 64, 32 for Dh 128, 64
 // VGPRs of K and V fragments per lane), each keeping an online softmax. QK^T runs on MFMA (q rows = the G query heads of the kv
-// head, padded to 16; K tile as the B operand: 16-byte fragments straight
-// from HBM, or, for one query row per workgroup, whole key rows turned into
-// fragments through the wave's LDS); P.V runs on the VALU in fp32 with one 16-byte V
+// head, padded to 16; K tile as the B operand: whole key rows turned into
+// fragments through the wave's LDS for one query row per workgroup, 16-byte
+// fragments straight from HBM for grouped rows); P.V runs on the VALU in fp32 with one 16-byte V
 // fragment per lane per key, so K and V are each read exactly once. The waves
 // merge through LDS in fixed order. A query whose keys fit one split (every
 // decode query up to 1024 keys) is finished in its workgroup; longer ones
@@ -74,15 +74,15 @@ __global__ __launch_bounds__(64 * NW) void attn_split_kernel(const T* __restrict
   constexpr int NR = QG * G;       // real MFMA rows
   static_assert(DH % KSTEP == 0 && 64 % LPR == 0 && TK % 16 == 0 && TK % RG == 0 && NR <= 16, "unsupported tile");
 
-  // K through LDS (KCO): one query row per workgroup in bf16, whose LDS is
-  // otherwise a few KB. A K fragment load (16 keys x 64 bytes per
+  // K through LDS (KCO): one query row per workgroup (NR = G <= 4 MFMA rows)
+  // in bf16, whose LDS is otherwise at most 20 KB. A K fragment load (16 keys x 64 bytes per
   // instruction) streams at about half the rate of whole key rows per
   // instruction; each wave instead loads its tile's key rows whole (KPI rows
   // per instruction, lane l: key KPI s + l / LPK, 16-byte piece
   // (l % LPK) ^ key), stores them to its LDS block as loaded, and reads the
   // MFMA B fragments back (lane l, step st: key l % 16, piece 4 st + l / 16).
   // The same values reach the same lanes, so the bits are the same.
-  constexpr bool KCO = NR == 1 && sizeof(T) == 2;
+  constexpr bool KCO = NR <= 4 && sizeof(T) == 2;
   constexpr int LPK = DH / V;    // 16-byte pieces (lanes) per key row
   constexpr int KPI = 64 / LPK;  // key rows per load instruction
   static_assert(!KCO || (64 % LPK == 0 && NDS * 64 == 16 * LPK), "key row layout");
