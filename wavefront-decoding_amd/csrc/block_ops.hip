@@ -384,6 +384,7 @@ __global__ __launch_bounds__(kRowThreads) void copy_rows_kernel(const T* __restr
 }
 
 constexpr int kArgThreads = 1024;
+constexpr int kArgUnroll = 8;  // a 32000-entry row: 8000 16-byte loads over 1024 threads
 
 __device__ __forceinline__ void argmax_merge(float& bv, int& bi, float ov, int oi) {
   if (ov > bv || (ov == bv && oi < bi)) {
@@ -405,10 +406,24 @@ __global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float* __rest
   float best = -INFINITY;
   int bi = 0x7fffffff;
   const int nv = ((ld & 3) == 0) ? Vocab / 4 : 0;  // 16-byte loads when rows stay aligned
-  for (int q = threadIdx.x; q < nv; q += kArgThreads) {
-    const u32x4 w = ld16(row + 4 * q);
+  // kArgUnroll loads in flight per thread before the first compare (the row
+  // was just written by other CUs: one round trip instead of one per load);
+  // the merge is order-free (value, then lowest index)
+  for (int q0 = threadIdx.x; q0 < nv; q0 += kArgThreads * kArgUnroll) {
+    u32x4 w[kArgUnroll];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) argmax_merge(best, bi, __uint_as_float(w[k]), 4 * q + k);
+    for (int u = 0; u < kArgUnroll; ++u) {
+      const int q = q0 + u * kArgThreads;
+      w[u] = q < nv ? ld16(row + 4 * q) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < kArgUnroll; ++u) {
+      const int q = q0 + u * kArgThreads;
+      if (q < nv) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) argmax_merge(best, bi, __uint_as_float(w[u][k]), 4 * q + k);
+      }
+    }
   }
   for (int e = 4 * nv + threadIdx.x; e < Vocab; e += kArgThreads) argmax_merge(best, bi, row[e], e);
 #pragma unroll
