@@ -266,8 +266,8 @@ def test_linear_row_invariant(gpu, dtype, N):
 def test_linear_split_k_same_bits(gpu, dtype, N, K):
     """Split-K projections: the slice sums of linear_partials, added in slice
     order in fp32 and rounded, equal the one-launch linear bit for bit (1 to 4
-    slices: K = 128 .. 5632; 2, 4 and 8 tiles per workgroup: 8 at 200 rows of
-    2048 columns), over contiguous and gathered rows; the norm that
+    slices: K = 128 .. 5632; 2 and 4 tiles per workgroup; row blocks with 1 to
+    64 rows), over contiguous and gathered rows; the norm that
     reduces them (add_rmsnorm_split) equals linear + add_rmsnorm, including
     the kept linear rows (a_out), and matches the oracle."""
     if K % ops.linear_k_multiple(dtype):
