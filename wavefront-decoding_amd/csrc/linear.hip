@@ -179,17 +179,38 @@ __device__ __forceinline__ int weight_row(int g, int c, int pair_off) {
 // their outputs first (or at launch), then store.
 struct RopePre {
   float c, s;
-  int64_t fr;
+  int64_t ro;  // k / v heads: the cache offset of the row's kv head 0
 };
 
-__device__ __forceinline__ RopePre rope_pre(const RopeArgs& ra, int row, int col) {
-  RopePre o{1.f, 0.f, 0};
-  const int head = col / ra.Dh;  // uniform over a 16-column tile (Dh % 16 == 0)
-  const int d = col - head * ra.Dh;
-  if (head >= ra.H) o.fr = ra.flat_row[row];
+// Head and in-head column of column 0 of tile g: uniform over the tile
+// (Dh % 16 == 0), so one scalar division per tile rather than one per lane.
+__device__ __forceinline__ int tile_head(const RopeArgs& ra, int g, int& dbase) {
+  const int c0 = __builtin_amdgcn_readfirstlane(16 * g);
+  const int head = c0 / ra.Dh;
+  dbase = c0 - head * ra.Dh;
+  return head;
+}
+
+// kv_offset(row, h) = kv_offset(row, 0) + h * kv_head_stride: the division
+// by the block size is paid once per row, not once per stored element.
+__device__ __forceinline__ int64_t kv_head_stride(const RopeArgs& ra) {
+  return ra.block_rows > 1 ? ra.block_rows * ra.Dh : (int64_t)ra.Dh;
+}
+
+__device__ __forceinline__ int64_t rope_row_off(const RopeArgs& ra, int row) {
+  return kv_offset(ra.flat_row[row], 0, ra.Hkv, ra.Dh, ra.block_rows);
+}
+
+__device__ __forceinline__ int rope_row_pos(const RopeArgs& ra, int row) {
+  const int p = ra.pos[row];
+  return p < 0 ? 0 : (p >= ra.tab_rows ? ra.tab_rows - 1 : p);
+}
+
+// The rotation of output (head, in-head column d) of a row at table position
+// p; `ro` = the row's rope_row_off, carried for the store.
+__device__ __forceinline__ RopePre rope_pre(const RopeArgs& ra, int p, int head, int d, int64_t ro) {
+  RopePre o{1.f, 0.f, ro};
   if (head < ra.H + ra.Hkv) {
-    int p = ra.pos[row];
-    p = p < 0 ? 0 : (p >= ra.tab_rows ? ra.tab_rows - 1 : p);
     const int half = ra.Dh >> 1;
     o.c = ra.cos_t[(int64_t)p * half + (d >> 1)];
     o.s = ra.sin_t[(int64_t)p * half + (d >> 1)];
@@ -197,44 +218,68 @@ __device__ __forceinline__ RopePre rope_pre(const RopeArgs& ra, int row, int col
   return o;
 }
 
-// Value v0 of output (row, col) and its RoPE partner v1 = value of column col ^ 1.
+// Value v0 of output (row, head, in-head column d) and its RoPE partner v1 =
+// the value of column d ^ 1.
 template <typename TO>
-__device__ __forceinline__ void store_rope(const RopeArgs& ra, const RopePre& o, int row, int col, float v0,
+__device__ __forceinline__ void store_rope(const RopeArgs& ra, const RopePre& o, int row, int head, int d, float v0,
                                            float v1) {
-  const int head = col / ra.Dh;
-  const int d = col - head * ra.Dh;
   TO* dst;
   float out;
   if (head >= ra.H + ra.Hkv) {
-    dst = (TO*)ra.v_cache + kv_offset(o.fr, head - ra.H - ra.Hkv, ra.Hkv, ra.Dh, ra.block_rows) + d;
+    dst = (TO*)ra.v_cache + o.ro + (head - ra.H - ra.Hkv) * kv_head_stride(ra) + d;
     out = v0;
   } else {
     const float xm = Elem<TO>::round(v0);
     const float xp = Elem<TO>::round(v1);
     out = (d & 1) ? fmaf(xp, o.s, xm * o.c) : fmaf(xm, o.c, -(xp * o.s));
     dst = head < ra.H ? (TO*)ra.q_out + ((int64_t)row * ra.H + head) * ra.Dh + d
-                      : (TO*)ra.k_cache + kv_offset(o.fr, head - ra.H, ra.Hkv, ra.Dh, ra.block_rows) + d;
+                      : (TO*)ra.k_cache + o.ro + (head - ra.H) * kv_head_stride(ra) + d;
   }
   Elem<TO>::store(dst, out);
 }
 
-// Table operands of a lane's epilogue outputs -- rows row4 .. row4 + 3 (rows
-// past n read row 0's, never stored) of tiles g0 .. g0 + NT - 1 (past the
-// last tile: the last one's) at column col -- all loaded before the first
-// store. A no-op for the other epilogues.
+// Operands of the QKV-RoPE-append epilogue for a lane's rows row4 .. row4 + 3
+// (rows past n read row 0's, never stored) in two parts: per row, the table
+// position and the cache offset of kv head 0, gathered at launch (their load
+// round trip overlaps the main loop; 3 VGPRs a row); per output of tiles
+// g0 .. g0 + NT - 1 (past the last tile: the last one's) at column col, the
+// cos / sin pair, gathered after the main loop from the rows' positions (one
+// round trip, and no table registers held through the loop). Loaded apart
+// from the stores: a store may alias the tables as far as the compiler
+// knows, so a load placed after one would wait for it. A no-op for the other
+// epilogues.
+struct RopeRows {
+  int p[4];
+  int64_t ro[4];
+};
+
+template <int EPI>
+__device__ __forceinline__ void gather_rope_rows(RopeRows& rr, const RopeArgs& ra, int row4, int n) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    rr.p[r] = 0;
+    rr.ro[r] = 0;
+    if constexpr (EPI == kEpiRope) {
+      const int row = row4 + r < n ? row4 + r : 0;
+      rr.p[r] = rope_row_pos(ra, row);
+      rr.ro[r] = rope_row_off(ra, row);
+    }
+  }
+}
+
 template <int EPI, int NT>
-__device__ __forceinline__ void gather_rope(RopePre (&rp)[NT][4], const RopeArgs& ra, int row4, int n, int g0,
+__device__ __forceinline__ void gather_rope(RopePre (&rp)[NT][4], const RopeArgs& ra, const RopeRows& rr, int g0,
                                             int tiles, int col) {
 #pragma unroll
-  for (int t = 0; t < NT; ++t)
+  for (int t = 0; t < NT; ++t) {
+    int dbase = 0, head = 0;
+    if constexpr (EPI == kEpiRope) head = tile_head(ra, g0 + t < tiles ? g0 + t : tiles - 1, dbase);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       rp[t][r] = RopePre{1.f, 0.f, 0};
-      if constexpr (EPI == kEpiRope) {
-        const int g = g0 + t < tiles ? g0 + t : tiles - 1;
-        rp[t][r] = rope_pre(ra, row4 + r < n ? row4 + r : 0, 16 * g + col);
-      }
+      if constexpr (EPI == kEpiRope) rp[t][r] = rope_pre(ra, rr.p[r], head, dbase + col, rr.ro[r]);
     }
+  }
 }
 
 // Store of output (row, column c of tile g); `partner` is the value of column
@@ -246,7 +291,9 @@ __device__ __forceinline__ void store_out(TO* __restrict__ y, int64_t ldy, const
   if (EPI == kEpiSwiGLU) {
     if (c < 8) Elem<TO>::store(y + (int64_t)row * ldy + 8 * g + c, (v / (1.0f + expf(-v))) * partner);
   } else if (EPI == kEpiRope) {
-    store_rope<TO>(ra, rp, row, 16 * g + c, v, partner);
+    int dbase;
+    const int head = tile_head(ra, g, dbase);
+    store_rope<TO>(ra, rp, row, head, dbase + c, v, partner);
   } else {
     Elem<TO>::store(y + (int64_t)row * ldy + 16 * g + c, v);
   }
@@ -407,7 +454,10 @@ __global__ __launch_bounds__(64 * WW) void linear_wide_kernel(
   if constexpr (EPI == kEpiRope) {
     if (threadIdx.x < 256) {
       const int orow = 4 * ((threadIdx.x >> 2) >> 4) + (threadIdx.x & 3);
-      rp = rope_pre(ra, orow < n ? orow : 0, 16 * g + ((threadIdx.x >> 2) & 15));
+      const int row = orow < n ? orow : 0;
+      int dbase;
+      const int head = tile_head(ra, g, dbase);
+      rp = rope_pre(ra, rope_row_pos(ra, row), head, dbase + ((threadIdx.x >> 2) & 15), rope_row_off(ra, row));
     }
   }
 
@@ -518,10 +568,11 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ 
     wtile[b] = W + packed_off<T>(gok[b] ? g : 0, 0, P, 0);
   }
 
-  // the RoPE epilogue's table operands are fetched at launch, so the tail
-  // after the last MFMA waits on no dependent loads
-  RopePre rp[NB][4];
-  gather_rope<EPI, NB>(rp, ra, row0 + 4 * grp, n, blockIdx.y * NB, tiles, col);
+  // the RoPE epilogue's per-row operands (position, cache offset) are
+  // fetched at launch, the cos / sin pairs after the main loop (at 64 rows
+  // 15.4 us against 16.9 with every operand at launch, held through the loop)
+  RopeRows rrows;
+  gather_rope_rows<EPI>(rrows, ra, row0 + 4 * grp, n);
 
   // two-stage register pipeline; every load is unconditional (the stage past
   // the last chunk re-reads chunk P-1 and is never used)
@@ -554,6 +605,8 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ 
     mma(acc, xb, wb);
     add(acc, p + 1);
   }
+  RopePre rp[NB][4];
+  gather_rope<EPI, NB>(rp, ra, rrows, blockIdx.y * NB, tiles, col);
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
     if (!gok[b]) continue;  // uniform over the workgroup
@@ -688,12 +741,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
 #pragma unroll
     for (int i = 0; i < FPW; ++i) wl[b][wave * FPW + i][lane] = wr[i];
   };
-  // with at most 2 tiles the RoPE epilogue's table operands are fetched at
-  // launch (the tail then waits on no dependent loads); with 4 their registers
-  // would cost the main loop occupancy, so they are fetched after it
+  // with 2 tiles the RoPE epilogue's operands are gathered at launch (the
+  // tail then waits on no dependent loads: at 128 rows 17.7 us against 18.4
+  // with the cos / sin pairs after the loop); with 4 the main loop has no
+  // registers to spare for them, so they follow it
   constexpr bool kRopeEarly = BT <= 2;
+  RopeRows rrows;
   RopePre rp[BT][4];
-  if constexpr (kRopeEarly) gather_rope<EPI, BT>(rp, ra, row0 + 4 * grp, n, tg * BT, tiles, col);
+  if constexpr (kRopeEarly) {
+    gather_rope_rows<EPI>(rrows, ra, row0 + 4 * grp, n);
+    gather_rope<EPI, BT>(rp, ra, rrows, tg * BT, tiles, col);
+  }
   SliceWalk walk(P, pb);
   f32x4 tot[BT], sl[BT], sub[BT];
 #pragma unroll
@@ -769,7 +827,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
     }
     return;
   }
-  if constexpr (!kRopeEarly) gather_rope<EPI, BT>(rp, ra, row0 + 4 * grp, n, tg * BT, tiles, col);
+  if constexpr (!kRopeEarly) {
+    gather_rope_rows<EPI>(rrows, ra, row0 + 4 * grp, n);
+    gather_rope<EPI, BT>(rp, ra, rrows, tg * BT, tiles, col);
+  }
 #pragma unroll
   for (int t = 0; t < BT; ++t) {
     const int g = tg * BT + t;
@@ -913,8 +974,10 @@ __global__ __launch_bounds__(256) void linear_stream_kernel(const T* __restrict_
     }
   }
   if (!rows) return;  // after the last barrier; every load of this wave has completed
+  RopeRows rrows;
+  gather_rope_rows<EPI>(rrows, ra, row0 + 4 * grp, n);
   RopePre rp[BT][4];
-  gather_rope<EPI, BT>(rp, ra, row0 + 4 * grp, n, blockIdx.y * BT, tiles, col);
+  gather_rope<EPI, BT>(rp, ra, rrows, blockIdx.y * BT, tiles, col);
 #pragma unroll
   for (int t = 0; t < BT; ++t) {
     const int g = blockIdx.y * BT + t;
