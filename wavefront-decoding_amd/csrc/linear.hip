@@ -1005,9 +1005,9 @@ static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const v
   // (not for SwiGLU, whose partner column c ^ 8 lies in the other half)
   const bool half = EPI != kEpiSwiGLU && tiles <= kHalfTileMax;
   // more tiles than two 1024-thread workgroups per CU hold: 8-wave workgroups
-  // (four per CU), so the whole launch is resident in one round (gate|up at
-  // 704 tiles: 11.5 -> 10.4 us); each wave then sums two sub-slices, so only
-  // for one chunk per sub-slice (K <= 16 chunks)
+  // (three per CU by their 48 KB of LDS), so the whole launch is resident in
+  // one round (gate|up at 704 tiles: 11.5 -> 10.4 us); each wave then sums
+  // two sub-slices, so only for one chunk per sub-slice (K <= 16 chunks)
   const bool ww8 = !half && tiles > kResidentWide && R == 1;
 #define WFD_WIDE(RMV)                                                                                             \
   if (half)                                                                                                       \
