@@ -41,8 +41,8 @@ enum { WFD_EPI_PLAIN = 0, WFD_EPI_SWIGLU = 1 };
 
 /* Message for the last failing call on this thread. */
 const char* wfd_last_error(void);
-/* Bumped whenever an entry point's signature changes (5: wfd_argmax's accept flags,
-   wfd_attn_varlen_rows). */
+/* Bumped whenever an entry point's signature changes or one is added (5: wfd_argmax's
+   accept flags, wfd_attn_varlen_rows; 6: wfd_linear_argmax, wfd_argmax_groups). */
 int wfd_abi_version(void);
 
 /*
@@ -333,6 +333,39 @@ int wfd_copy_rows(const void* src, const int32_t* src_rows, int64_t lds, void* d
  */
 int wfd_argmax(const float* logits, int64_t ld, int64_t* out, int64_t* ring, const int32_t* ring_rows,
                int64_t ring_len, const int64_t* expect, int32_t* accept, int n, int vocab, wfd_stream_t stream);
+
+/*
+ * Column groups of wfd_linear_argmax for this shape: the few-row launch's
+ * workgroups (a 16-column tile, or half a tile when there are few tiles), or
+ * 0 where wfd_linear would not take the few-row kernel (n above 16, a K too
+ * long for it) or dtype is not WFD_BF16.
+ */
+int wfd_linear_argmax_groups(int n, int N, int K, int dtype);
+
+/*
+ * wfd_linear with bf16 x / W and fp32 y (plain epilogue; the same kernel, so
+ * y has the same bits) that also leaves, for each row m and column group
+ * s < G = wfd_linear_argmax_groups(n, N, K, dtype), the first largest value of
+ * y[m] over the group's columns and its column index: part_val[m * G + s],
+ * part_idx[m * G + s]. wfd_argmax_groups over them gives wfd_argmax(y)'s ids
+ * while reading G entries per row instead of N. WFD_UNSUPPORTED where G is 0.
+ * Replaces: the lm_head call of the coda (src/decoding/huginn_blocks.py:291;
+ *   huginn_blocks_batch.py:345) together with the logits read of
+ *   greedy_sample's argmax (src/decoding/acceptance.py:40-44).
+ */
+int wfd_linear_argmax(const void* x, const int32_t* x_rows, int64_t ldx, const void* W, float* y, int64_t ldy, int n,
+                      int N, int K, int dtype, float* part_val, int32_t* part_idx, wfd_stream_t stream);
+
+/*
+ * wfd_argmax from the column-group bests wfd_linear_argmax left (groups per
+ * row): out[i] = the first index of row i's largest value, with the same ring
+ * and expect / accept semantics as wfd_argmax.
+ * Replaces: greedy_sample's argmax and greedy_accept's comparison
+ *   (src/decoding/acceptance.py:40-58; huginn_blocks_batch.py:345-346), as wfd_argmax.
+ */
+int wfd_argmax_groups(const float* part_val, const int32_t* part_idx, int groups, int64_t* out, int64_t* ring,
+                      const int32_t* ring_rows, int64_t ring_len, const int64_t* expect, int32_t* accept, int n,
+                      wfd_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -34,7 +34,21 @@ def test_library_loads_and_exports_every_symbol():
 
 def test_host_only_entry_points():
     lib = _lib.load()
-    assert lib.wfd_abi_version() == 5
+    assert lib.wfd_abi_version() == 6
+    # column groups of the tile argmax: 2000 tiles at <= 16 rows (lm_head), half tiles below 256 tiles,
+    # none at 17 rows, for fp32 or for a K the few-row kernel does not take
+    assert lib.wfd_linear_argmax_groups(8, 32000, 2048, _lib.BF16) == 2000
+    assert lib.wfd_linear_argmax_groups(16, 2048, 2048, _lib.BF16) == 256
+    assert lib.wfd_linear_argmax_groups(17, 32000, 2048, _lib.BF16) == 0
+    assert lib.wfd_linear_argmax_groups(8, 32000, 2048, _lib.F32) == 0
+    assert lib.wfd_linear_argmax_groups(8, 32000, 128 * 49, _lib.BF16) == 0
+    rc = lib.wfd_linear_argmax(None, None, 2048, None, None, 32000, 17, 32000, 2048, 1, None, None, None)
+    assert rc == -2 and b"no column groups" in lib.wfd_last_error()
+    rc = lib.wfd_linear_argmax(None, None, 2048, None, None, 32000, 8, 32000, 2048, 1, None, None, None)
+    assert rc == -1 and b"null pointer" in lib.wfd_last_error()
+    assert lib.wfd_argmax_groups(None, None, 0, None, None, None, 0, None, None, 1, None) == -1
+    assert lib.wfd_argmax_groups(None, None, 2000, None, None, None, 0, None, None, 0, None) == 0
+    assert lib.wfd_argmax_groups(None, None, 2000, None, None, None, 0, None, None, 1, None) == -1
     assert lib.wfd_swiglu(None, 16, None, 8, 1, 12, 1, None) == -1  # F not a multiple of 8 (bf16)
     assert lib.wfd_swiglu(None, 16, None, 8, 0, 8, 1, None) == 0
     assert [lib.wfd_attn_group_max_rows(16, k) for k in (16, 8, 4, 3)] == [8, 4, 2, 0]

@@ -537,6 +537,52 @@ def test_token_ring_round_trip(gpu):
     assert torch.equal(e, table[want])
 
 
+@pytest.mark.parametrize("N", [32000, 2048, 1024])
+def test_linear_argmax_groups_same_ids_and_bits(gpu, N):
+    """lm_head with the column-group argmax: y has the bits of the plain
+    linear, and the ids (with ring and accept flags) from the group bests equal
+    wfd_argmax over y -- including ties across groups and within one group
+    (first index wins), an all-zero row (every logit +0: id 0) and a row that
+    needs the half-tile groups (N <= 4096)."""
+    g = torch.Generator().manual_seed(N)
+    K = 2048
+    W = (0.02 * torch.randn(N, K, generator=g)).to(torch.bfloat16)
+    x = torch.randn(16, K, generator=g).to(torch.bfloat16)
+    x[2] = 0
+    big = 0.05 * x.float() / x.float().norm(dim=1, keepdim=True) * math.sqrt(K)
+    j1, j2 = 16 * 3 + 5, N - 16 + 2          # different groups, row 0
+    j3, j4 = 16 * 7 + 3, 16 * 7 + 9          # one group, row 1
+    W[j1] = W[j2] = big[0].to(torch.bfloat16)
+    W[j3] = W[j4] = big[1].to(torch.bfloat16)
+    Wp = ops.pack_linear(W.to(gpu))
+    xg = x.to(gpu)
+    for n in (1, 3, 8, 16):
+        G = ops.linear_argmax_groups(n, Wp)
+        assert G == (N // 16 if N // 16 > 256 else N // 8)
+        ref = ops.linear(xg, Wp, n=n, out_dtype=torch.float32)
+        y, pv, pi = ops.linear_argmax(xg, Wp, n=n)
+        assert torch.equal(y[:n].view(torch.int32), ref[:n].view(torch.int32))
+        ids = ops.argmax_groups(pv, pi, G, n=n)
+        want = ops.argmax(ref, n=n)
+        assert ids.tolist() == want.tolist() == ref[:n].argmax(dim=-1).tolist()
+        if n >= 3:
+            assert ids[0].item() == j1 and ids[1].item() == j3 and ids[2].item() == 0
+        # ring and greedy accept flags, as wfd_argmax leaves them
+        expect = torch.tensor([want[0].item(), -2, (want[-1].item() + 1) % N] + [-(1 << 62)] * (n - 3),
+                              dtype=torch.int64, device=gpu)[:n] if n >= 3 else want[:n].clone()
+        ring_a = torch.full((9,), -7, dtype=torch.int64, device=gpu)
+        ring_a[1] = want[min(1, n - 1)]
+        ring_b = ring_a.clone()
+        rows = torch.arange(n, dtype=torch.int32, device=gpu) + 2
+        fa = torch.full((n,), -5, dtype=torch.int32, device=gpu)
+        fb = fa.clone()
+        ops.argmax(ref, n=n, ring=ring_a, ring_rows=rows, expect=expect, accept=fa)
+        ops.argmax_groups(pv, pi, G, n=n, ring=ring_b, ring_rows=rows, expect=expect, accept=fb)
+        assert fa.tolist() == fb.tolist() and torch.equal(ring_a, ring_b)
+    with pytest.raises(Exception, match="no column groups"):
+        ops.linear_argmax(torch.zeros(17, K, dtype=torch.bfloat16, device=gpu), Wp, n=17)
+
+
 def test_argmax_accept_flags_into_mapped_host_memory(gpu):
     """The greedy verify flags stored straight into mapped, coherent pinned
     host memory (what the engine polls): the same flags as into a device

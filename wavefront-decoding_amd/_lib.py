@@ -61,6 +61,9 @@ SIGNATURES: dict[str, tuple] = {
                                  _vp, _i64, _i32, _i32, _i32, _f32, _i32, _vp]),
     "wfd_copy_rows": (_i32, [_vp, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _i32, _vp]),
     "wfd_argmax": (_i32, [_vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i32, _i32, _vp]),
+    "wfd_linear_argmax_groups": (_i32, [_i32, _i32, _i32, _i32]),
+    "wfd_linear_argmax": (_i32, [_vp, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
+    "wfd_argmax_groups": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _i64, _vp, _vp, _i32, _vp]),
 }
 
 _LIB: ctypes.CDLL | None = None

@@ -386,10 +386,26 @@ __global__ __launch_bounds__(kRowThreads) void copy_rows_kernel(const T* __restr
 constexpr int kArgThreads = 1024;
 constexpr int kArgUnroll = 8;  // a 32000-entry row: 8000 16-byte loads over 1024 threads
 
-__device__ __forceinline__ void argmax_merge(float& bv, int& bi, float ov, int oi) {
-  if (ov > bv || (ov == bv && oi < bi)) {
-    bv = ov;
-    bi = oi;
+// Row i's id ix: out[i], the accept flag, the token ring.
+__device__ __forceinline__ void argmax_finish(int i, int ix, int64_t* __restrict__ out, int64_t* __restrict__ ring,
+                                              const int32_t* __restrict__ ring_rows, int64_t ring_len,
+                                              const int64_t* __restrict__ expect, int32_t* __restrict__ accept) {
+  out[i] = (int64_t)ix;
+  if (accept) {
+    // greedy acceptance on the device: the token speculated at the next
+    // position is a plain id (>= 0) or a ring handle -(slot + 1) written by
+    // an earlier pass; anything else is "nothing to compare" (reads 0)
+    const int64_t e = expect[i];
+    int64_t want = -1;
+    if (e >= 0)
+      want = e;
+    else if (ring && e >= -ring_len)
+      want = ring[-e - 1];
+    accept[i] = want == (int64_t)ix ? 1 : 0;
+  }
+  if (ring) {
+    const int32_t r = ring_rows[i];
+    if (r >= 0 && r < ring_len) ring[r] = (int64_t)ix;
   }
 }
 
@@ -442,23 +458,56 @@ __global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float* __rest
     float b = sv[0];
     int ix = si[0];
     for (int w = 1; w < kArgThreads / 64; ++w) argmax_merge(b, ix, sv[w], si[w]);
-    out[i] = (int64_t)ix;
-    if (accept) {
-      // greedy acceptance on the device: the token speculated at the next
-      // position is a plain id (>= 0) or a ring handle -(slot + 1) written by
-      // an earlier pass; anything else is "nothing to compare" (reads 0)
-      const int64_t e = expect[i];
-      int64_t want = -1;
-      if (e >= 0)
-        want = e;
-      else if (ring && e >= -ring_len)
-        want = ring[-e - 1];
-      accept[i] = want == (int64_t)ix ? 1 : 0;
+    argmax_finish(i, ix, out, ring, ring_rows, ring_len, expect, accept);
+  }
+}
+
+// The same ids from the per-column-group bests a few-row linear leaves
+// (val / idx[i * groups + s]): the merge is order-free, so merging the group
+// bests gives the first index of the row's largest value, as over the row.
+// One 256-thread workgroup per row.
+constexpr int kArgGroupThreads = 256;
+__global__ __launch_bounds__(kArgGroupThreads) void argmax_groups_kernel(
+    const float* __restrict__ val, const int32_t* __restrict__ idx, int groups, int64_t* __restrict__ out,
+    int64_t* __restrict__ ring, const int32_t* __restrict__ ring_rows, int64_t ring_len,
+    const int64_t* __restrict__ expect, int32_t* __restrict__ accept) {
+  __shared__ float sv[kArgGroupThreads / 64];
+  __shared__ int si[kArgGroupThreads / 64];
+  const int i = blockIdx.x;
+  const float* v = val + (int64_t)i * groups;
+  const int32_t* x = idx + (int64_t)i * groups;
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+  constexpr int U = 8;  // loads in flight per thread (2000 groups: one round)
+  for (int s0 = threadIdx.x; s0 < groups; s0 += kArgGroupThreads * U) {
+    float ov[U];
+    int oi[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int s = s0 + u * kArgGroupThreads;
+      ov[u] = s < groups ? v[s] : -INFINITY;
+      oi[u] = s < groups ? x[s] : 0x7fffffff;
     }
-    if (ring) {
-      const int32_t r = ring_rows[i];
-      if (r >= 0 && r < ring_len) ring[r] = (int64_t)ix;
-    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) argmax_merge(best, bi, ov[u], oi[u]);
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ov = __shfl_xor(best, m, 64);
+    const int oi = __shfl_xor(bi, m, 64);
+    argmax_merge(best, bi, ov, oi);
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    sv[wave] = best;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float b = sv[0];
+    int ix = si[0];
+    for (int w = 1; w < kArgGroupThreads / 64; ++w) argmax_merge(b, ix, sv[w], si[w]);
+    argmax_finish(i, ix, out, ring, ring_rows, ring_len, expect, accept);
   }
 }
 
@@ -490,7 +539,7 @@ extern "C" {
 
 const char* wfd_last_error(void) { return wfd::g_err; }
 
-int wfd_abi_version(void) { return 5; }
+int wfd_abi_version(void) { return 6; }
 
 int wfd_add_rmsnorm(const void* a, const int32_t* a_rows, int64_t lda, const void* res, int64_t ldr, const void* w1,
                     const void* w2, void* x_out, const int32_t* out_rows, int64_t ldo, void* h_out, int64_t ldh, int n,
@@ -764,6 +813,25 @@ int wfd_argmax(const float* logits, int64_t ld, int64_t* out, int64_t* ring, con
   hipLaunchKernelGGL(argmax_kernel, dim3(n), dim3(kArgThreads), 0, stream, logits, ld, out, ring, ring_rows,
                      ring_len, expect, accept, vocab);
   return launch_status("wfd_argmax");
+}
+
+int wfd_argmax_groups(const float* part_val, const int32_t* part_idx, int groups, int64_t* out, int64_t* ring,
+                      const int32_t* ring_rows, int64_t ring_len, const int64_t* expect, int32_t* accept, int n,
+                      hipStream_t stream) {
+  using namespace wfd;
+  if (n < 0 || groups <= 0) {
+    set_error("wfd_argmax_groups: bad shape n=%d groups=%d", n, groups);
+    return kBadArg;
+  }
+  if (n == 0) return kOk;
+  if (!part_val || !part_idx || !out || (ring && (!ring_rows || ring_len <= 0)) || (!expect != !accept)) {
+    set_error("wfd_argmax_groups: null pointer argument (ring needs ring_rows and a length; expect and accept go "
+              "together)");
+    return kBadArg;
+  }
+  hipLaunchKernelGGL(argmax_groups_kernel, dim3(n), dim3(kArgGroupThreads), 0, stream, part_val, part_idx, groups,
+                     out, ring, ring_rows, ring_len, expect, accept);
+  return launch_status("wfd_argmax_groups");
 }
 
 }  // extern "C"

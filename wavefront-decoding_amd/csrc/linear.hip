@@ -69,6 +69,8 @@
 // straight into the slot cache row flat_row[m] (src/decoding/huginn_blocks.py:77-87
 // + kv_cache.py:97-104 fused into the projection; the separate qkv_rope_append
 // pass and its qkv round trip vanish).
+#include <type_traits>
+
 #include "wfd_common.h"
 
 namespace wfd {
@@ -158,6 +160,14 @@ struct RopeArgs {
   void* v_cache;
   int64_t block_rows;       // cache layout (kv_offset)
   int H, Hkv, Dh;
+};
+
+// Optional output of the few-row kernel (plain epilogue, fp32 y): per row m
+// and column group s (the workgroup: a tile, or half a tile), the first
+// largest value of y[m, group s] and its column at val / idx[m * groups + s].
+struct TileArgmax {
+  float* val;
+  int32_t* idx;
 };
 
 template <typename T>
@@ -428,7 +438,7 @@ __device__ __forceinline__ void chunk_mma(f32x4 (&acc)[NT], const u32x4 (&xf)[kC
 template <typename T, typename TO, int EPI, int RM, bool HALF, int WW>
 __global__ __launch_bounds__(64 * WW) void linear_wide_kernel(
     const T* __restrict__ x, const int32_t* __restrict__ x_rows, int64_t ldx, const T* __restrict__ W,
-    TO* __restrict__ y, int64_t ldy, int n, int K, int pair_off, const RopeArgs ra) {
+    TO* __restrict__ y, int64_t ldy, int n, int K, int pair_off, const RopeArgs ra, const TileArgmax am) {
   constexpr int KPW = kSlices * kSubSlices / WW;  // sub-slices per wave
   static_assert(KPW * WW == kSlices * kSubSlices, "16 or 8 waves");
   __shared__ f32x4 red[kSlices * kSubSlices][64];  // sub-slice sums [sub-slice][lane]
@@ -534,8 +544,26 @@ __global__ __launch_bounds__(64 * WW) void linear_wide_kernel(
     const float partner = EPI == kEpiRope     ? __shfl_xor(v, 4, 64)
                           : EPI == kEpiSwiGLU ? __shfl_xor(v, 32, 64)
                                               : 0.f;
-    if (row < n && (!HALF || ((ln & 15) >> 3) == half))
-      store_out<TO, EPI>(y, ldy, ra, row, g, ln & 15, v, partner, rp);
+    const bool mine = !HALF || ((ln & 15) >> 3) == half;
+    if (row < n && mine) store_out<TO, EPI>(y, ldy, ra, row, g, ln & 15, v, partner, rp);
+    if constexpr (EPI == kEpiPlain && std::is_same<TO, float>::value) {
+      if (am.val) {  // uniform
+        // a row's 16 columns sit in lanes 4 c + r of this wave (c = ln & 15)
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+        if (mine) argmax_merge(bv, bi, v, 16 * g + (ln & 15));
+#pragma unroll
+        for (int m = 4; m < 64; m <<= 1) {
+          const float ov = __shfl_xor(bv, m, 64);
+          const int oi = __shfl_xor(bi, m, 64);
+          argmax_merge(bv, bi, ov, oi);
+        }
+        if (row < n && (ln & 15) == 0) {
+          am.val[(int64_t)row * gridDim.x + blockIdx.x] = bv;
+          am.idx[(int64_t)row * gridDim.x + blockIdx.x] = bi;
+        }
+      }
+    }
   }
 }
 
@@ -994,32 +1022,46 @@ __global__ __launch_bounds__(256) void linear_stream_kernel(const T* __restrict_
   }
 }
 
-template <typename T, typename TO, int EPI>
-static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const void* W, void* y, int64_t ldy, int n,
-                          int N, int K, int pair_off, const RopeArgs& ra, hipStream_t st) {
-  const int tiles = N / 16;
-  const int P = K / LinTraits<T>::KC;
-  const int R = sub_chunks(P);  // chunks per sub-slice: one sub-slice per wave (two with 8 waves)
-  const bool wide = n <= kWideMaxRows && R <= kWideMaxChunksPerWave;
+// The few-row regime's launch shape for n rows, `tiles` 16-column tiles and R
+// chunks per sub-slice.
+struct WidePlan {
+  bool wide, half, ww8;
+  int groups;  // workgroups of the few-row launch (0 if not few-row)
+};
+static WidePlan wide_plan(int n, int tiles, int R, bool swiglu) {
+  WidePlan w;
+  w.wide = n <= kWideMaxRows && R <= kWideMaxChunksPerWave;
   // fewer tiles than half the chip's 256 CUs x 2: split tiles into column halves
   // (not for SwiGLU, whose partner column c ^ 8 lies in the other half)
-  const bool half = EPI != kEpiSwiGLU && tiles <= kHalfTileMax;
+  w.half = !swiglu && tiles <= kHalfTileMax;
   // more tiles than two 1024-thread workgroups per CU hold: 8-wave workgroups
   // (three per CU by their 48 KB of LDS), so the whole launch is resident in
   // one round (gate|up at 704 tiles: 11.5 -> 10.4 us); each wave then sums
   // two sub-slices, so only for one chunk per sub-slice (K <= 16 chunks)
-  const bool ww8 = !half && tiles > kResidentWide && R == 1;
+  w.ww8 = !w.half && tiles > kResidentWide && R == 1;
+  w.groups = w.wide ? (w.half ? 2 * tiles : tiles) : 0;
+  return w;
+}
+
+template <typename T, typename TO, int EPI>
+static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const void* W, void* y, int64_t ldy, int n,
+                          int N, int K, int pair_off, const RopeArgs& ra, hipStream_t st,
+                          const TileArgmax& am = TileArgmax{nullptr, nullptr}) {
+  const int tiles = N / 16;
+  const int R = sub_chunks(K / LinTraits<T>::KC);  // chunks per sub-slice: one sub-slice per wave (two with 8 waves)
+  const WidePlan wp = wide_plan(n, tiles, R, EPI == kEpiSwiGLU);
+  const bool wide = wp.wide, half = wp.half, ww8 = wp.ww8;
 #define WFD_WIDE(RMV)                                                                                             \
   if (half)                                                                                                       \
     hipLaunchKernelGGL((linear_wide_kernel<T, TO, EPI, RMV, true, kWideWaves>), dim3(2 * tiles),                 \
                        dim3(64 * kWideWaves), 0, st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K,       \
-                       pair_off, ra);                                                                             \
+                       pair_off, ra, am);                                                                         \
   else                                                                                                            \
     hipLaunchKernelGGL((linear_wide_kernel<T, TO, EPI, RMV, false, kWideWaves>), dim3(tiles), dim3(64 * kWideWaves), \
-                       0, st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra);
+                       0, st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra, am);
 #define WFD_WIDE8(RMV)                                                                                          \
   hipLaunchKernelGGL((linear_wide_kernel<T, TO, EPI, RMV, false, 8>), dim3(tiles), dim3(64 * 8), 0, st,        \
-                     (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra);
+                     (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra, am);
   if (wide && ww8) {
     WFD_WIDE8(1)
   } else if (wide && R == 1) {
@@ -1242,6 +1284,47 @@ int wfd_linear(const void* x, const int32_t* x_rows, int64_t ldx, const void* W,
     return kUnsupported;
   }
   return launch_status("wfd_linear");
+}
+
+int wfd_linear_argmax_groups(int n, int N, int K, int dtype) {
+  using namespace wfd;
+  if (n <= 0 || N <= 0 || N % 16 != 0 || dtype != kBF16 || K <= 0 || K % wfd_linear_k_multiple(dtype) != 0) return 0;
+  return wide_plan(n, N / 16, sub_chunks(K / LinTraits<bf16_t>::KC), false).groups;
+}
+
+int wfd_linear_argmax(const void* x, const int32_t* x_rows, int64_t ldx, const void* W, float* y, int64_t ldy, int n,
+                      int N, int K, int dtype, float* part_val, int32_t* part_idx, hipStream_t stream) {
+  using namespace wfd;
+  if (n <= 0 || N <= 0 || K <= 0 || ldx < K) {
+    set_error("wfd_linear_argmax: bad shape n=%d N=%d K=%d ldx=%lld", n, N, K, (long long)ldx);
+    return kBadArg;
+  }
+  if (wfd_linear_argmax_groups(n, N, K, dtype) <= 0) {
+    set_error("wfd_linear_argmax: n=%d N=%d K=%d dtype=%d is not a few-row bf16 launch (no column groups)", n, N, K,
+              dtype);
+    return kUnsupported;
+  }
+  if (!x || !W || !y || !part_val || !part_idx) {
+    set_error("wfd_linear_argmax: null pointer argument");
+    return kBadArg;
+  }
+  const int64_t esz = 2;
+  if (!x_rows && (int64_t)n * ldx * esz >= (int64_t)kBufInvalid) {
+    set_error("wfd_linear_argmax: the x operand must span less than 2 GiB");
+    return kBadArg;
+  }
+  if ((((uintptr_t)x | (uintptr_t)W) & 15) || ((ldx * esz) & 15)) {
+    set_error("wfd_linear_argmax: x rows and W must be 16-byte aligned (ldx=%lld)", (long long)ldx);
+    return kBadArg;
+  }
+  if (ldy < N) {
+    set_error("wfd_linear_argmax: ldy=%lld < N=%d", (long long)ldy, N);
+    return kBadArg;
+  }
+  const RopeArgs ra{};
+  launch_linear<bf16_t, float, kEpiPlain>(x, x_rows, ldx, W, y, ldy, n, N, K, 0, ra, stream,
+                                          TileArgmax{part_val, part_idx});
+  return launch_status("wfd_linear_argmax");
 }
 
 int wfd_linear_qkv_rope_append(const void* x, const int32_t* x_rows, int64_t ldx, const void* Wqkv, int n, int K,

@@ -202,4 +202,15 @@ __device__ __forceinline__ float wave_sum(float v) {
 namespace wfd {
 void set_error(const char* fmt, ...);
 int launch_status(const char* what);
+
+// Greedy argmax step: (ov, oi) replaces (bv, bi) if larger, or equal with a
+// lower index. Starting from (-inf, INT_MAX) a NaN never enters, so merging
+// in any order and grouping gives the first index of the largest value.
+__device__ __forceinline__ void argmax_merge(float& bv, int& bi, float ov, int oi) {
+  if (ov > bv || (ov == bv && oi < bi)) {
+    bv = ov;
+    bi = oi;
+  }
+}
+
 }  // namespace wfd

@@ -212,6 +212,9 @@ class LoopedModel:
         self.sc = self._scratch(self.max_rows)
         self.sc["logits"] = torch.empty(self.max_rows, cfg.vocab_size, dtype=torch.float32, device=self.device)
         self.sc["ids"] = torch.empty(self.max_rows, dtype=torch.int64, device=self.device)
+        # column-group argmax bests of a few-row lm_head (at most 16 rows x N / 8 groups)
+        self.sc["am_val"] = torch.empty(2 * cfg.vocab_size, dtype=torch.float32, device=self.device)
+        self.sc["am_idx"] = torch.empty(2 * cfg.vocab_size, dtype=torch.int32, device=self.device)
         self.attn_ws = torch.zeros(ops.attn_workspace_bytes(self.max_rows, cfg.n_heads, cfg.head_dim, max_seq_len),
                                    dtype=torch.uint8, device=self.device)
         self.staging = _Staging(self.device)
@@ -403,9 +406,16 @@ class LoopedModel:
                 nxt = W[f"coda.{i + 1}.norm_1"] if i + 1 < L else W["ln_f"]
                 self._block(f"coda.{i}.", nb, sc, pos_d, kvlen_d, rb(i), fr(i), kv_max, ws, cache, nxt,
                             group_first=gf)
-            ops.linear(sc["h"], W["lm_head"], n=nb, out=sc["logits"], out_dtype=torch.float32)
-            ops.argmax(sc["logits"], n=nb, out=sc["ids"], ring=self.tok_ring, ring_rows=t32[3 * nb: 4 * nb],
-                       expect=t64[2 * L * nb: 2 * L * nb + nb], accept_mapped=(self._flags_dev, self.max_rows))
+            am = dict(out=sc["ids"], ring=self.tok_ring, ring_rows=t32[3 * nb: 4 * nb],
+                      expect=t64[2 * L * nb: 2 * L * nb + nb], accept_mapped=(self._flags_dev, self.max_rows))
+            G = ops.linear_argmax_groups(nb, W["lm_head"]) if W["lm_head"].dtype == torch.bfloat16 else 0
+            if G > 0:  # few rows: the argmax reads each 16-column group's best, not the whole vocabulary
+                ops.linear_argmax(sc["h"], W["lm_head"], n=nb, out=sc["logits"], part_val=sc["am_val"],
+                                  part_idx=sc["am_idx"])
+                ops.argmax_groups(sc["am_val"], sc["am_idx"], G, n=nb, **am)
+            else:
+                ops.linear(sc["h"], W["lm_head"], n=nb, out=sc["logits"], out_dtype=torch.float32)
+                ops.argmax(sc["logits"], n=nb, **am)
 
     # -- a tick: row tables, upload, launch -------------------------------------------
     def _tick_params(self, cache) -> tuple:

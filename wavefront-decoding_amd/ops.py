@@ -538,12 +538,22 @@ def argmax(logits: torch.Tensor, *, n: int | None = None, out: torch.Tensor | No
     _need(logits.dtype == torch.float32 and logits.dim() == 2 and logits.stride(1) == 1, "logits: float32 (n, V)")
     n = logits.shape[0] if n is None else n
     _need(0 <= n <= logits.shape[0], f"n={n} outside the {logits.shape[0]} logits rows")
+    out, acc = _argmax_outputs(n, logits.device, out, ring, ring_rows, expect, accept, accept_mapped)
+    rc = _lib.load().wfd_argmax(logits.data_ptr(), logits.stride(0), out.data_ptr(), _p(ring), _p(ring_rows),
+                                ring.numel() if ring is not None else 0, _p(expect), acc, n, logits.shape[1],
+                                _stream())
+    _lib.check(rc, "wfd_argmax")
+    return out
+
+
+def _argmax_outputs(n, device, out, ring, ring_rows, expect, accept, accept_mapped):
+    """Checks argmax's ring / expect / accept operands; returns (out, accept address)."""
     if ring is not None:
         _need(ring.dtype == torch.int64 and ring.is_contiguous(), "ring: int64 contiguous")
         _rows(ring_rows, n, "ring_rows")
         _need(ring_rows is not None, "ring needs ring_rows")
     if out is None:
-        out = torch.empty(n, dtype=torch.int64, device=logits.device)
+        out = torch.empty(n, dtype=torch.int64, device=device)
     _need(out.dtype == torch.int64 and out.is_contiguous() and out.numel() >= n, "out: int64 (>= n,)")
     _need(accept is None or accept_mapped is None, "accept or accept_mapped, not both")
     _need((expect is None) == (accept is None and accept_mapped is None), "expect and accept go together")
@@ -556,8 +566,68 @@ def argmax(logits: torch.Tensor, *, n: int | None = None, out: torch.Tensor | No
             _need(accept_mapped[0] != 0 and accept_mapped[0] % 4 == 0 and accept_mapped[1] >= n,
                   "accept_mapped: (aligned device address, capacity >= n)")
     acc = _p(accept) if accept is not None else (accept_mapped[0] if accept_mapped is not None else None)
-    rc = _lib.load().wfd_argmax(logits.data_ptr(), logits.stride(0), out.data_ptr(), _p(ring), _p(ring_rows),
-                                ring.numel() if ring is not None else 0, _p(expect), acc, n, logits.shape[1],
-                                _stream())
-    _lib.check(rc, "wfd_argmax")
+    return out, acc
+
+
+def linear_argmax_groups(n: int, W) -> int:
+    """Column groups per row that linear_argmax leaves for n rows of the
+    packed plain weight W (0 where the few-row kernel would not run)."""
+    Wp = _packed(W, False)
+    return int(_lib.load().wfd_linear_argmax_groups(n, Wp.N, Wp.K, _DT[Wp.dtype]))
+
+
+def linear_argmax(x: torch.Tensor, W, *, n: int | None = None, x_rows: torch.Tensor | None = None,
+                  out: torch.Tensor | None = None, part_val: torch.Tensor | None = None,
+                  part_idx: torch.Tensor | None = None):
+    """linear(x, W, out_dtype=float32) for bf16 x / W -- the same kernel, so
+    the same bits -- that also leaves, per row and column group (G =
+    linear_argmax_groups(n, W)), the first largest logit and its column in
+    part_val / part_idx (m * G + s). Returns (out, part_val, part_idx)."""
+    _need_cuda(x, x_rows, out, part_val, part_idx)
+    Wp = _packed(W, False)
+    _need_cuda(Wp.data)
+    _need(x.dim() == 2 and x.stride(1) == 1 and x.dtype == torch.bfloat16 and Wp.dtype == torch.bfloat16,
+          "x (rows, K+) and W bf16")
+    N, K = Wp.N, Wp.K
+    n = x.shape[0] if (n is None and x_rows is None) else (n if n is not None else x_rows.numel())
+    _rows(x_rows, n, "x_rows")
+    _need(x.shape[1] >= K, f"x width {x.shape[1]} < K={K}")
+    _need(n >= 1 and (x_rows is not None or x.shape[0] >= n), f"x holds {x.shape[0]} rows < n={n}")
+    G = linear_argmax_groups(n, Wp)
+    _need(G > 0, f"n={n} N={N} K={K}: not a few-row launch (no column groups)")
+    if out is None:
+        out = torch.empty(n, N, dtype=torch.float32, device=x.device)
+    _need(out.dim() == 2 and out.stride(1) == 1 and out.shape[0] >= n and out.shape[1] >= N
+          and out.dtype == torch.float32, "out: float32 (>= n, >= N)")
+    if part_val is None:
+        part_val = torch.empty(n * G, dtype=torch.float32, device=x.device)
+    if part_idx is None:
+        part_idx = torch.empty(n * G, dtype=torch.int32, device=x.device)
+    _need(part_val.dtype == torch.float32 and part_val.is_contiguous() and part_val.numel() >= n * G,
+          f"part_val: float32 (>= {n * G},)")
+    _need(part_idx.dtype == torch.int32 and part_idx.is_contiguous() and part_idx.numel() >= n * G,
+          f"part_idx: int32 (>= {n * G},)")
+    rc = _lib.load().wfd_linear_argmax(x.data_ptr(), _p(x_rows), x.stride(0), Wp.data.data_ptr(), out.data_ptr(),
+                                       out.stride(0), n, N, K, _dt(x), part_val.data_ptr(), part_idx.data_ptr(),
+                                       _stream())
+    _lib.check(rc, "wfd_linear_argmax")
+    return out, part_val, part_idx
+
+
+def argmax_groups(part_val: torch.Tensor, part_idx: torch.Tensor, groups: int, *, n: int,
+                  out: torch.Tensor | None = None, ring: torch.Tensor | None = None,
+                  ring_rows: torch.Tensor | None = None, expect: torch.Tensor | None = None,
+                  accept: torch.Tensor | None = None, accept_mapped: tuple[int, int] | None = None) -> torch.Tensor:
+    """argmax from the column-group bests linear_argmax left (`groups` per
+    row): the same ids, ring and accept flags as argmax over the logits."""
+    _need_cuda(part_val, part_idx, out, ring, ring_rows, expect, accept)
+    _need(n >= 0 and groups >= 1, f"n={n} groups={groups}")
+    _need(part_val.dtype == torch.float32 and part_val.is_contiguous() and part_val.numel() >= n * groups
+          and part_idx.dtype == torch.int32 and part_idx.is_contiguous() and part_idx.numel() >= n * groups,
+          f"part_val float32 / part_idx int32 (>= {n * groups},)")
+    out, acc = _argmax_outputs(n, part_val.device, out, ring, ring_rows, expect, accept, accept_mapped)
+    rc = _lib.load().wfd_argmax_groups(part_val.data_ptr(), part_idx.data_ptr(), groups, out.data_ptr(), _p(ring),
+                                       _p(ring_rows), ring.numel() if ring is not None else 0, _p(expect), acc, n,
+                                       _stream())
+    _lib.check(rc, "wfd_argmax_groups")
     return out
