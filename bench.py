@@ -62,7 +62,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--quick", action="store_true", help="fewer extras (development)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--only", default="", help="comma list of sections: bs1,roofline,attn,linrows,bs32,prefill,c5,gqa,cpu")
+    ap.add_argument("--only", default="", help="comma list of sections: bs1,roofline,attn,linrows,bs32,prefill,c5,gqa,cpu (and the opt-in attnkeys)")
     ap.add_argument("--eager", action="store_true", help="launch every pass eagerly (no hipGraph capture)")
     return ap.parse_args()
 
@@ -445,6 +445,24 @@ def attn_section(args, dev, res):
     _calibration_copy(dev)
 
 
+def attnkeys_section(args, dev, res):
+    """Opt-in (`--only attnkeys`): the bs=1 tick's attention launch (8 rows x
+    16 heads x Dh 128, two column halves: 256 workgroups) with every row at
+    the same key count, from 1 key up, and one row alone. The 1-key launch is
+    the launch's fixed part (dispatch, the row-table and first K/V loads, the
+    wave merge, the store); each further round of 8 waves x 32-key tiles
+    adds its bytes at the rate the chip streams them."""
+    out = {}
+    for L in (1, 32, 64, 128, 256, 512, 650, 1024):
+        us, by = attn_bench(dev, 8, 16, 16, 128, [L] * 8)
+        out[f"tick8_L{L}"] = {"us": round(us, 2), "GBs": round(by / us / 1e3, 1)}
+    for L in (1, 256, 650, 1024):
+        us, by = attn_bench(dev, 1, 16, 16, 128, [L])
+        out[f"row1_L{L}"] = {"us": round(us, 2), "GBs": round(by / us / 1e3, 1)}
+    res["extra"]["attention_key_sweep"] = out
+    log(f"attnkeys: {out}")
+
+
 def gqa_section(args, dev, res):
     """Long-context GQA decode: one R tick for 4 sequences x W=16 rows over a
     32k random-filled prompt cache (prefill of 4 x 32k prompts is out of scope)."""
@@ -774,6 +792,8 @@ def main():
         c5_section(args, dev, res)
     if want("gqa"):
         gqa_section(args, dev, res)
+    if "attnkeys" in only:  # opt-in only: not part of the default run
+        attnkeys_section(args, dev, res)
     if want("cpu") and not args.no_cpu:
         cpu_section(args, res, w)
     print(json.dumps(res))
