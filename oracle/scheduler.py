@@ -10,7 +10,8 @@ LM of oracle/looped_lm.py.
   ar_batch    src/decoding/scheduler_batch.py:185-222
   wfd_single  src/decoding/scheduler.py:88-224 with the R_dyn routing of
               src/decoding/parcae_blocks.py:540-581 and the C_multi_dyn
-              ordering of parcae_blocks.py:583-597
+              ordering of parcae_blocks.py:583-597; emulated acceptance as
+              src/decoding/scheduler_emu.py:33-155
   ar_single   src/decoding/ar_baseline.py:133-193
 """
 from __future__ import annotations
@@ -241,8 +242,11 @@ def ar_batch(blocks, prompts, max_new_tokens, T_total: int) -> BatchResult:
     return res
 
 
-def wfd_single(blocks, prompt, max_new_tokens: int, T_total: int, T_draft: int) -> Counters:
-    """B = 1 dynamic loop; returns the counters (tokens in .tokens)."""
+def wfd_single(blocks, prompt, max_new_tokens: int, T_total: int, T_draft: int, emu=None,
+               eos: int | None = None) -> Counters:
+    """B = 1 dynamic loop; returns the counters (tokens in .tokens). With
+    `emu` each accept is its next draw (src/decoding/scheduler_emu.py:33-155);
+    `eos` stops at a committed eos token, the first included."""
     cache, first = _first_tokens(blocks, [prompt])
     L = _lens([prompt])[0]
     c = Counters()
@@ -258,7 +262,7 @@ def wfd_single(blocks, prompt, max_new_tokens: int, T_total: int, T_draft: int) 
         return None
 
     c.tokens.append(first[0])
-    if len(c.tokens) >= max_new_tokens:
+    if len(c.tokens) >= max_new_tokens or first[0] == eos:
         return c
     P.append(Tok(first[0], L, "draft"))
     c.n_p_calls += 1
@@ -308,7 +312,7 @@ def wfd_single(blocks, prompt, max_new_tokens: int, T_total: int, T_draft: int) 
                 c.n_p_calls += 1
             else:
                 c.n_drafts_proposed += 1
-                if gold[i] == nxt.token_id:
+                if (gold[i] == nxt.token_id) if emu is None else emu.draw():
                     c.n_drafts_accepted += 1
                     c.tokens.append(nxt.token_id)
                 else:
@@ -322,7 +326,7 @@ def wfd_single(blocks, prompt, max_new_tokens: int, T_total: int, T_draft: int) 
                     cache.drop_positions_at_and_after(0, np_)
                     P.append(Tok(gold[i], np_, "draft"))
                     c.n_p_calls += 1
-            stop = len(c.tokens) >= max_new_tokens
+            stop = len(c.tokens) >= max_new_tokens or c.tokens[-1] == eos
             if stop or rej or nxt is None:
                 break
         if stop:

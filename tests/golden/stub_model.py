@@ -11,6 +11,8 @@ see the same model and must produce the same traces.
 """
 from __future__ import annotations
 
+import copy
+
 import torch
 
 MASK64 = (1 << 64) - 1
@@ -106,4 +108,126 @@ def trace_record(bt, blocks: StubBatchBlocks, cache: StubCache | None, emus) -> 
         "drops": [list(d) for d in cache.drops] if cache is not None else [],
         "calls": [[k, [list(x) for x in rows]] for k, rows in blocks.calls],
         "emu": [[e.n_draws, e.n_accepts] for e in emus] if emus else None,
+    }
+
+
+class StubSingleCache:
+    """Single-sequence cache stand-in: a rollback at `position` is recorded as
+    (0, position) on the batch stub's cache."""
+
+    def __init__(self, inner: StubCache):
+        self.inner = inner
+
+    def drop_positions_at_and_after(self, position: int) -> None:
+        self.inner.drop_positions_at_and_after(0, position)
+
+
+class _Seed:
+    """What the stub's prelude fills for one token (prelude_forward's row)."""
+
+    def __init__(self, token_id: int, position: int):
+        self.token_id = token_id
+        self.position = position
+
+
+class StubRecursiveBlocks:
+    """The single-sequence block interface a dynamic WFD scheduler drives
+    (prefill, P_dyn, R_dyn, C_multi_dyn; prelude_forward, advance_one_step,
+    coda_logits for draft-then-verify) over the stub model at B = 1, with
+    the routing that interface documents (src/decoding/blocks.py:46-66):
+    R advances every alive active_r token one step; the position-ordered
+    prefix of tokens at step == T_total is promoted to "verify" and moved to
+    active_c; a token at step == T_draft is copied there as "draft". C returns
+    one-hot logits (verifies in position order, then the draft).
+
+    Mixed into a scheduler's own abstract blocks class: `state_cls` is that
+    scheduler's WavefrontState."""
+
+    state_cls = None
+
+    def __init__(self, T_total: int, agree_pct: int = 70):
+        self.stub = StubBatchBlocks(T_total, 1, agree_pct=agree_pct)
+        self.T_total = T_total
+
+    def _onehot(self, tok: int) -> torch.Tensor:
+        v = torch.zeros(self.stub.vocab)
+        v[tok] = 1.0
+        return v
+
+    def prefill(self, input_ids, T_total, T_draft):
+        ids = torch.as_tensor(input_ids).reshape(-1)
+        cache, logits = self.stub.prefill([ids])
+        state = self.state_cls(prefix_len=len(ids), kv_cache=StubSingleCache(cache), T_total=T_total,
+                               T_draft=T_draft, last_committed_position=len(ids) - 1)
+        return state, logits[0]
+
+    def P_dyn(self, state):
+        if state.active_p:
+            self.stub.prelude_union([0] * len(state.active_p), state.active_p, state.kv_cache)
+        state.active_r.extend(state.active_p)
+        state.active_p = []
+        return state, True
+
+    def R_dyn(self, state):
+        toks = [t for t in state.active_r if t.is_alive]
+        if toks:
+            self.stub.advance_union([0] * len(toks), toks, state.kv_cache)
+        front = []
+        for t in sorted(toks, key=lambda t: t.position):
+            if t.step != state.T_total:
+                break
+            front.append(t)
+        moved = {id(t) for t in front}
+        keep, any_c = [], False
+        for t in toks:
+            if id(t) in moved:
+                t.role = "verify"
+                state.active_c.append(t)
+                any_c = True
+                continue
+            keep.append(t)
+            if t.step == state.T_draft:
+                c = copy.copy(t)
+                c.role = "draft"
+                state.active_c.append(c)
+                any_c = True
+        state.active_r = keep
+        return state, any_c
+
+    def C_multi_dyn(self, state):
+        verify = sorted((t for t in state.active_c if t.role == "verify"), key=lambda t: t.position)
+        draft = [t for t in state.active_c if t.role == "draft"]
+        rows = verify + draft
+        if not rows:
+            return state, 0, []
+        ids = self.stub.coda_argmax_union([0] * len(rows), rows, state.kv_cache)
+        return state, len(verify), [self._onehot(i) for i in ids]
+
+    def ar_generate(self, prompt_ids, max_new_tokens, eos_token_id=None, sampler=None):
+        raise NotImplementedError("the stub model serves the WFD and draft-then-verify schedulers only")
+
+    def prelude_forward(self, cache, token_id: int, position: int):
+        row = _Seed(token_id, position)
+        self.stub.prelude_union([0], [row], cache)
+        return row.hidden, row.static_state
+
+    def advance_one_step(self, toks, cache) -> None:
+        if toks:
+            self.stub.advance_union([0] * len(toks), toks, cache)
+
+    def coda_logits(self, state, toks):
+        return [self._onehot(i) for i in self.stub.coda_argmax_union([0] * len(toks), toks, None)]
+
+
+def single_record(tokens, trace, blocks: StubRecursiveBlocks, emu, keep_calls: bool) -> dict:
+    """What a single-sequence trace pins: tokens, counters, rollbacks, the
+    per-call (pos, step) schedule (short runs) and the emulated draws."""
+    cache = blocks.stub.last_cache
+    return {
+        "tokens": list(tokens),
+        "counters": {k: getattr(trace, k) for k in ("n_r_calls", "n_p_calls", "n_c_calls", "n_drafts_proposed",
+                                                    "n_drafts_accepted", "n_drafts_rejected", "n_rollback_events")},
+        "drops": [list(d) for d in cache.drops] if cache is not None else [],
+        "calls": [[k, [list(x) for x in rows]] for k, rows in blocks.stub.calls] if keep_calls else None,
+        "emu": [emu.n_draws, emu.n_accepts] if emu is not None else None,
     }

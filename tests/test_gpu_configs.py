@@ -10,14 +10,17 @@ or against sequential decode (GPU).
   model: a mix of accepts and rejects); WFD and draft-then-verify still
   commit exactly the sequential tokens, eager and captured.
 * C3 (2048-d bf16, 512-token prompt): greedy WFD with T_draft = 2 (W = 8) for
-  64 tokens commits exactly the sequential tokens, eager and captured, on the
-  random-init model (drafts rejected) and on the accepting variant.
-* C4 (2048-d bf16, B = 32, ragged prompts): the reference's batch gates
-  (experiments/exp4_emu/verify_batch.py:88-141): each sequence's tokens and
-  counters equal its solo run (emulated alpha = 0.7), replicas of one prompt
-  commit the same tokens, alpha = 0 next to alpha = 1 leaves the alpha = 1
-  sequence untouched, batch prefill equals single-sequence prefill, AR R calls
-  = (N - 1) T_total, and real greedy batch WFD equals sequential decode.
+  all 256 tokens commits exactly the sequential tokens, eager and captured, on
+  the random-init model (drafts rejected) and on the accepting variant.
+* C4 (2048-d bf16, B = 32, prompts U[128, 2048], generation U[64, 512]): the
+  reference's batch gates (experiments/exp4_emu/verify_batch.py:88-141) over
+  the whole workload: each sequence's tokens and counters equal its solo run
+  (emulated alpha = 0.9 and 0.5), replicas of one prompt commit the same
+  tokens, alpha = 0 next to alpha = 1 leaves the alpha = 1 sequence
+  untouched, batch prefill equals single-sequence prefill, AR R calls =
+  (N - 1) T_total, and real greedy batch WFD equals lockstep sequential
+  decode; one ragged 256-row R tick (multi-split prefixes, grouped rows)
+  against the oracle.
 * C5 (GQA 16 q / 4 kv, Dh 128): decode attention over 32k-key prefixes
   (33 splits + the combine) against the oracle, and one R tick of the GQA
   model (16 rows at depths 0..30) against the oracle.
@@ -40,7 +43,7 @@ from wavefront_decoding_amd.emu import EmulatedAcceptance
 from wavefront_decoding_amd.engine import LoopedModel
 from wavefront_decoding_amd.policy import SsdPolicy
 from wavefront_decoding_amd.scheduler import generate_draft_then_verify, generate_wavefront_dynamic
-from wavefront_decoding_amd.scheduler_batch import ar_generate_batch, generate_wavefront_batch
+from wavefront_decoding_amd.scheduler_batch import ar_generate_batch, generate_wavefront_batch, prefill_once
 
 pytestmark = pytest.mark.gpu
 
@@ -196,11 +199,11 @@ def w2048():
 
 @pytest.mark.parametrize("variant", ["random_init", "accepting"])
 def test_c3_greedy_wfd_is_lossless(gpu, w2048, variant):
-    """64 tokens of greedy WFD (T_total 16, T_draft 2) from the 512-token
-    prompt equal sequential looped decode, eager and captured."""
+    """All 256 tokens of greedy WFD (T_total 16, T_draft 2) from the
+    512-token prompt equal sequential looped decode, eager and captured."""
     w = w2048 if variant == "random_init" else accepting(C3, w2048, 0.0)
     ids = _prompt(512, 0, C3.vocab_size).to(gpu)
-    N = 64
+    N = 256
     ref = None
     for graphs in (False, True):
         print(f"[C3] {variant} graphs={graphs}", flush=True)
@@ -222,74 +225,160 @@ def test_c3_greedy_wfd_is_lossless(gpu, w2048, variant):
 
 
 # ---------------------------------------------------------------------------
-# C4: the 2048-d model at B = 32, ragged prompts
+# C4: the 2048-d model at B = 32, prompts U[128, 2048], generation U[64, 512]
+# (seed 0): the workload the bs=32 benchmark decodes
 # ---------------------------------------------------------------------------
 B4 = 32
 
 
+def c4_workload(seed: int = 0):
+    """(prompt lengths, generation lengths, prompts) of the B = 32 workload."""
+    g = torch.Generator().manual_seed(seed)
+    plen = torch.randint(128, 2049, (B4,), generator=g).tolist()
+    glen = torch.randint(64, 513, (B4,), generator=g).tolist()
+    prompts = [torch.randint(0, C3.vocab_size, (p,), generator=g) for p in plen]
+    return plen, glen, prompts
+
+
 @pytest.fixture(scope="module")
 def c4(gpu, w2048):
-    g = torch.Generator().manual_seed(0)
-    plen = torch.randint(16, 97, (B4,), generator=g).tolist()
-    glen = torch.randint(8, 25, (B4,), generator=g).tolist()
-    prompts = [torch.randint(0, C3.vocab_size, (p,), generator=g).to(gpu) for p in plen]
-    model = LoopedModel(C3, w2048, gpu, max_seq_len=max(plen) + max(glen) + 16, max_batch=B4)
-    yield model, prompts, glen
-    del model
+    plen, glen, prompts = c4_workload()
+    prompts = [p.to(gpu) for p in prompts]
+    model = LoopedModel(C3, w2048, gpu, max_seq_len=max(plen) + max(glen) + 16, max_batch=B4, use_graphs=True)
+    bb = LoopedBlocksBatch(model, batch_size=B4)
+    print(f"[C4] prefill of {sum(plen)} prompt tokens ({min(plen)}-{max(plen)} per sequence)", flush=True)
+    pf = prefill_once(bb, prompts)
+    yield model, bb, pf, prompts, glen
+    del model, bb, pf
     torch.cuda.empty_cache()
 
 
-def test_c4_batch_equals_solo_runs(gpu, c4):
-    """Emulated alpha = 0.7 (seeds 1000 + b): every sequence of the 32-wide
-    batch commits its solo run's tokens with its solo run's counters."""
-    model, prompts, glen = c4
+@pytest.mark.parametrize("alpha", [0.9, 0.5])
+def test_c4_batch_equals_solo_runs(gpu, c4, alpha):
+    """Emulated acceptance (seeds 1000 + b): every sequence of the 32-wide
+    batch commits its solo run's tokens with its solo run's counters, over
+    the whole generation (64-512 tokens after a 128-2048-token prompt)."""
+    model, bb, pf, prompts, glen = c4
     policy = SsdPolicy(C3.T_total, 2)
-    print("[C4] batch of 32", flush=True)
-    bt = generate_wavefront_batch(LoopedBlocksBatch(model, batch_size=B4), prompts, glen, policy,
-                                  [EmulatedAcceptance(0.7, 1000 + b) for b in range(B4)])
+    print(f"[C4] batch of 32, alpha={alpha}", flush=True)
+    bt = generate_wavefront_batch(bb, prompts, glen, policy, [EmulatedAcceptance(alpha, 1000 + b) for b in range(B4)],
+                                  prefilled=pf)
     assert bt.r_union_max > 100  # the sequences' waves really shared unions
+    assert [len(t.tokens) for t in bt.per_seq] == glen
     solo_blocks = LoopedBlocksBatch(model, batch_size=1)
     for b in range(B4):
         solo = generate_wavefront_batch(solo_blocks, [prompts[b]], [glen[b]], policy,
-                                        [EmulatedAcceptance(0.7, 1000 + b)])
+                                        [EmulatedAcceptance(alpha, 1000 + b)])
         assert bt.per_seq[b].tokens == solo.per_seq[0].tokens, b
         assert bt.per_seq[b].counters() == solo.per_seq[0].counters(), b
+    print(f"[C4] alpha={alpha}: {bt.n_tokens} tokens, {bt.n_r_calls} R ticks, acceptance "
+          f"{bt.acceptance_rate:.3f}", flush=True)
 
 
 def test_c4_greedy_batch_equals_sequential(gpu, c4):
-    """Real greedy acceptance over the ragged 32-wide batch commits exactly
-    the lockstep sequential decode's tokens; AR R calls = (N - 1) T_total."""
-    model, prompts, glen = c4
-    bb = LoopedBlocksBatch(model, batch_size=B4)
-    print("[C4] greedy batch vs sequential", flush=True)
-    wfd = generate_wavefront_batch(bb, prompts, glen, SsdPolicy(C3.T_total, 2))
-    ar = ar_generate_batch(bb, prompts, glen)
+    """Real greedy acceptance (decided on the device) over the ragged 32-wide
+    batch commits exactly the lockstep sequential decode's tokens for every
+    sequence's whole generation; AR R calls = (N - 1) T_total."""
+    model, bb, pf, prompts, glen = c4
+    print("[C4] greedy batch WFD vs lockstep sequential decode", flush=True)
+    wfd = generate_wavefront_batch(bb, prompts, glen, SsdPolicy(C3.T_total, 2), prefilled=pf)
+    ar = ar_generate_batch(bb, prompts, glen, prefilled=pf)
     assert [t.tokens for t in wfd.per_seq] == [t.tokens for t in ar.per_seq]
     for t, n in zip(ar.per_seq, glen):
         assert t.n_r_calls == (n - 1) * C3.T_total and len(t.tokens) == n
+    print(f"[C4] greedy: {wfd.n_tokens} tokens, {wfd.n_r_calls} R ticks, acceptance {wfd.acceptance_rate:.3f}",
+          flush=True)
 
 
 def test_c4_replicas_isolation_and_prefill(gpu, c4):
     """Replicas of one prompt commit identical tokens and counters; an
     alpha = 0 neighbour leaves an alpha = 1 sequence's run unchanged; batch
     prefill logits equal the single-sequence prefill's."""
-    model, prompts, glen = c4
+    model, bb, pf, prompts, glen = c4
     policy = SsdPolicy(C3.T_total, 1)
     bb4 = LoopedBlocksBatch(model, batch_size=4)
-    bt = generate_wavefront_batch(bb4, [prompts[0]] * 4, 12, policy, [EmulatedAcceptance(1.0, 11) for _ in range(4)])
+    bt = generate_wavefront_batch(bb4, [prompts[0]] * 4, 40, policy, [EmulatedAcceptance(1.0, 11) for _ in range(4)])
     assert all(t.tokens == bt.per_seq[0].tokens and t.counters() == bt.per_seq[0].counters() for t in bt.per_seq)
     bb1 = LoopedBlocksBatch(model, batch_size=1)
-    solo = generate_wavefront_batch(bb1, [prompts[1]], 12, policy, [EmulatedAcceptance(1.0, 31)])
+    solo = generate_wavefront_batch(bb1, [prompts[1]], 40, policy, [EmulatedAcceptance(1.0, 31)])
     bb2 = LoopedBlocksBatch(model, batch_size=2)
-    mix = generate_wavefront_batch(bb2, [prompts[1]] * 2, 12, policy,
+    mix = generate_wavefront_batch(bb2, [prompts[1]] * 2, 40, policy,
                                    [EmulatedAcceptance(0.0, 99), EmulatedAcceptance(1.0, 31)])
     assert solo.per_seq[0].counters() == mix.per_seq[1].counters()
     assert solo.per_seq[0].tokens == mix.per_seq[1].tokens
     t0 = mix.per_seq[0]
-    assert t0.n_drafts_proposed > 0 and t0.n_drafts_accepted == 0 and len(t0.tokens) == 12
+    assert t0.n_drafts_proposed > 0 and t0.n_drafts_accepted == 0 and len(t0.tokens) == 40
     _, lb = bb2.prefill([prompts[2], prompts[2]])
     _, ls = LoopedBlocks(model).prefill(prompts[2], C3.T_total, 2)
     assert rel_err(lb[0].cpu().numpy(), ls.cpu().numpy()) <= 1e-6
+
+
+def test_c4_ragged_r_tick_matches_oracle(gpu, w2048):
+    """One union R tick of the B = 32 workload: 256 rows, each sequence at a
+    position inside its own generation (key prefixes 178-2381, the shortest
+    prompt's first wave to the longest sequence's last token; most rows span
+    2-3 of the attention's 1024-key splits), over random K/V. 28 sequences carry a WFD wave (8 rows at depths 0, 2, .., 14); 4
+    carry draft-then-verify-like rows (4 rows at one depth, adjacent, so the
+    attention groups them, next to 4 rows at other depths). Rows of every
+    kind are compared with the fp32 oracle's core fed the same bf16 values:
+    <= 2e-2."""
+    plen, glen, _ = c4_workload()
+    S = max(plen) + max(glen) + 16
+    model = LoopedModel(C3, w2048, gpu, max_seq_len=S, max_batch=B4, use_graphs=True)
+    cache = model.create_cache(B4)
+    g = torch.Generator(device=gpu).manual_seed(44)
+    for t in (cache.flat_k, cache.flat_v):
+        t.copy_(torch.randn(t.shape, generator=g, device=gpu).to(torch.bfloat16))
+    # sequence b's newest row sits k_b / 11 of the way through its generation:
+    # the shortest prompt at its start, the longest prompt + generation at its end
+    k = [(b * 7) % 12 for b in range(B4)]
+    k[int(np.argmin(plen))] = 0
+    k[int(np.argmax(np.add(plen, glen)))] = 11
+    seqs, pos, steps = [], [], []
+    for b in range(B4):
+        p = plen[b] + 7 + (glen[b] - 8) * k[b] // 11
+        if b % 8 == 7:
+            d = (b // 8) * 3
+            rows = [(p + i, d) for i in range(4)] + [(p - 1 - i, d + 1 + i) for i in range(4)]
+        else:
+            rows = [(p - i, 2 * i) for i in range(8)]
+        for q, d in rows:
+            seqs.append(b)
+            pos.append(q)
+            steps.append(d)
+    assert len(seqs) == 256 and max(steps) < C3.T_total and max(pos) < S - 1
+    assert min(pos) + 1 == min(plen) + 1 and max(pos) + 1 == max(np.add(plen, glen))
+    pool_rows = [model.pool_row(b, q) for b, q in zip(seqs, pos)]
+    assert len(set(pool_rows)) == 256
+    gh = torch.Generator().manual_seed(45)
+    state = torch.randn(256, 2 * C3.d_model, generator=gh).to(torch.bfloat16)
+    model.pool[pool_rows] = state.to(gpu)
+    tick = model._tick
+    prm = model._tick_params(cache)
+    t32, t64 = model._table_scratch(1)
+    grouped = tick.plan_pass(t32, 0, t64, 0, prm, "R", seqs, pos, steps, -1, -1, -1)[3]
+    assert grouped  # the adjacent same-depth rows share their prefix reads
+    print("[C4] ragged R tick, 256 rows", flush=True)
+    model.core_union(cache, seqs, pos, steps)
+    got = model.pool[pool_rows, : C3.d_model].float().cpu().numpy()
+    lm = OracleLM(C3, M.weights_numpy(w2048), S, 1, None, None)
+    st = state.float().numpy()
+    # the longest and shortest prefixes, grouped rows, each depth of a wave
+    check = sorted({int(np.argmax(pos)), int(np.argmin(pos)), 7 * 8, 7 * 8 + 1, 7 * 8 + 3, 7 * 8 + 6, 15 * 8 + 2,
+                    3 * 8 + 0, 3 * 8 + 7, 12 * 8 + 4, 20 * 8 + 5, 31 * 8 + 3})
+    for i in check:
+        b, d = seqs[i], steps[i]
+        # the oracle's one sequence gets sequence b's slots of this depth as the
+        # tick left them (other rows' appends included, as the GPU read them)
+        for l in range(C3.n_core):
+            sl = model.slot_core(d, l)
+            lm.Kc[sl, 0] = cache.K[sl, b].float().cpu().numpy()
+            lm.Vc[sl, 0] = cache.V[sl, b].float().cpu().numpy()
+        ref = lm.core(0, pos[i], d, st[i, : C3.d_model], st[i, C3.d_model:])
+        err = rel_err(got[i], ref)
+        assert err <= 2e-2, (i, b, pos[i], steps[i], err)
+    del model, cache
+    torch.cuda.empty_cache()
 
 
 # ---------------------------------------------------------------------------

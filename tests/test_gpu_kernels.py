@@ -479,12 +479,17 @@ def test_embed_copy_argmax(gpu):
     ops.copy_rows(table, dst, n=2, width=256, src_rows=torch.tensor([5, 6], dtype=torch.int32, device=gpu),
                   dst_rows=torch.tensor([7, 1], dtype=torch.int32, device=gpu))
     assert torch.equal(dst[7, :256], table[5]) and torch.equal(dst[1, :256], table[6])
-    logits = torch.randn(5, 32000, generator=g).to(gpu)
+    logits = torch.randn(7, 32000, generator=g).to(gpu)
     logits[2, 17] = 100.0
     logits[2, 30000] = 100.0  # tie: first index wins, as torch.argmax
+    logits[4, 31000] = float("nan")  # NaN ranks above every number, as torch.argmax: first NaN wins
+    logits[4, 20000] = float("nan")
+    logits[4, 5] = float("inf")
+    logits[5] = float("nan")  # an all-NaN row: id 0
+    logits[6] = float("-inf")  # an all -inf row: id 0
     am = ops.argmax(logits)
     assert am.tolist() == logits.argmax(dim=-1).tolist()
-    assert am[2].item() == 17
+    assert am[2].item() == 17 and am[4].item() == 20000 and am[5].item() == 0 and am[6].item() == 0
 
 
 @pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 2048), (torch.bfloat16, 256), (torch.float32, 256)])
@@ -537,15 +542,17 @@ def test_token_ring_round_trip(gpu):
     assert torch.equal(e, table[want])
 
 
-@pytest.mark.parametrize("N", [32000, 2048, 1024])
-def test_linear_argmax_groups_same_ids_and_bits(gpu, N):
+@pytest.mark.parametrize("N,K", [(32000, 2048), (2048, 2048), (1024, 2048), (8192, 2048), (32000, 4096),
+                                 (8192, 6144)])
+def test_linear_argmax_groups_same_ids_and_bits(gpu, N, K):
     """lm_head with the column-group argmax: y has the bits of the plain
     linear, and the ids (with ring and accept flags) from the group bests equal
     wfd_argmax over y -- including ties across groups and within one group
-    (first index wins), an all-zero row (every logit +0: id 0) and a row that
-    needs the half-tile groups (N <= 4096)."""
-    g = torch.Generator().manual_seed(N)
-    K = 2048
+    (first index wins), an all-zero row (every logit +0: id 0), NaN logits
+    (the first NaN wins, as torch.argmax), and every form of the few-row
+    launch: half-tile groups (N <= 4096), 8-wave and 16-wave full tiles
+    (N 32000 / 8192), one to three chunks per sub-slice (K 2048 / 4096 / 6144)."""
+    g = torch.Generator().manual_seed(N + K)
     W = (0.02 * torch.randn(N, K, generator=g)).to(torch.bfloat16)
     x = torch.randn(16, K, generator=g).to(torch.bfloat16)
     x[2] = 0
@@ -579,6 +586,17 @@ def test_linear_argmax_groups_same_ids_and_bits(gpu, N):
         ops.argmax(ref, n=n, ring=ring_a, ring_rows=rows, expect=expect, accept=fa)
         ops.argmax_groups(pv, pi, G, n=n, ring=ring_b, ring_rows=rows, expect=expect, accept=fb)
         assert fa.tolist() == fb.tolist() and torch.equal(ring_a, ring_b)
+    # a NaN weight makes its column NaN in every row (x rows are nonzero or 0 * NaN);
+    # two such columns in different groups: the first one wins everywhere
+    Wn = W.clone()
+    Wn[j3, 1] = float("nan")
+    Wn[j1, 0] = float("nan")
+    Wnp = ops.pack_linear(Wn.to(gpu))
+    for n in (1, 8):
+        ref = ops.linear(xg, Wnp, n=n, out_dtype=torch.float32)
+        y, pv, pi = ops.linear_argmax(xg, Wnp, n=n)
+        ids = ops.argmax_groups(pv, pi, ops.linear_argmax_groups(n, Wnp), n=n)
+        assert ids.tolist() == ops.argmax(ref, n=n).tolist() == ref[:n].argmax(dim=-1).tolist() == [min(j1, j3)] * n
     with pytest.raises(Exception, match="no column groups"):
         ops.linear_argmax(torch.zeros(17, K, dtype=torch.bfloat16, device=gpu), Wp, n=17)
 

@@ -203,11 +203,15 @@ namespace wfd {
 void set_error(const char* fmt, ...);
 int launch_status(const char* what);
 
-// Greedy argmax step: (ov, oi) replaces (bv, bi) if larger, or equal with a
-// lower index. Starting from (-inf, INT_MAX) a NaN never enters, so merging
-// in any order and grouping gives the first index of the largest value.
+// Greedy argmax step: (ov, oi) replaces (bv, bi) if it ranks higher, or ranks
+// the same with a lower index. NaN ranks above every number, as in
+// torch.argmax, so a row holding a NaN yields its first NaN's index. The rank
+// is a total order on (value, index), so merging in any order and grouping
+// gives the same id: the first index of the largest value.
 __device__ __forceinline__ void argmax_merge(float& bv, int& bi, float ov, int oi) {
-  if (ov > bv || (ov == bv && oi < bi)) {
+  const bool onan = ov != ov, bnan = bv != bv;
+  const bool take = onan ? (!bnan || oi < bi) : (!bnan && (ov > bv || (ov == bv && oi < bi)));
+  if (take) {
     bv = ov;
     bi = oi;
   }

@@ -57,6 +57,22 @@ def generate_wavefront_dynamic(blocks, prompt_ids: torch.Tensor, max_new_tokens:
                                eos_token_id: int | None = None) -> tuple[list[int], GenerationTrace]:
     """Greedy lossless WFD for one sequence. Stops at max_new_tokens or when a
     committed token equals eos_token_id. Returns (tokens, trace)."""
+    return wavefront_single(blocks, prompt_ids, max_new_tokens, policy, None, eos_token_id)
+
+
+def _decide(sampler, emu, draft_token: int, draft_probs, logits, position: int) -> tuple[bool, int]:
+    """(accept, gold) for a draft at `position`: the greedy comparison, or the
+    next Bernoulli draw of an emulated-acceptance stream (gold is still the
+    full-depth argmax, committed on a reject)."""
+    if emu is None:
+        return sampler.verify(draft_token, draft_probs, logits, position)
+    return emu.draw(), sampler(logits, position)
+
+
+def wavefront_single(blocks, prompt_ids: torch.Tensor, max_new_tokens: int, policy: SsdPolicy, emu=None,
+                     eos_token_id: int | None = None) -> tuple[list[int], GenerationTrace]:
+    """The WFD loop behind generate_wavefront_dynamic (emu None: greedy
+    comparisons) and generate_wavefront_emu (each accept decided by emu.draw())."""
     trace = GenerationTrace()
     device = prompt_ids.device
     sampler = policy.make_sampler()
@@ -100,7 +116,7 @@ def generate_wavefront_dynamic(blocks, prompt_ids: torch.Tensor, max_new_tokens:
                 commit(gold, nxt_pos)
                 enqueue(gold, nxt_pos)
             else:
-                ok, gold = sampler.verify(nxt.token_id, nxt.draft_probs, logits[i], nxt_pos)
+                ok, gold = _decide(sampler, emu, nxt.token_id, nxt.draft_probs, logits[i], nxt_pos)
                 trace.n_drafts_proposed += 1
                 if ok:
                     trace.n_drafts_accepted += 1
@@ -153,6 +169,13 @@ def generate_draft_then_verify(blocks, prompt_ids: torch.Tensor, max_new_tokens:
     and drops every slot row from there on; if all K match, the last source's
     gold is a free bonus token. Lossless: every committed token is a
     full-depth argmax. Stops at max_new_tokens or a committed eos_token_id."""
+    return dtv_single(blocks, prompt_ids, max_new_tokens, policy, draft_length, None, eos_token_id)
+
+
+def dtv_single(blocks, prompt_ids: torch.Tensor, max_new_tokens: int, policy: SsdPolicy, draft_length: int,
+               emu=None, eos_token_id: int | None = None) -> tuple[list[int], GenerationTrace]:
+    """The draft-then-verify loop behind generate_draft_then_verify (emu None)
+    and generate_dtv_emu (each accept decided by emu.draw())."""
     if draft_length < 1 or draft_length + 1 > getattr(blocks, "max_in_flight", draft_length + 1):
         raise ValueError(f"draft_length={draft_length}: a round keeps draft_length + 1 sources in flight, "
                          f"at most {getattr(blocks, 'max_in_flight', '?')} fit")
@@ -202,7 +225,7 @@ def generate_draft_then_verify(blocks, prompt_ids: torch.Tensor, max_new_tokens:
         trace.n_c_calls += 1
         rejected = False
         for i in range(K):
-            ok, gold = sampler.verify(drafts[i], None, golds[i], p + i + 1)
+            ok, gold = _decide(sampler, emu, drafts[i], None, golds[i], p + i + 1)
             trace.n_drafts_proposed += 1
             if ok:
                 trace.n_drafts_accepted += 1
