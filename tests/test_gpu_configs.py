@@ -3,7 +3,9 @@ or against sequential decode (GPU).
 
 * C1 (tiny fp32, 128-token prompt, 64 tokens): WFD at T_draft 1 and 2 commits
   the oracle's sequential tokens with the oracle's counters; captured graphs
-  and the device token ring give the same tokens and counters as the oracle.
+  and the device token ring give the same tokens and counters as the oracle;
+  the emulated-acceptance schedulers meet the reference's empirical-alpha
+  gate over 384 tokens and match the oracle's emulated run.
 * Accepted drafts under real greedy acceptance: an adapter [c R | I]
   (R the random init block) makes shallow drafts agree with the full depth
   (c = 0: every loop step sees e, so every draft is exact; c = 1 on the tiny
@@ -43,6 +45,7 @@ from wavefront_decoding_amd.emu import EmulatedAcceptance
 from wavefront_decoding_amd.engine import LoopedModel
 from wavefront_decoding_amd.policy import SsdPolicy
 from wavefront_decoding_amd.scheduler import generate_draft_then_verify, generate_wavefront_dynamic
+from wavefront_decoding_amd.scheduler_emu import generate_dtv_emu, generate_wavefront_emu
 from wavefront_decoding_amd.scheduler_batch import ar_generate_batch, generate_wavefront_batch, prefill_once
 
 pytestmark = pytest.mark.gpu
@@ -99,6 +102,31 @@ def test_c1_wfd_64_tokens_match_oracle(gpu, tiny_w, T_draft, graphs):
     assert toks == oc.tokens and len(toks) == N
     assert trace.counters() == {k: getattr(oc, k) for k in trace.counters()}
     assert toks == osched.ar_single(_oracle(TINY, tiny_w, 256), ids.tolist(), N, TINY.T_total)
+
+
+@pytest.mark.parametrize("alpha", [0.5, 0.8])
+def test_emulated_alpha_gate_tiny(gpu, tiny_w, alpha):
+    """The reference's emulated-acceptance gate (experiments/exp4_emu/
+    verify_step1.py:84-95) on the device path: 384 tokens of
+    generate_wavefront_emu and generate_dtv_emu (draft length 4) on the tiny
+    model, T_total 4, T_draft 1, seed 7: the empirical acceptance is within
+    0.06 of alpha; the WFD run's tokens and counters equal the oracle's
+    emulated run, draw for draw."""
+    ids = _prompt(128)
+    blocks = LoopedBlocks(LoopedModel(TINY, tiny_w, gpu, max_seq_len=128 + 400, use_graphs=True))
+    policy = SsdPolicy(TINY.T_total, 1)
+    print(f"[emu gate] alpha={alpha}", flush=True)
+    emu = EmulatedAcceptance(alpha, 7)
+    toks, tr = generate_wavefront_emu(blocks, ids.to(gpu), 384, policy, emu=emu)
+    assert len(toks) == 384 and abs(emu.empirical_rate - alpha) < 0.06, emu.empirical_rate
+    oemu = osched.Emu(alpha, 7)
+    oc = osched.wfd_single(_oracle(TINY, tiny_w, 128 + 400), ids.tolist(), 384, TINY.T_total, 1, emu=oemu)
+    assert toks == oc.tokens
+    assert tr.counters() == {k: getattr(oc, k) for k in tr.counters()}
+    assert (emu.n_draws, emu.n_accepts) == (oemu.n_draws, oemu.n_accepts)
+    emu = EmulatedAcceptance(alpha, 7)
+    toks, tr = generate_dtv_emu(blocks, ids.to(gpu), 384, policy, 4, emu=emu)
+    assert len(toks) == 384 and abs(emu.empirical_rate - alpha) < 0.06, emu.empirical_rate
 
 
 def test_graph_batch_and_token_ring_match_oracle(gpu, tiny_w):

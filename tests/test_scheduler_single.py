@@ -7,6 +7,17 @@ golden trace (tokens and counters) -- the reference's own gate that the
 single-sequence and batch schedulers agree at B = 1
 (experiments/exp4_emu/verify_batch.py:105-125). The oracle's wfd_single is
 held to the same traces.
+
+They are also held to traces of the reference's own single-sequence
+schedulers (src/decoding/scheduler.py generate_wavefront_dynamic /
+generate_draft_then_verify, src/decoding/scheduler_emu.py
+generate_wavefront_emu / generate_dtv_emu; tests/golden/
+scheduler_single_traces.json): greedy at 70 % and 95 % draft agreement,
+emulated alpha 0 / 0.5 / 0.9 / 1, eos stops -- tokens, counters, rollbacks,
+the per-call schedule and the draws. The reference's emulated-alpha gate
+(experiments/exp4_emu/verify_step1.py:84-95: empirical acceptance within 0.06
+of alpha over 384 tokens at alpha 0.5 / 0.8) holds for the product's emulated
+schedulers.
 """
 from __future__ import annotations
 
@@ -21,12 +32,16 @@ from tests.golden.stub_model import StubBatchBlocks, stub_prompts
 from wavefront_decoding_amd.acceptance import RowLogits
 from wavefront_decoding_amd.blocks import LoopedBlocks
 from wavefront_decoding_amd.policy import SsdPolicy
+from wavefront_decoding_amd.emu import EmulatedAcceptance
 from wavefront_decoding_amd.scheduler import generate_draft_then_verify, generate_wavefront_dynamic
+from wavefront_decoding_amd.scheduler_emu import generate_dtv_emu, generate_wavefront_emu
 from wavefront_decoding_amd.state import WavefrontState
 
 GOLDEN = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "scheduler_traces.json")))
 B1 = [r for r in GOLDEN["wfd"] if r["B"] == 1 and r["alpha"] is None]
 B1_DTV = [r for r in GOLDEN["dtv"] if r["B"] == 1 and r["alpha"] is None]
+# traces of the reference's own single-sequence schedulers (scheduler.py / scheduler_emu.py)
+SINGLE = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "scheduler_single_traces.json")))
 
 
 class _SingleCache:
@@ -40,8 +55,8 @@ class _SingleCache:
 class StubSingleBlocks(LoopedBlocks):
     """Product routing over stub compute."""
 
-    def __init__(self, T_total: int):  # noqa: D401 -- no engine on the CPU
-        self.stub = StubBatchBlocks(T_total, 1)
+    def __init__(self, T_total: int, agree_pct: int = 70):  # noqa: D401 -- no engine on the CPU
+        self.stub = StubBatchBlocks(T_total, 1, agree_pct=agree_pct)
         self.T_total = T_total
         self.device = torch.device("cpu")
 
@@ -151,3 +166,94 @@ def test_dtv_single_matches_batch_b1_trace(ref):
     assert [list(d) for d in blocks.stub.last_cache.drops] == ref["drops"]
     if ref["calls"] is not None:
         assert [[k, [list(x) for x in rows]] for k, rows in blocks.stub.calls] == ref["calls"]
+
+
+def _single_id(r):
+    a = "greedy" if r["alpha"] is None else f"a{r['alpha']}"
+    k = f"-K{r['draft_length']}" if "draft_length" in r else ""
+    e = "" if r["eos"] is None else f"-eos{r['eos']}"
+    return f"T{r['T_total']}/{r['T_draft']}{k}-N{r['max_new_tokens']}-{a}-agree{r['agree_pct']}{e}"
+
+
+def _check_single(ref, toks, trace, blocks, emu):
+    assert toks == ref["tokens"]
+    assert trace.counters() == ref["counters"]
+    assert [list(d) for d in blocks.stub.last_cache.drops] == ref["drops"]
+    if ref["calls"] is not None:
+        assert [[k, [list(x) for x in rows]] for k, rows in blocks.stub.calls] == ref["calls"]
+    assert ([emu.n_draws, emu.n_accepts] if emu is not None else None) == ref["emu"]
+
+
+@pytest.mark.parametrize("ref", SINGLE["wfd"], ids=_single_id)
+def test_wfd_single_matches_reference_single_trace(ref):
+    blocks = StubSingleBlocks(ref["T_total"], ref["agree_pct"])
+    policy = SsdPolicy(T_total=ref["T_total"], T_draft=ref["T_draft"])
+    emu = None if ref["alpha"] is None else EmulatedAcceptance(ref["alpha"], ref["seed"])
+    if emu is None:
+        toks, trace = generate_wavefront_dynamic(blocks, stub_prompts(1, 5)[0], ref["max_new_tokens"], policy,
+                                                 eos_token_id=ref["eos"])
+    else:
+        toks, trace = generate_wavefront_emu(blocks, stub_prompts(1, 5)[0], ref["max_new_tokens"], policy, emu=emu,
+                                             eos_token_id=ref["eos"])
+    _check_single(ref, toks, trace, blocks, emu)
+
+
+@pytest.mark.parametrize("ref", SINGLE["dtv"], ids=_single_id)
+def test_dtv_single_matches_reference_single_trace(ref):
+    blocks = StubSingleBlocks(ref["T_total"], ref["agree_pct"])
+    policy = SsdPolicy(T_total=ref["T_total"], T_draft=ref["T_draft"])
+    emu = None if ref["alpha"] is None else EmulatedAcceptance(ref["alpha"], ref["seed"])
+    args = (blocks, stub_prompts(1, 5)[0], ref["max_new_tokens"], policy, ref["draft_length"])
+    if emu is None:
+        toks, trace = generate_draft_then_verify(*args, eos_token_id=ref["eos"])
+    else:
+        toks, trace = generate_dtv_emu(*args, emu=emu, eos_token_id=ref["eos"])
+    _check_single(ref, toks, trace, blocks, emu)
+
+
+@pytest.mark.parametrize("ref", SINGLE["wfd"], ids=_single_id)
+def test_oracle_wfd_single_matches_reference_single_trace(ref):
+    blocks = StubBatchBlocks(ref["T_total"], 1, agree_pct=ref["agree_pct"])
+    emu = None if ref["alpha"] is None else osched.Emu(ref["alpha"], ref["seed"])
+    c = osched.wfd_single(blocks, stub_prompts(1, 5)[0].tolist(), ref["max_new_tokens"], ref["T_total"],
+                          ref["T_draft"], emu=emu, eos=ref["eos"])
+    assert c.tokens == ref["tokens"]
+    assert {k: getattr(c, k) for k in ref["counters"]} == ref["counters"]
+    assert [list(d) for d in blocks.last_cache.drops] == ref["drops"]
+    assert ([emu.n_draws, emu.n_accepts] if emu is not None else None) == ref["emu"]
+
+
+@pytest.mark.parametrize("alpha", [0.5, 0.8])
+@pytest.mark.parametrize("kind", ["wfd", "dtv"])
+def test_emulated_alpha_gate(kind, alpha):
+    """The reference's gate 3 (experiments/exp4_emu/verify_step1.py:84-95):
+    T_total 4, T_draft 1, 384 tokens, seed 7 (draft length 4 for DtV): the
+    empirical acceptance is within 0.06 of alpha, and the run is the
+    reference's own, draw for draw."""
+    ref = next(r for r in SINGLE[kind] if r["max_new_tokens"] == 384 and r["alpha"] == alpha)
+    blocks = StubSingleBlocks(4)
+    emu = EmulatedAcceptance(alpha, 7)
+    policy = SsdPolicy(T_total=4, T_draft=1)
+    if kind == "wfd":
+        toks, trace = generate_wavefront_emu(blocks, stub_prompts(1, 5)[0], 384, policy, emu=emu)
+    else:
+        toks, trace = generate_dtv_emu(blocks, stub_prompts(1, 5)[0], 384, policy, 4, emu=emu)
+    assert len(toks) == 384 and abs(emu.empirical_rate - alpha) < 0.06, emu.empirical_rate
+    _check_single(ref, toks, trace, blocks, emu)
+
+
+def test_emulated_alpha_one_and_equivalence():
+    """The reference's gates 1 and 2 (verify_step1.py:55-82): emu=None is the
+    greedy scheduler exactly; alpha = 1 gives no rejects and exactly N commits."""
+    for T_draft in (1, 2):
+        pol = SsdPolicy(T_total=4, T_draft=T_draft)
+        a = generate_wavefront_dynamic(StubSingleBlocks(4), stub_prompts(1, 5)[0], 48, pol)
+        b = generate_wavefront_emu(StubSingleBlocks(4), stub_prompts(1, 5)[0], 48, pol, emu=None)
+        assert a[0] == b[0] and a[1].counters() == b[1].counters()
+    pol = SsdPolicy(T_total=4, T_draft=1)
+    a = generate_draft_then_verify(StubSingleBlocks(4), stub_prompts(1, 5)[0], 48, pol, 4)
+    b = generate_dtv_emu(StubSingleBlocks(4), stub_prompts(1, 5)[0], 48, pol, 4, emu=None)
+    assert a[0] == b[0] and a[1].counters() == b[1].counters()
+    for fn, extra in ((generate_wavefront_emu, ()), (generate_dtv_emu, (4,))):
+        toks, tr = fn(StubSingleBlocks(4), stub_prompts(1, 5)[0], 48, pol, *extra, emu=EmulatedAcceptance(1.0, 0))
+        assert tr.n_drafts_rejected == 0 and len(toks) == 48
