@@ -14,7 +14,7 @@ def test_backend_names():
     for name in ("torch", "fa4", "hip"):  # the reference's fused backends map to the HIP kernels
         A.set_backend(name)
         assert A.backend() == "hip"
-    with pytest.raises(ValueError, match="test references"):
+    with pytest.raises(ValueError, match="parity reference"):
         A.set_backend("sdpa")
     with pytest.raises(ValueError, match="unknown"):
         A.set_backend("triton")

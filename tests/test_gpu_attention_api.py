@@ -136,3 +136,77 @@ def test_compute_qkv_matches_oracle(gpu):
         assert rel_err(_np(q).reshape(B * T, 4, 64)[r], qr) <= 1e-4
         assert rel_err(_np(k).reshape(B * T, 2, 64)[r], kr) <= 1e-4
         assert rel_err(_np(v).reshape(B * T, 2, 64)[r], qkv[r, 384:].reshape(2, 64)) <= 1e-4
+
+
+@pytest.mark.parametrize("dtype,H,Hkv,Dh", [(torch.bfloat16, 16, 16, 128), (torch.bfloat16, 16, 4, 128),
+                                            (torch.float32, 4, 2, 64)])
+def test_compute_qkv_reference_form(gpu, dtype, H, Hkv, Dh):
+    """The reference's call form (src/decoding/fa4_attention.py:128-152):
+    separate bias-free c_q / c_k / c_v nn.Linear projections and complex
+    freqs_cis shaped (1, T, 1, Dh/2). q and k are the projections rotated as
+    complex numbers (x[2j] + i x[2j+1]) * freqs[t, j], v the plain projection
+    (numpy, float64); the fused-Wqkv form gives the same bits; use_rope =
+    False returns the plain projections; a weight changed in place is seen."""
+    g = torch.Generator().manual_seed(H + Hkv + Dh)
+    B, T, C = 2, 7, 512
+
+    class Attn(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.n_head, self.n_kv_head, self.head_dim = H, Hkv, Dh
+            self.c_q = torch.nn.Linear(C, H * Dh, bias=False)
+            self.c_k = torch.nn.Linear(C, Hkv * Dh, bias=False)
+            self.c_v = torch.nn.Linear(C, Hkv * Dh, bias=False)
+
+    attn = Attn()
+    with torch.no_grad():
+        for m in (attn.c_q, attn.c_k, attn.c_v):
+            m.weight.copy_(0.05 * torch.randn(m.weight.shape, generator=g))
+    attn = attn.to(device=gpu, dtype=dtype)
+    x = torch.randn(B, T, C, generator=g).to(device=gpu, dtype=dtype)
+    ang = torch.rand(T, Dh // 2, generator=g, dtype=torch.float64) * 6.0
+    freqs = torch.polar(torch.ones_like(ang), ang).to(torch.complex64).view(1, T, 1, Dh // 2)
+
+    def reference(x, attn):
+        xs = _np(x).reshape(B * T, C)
+        qs = xs @ _np(attn.c_q.weight).T
+        ks = xs @ _np(attn.c_k.weight).T
+        vs = xs @ _np(attn.c_v.weight).T
+        f = freqs.view(T, Dh // 2).to(torch.complex128).numpy()
+
+        def rot(a, heads):
+            a = a.reshape(B, T, heads, Dh // 2, 2)
+            z = (a[..., 0] + 1j * a[..., 1]) * f[None, :, None, :]
+            return np.stack([z.real, z.imag], axis=-1).reshape(B, T, heads, Dh)
+
+        return rot(qs, H), rot(ks, Hkv), vs.reshape(B, T, Hkv, Dh)
+
+    q, k, v = A.compute_qkv(attn, x, freqs, None, None)
+    rq, rk, rv = reference(x, attn)
+    tol = TOL[dtype]
+    assert rel_err(_np(q), rq) <= tol and rel_err(_np(k), rk) <= tol and rel_err(_np(v), rv) <= tol
+
+    class Fused:
+        n_head, n_kv_head, head_dim = H, Hkv, Dh
+        Wqkv = torch.cat([attn.c_q.weight, attn.c_k.weight, attn.c_v.weight]).detach().contiguous()
+
+    q2, k2, v2 = A.compute_qkv(Fused, x, freqs)
+    assert torch.equal(q2, q) and torch.equal(k2, k) and torch.equal(v2, v)
+
+    class NoRope:
+        class rope_settings:
+            use_rope = False
+        clip_qkv = None
+        qk_bias = False
+        qk_norm = False
+
+    q3, k3, v3 = A.compute_qkv(attn, x, freqs, None, NoRope)
+    xs = _np(x).reshape(B * T, C)
+    assert rel_err(_np(q3).reshape(B * T, -1), xs @ _np(attn.c_q.weight).T) <= tol
+    assert rel_err(_np(k3).reshape(B * T, -1), xs @ _np(attn.c_k.weight).T) <= tol
+    assert torch.equal(v3, v)
+
+    with torch.no_grad():
+        attn.c_k.weight.mul_(-1)  # in place: the packed copy must be rebuilt
+    q4, k4, v4 = A.compute_qkv(attn, x, freqs)
+    assert torch.equal(q4, q) and torch.equal(v4, v) and torch.equal(k4, -k)

@@ -36,6 +36,16 @@ def test_state_init_matches_product_recipe():
     assert np.abs(a).max() <= 3 * 0.02 + 1e-7 and 0.01 < a.std() < 0.03
 
 
+def test_prompt_state_stream_is_prefix_consistent():
+    """The engine draws the prompt's initial loop state once for the longest
+    prompt and slices it: rows [0, L) of any longer draw must be the draw of
+    length L, at the 2048-d model's width too."""
+    for cfg in (CFG, M.CONFIGS["looped-2048"]):
+        long = M.initial_state_prefill(cfg, 3000, state_seed=2)
+        for L in (1, 2, 7, 512, 1999, 3000):
+            assert torch.equal(M.initial_state_prefill(cfg, L, state_seed=2), long[:L]), (cfg.name, L)
+
+
 @pytest.mark.parametrize("T_draft", [1, 2])
 def test_oracle_wfd_equals_sequential(T_draft):
     ids = prompt()[0].tolist()

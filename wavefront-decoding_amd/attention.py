@@ -19,8 +19,9 @@ runs a HIP kernel of libwfd.so on torch's current stream:
                   reference pads each to two causal rows to steer FA2's tile
                   choice; the decode kernel has no such template switch, and
                   the kept row's result is the same full-segment attention)
-  compute_qkv     the fused Wqkv projection (wfd_linear) and RoPE
-                  (wfd_qkv_rope_append into a scratch buffer)
+  compute_qkv     the reference's c_q / c_k / c_v (packed together once) or
+                  a fused Wqkv, with RoPE from its complex freqs_cis, in one
+                  launch (wfd_linear_qkv_rope_append into fresh buffers)
 
 A query row with no keys (bottom-right causal with k_len < q_len) gets a
 zero row, the flash-attention convention the reference's default backend
@@ -52,7 +53,9 @@ def set_backend(name: str) -> None:
         _BACKEND = "hip"
         return
     if name == "sdpa":
-        raise ValueError("the 'sdpa' twins are test references, not a product backend (see oracle.kernels)")
+        raise ValueError("set_backend('sdpa'): the reference's slow explicit-mask twins are a parity reference, "
+                         "not a product backend, and this library runs only its HIP kernels; the explicit-mask "
+                         "reference for parity checks is the test oracle (oracle.kernels.attention)")
     raise ValueError(f"unknown attention backend {name!r}")
 
 
@@ -162,14 +165,70 @@ def attn_varlen_q1_padded(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_
     return attn_varlen(q, k, v, cu_q, cu_k, 1, max_k, causal=False)
 
 
+def _fused_qkv_weight(attn):
+    """The projection weight of `attn`: its fused Wqkv, or c_q / c_k / c_v
+    (the reference's separate bias-free nn.Linear modules) concatenated and
+    packed once; the packed copy is kept on the module and rebuilt when any
+    of the three weights is replaced or changed in place."""
+    W = getattr(attn, "Wqkv", None)
+    if W is not None:
+        return W
+    if not all(hasattr(attn, m) for m in ("c_q", "c_k", "c_v")):
+        raise _lib.WfdError("compute_qkv: attn needs c_q / c_k / c_v projections or a fused Wqkv weight")
+    mods = (attn.c_q, attn.c_k, attn.c_v)
+    if any(getattr(m, "bias", None) is not None for m in mods):
+        raise _lib.WfdError("compute_qkv: projections with a bias are not supported (the reference's are bias-free)")
+    key = tuple((m.weight.data_ptr(), m.weight._version) for m in mods)
+    cached = attn.__dict__.get("_wfd_packed_qkv")
+    if cached is None or cached[0] != key:
+        fused = torch.cat([m.weight.detach() for m in mods]).contiguous()
+        cached = (key, ops.pack_linear(fused))
+        attn.__dict__["_wfd_packed_qkv"] = cached
+    return cached[1]
+
+
+def _rope_tables(freqs, B: int, T: int, Dh: int, device):
+    """(cos, sin, per-row positions) for the QKV epilogue from the
+    reference's complex freqs_cis (row t = position t's rotation, the same
+    for every batch row) or from a (cos, sin, positions) tuple."""
+    if torch.is_tensor(freqs) and freqs.is_complex():
+        f = freqs.reshape(-1, Dh // 2)
+        if f.shape[0] != T:
+            raise _lib.WfdError(f"compute_qkv: freqs_cis holds {f.shape[0]} positions for T={T}")
+        f = f.to(device)
+        cos = f.real.to(torch.float32).contiguous()
+        sin = f.imag.to(torch.float32).contiguous()
+        pos = torch.arange(T, dtype=torch.int32, device=device)
+    else:
+        cos, sin, positions = freqs
+        if isinstance(positions, int):
+            positions = torch.arange(positions, positions + T, dtype=torch.int32, device=device)
+        pos = positions.to(device=device, dtype=torch.int32).reshape(-1)
+        if pos.numel() != T:
+            raise _lib.WfdError(f"compute_qkv: {pos.numel()} positions for T={T}")
+    return cos, sin, pos.repeat(B).contiguous()
+
+
 def compute_qkv(attn, x: torch.Tensor, freqs, ve=None, config=None):
-    """x (B, T, C) -> q (B, T, H, Dh), k / v (B, T, Hkv, Dh): the fused Wqkv
-    projection then RoPE on q and k (interleaved pairs). `attn` carries
-    Wqkv (a PackedWeight or an (N, C) weight), n_head, n_kv_head (or
-    n_kv_heads) and head_dim; `freqs` is (cos, sin, positions): float32
-    (S, Dh/2) tables and the T positions (int32 tensor, or a start position).
-    The parcae-only extras (value embeddings, clipping, qk bias, qk norm) are
-    absent from this model family: asking for one raises."""
+    """x (B, T, C) -> q (B, T, H, Dh), k / v (B, T, Hkv, Dh): the Q/K/V
+    projections, then RoPE on q and k (src/decoding/fa4_attention.py:128-152),
+    as one launch -- the fused projection with RoPE in its epilogue
+    (wfd_linear_qkv_rope_append) -- or the projection alone when
+    config.rope_settings.use_rope is False.
+
+    attn: the reference's attention module (separate bias-free c_q / c_k /
+    c_v projections, packed together once and kept on the module) or any
+    object with a fused `Wqkv` ((H + 2 Hkv) Dh, C) weight or PackedWeight;
+    plus n_head, n_kv_head (or n_kv_heads) and head_dim.
+    freqs: the reference's freqs_cis -- complex, T x Dh/2 values (e.g. shaped
+    (T, Dh/2) or (1, T, 1, Dh/2)), row t rotating position t of every batch
+    row -- or (cos, sin, positions): float32 (S, Dh/2) tables and the T
+    positions (int32 tensor, or a start position).
+    RoPE rotates interleaved pairs: (x[2j], x[2j+1]) as the complex number
+    x[2j] + i x[2j+1] times the rotation of pair j.
+    The parcae-only extras the reference also handles (value embeddings,
+    clip_qkv, qk_bias, qk_norm) are absent from this model family: asking
+    for one raises."""
     if ve is not None or (config is not None and any(getattr(config, f, None) for f in
                                                      ("clip_qkv", "qk_bias", "qk_norm"))):
         raise _lib.WfdError("compute_qkv: value embeddings / clip_qkv / qk_bias / qk_norm are not supported")
@@ -177,16 +236,19 @@ def compute_qkv(attn, x: torch.Tensor, freqs, ve=None, config=None):
     H = attn.n_head
     Hkv = getattr(attn, "n_kv_head", None) or attn.n_kv_heads
     Dh = attn.head_dim
-    cos, sin, positions = freqs
-    if isinstance(positions, int):
-        positions = torch.arange(positions, positions + T, dtype=torch.int32, device=x.device)
-    pos = positions.to(device=x.device, dtype=torch.int32).reshape(-1)
-    if pos.numel() != T:
-        raise _lib.WfdError(f"compute_qkv: {pos.numel()} positions for T={T}")
+    W = _fused_qkv_weight(attn)
     n = B * T
-    qkv = ops.linear(x.contiguous().view(n, C), attn.Wqkv)
+    xf = x.contiguous().view(n, C)
+    rope = getattr(getattr(config, "rope_settings", None), "use_rope", True)
+    if not rope:
+        qkv = ops.linear(xf, W)
+        q = qkv[:, : H * Dh].view(B, T, H, Dh)
+        k = qkv[:, H * Dh: (H + Hkv) * Dh].view(B, T, Hkv, Dh)
+        v = qkv[:, (H + Hkv) * Dh:].view(B, T, Hkv, Dh)
+        return q, k, v
+    cos, sin, pos = _rope_tables(freqs, B, T, Dh, x.device)
     kbuf = torch.empty(n, Hkv, Dh, dtype=x.dtype, device=x.device)
     vbuf = torch.empty_like(kbuf)
     rows = torch.arange(n, dtype=torch.int64, device=x.device)
-    q = ops.qkv_rope_append(qkv, pos.repeat(B), cos, sin, rows, kbuf, vbuf, H, Hkv, Dh)
+    q = ops.linear_qkv_rope_append(xf, W, pos, cos, sin, rows, kbuf, vbuf, H, Hkv, Dh)
     return q.view(B, T, H, Dh), kbuf.view(B, T, Hkv, Dh), vbuf.view(B, T, Hkv, Dh)

@@ -197,6 +197,7 @@ class LoopedModel:
         self.rope_sin = sin.to(self.device)
         self.s0 = initial_state_tokens(cfg, range(max_seq_len), state_seed, state_init).to(
             device=self.device, dtype=self.dtype)
+        self._s0_prompt: torch.Tensor | None = None  # the prompt pass's s0 stream, see _prompt_s0
         self.R = cfg.T_total + 2
         D = cfg.d_model
         # pool rows: R per sequence + one trash row for padding rows
@@ -670,6 +671,21 @@ class LoopedModel:
         return [int(host[-v - 1]) if v < 0 else v for v in values]
 
     # -- prefill -----------------------------------------------------------------------
+    def _prompt_s0(self, L: int) -> torch.Tensor:
+        """Rows [0, L) of the prompt pass's initial loop state, on the device.
+        It is one stream for every prompt (model.initial_state_prefill), and
+        its generator fills rows in order, so rows [0, L) of a longer draw are
+        the draw of length L (tested): the stream is drawn once for the longest
+        prompt so far (at least doubling) and sliced, not redrawn on the host
+        for every prompt."""
+        t = self._s0_prompt
+        if t is None or t.shape[0] < L:
+            n = max(L, min(2 * (0 if t is None else t.shape[0]), self.max_seq_len))
+            t = initial_state_prefill(self.cfg, n, self.state_seed, self.state_init).to(device=self.device,
+                                                                                        dtype=self.dtype)
+            self._s0_prompt = t
+        return t[:L]
+
     def prefill_seq(self, cache, b: int, token_ids) -> torch.Tensor:
         """Whole prompt of sequence b at positions [0, L): fills every slot's
         [0, L) and returns the last position's logits (V,) float32. Runs eagerly
@@ -710,8 +726,7 @@ class LoopedModel:
             nxt = W[f"prelude.{i + 1}.norm_1"] if i + 1 < c.n_prelude else None
             self._block(f"prelude.{i}.", L, sc, pos_d, kvlen_d, rb_l(i), fr_l(i), L, ws, cache, nxt,
                         final_out=state[:, D:], segments=seg_l(i), dense=dense)
-        s0 = initial_state_prefill(c, L, self.state_seed, self.state_init)
-        state[:, :D].copy_(s0.to(device=self.device, dtype=self.dtype))
+        state[:, :D].copy_(self._prompt_s0(L))
         for r in range(c.T_total):
             if dense:
                 torch.mm(state, self.Wd["adapter"].t(), out=sc["x"][:L])
