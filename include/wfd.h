@@ -42,8 +42,54 @@ enum { WFD_EPI_PLAIN = 0, WFD_EPI_SWIGLU = 1 };
 /* Message for the last failing call on this thread. */
 const char* wfd_last_error(void);
 /* Bumped whenever an entry point's signature changes or one is added (5: wfd_argmax's
-   accept flags, wfd_attn_varlen_rows; 6: wfd_linear_argmax, wfd_argmax_groups). */
+   accept flags, wfd_attn_varlen_rows; 6: wfd_linear_argmax, wfd_argmax_groups;
+   7: folded norm pairs -- wfd_linear_prep, wfd_norm_prep, the row-scale argument of
+   wfd_linear, wfd_linear_qkv_rope_append and wfd_linear_argmax). */
 int wfd_abi_version(void);
+
+/*
+ * Folded RMSNorm pairs (decode). A block's residual stream is kept as r (one
+ * dtype row per token) and the per-row scale s of the norm that last
+ * normalized it: the residual the block adds is x = round((r * s) * w) (w
+ * that norm's weight; without a norm, x = r). A linear that reads a pair of
+ * norms -- first a (weight wa; may be absent), then b (weight wb) -- of
+ * r does not read the normalized row: it reads A = round((r * wa) * wb) and
+ * multiplies its fp32 output by scale = s_a * s_b, where
+ *   s_a = 1 / sqrt(sum(r^2) / D + eps)             (1 when a is absent),
+ *   s_b = 1 / sqrt(s_a^2 * sum((r * wa)^2) / D + eps),
+ * which is norm_b(norm_a(r)) applied after the product instead of before it.
+ * The linear that produces r (proj, the MLP down projection, the adapter)
+ * computes r = round(y + x), A and the sums in its epilogue, so no launch
+ * sits between the two linears. The sums are reduced in one fixed order
+ * wherever they are formed: per 8-column group g (columns 8g..8g+7) the tree
+ * ((c0+c1)+(c2+c3))+((c4+c5)+(c6+c7)) of the squares, then lane L of a wave
+ * adds groups L, L+64, L+128, ... in order from +0 and the 64 lane sums meet
+ * in a butterfly (xor 32, 16, ..., 1); every product and sum is rounded on
+ * its own (no fused multiply-add). So a row's bits never depend on n or on
+ * which kernels formed them.
+ */
+typedef struct wfd_prep {
+  const void* r_in;   /* residual stream to add (NULL: none) ... */
+  int64_t ld_in;
+  const float* s_in;  /* ... its per-row scale (NULL: 1) ... */
+  const void* w_in;   /* ... and norm weight (NULL: none): x = round((r_in * s_in) * w_in) */
+  void* r_out;        /* r = round(y + x), or y without r_in (NULL: not kept) */
+  int64_t ld_out;
+  void* a_out;        /* the next linear's operand A = round((r * wa) * wb) */
+  int64_t ld_a;
+  const void* wa;     /* the next pair's weights (wa NULL: norm a absent) */
+  const void* wb;
+  float* part;        /* wfd_linear_prep: the sums per 8-column group, part[(m * D / 8 + g) * 2 + {0, 1}] */
+} wfd_prep_t;
+
+typedef struct wfd_rowscale {
+  const float* scale; /* the per-row scale s_a * s_b (from wfd_norm_prep), or NULL and ... */
+  const float* part;  /* ... the group sums a wfd_linear_prep left (few-row launches only) */
+  int D;              /* row width of r (D / 8 groups) */
+  int two;            /* 1: norm a present; 0: absent (s_a = 1) */
+  float eps;
+  float* s_out;       /* with part: s_a per row (NULL: not kept) */
+} wfd_rowscale_t;
 
 /*
  * Wavefront decode attention (per-query slot prefix, read in place).
@@ -208,7 +254,43 @@ int wfd_linear_pack(const void* W, void* W_packed, int N, int K, int dtype, int 
  *   huginn_blocks_batch.py:149,160-161,299,345).
  */
 int wfd_linear(const void* x, const int32_t* x_rows, int64_t ldx, const void* W, void* y, int64_t ldy, int n, int N,
-               int K, int dtype, int out_dtype, int epilogue, int pair_off, wfd_stream_t stream);
+               int K, int dtype, int out_dtype, int epilogue, int pair_off, const wfd_rowscale_t* rs,
+               wfd_stream_t stream);
+/* rs (NULL: none): x holds the A rows of a folded norm pair (see wfd_prep_t) and
+ * each output row is multiplied by its scale before the epilogue (SwiGLU after
+ * the scale). rs->part (group sums) is accepted for n <= 16 only. */
+
+/*
+ * A d_model-output linear (plain epilogue, n <= 16) whose epilogue prepares
+ * the residual stream and the next linear's operand: with y the linear's fp32
+ * output, r = round(y + x) (see wfd_prep_t; x from r_in / s_in / w_in),
+ * A = round((r * wa) * wb), and the group sums of r^2 and (r * wa)^2 for the
+ * consumer's row scale. W packed (plain). n <= 16 and N a multiple of 16.
+ * Replaces: proj / the MLP down projection / the adapter with the residual
+ *   add and the residual norms after them (src/decoding/huginn_blocks.py:95,
+ *   100-102,216; huginn_blocks_batch.py:159-161,299), whose full-row sums
+ *   move into the consuming linear.
+ */
+int wfd_linear_prep(const void* x, const int32_t* x_rows, int64_t ldx, const void* W, int n, int N, int K, int dtype,
+                    const wfd_prep_t* pp, wfd_stream_t stream);
+
+/*
+ * The row form of a folded norm pair, one wave per row: the row y is
+ * a[i * lda] (part NULL) or the in-order slice sum of wfd_linear_partials'
+ * part (rounded to dtype, wfd_linear's output bit for bit); r, A as
+ * wfd_linear_prep computes them, and scale_out[i] = s_a * s_b, s_out[i] = s_a
+ * (same sums, same order). With h_out instead (final form): h_out[h_rows ?
+ * h_rows[i] : i] = round((r * s_a) * wa) with s_a from sum(r^2), the block's
+ * last norm (pp->wb, a_out, scale_out unused). D a multiple of 128 (bf16) /
+ * 64 (fp32), D <= 4096.
+ * Replaces: the residual norms after proj, the MLP down projection and the
+ *   adapter (src/decoding/huginn_blocks.py:95,101-102,216;
+ *   huginn_blocks_batch.py:159-161,299), for many-row unions and for the
+ *   last norm of a pass.
+ */
+int wfd_norm_prep(const void* a, int64_t lda, const float* part, int64_t slice_stride, int nslices,
+                  const wfd_prep_t* pp, int two, float eps, float* scale_out, float* s_out, void* h_out,
+                  const int32_t* h_rows, int64_t ldh, int n, int D, int dtype, wfd_stream_t stream);
 
 /* Number of K slices of wfd_linear's arithmetic contract for this K (1..4);
  * 0 if K is not a positive multiple of wfd_linear_k_multiple(dtype). */
@@ -244,7 +326,10 @@ int wfd_linear_partials(const void* x, const int32_t* x_rows, int64_t ldx, const
 int wfd_linear_qkv_rope_append(const void* x, const int32_t* x_rows, int64_t ldx, const void* Wqkv, int n, int K,
                                const int32_t* pos, const float* rope_cos, const float* rope_sin, int rope_rows,
                                const int64_t* flat_row, void* q_out, void* k_cache, void* v_cache,
-                               int64_t kv_block_rows, int H, int Hkv, int Dh, int dtype, wfd_stream_t stream);
+                               int64_t kv_block_rows, int H, int Hkv, int Dh, int dtype, const wfd_rowscale_t* rs,
+                               wfd_stream_t stream);
+/* rs as for wfd_linear: the row scale multiplies the qkv values before they are
+ * rounded and rotated. */
 
 /*
  * x_out[out_rows ? out_rows[i] : i] = rmsnorm(a[a_rows ? a_rows[i] : i] + res[i]) * w1
@@ -354,7 +439,9 @@ int wfd_linear_argmax_groups(int n, int N, int K, int dtype);
  *   greedy_sample's argmax (src/decoding/acceptance.py:40-44).
  */
 int wfd_linear_argmax(const void* x, const int32_t* x_rows, int64_t ldx, const void* W, float* y, int64_t ldy, int n,
-                      int N, int K, int dtype, float* part_val, int32_t* part_idx, wfd_stream_t stream);
+                      int N, int K, int dtype, float* part_val, int32_t* part_idx, const wfd_rowscale_t* rs,
+                      wfd_stream_t stream);
+/* rs as for wfd_linear: the logits are scaled before the group bests are taken. */
 
 /*
  * wfd_argmax from the column-group bests wfd_linear_argmax left (groups per

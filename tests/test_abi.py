@@ -1,6 +1,7 @@
 """The C-ABI library loads on a host without a GPU and exports exactly what include/wfd.h declares (CPU)."""
 from __future__ import annotations
 
+import ctypes
 import os
 import re
 import subprocess
@@ -34,7 +35,7 @@ def test_library_loads_and_exports_every_symbol():
 
 def test_host_only_entry_points():
     lib = _lib.load()
-    assert lib.wfd_abi_version() == 6
+    assert lib.wfd_abi_version() == 7
     # column groups of the tile argmax: 2000 tiles at <= 16 rows (lm_head), half tiles below 256 tiles,
     # none at 17 rows, for fp32 or for a K the few-row kernel does not take
     assert lib.wfd_linear_argmax_groups(8, 32000, 2048, _lib.BF16) == 2000
@@ -42,10 +43,20 @@ def test_host_only_entry_points():
     assert lib.wfd_linear_argmax_groups(17, 32000, 2048, _lib.BF16) == 0
     assert lib.wfd_linear_argmax_groups(8, 32000, 2048, _lib.F32) == 0
     assert lib.wfd_linear_argmax_groups(8, 32000, 128 * 49, _lib.BF16) == 0
-    rc = lib.wfd_linear_argmax(None, None, 2048, None, None, 32000, 17, 32000, 2048, 1, None, None, None)
+    rc = lib.wfd_linear_argmax(None, None, 2048, None, None, 32000, 17, 32000, 2048, 1, None, None, None, None)
     assert rc == -2 and b"no column groups" in lib.wfd_last_error()
-    rc = lib.wfd_linear_argmax(None, None, 2048, None, None, 32000, 8, 32000, 2048, 1, None, None, None)
+    rc = lib.wfd_linear_argmax(None, None, 2048, None, None, 32000, 8, 32000, 2048, 1, None, None, None, None)
     assert rc == -1 and b"null pointer" in lib.wfd_last_error()
+    # folded norm pairs: the prep epilogue has a few-row form only; the row form checks its shape first
+    pp = _lib.PrepArgs()
+    rc = lib.wfd_linear_prep(None, None, 2048, None, 17, 2048, 2048, 1, ctypes.addressof(pp), None)
+    assert rc == -1 and b"null pointer" in lib.wfd_last_error()
+    assert lib.wfd_norm_prep(None, 0, None, 0, 0, ctypes.addressof(pp), 1, 1e-6, None, None, None, None, 0, 1, 4096,
+                             1, None) == -1  # D beyond the folded form's 2048
+    assert b"at most 2048" in lib.wfd_last_error()
+    assert lib.wfd_norm_prep(None, 0, None, 0, 0, ctypes.addressof(pp), 1, 1e-6, None, None, None, None, 0, 0, 2048,
+                             1, None) == 0   # no rows: nothing to do
+    assert ctypes.sizeof(_lib.RowScaleArgs) == 40 and ctypes.sizeof(_lib.PrepArgs) == 88
     assert lib.wfd_argmax_groups(None, None, 0, None, None, None, 0, None, None, 1, None) == -1
     assert lib.wfd_argmax_groups(None, None, 2000, None, None, None, 0, None, None, 0, None) == 0
     assert lib.wfd_argmax_groups(None, None, 2000, None, None, None, 0, None, None, 1, None) == -1
@@ -66,7 +77,7 @@ def test_host_only_entry_points():
     rc = lib.wfd_attn_prefill(None, None, None, 0, None, None, None, None, 1, 10, 16, 3, 64, 1, 0.1, None)
     assert rc == -1 and b"wfd_attn_prefill: bad shape" in lib.wfd_last_error()
     assert lib.wfd_attn_prefill(None, None, None, 0, None, None, None, None, 0, 10, 16, 4, 64, 1, 0.1, None) == 0
-    rc = lib.wfd_linear(None, None, 100, None, None, 16, 2, 16, 100, 1, 1, 0, 0, None)
+    rc = lib.wfd_linear(None, None, 100, None, None, 16, 2, 16, 100, 1, 1, 0, 0, None, None)
     assert rc == -1
     # packing: shape and aliasing are checked on the host
     assert lib.wfd_linear_pack(8, 16, 24, 128, 1, 0, 0, None) == -1      # N not a multiple of 16
@@ -82,12 +93,12 @@ def test_alignment_and_grid_checks_reject_before_launch():
     happens on the host, before any launch."""
     lib = _lib.load()
     # 16-byte loads of x rows and packed weights: pointers and the x pitch are checked
-    rc = lib.wfd_linear(4096 + 8, None, 128, 8192, 8192, 16, 2, 16, 128, 1, 1, 0, 0, None)
+    rc = lib.wfd_linear(4096 + 8, None, 128, 8192, 8192, 16, 2, 16, 128, 1, 1, 0, 0, None, None)
     assert rc == -1 and b"16-byte aligned" in lib.wfd_last_error()
-    rc = lib.wfd_linear(4096, None, 132, 8192, 8192, 16, 2, 16, 128, 1, 1, 0, 0, None)
+    rc = lib.wfd_linear(4096, None, 132, 8192, 8192, 16, 2, 16, 128, 1, 1, 0, 0, None, None)
     assert rc == -1 and b"16-byte aligned" in lib.wfd_last_error()
     rc = lib.wfd_linear_qkv_rope_append(4096, None, 132, 8192, 2, 128, 16, 16, 16, 8, 16, 16, 16, 16, 0, 1, 1, 16, 1,
-                                        None)
+                                        None, None)
     assert rc == -1 and b"16-byte aligned" in lib.wfd_last_error()
     assert lib.wfd_attn_decode(None, None, None, 0, None, None, None, None, 0, 16, 16, 64, 1, 0.1, 10, None, 0, None) == 0
     rc = lib.wfd_attn_decode(4096, 4096 + 4, 4096, 0, 16, 16, None, 4096, 1, 16, 16, 64, 1, 0.1, 10, 4096, 1 << 20, None)

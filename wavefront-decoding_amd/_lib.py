@@ -47,9 +47,12 @@ SIGNATURES: dict[str, tuple] = {
                                    _i32, _i32, _vp]),
     "wfd_linear_k_multiple": (_i32, [_i32]),
     "wfd_linear_pack": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
-    "wfd_linear": (_i32, [_vp, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
+    "wfd_linear": (_i32, [_vp, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp]),
+    "wfd_linear_prep": (_i32, [_vp, _vp, _i64, _vp, _i32, _i32, _i32, _i32, _vp, _vp]),
+    "wfd_norm_prep": (_i32, [_vp, _i64, _vp, _i64, _i32, _vp, _i32, _f32, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32,
+                             _vp]),
     "wfd_linear_qkv_rope_append": (_i32, [_vp, _vp, _i64, _vp, _i32, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp,
-                                          _i64, _i32, _i32, _i32, _i32, _vp]),
+                                          _i64, _i32, _i32, _i32, _i32, _vp, _vp]),
     "wfd_add_rmsnorm": (_i32, [_vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i32, _i32, _f32,
                                _i32, _vp]),
     "wfd_linear_slices": (_i32, [_i32, _i32]),
@@ -62,9 +65,24 @@ SIGNATURES: dict[str, tuple] = {
     "wfd_copy_rows": (_i32, [_vp, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _i32, _vp]),
     "wfd_argmax": (_i32, [_vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _i32, _i32, _vp]),
     "wfd_linear_argmax_groups": (_i32, [_i32, _i32, _i32, _i32]),
-    "wfd_linear_argmax": (_i32, [_vp, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
+    "wfd_linear_argmax": (_i32, [_vp, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "wfd_argmax_groups": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _i64, _vp, _vp, _i32, _vp]),
 }
+
+
+
+class PrepArgs(ctypes.Structure):
+    """wfd_prep_t (include/wfd.h): the residual stream and operand of a folded norm pair."""
+
+    _fields_ = [("r_in", _vp), ("ld_in", _i64), ("s_in", _vp), ("w_in", _vp), ("r_out", _vp), ("ld_out", _i64),
+                ("a_out", _vp), ("ld_a", _i64), ("wa", _vp), ("wb", _vp), ("part", _vp)]
+
+
+class RowScaleArgs(ctypes.Structure):
+    """wfd_rowscale_t (include/wfd.h): where a linear finds its rows' scales."""
+
+    _fields_ = [("scale", _vp), ("part", _vp), ("D", _i32), ("two", _i32), ("eps", _f32), ("s_out", _vp)]
+
 
 _LIB: ctypes.CDLL | None = None
 

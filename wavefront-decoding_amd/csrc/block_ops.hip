@@ -303,6 +303,176 @@ static void launch_add_rmsnorm(int dtype, const void* a, const int32_t* a_rows, 
                               stream);
 }
 
+// Folded norm pairs, the row form (wfd_norm_prep; wfd_prep_t in wfd.h). One
+// wave per row, the lane layout of add_rmsnorm_kernel: lane (j, c) holds, per
+// round rr, chunk p = 16 rr + c, steps s, elements p KC + s KSTEP + j V ..
+// + V -- for bf16 one whole 8-column group per (rr, s), for fp32 half of one
+// (the other half in lane j ^ 1). Each element is wfd_linear_prep's epilogue
+// value (prep_value), the group sums are the same trees, gathered per row in
+// LDS and reduced in the one order (fold_load / fold_sums), so the scales
+// equal what a consumer computes from wfd_linear_prep's group sums, bit for
+// bit. SPLIT: y is the in-order slice sum of wfd_linear_partials (the
+// linear's output before its rounding); else y = a[i] (already rounded).
+// FINAL: h = round((r * s_a) * wa) for the rows h_rows, instead of A and the
+// scales.
+template <typename T, bool SPLIT, bool RES, bool FINAL, int MAXR>
+__global__ __launch_bounds__(256) void norm_prep_kernel(const T* __restrict__ a, int64_t lda,
+                                                        const float* __restrict__ part, int64_t slice_stride,
+                                                        int nslices, const wfd_prep_t pp, int two, float eps,
+                                                        float* __restrict__ scale_out, float* __restrict__ s_out,
+                                                        T* __restrict__ h_out, const int32_t* __restrict__ h_rows,
+                                                        int64_t ldh, int n, int D) {
+  constexpr int V = Chunk<T>::V;
+  constexpr int KSTEP = Chunk<T>::KSTEP;
+  constexpr int KC = Chunk<T>::KC;
+  __shared__ float2 gps[4][kFoldMaxD / 8];  // each row's group sums
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int i = blockIdx.x * (blockDim.x >> 6) + wv;
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15;
+  const int j = lane >> 4;
+  if (i >= n) return;  // no barriers below
+  const int P = D / KC;
+  const int G = D / 8;
+  const T* wa_t = (const T*)pp.wa;
+  const T* wb_t = (const T*)pp.wb;
+  float r[MAXR][kChunkSteps][V];
+  float A[MAXR][kChunkSteps][V];
+  float s_in = 1.f;
+  if constexpr (RES) {
+    if (pp.s_in) s_in = pp.s_in[i];
+  }
+#pragma unroll
+  for (int rr = 0; rr < MAXR; ++rr) {
+    const int p = rr * 16 + c < P ? rr * 16 + c : P - 1;  // lanes past the last chunk re-read it (never used)
+#pragma unroll
+    for (int s = 0; s < kChunkSteps; ++s) {
+      const int64_t off = (int64_t)p * KC + s * KSTEP + j * V;
+      float y[V];
+      if constexpr (SPLIT) {
+        // slices in order from +0 (a slice past nslices re-reads slice 0 and adds +0)
+#pragma unroll
+        for (int e = 0; e < V; ++e) y[e] = 0.f;
+#pragma unroll
+        for (int q = 0; q < kSplitMaxSlices; ++q) {
+          const bool live = q < nslices;
+          const float* src = part + (live ? q : 0) * slice_stride + (int64_t)i * D + off;
+#pragma unroll
+          for (int h = 0; h < V / 4; ++h) {
+            const u32x4 w = ld16(src + 4 * h);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[4 * h + e] += live ? __uint_as_float(w[e]) : 0.f;
+          }
+        }
+      } else {
+        Elem<T>::unpack(ld16(a + (int64_t)i * lda + off), y);
+      }
+      float rin[V], win[V], wa[V], wb[V];
+#pragma unroll
+      for (int e = 0; e < V; ++e) rin[e] = win[e] = wa[e] = wb[e] = 1.f;
+      if constexpr (RES) {
+        Elem<T>::unpack(ld16((const T*)pp.r_in + (int64_t)i * pp.ld_in + off), rin);
+        if (pp.w_in) Elem<T>::unpack(ld16((const T*)pp.w_in + off), win);
+      }
+      if (wa_t) Elem<T>::unpack(ld16(wa_t + off), wa);
+      if constexpr (!FINAL) Elem<T>::unpack(ld16(wb_t + off), wb);
+      float sr[V], su[V];
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        const PrepVal pv = prep_value<T>(y[e], RES, rin[e], s_in, win[e], wa[e], wb[e]);
+        r[rr][s][e] = pv.r;
+        A[rr][s][e] = pv.A;
+        sr[e] = pv.sr;
+        su[e] = pv.su;
+      }
+      // the group's tree: ((c0+c1)+(c2+c3))+((c4+c5)+(c6+c7))
+      float gr = tree4(sr[0], sr[1], sr[2], sr[3]);
+      float gu = tree4(su[0], su[1], su[2], su[3]);
+      if constexpr (V == 8) {
+        gr = add_rn(gr, tree4(sr[4], sr[5], sr[6], sr[7]));
+        gu = add_rn(gu, tree4(su[4], su[5], su[6], su[7]));
+      } else {  // the other half of the group sits in lane j ^ 1
+        gr = add_rn(gr, __shfl_xor(gr, 16, 64));
+        gu = add_rn(gu, __shfl_xor(gu, 16, 64));
+      }
+      if (rr * 16 + c < P && (V == 8 || (j & 1) == 0)) gps[wv][off >> 3] = float2{gr, gu};
+    }
+  }
+  asm volatile("" ::: "memory");  // the lanes' group sums are in LDS before any lane reads them (one wave)
+  float2 gpv[kFoldGroupsPerLane];
+  fold_load(gpv, gps[wv], G, lane);
+  float srow, surow;
+  fold_sums(gpv, srow, surow);
+  float s_a, scale;
+  pair_scale(srow, surow, D, eps, two != 0, s_a, scale);
+  if constexpr (FINAL) {
+    const int64_t orow = h_rows ? h_rows[i] : i;
+#pragma unroll
+    for (int rr = 0; rr < MAXR; ++rr)
+#pragma unroll
+      for (int s = 0; s < kChunkSteps; ++s) {
+        const int p = rr * 16 + c;
+        float wa[V], h[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) wa[e] = 1.f;
+        if (wa_t) Elem<T>::unpack(ld16(wa_t + (int64_t)(p < P ? p : P - 1) * KC + s * KSTEP + j * V), wa);
+#pragma unroll
+        for (int e = 0; e < V; ++e) h[e] = norm_value<T>(r[rr][s][e], s_a, wa[e]);
+        if (p < P)
+          *reinterpret_cast<u32x4*>(h_out + orow * ldh + (int64_t)p * KC + s * KSTEP + j * V) = Elem<T>::pack(h);
+      }
+  } else {
+#pragma unroll
+    for (int rr = 0; rr < MAXR; ++rr)
+#pragma unroll
+      for (int s = 0; s < kChunkSteps; ++s) {
+        const int p = rr * 16 + c;
+        if (p >= P) continue;
+        const int64_t off = (int64_t)p * KC + s * KSTEP + j * V;
+        if (pp.r_out) *reinterpret_cast<u32x4*>((T*)pp.r_out + (int64_t)i * pp.ld_out + off) = Elem<T>::pack(r[rr][s]);
+        *reinterpret_cast<u32x4*>((T*)pp.a_out + (int64_t)i * pp.ld_a + off) = Elem<T>::pack(A[rr][s]);
+      }
+    if (lane == 0) {
+      scale_out[i] = scale;
+      if (s_out) s_out[i] = s_a;
+    }
+  }
+}
+
+template <typename T, bool SPLIT, bool RES, bool FINAL>
+static void launch_norm_prep_t(const void* a, int64_t lda, const float* part, int64_t slice_stride, int nslices,
+                               const wfd_prep_t& pp, int two, float eps, float* scale_out, float* s_out, void* h_out,
+                               const int32_t* h_rows, int64_t ldh, int n, int D, hipStream_t stream) {
+  const int rpw = n >= kNormRowsPerCuLaunch ? 4 : 1;  // as add_rmsnorm: rows spread one per CU below 1024
+  const dim3 grid((n + rpw - 1) / rpw), block(64 * rpw);
+  if (D <= 16 * Chunk<T>::KC)
+    hipLaunchKernelGGL((norm_prep_kernel<T, SPLIT, RES, FINAL, 1>), grid, block, 0, stream, (const T*)a, lda, part,
+                       slice_stride, nslices, pp, two, eps, scale_out, s_out, (T*)h_out, h_rows, ldh, n, D);
+  else
+    hipLaunchKernelGGL((norm_prep_kernel<T, SPLIT, RES, FINAL, kFoldMaxD / (16 * Chunk<T>::KC)>), grid, block, 0,
+                       stream, (const T*)a, lda, part, slice_stride, nslices, pp, two, eps, scale_out, s_out,
+                       (T*)h_out, h_rows, ldh, n, D);
+}
+
+template <typename T>
+static void launch_norm_prep(const void* a, int64_t lda, const float* part, int64_t slice_stride, int nslices,
+                             const wfd_prep_t& pp, int two, float eps, float* scale_out, float* s_out, void* h_out,
+                             const int32_t* h_rows, int64_t ldh, int n, int D, hipStream_t stream) {
+#define WFD_NP(SP, RS, FI)                                                                                         \
+  launch_norm_prep_t<T, SP, RS, FI>(a, lda, part, slice_stride, nslices, pp, two, eps, scale_out, s_out, h_out, \
+                                    h_rows, ldh, n, D, stream)
+  const bool sp = part != nullptr, rs = pp.r_in != nullptr, fi = h_out != nullptr;
+  if (sp && rs && fi) WFD_NP(true, true, true);
+  else if (sp && rs) WFD_NP(true, true, false);
+  else if (sp && fi) WFD_NP(true, false, true);
+  else if (sp) WFD_NP(true, false, false);
+  else if (rs && fi) WFD_NP(false, true, true);
+  else if (rs) WFD_NP(false, true, false);
+  else if (fi) WFD_NP(false, false, true);
+  else WFD_NP(false, false, false);
+#undef WFD_NP
+}
+
 template <typename T>
 __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
     const T* __restrict__ qkv, int64_t ldq, const int32_t* __restrict__ pos, const float* __restrict__ cos_t,
@@ -539,7 +709,7 @@ extern "C" {
 
 const char* wfd_last_error(void) { return wfd::g_err; }
 
-int wfd_abi_version(void) { return 6; }
+int wfd_abi_version(void) { return 7; }
 
 int wfd_add_rmsnorm(const void* a, const int32_t* a_rows, int64_t lda, const void* res, int64_t ldr, const void* w1,
                     const void* w2, void* x_out, const int32_t* out_rows, int64_t ldo, void* h_out, int64_t ldh, int n,
@@ -608,6 +778,46 @@ int wfd_add_rmsnorm_split(const float* part, int64_t slice_stride, int nslices, 
   launch_add_rmsnorm<kSrcSplit>(dtype, nullptr, nullptr, 0, res, ldr, w1, w2, x_out, out_rows, ldo, h_out, ldh, n, D,
                                 eps, sp, stream);
   return launch_status("wfd_add_rmsnorm_split");
+}
+
+int wfd_norm_prep(const void* a, int64_t lda, const float* part, int64_t slice_stride, int nslices,
+                  const wfd_prep_t* pp, int two, float eps, float* scale_out, float* s_out, void* h_out,
+                  const int32_t* h_rows, int64_t ldh, int n, int D, int dtype, hipStream_t stream) {
+  using namespace wfd;
+  if (dtype != kBF16 && dtype != kF32) {
+    set_error("wfd_norm_prep: unsupported dtype %d", dtype);
+    return kUnsupported;
+  }
+  const int kc = dtype == kBF16 ? Chunk<bf16_t>::KC : Chunk<float>::KC;
+  if (n < 0 || D <= 0 || D > kFoldMaxD || D % kc != 0 ||
+      (part && (nslices < 1 || nslices > kSplitMaxSlices || slice_stride < (int64_t)n * D))) {
+    set_error("wfd_norm_prep: bad shape n=%d D=%d (a multiple of %d, at most %d) nslices=%d", n, D, kc, kFoldMaxD,
+              nslices);
+    return kBadArg;
+  }
+  if (n == 0) return kOk;
+  const bool fin = h_out != nullptr;
+  if (!pp || (!part && !a) || (fin && (!pp->wa || !two)) || (!fin && (!pp->a_out || !pp->wb || !scale_out))) {
+    set_error("wfd_norm_prep: null pointer argument (the final form needs h_out, pp->wa and two; the prep form "
+              "pp->a_out, pp->wb and scale_out)");
+    return kBadArg;
+  }
+  const int esz = dtype == kBF16 ? 2 : 4;
+  if ((((uintptr_t)a | (uintptr_t)part | (uintptr_t)pp->r_in | (uintptr_t)pp->w_in | (uintptr_t)pp->r_out |
+        (uintptr_t)pp->a_out | (uintptr_t)pp->wa | (uintptr_t)pp->wb | (uintptr_t)h_out) & 15) ||
+      ((slice_stride * 4) & 15) || (a && ((lda * esz) & 15)) || (pp->r_in && ((pp->ld_in * esz) & 15)) ||
+      (pp->r_out && ((pp->ld_out * esz) & 15)) || (pp->a_out && ((pp->ld_a * esz) & 15)) ||
+      (h_out && ((ldh * esz) & 15))) {
+    set_error("wfd_norm_prep: rows must be 16-byte aligned");
+    return kBadArg;
+  }
+  if (dtype == kBF16)
+    launch_norm_prep<bf16_t>(a, lda, part, slice_stride, nslices, *pp, two, eps, scale_out, s_out, h_out, h_rows, ldh,
+                             n, D, stream);
+  else
+    launch_norm_prep<float>(a, lda, part, slice_stride, nslices, *pp, two, eps, scale_out, s_out, h_out, h_rows, ldh,
+                            n, D, stream);
+  return launch_status("wfd_norm_prep");
 }
 
 int wfd_embed_rmsnorm(const int64_t* ids, const int64_t* ring, int64_t ring_len, const void* table, float scale,

@@ -88,7 +88,9 @@ constexpr int kGemmMinBlockTiles = 512;
 // stream kernel, with this many LDS stages
 constexpr int kStreamMaxTiles = 256;
 constexpr int kStreamStages = 4;
-enum Epilogue : int { kEpiPlain = 0, kEpiSwiGLU = 1, kEpiRope = 2 };
+// kEpiPrep: a d_model-output linear whose epilogue prepares the residual
+// stream of a folded norm pair (wfd_prep_t), few-row launches only
+enum Epilogue : int { kEpiPlain = 0, kEpiSwiGLU = 1, kEpiRope = 2, kEpiPrep = 3 };
 
 // K slices and sub-slices of the arithmetic contract (see the header): at most
 // 4 slices of Q = ceil(P / 4) chunks, each of at most 4 sub-slices of
@@ -292,6 +294,13 @@ __device__ __forceinline__ void gather_rope(RopePre (&rp)[NT][4], const RopeArgs
   }
 }
 
+// A lane's rows row4 .. row4 + 3 of a folded norm pair's per-row scales
+// (rows past n read row 0's; 1 without scales).
+__device__ __forceinline__ void load_row_scales(float (&rsv)[4], const float* __restrict__ rscale, int row4, int n) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) rsv[r] = rscale ? rscale[row4 + r < n ? row4 + r : 0] : 1.f;
+}
+
 // Store of output (row, column c of tile g); `partner` is the value of column
 // c ^ 1 (RoPE) or c ^ 8 (SwiGLU: the up value of gate column c < 8). Every
 // lane fetches its partner before any lane branches here.
@@ -435,14 +444,54 @@ __device__ __forceinline__ void chunk_mma(f32x4 (&acc)[NT], const u32x4 (&xf)[kC
 // traffic), so a 2048-column projection spreads over 256 workgroups instead
 // of 128. The MFMA output of a column does not depend on the other columns'
 // operands, so both forms give the same bits.
+// The consumer side of a folded norm pair in the few-row kernel (rs.part: each
+// row's group sums, reduced by the row's wave; rs.scale: the scales
+// precomputed): issued first, so their loads are the oldest of the launch.
+
+// The producer side (EPI == kEpiPrep): thread (ln, r) of the epilogue owns
+// output (row 4 (ln / 16) + r, column 16 g + ln % 16); the operands of its
+// element, fetched at launch.
+struct PrepPre {
+  float rin, sin, win, wa, wb;
+};
+
 template <typename T, typename TO, int EPI, int RM, bool HALF, int WW>
-__global__ __launch_bounds__(64 * WW) void linear_wide_kernel(
+__global__ __launch_bounds__(64 * WW) __attribute__((amdgpu_waves_per_eu(WW == 8 && EPI != kEpiRope ? 6 : 1))) void linear_wide_kernel(
     const T* __restrict__ x, const int32_t* __restrict__ x_rows, int64_t ldx, const T* __restrict__ W,
-    TO* __restrict__ y, int64_t ldy, int n, int K, int pair_off, const RopeArgs ra, const TileArgmax am) {
+    TO* __restrict__ y, int64_t ldy, int n, int K, int pair_off, const RopeArgs ra, const TileArgmax am,
+    const wfd_rowscale_t rs, const wfd_prep_t pp) {
   constexpr int KPW = kSlices * kSubSlices / WW;  // sub-slices per wave
   static_assert(KPW * WW == kSlices * kSubSlices, "16 or 8 waves");
   __shared__ f32x4 red[kSlices * kSubSlices][64];  // sub-slice sums [sub-slice][lane]
   __shared__ __align__(16) u32x4 xl[WW][kXcUnits];  // each wave's x chunk (coalesced load -> fragments)
+  __shared__ float rsc[kWideMaxRows];               // the rows' scales (rs.part)
+  // folded norm pair, consumer side: row `wave`'s group sums (rs.part) or
+  // this epilogue thread's row scale (rs.scale), loaded before anything else
+  const bool by_part = EPI != kEpiPrep && rs.part != nullptr;
+  constexpr int RPW = kWideMaxRows / WW;  // rows whose sums a wave reduces: wave, wave + WW
+  // 16 waves: the group sums are loaded at launch and held through the main
+  // loop; 8 waves (three workgroups per CU by LDS, a register budget of 80)
+  // load them after it, one more round trip instead of a third of the residency
+  constexpr bool kEarlyGroups = WW == kWideWaves;
+  float2 gpv[RPW][kFoldGroupsPerLane];
+  float esc = 1.f;
+  auto load_groups = [&]() {
+    const int G = rs.D >> 3;
+    const int wv = threadIdx.x >> 6;
+#pragma unroll
+    for (int q = 0; q < RPW; ++q) {
+      const int rw = wv + WW * q;
+      if (by_part && rw < n)  // uniform over the wave
+        fold_load(gpv[q], reinterpret_cast<const float2*>(rs.part) + (int64_t)rw * G, G, threadIdx.x & 63);
+    }
+  };
+  {
+    if constexpr (kEarlyGroups) load_groups();
+    if (EPI != kEpiPrep && rs.scale != nullptr && threadIdx.x < 256) {
+      const int orow = 4 * ((threadIdx.x >> 2) >> 4) + (threadIdx.x & 3);
+      esc = rs.scale[orow < n ? orow : 0];
+    }
+  }
   constexpr int V = LinTraits<T>::V;
   const int P = K / LinTraits<T>::KC;
   const int Q = slice_chunks(P);
@@ -468,6 +517,19 @@ __global__ __launch_bounds__(64 * WW) void linear_wide_kernel(
       int dbase;
       const int head = tile_head(ra, g, dbase);
       rp = rope_pre(ra, rope_row_pos(ra, row), head, dbase + ((threadIdx.x >> 2) & 15), rope_row_off(ra, row));
+    }
+  }
+  PrepPre pq{0.f, 1.f, 1.f, 1.f, 1.f};
+  if constexpr (EPI == kEpiPrep) {
+    if (threadIdx.x < 256) {
+      const int orow = 4 * ((threadIdx.x >> 2) >> 4) + (threadIdx.x & 3);
+      const int row = orow < n ? orow : 0;
+      const int k = 16 * g + ((threadIdx.x >> 2) & 15);
+      if (pp.r_in) pq.rin = Elem<T>::load((const T*)pp.r_in + (int64_t)row * pp.ld_in + k);
+      if (pp.s_in) pq.sin = pp.s_in[row];
+      if (pp.w_in) pq.win = Elem<T>::load((const T*)pp.w_in + k);
+      if (pp.wa) pq.wa = Elem<T>::load((const T*)pp.wa + k);
+      pq.wb = Elem<T>::load((const T*)pp.wb + k);
     }
   }
 
@@ -521,6 +583,21 @@ __global__ __launch_bounds__(64 * WW) void linear_wide_kernel(
     }
     red[wave + WW * i][lane] = sub;
   }
+  if constexpr (!kEarlyGroups) load_groups();
+#pragma unroll
+  for (int q = 0; q < RPW; ++q) {
+    const int rw = wave + WW * q;
+    if (by_part && rw < n) {  // row rw's scale from its group sums (uniform over the wave)
+      float sr, su;
+      fold_sums(gpv[q], sr, su);
+      float s_a, scale;
+      pair_scale(sr, su, rs.D, rs.eps, rs.two != 0, s_a, scale);
+      if (lane == 0) {
+        rsc[rw] = scale;
+        if (rs.s_out && blockIdx.x == 0) rs.s_out[rw] = s_a;
+      }
+    }
+  }
   __syncthreads();
 
   // threads 0..255: one (lane', r) output each, the 16 sub-slice sums added
@@ -540,11 +617,35 @@ __global__ __launch_bounds__(64 * WW) void linear_wide_kernel(
       for (int u = 0; u < kSubSlices; ++u) sl += us[q * kSubSlices + u];
       v += sl;
     }
+    if (by_part) v = mul_rn(v, rsc[row < n ? row : 0]);  // a folded norm pair's row scale
+    else if (EPI != kEpiPrep && rs.scale != nullptr) v = mul_rn(v, esc);
+    const bool mine = !HALF || ((ln & 15) >> 3) == half;
+    if constexpr (EPI == kEpiPrep) {
+      // the residual stream, the next linear's operand and the row's sums per
+      // 8-column group: the group's columns are threads ^ 4, ^ 8, ^ 16 (column
+      // bits 0, 1, 2), added as ((c0+c1)+(c2+c3))+((c4+c5)+(c6+c7))
+      const PrepVal pv = prep_value<T>(v, pp.r_in != nullptr, pq.rin, pq.sin, pq.win, pq.wa, pq.wb);
+      float tr = pv.sr, tu = pv.su;
+#pragma unroll
+      for (int m = 4; m <= 16; m <<= 1) {
+        tr = add_rn(tr, __shfl_xor(tr, m, 64));
+        tu = add_rn(tu, __shfl_xor(tu, m, 64));
+      }
+      if (row < n && mine) {
+        const int k = 16 * g + (ln & 15);
+        if (pp.r_out) Elem<T>::store((T*)pp.r_out + (int64_t)row * pp.ld_out + k, pv.r);
+        if (pp.a_out) Elem<T>::store((T*)pp.a_out + (int64_t)row * pp.ld_a + k, pv.A);
+        if ((k & 7) == 0 && pp.part) {
+          float2* gp = reinterpret_cast<float2*>(pp.part) + (int64_t)row * (16 * gridDim.x / (HALF ? 2 : 1) / 8);
+          gp[k >> 3] = float2{tr, tu};
+        }
+      }
+      return;
+    }
     // column ln ^ 1 lives in thread threadIdx.x ^ 4, column ln ^ 8 in threadIdx.x ^ 32
     const float partner = EPI == kEpiRope     ? __shfl_xor(v, 4, 64)
                           : EPI == kEpiSwiGLU ? __shfl_xor(v, 32, 64)
                                               : 0.f;
-    const bool mine = !HALF || ((ln & 15) >> 3) == half;
     if (row < n && mine) store_out<TO, EPI>(y, ldy, ra, row, g, ln & 15, v, partner, rp);
     if constexpr (EPI == kEpiPlain && std::is_same<TO, float>::value) {
       if (am.val) {  // uniform
@@ -574,13 +675,15 @@ template <typename T, typename TO, int EPI, int NB>
 __global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ x, const int32_t* __restrict__ x_rows,
                                                           int64_t ldx, const T* __restrict__ W, TO* __restrict__ y,
                                                           int64_t ldy, int n, int K, int pair_off, int tiles,
-                                                          const RopeArgs ra) {
+                                                          const RopeArgs ra, const float* __restrict__ rscale) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int col = lane & 15;
   const int grp = lane >> 4;
   const int row0 = (blockIdx.x * 4 + wave) * 16;
   if (row0 >= n) return;  // no barriers in this kernel
+  float rsv[4];
+  load_row_scales(rsv, rscale, row0 + 4 * grp, n);
   const int P = K / LinTraits<T>::KC;
   __shared__ __align__(16) u32x4 xl[4][kXcUnits];  // each wave's x chunk (coalesced load -> fragments)
   uint32_t xoff[kChunkSteps];
@@ -642,11 +745,12 @@ __global__ __launch_bounds__(256) void linear_tile_kernel(const T* __restrict__ 
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int orow = row0 + 4 * grp + r;
+      const float v = rscale ? mul_rn(tot[b][r], rsv[r]) : tot[b][r];  // a folded norm pair's row scale
       // column col ^ 1 lives in lane ^ 1, column col ^ 8 in lane ^ 8 (the whole wave takes part)
-      const float partner = EPI == kEpiRope     ? __shfl_xor(tot[b][r], 1, 64)
-                            : EPI == kEpiSwiGLU ? __shfl_xor(tot[b][r], 8, 64)
+      const float partner = EPI == kEpiRope     ? __shfl_xor(v, 1, 64)
+                            : EPI == kEpiSwiGLU ? __shfl_xor(v, 8, 64)
                                                 : 0.f;
-      if (orow < n) store_out<TO, EPI>(y, ldy, ra, orow, g, col, tot[b][r], partner, rp[b][r]);
+      if (orow < n) store_out<TO, EPI>(y, ldy, ra, orow, g, col, v, partner, rp[b][r]);
     }
   }
 }
@@ -719,7 +823,8 @@ template <typename T, typename TO, int EPI, int BT, bool PART>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void linear_gemm_kernel(const T* __restrict__ x, const int32_t* __restrict__ x_rows,
                                                           int64_t ldx, const T* __restrict__ W, TO* __restrict__ y,
                                                           int64_t ldy, int n, int K, int pair_off, int tiles,
-                                                          const RopeArgs ra, float* __restrict__ part) {
+                                                          const RopeArgs ra, float* __restrict__ part,
+                                                          const float* __restrict__ rscale) {
   constexpr int V = LinTraits<T>::V;
   constexpr int FR = BT * kChunkSteps;  // 1 KB fragments per chunk: (tile, step)
   constexpr int FPW = FR / 4;           // fragments each wave stages per chunk
@@ -774,6 +879,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
   // with the cos / sin pairs after the loop); with 4 the main loop has no
   // registers to spare for them, so they follow it
   constexpr bool kRopeEarly = BT <= 2;
+  float rsv[4];  // folded norm pairs' row scales: early with the RoPE operands, else after the loop
+  if constexpr (kRopeEarly) load_row_scales(rsv, PART ? nullptr : rscale, row0 + 4 * grp, n);
   RopeRows rrows;
   RopePre rp[BT][4];
   if constexpr (kRopeEarly) {
@@ -856,6 +963,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
     return;
   }
   if constexpr (!kRopeEarly) {
+    load_row_scales(rsv, rscale, row0 + 4 * grp, n);
     gather_rope_rows<EPI>(rrows, ra, row0 + 4 * grp, n);
     gather_rope<EPI, BT>(rp, ra, rrows, tg * BT, tiles, col);
   }
@@ -866,11 +974,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void l
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int orow = row0 + 4 * grp + r;
+      const float v = rscale ? mul_rn(tot[t][r], rsv[r]) : tot[t][r];  // a folded norm pair's row scale
       // column col ^ 1 lives in lane ^ 1, column col ^ 8 in lane ^ 8 (the whole wave takes part)
-      const float partner = EPI == kEpiRope     ? __shfl_xor(tot[t][r], 1, 64)
-                            : EPI == kEpiSwiGLU ? __shfl_xor(tot[t][r], 8, 64)
+      const float partner = EPI == kEpiRope     ? __shfl_xor(v, 1, 64)
+                            : EPI == kEpiSwiGLU ? __shfl_xor(v, 8, 64)
                                                 : 0.f;
-      if (orow < n) store_out<TO, EPI>(y, ldy, ra, orow, g, col, tot[t][r], partner, rp[t][r]);
+      if (orow < n) store_out<TO, EPI>(y, ldy, ra, orow, g, col, v, partner, rp[t][r]);
     }
   }
 }
@@ -935,7 +1044,7 @@ template <typename T, typename TO, int EPI, int BT, int NS>
 __global__ __launch_bounds__(256) void linear_stream_kernel(const T* __restrict__ x, const int32_t* __restrict__ x_rows,
                                                             int64_t ldx, const T* __restrict__ W, TO* __restrict__ y,
                                                             int64_t ldy, int n, int K, int pair_off, int tiles,
-                                                            const RopeArgs ra) {
+                                                            const RopeArgs ra, const float* __restrict__ rscale) {
   constexpr int V = LinTraits<T>::V;
   constexpr int KC = LinTraits<T>::KC;
   constexpr int FR = BT * kChunkSteps;   // weight fragments (tile, step) per chunk, 1 KB each
@@ -1002,6 +1111,8 @@ __global__ __launch_bounds__(256) void linear_stream_kernel(const T* __restrict_
     }
   }
   if (!rows) return;  // after the last barrier; every load of this wave has completed
+  float rsv[4];
+  load_row_scales(rsv, rscale, row0 + 4 * grp, n);
   RopeRows rrows;
   gather_rope_rows<EPI>(rrows, ra, row0 + 4 * grp, n);
   RopePre rp[BT][4];
@@ -1013,11 +1124,12 @@ __global__ __launch_bounds__(256) void linear_stream_kernel(const T* __restrict_
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int orow = row0 + 4 * grp + r;
+      const float v = rscale ? mul_rn(tot[t][r], rsv[r]) : tot[t][r];  // a folded norm pair's row scale
       // column col ^ 1 lives in lane ^ 1, column col ^ 8 in lane ^ 8 (the whole wave takes part)
-      const float partner = EPI == kEpiRope     ? __shfl_xor(tot[t][r], 1, 64)
-                            : EPI == kEpiSwiGLU ? __shfl_xor(tot[t][r], 8, 64)
+      const float partner = EPI == kEpiRope     ? __shfl_xor(v, 1, 64)
+                            : EPI == kEpiSwiGLU ? __shfl_xor(v, 8, 64)
                                                 : 0.f;
-      if (orow < n) store_out<TO, EPI>(y, ldy, ra, orow, g, col, tot[t][r], partner, rp[t][r]);
+      if (orow < n) store_out<TO, EPI>(y, ldy, ra, orow, g, col, v, partner, rp[t][r]);
     }
   }
 }
@@ -1046,7 +1158,8 @@ static WidePlan wide_plan(int n, int tiles, int R, bool swiglu) {
 template <typename T, typename TO, int EPI>
 static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const void* W, void* y, int64_t ldy, int n,
                           int N, int K, int pair_off, const RopeArgs& ra, hipStream_t st,
-                          const TileArgmax& am = TileArgmax{nullptr, nullptr}) {
+                          const TileArgmax& am = TileArgmax{nullptr, nullptr}, const wfd_rowscale_t& rs = {},
+                          const wfd_prep_t& pp = {}) {
   const int tiles = N / 16;
   const int R = sub_chunks(K / LinTraits<T>::KC);  // chunks per sub-slice: one sub-slice per wave (two with 8 waves)
   const WidePlan wp = wide_plan(n, tiles, R, EPI == kEpiSwiGLU);
@@ -1055,13 +1168,13 @@ static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const v
   if (half)                                                                                                       \
     hipLaunchKernelGGL((linear_wide_kernel<T, TO, EPI, RMV, true, kWideWaves>), dim3(2 * tiles),                 \
                        dim3(64 * kWideWaves), 0, st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K,       \
-                       pair_off, ra, am);                                                                         \
+                       pair_off, ra, am, rs, pp);                                                                 \
   else                                                                                                            \
     hipLaunchKernelGGL((linear_wide_kernel<T, TO, EPI, RMV, false, kWideWaves>), dim3(tiles), dim3(64 * kWideWaves), \
-                       0, st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra, am);
+                       0, st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra, am, rs, pp);
 #define WFD_WIDE8(RMV)                                                                                          \
   hipLaunchKernelGGL((linear_wide_kernel<T, TO, EPI, RMV, false, 8>), dim3(tiles), dim3(64 * 8), 0, st,        \
-                     (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra, am);
+                     (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, ra, am, rs, pp);
   if (wide && ww8) {
     WFD_WIDE8(1)
   } else if (wide && R == 1) {
@@ -1070,9 +1183,10 @@ static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const v
     WFD_WIDE(2)
   } else if (wide) {
     WFD_WIDE(3)
-  } else {
+  } else if constexpr (EPI != kEpiPrep) {  // the prep epilogue has a few-row form only (checked on entry)
 #undef WFD_WIDE8
 #undef WFD_WIDE
+    const float* rsc = rs.scale;  // many rows: the scales precomputed (group sums are few-row only)
     const int rb = (n + 63) / 64;
     if (tiles <= kStreamMaxTiles) {
       // few weight tiles: each workgroup walks all of K, so its chunk chain is
@@ -1082,10 +1196,10 @@ static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const v
       // long as 192 two-tile ones).
       if (rb * tiles > 256)
         hipLaunchKernelGGL((linear_stream_kernel<T, TO, EPI, 2, kStreamStages>), dim3(rb, (tiles + 1) / 2), dim3(256),
-                           0, st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra);
+                           0, st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra, rsc);
       else
         hipLaunchKernelGGL((linear_stream_kernel<T, TO, EPI, 1, kStreamStages>), dim3(rb, tiles), dim3(256), 0, st,
-                           (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra);
+                           (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra, rsc);
       return;
     }
     // few (row block, tile) pairs, or at most 32 rows where four-tile gemm
@@ -1095,7 +1209,7 @@ static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const v
     if (rb * tiles <= kGemmMinBlockTiles || (n <= 32 && (tiles + 3) / 4 < 256)) {
       constexpr int NB = 2;
       hipLaunchKernelGGL((linear_tile_kernel<T, TO, EPI, NB>), dim3(rb, (tiles + NB - 1) / NB), dim3(256), 0, st,
-                         (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra);
+                         (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra, rsc);
       return;
     }
     // weights through LDS, shared by the 4 waves: 4 tiles per workgroup
@@ -1109,10 +1223,10 @@ static void launch_linear(const void* x, const int32_t* xr, int64_t ldx, const v
     // one-launch shape (Wqkv + RoPE at 192 rows 28 -> 48 us).
     if (rb * ((tiles + 3) / 4) >= (EPI == kEpiRope ? 256 : 128))
       hipLaunchKernelGGL((linear_gemm_kernel<T, TO, EPI, 4, false>), dim3(xcd_grid(rb, (tiles + 3) / 4)), dim3(256), 0,
-                         st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra, nullptr);
+                         st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra, nullptr, rsc);
     else
       hipLaunchKernelGGL((linear_gemm_kernel<T, TO, EPI, 2, false>), dim3(xcd_grid(rb, (tiles + 1) / 2)), dim3(256), 0,
-                         st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra, nullptr);
+                         st, (const T*)x, xr, ldx, (const T*)W, (TO*)y, ldy, n, K, pair_off, tiles, ra, nullptr, rsc);
   }
 }
 
@@ -1131,12 +1245,37 @@ static void launch_linear_partials(const void* x, const int32_t* xr, int64_t ldx
   const int bt = gemm_tiles_per_workgroup(rb, tiles, S);
 #define WFD_GEMM_PART(BTV)                                                                                          \
   hipLaunchKernelGGL((linear_gemm_kernel<T, T, kEpiPlain, BTV, true>), dim3(xcd_grid(rb, (tiles + BTV - 1) / BTV), S), \
-                     dim3(256), 0, st, (const T*)x, xr, ldx, (const T*)W, (T*)nullptr, 0, n, K, 0, tiles, ra, part)
+                     dim3(256), 0, st, (const T*)x, xr, ldx, (const T*)W, (T*)nullptr, 0, n, K, 0, tiles, ra, part,  \
+                     nullptr)
   if (bt == 4)
     WFD_GEMM_PART(4);
   else
     WFD_GEMM_PART(2);
 #undef WFD_GEMM_PART
+}
+
+// The row-scale argument of the consumer entry points: NULL (none), the
+// precomputed scales, or group sums (few-row launches only). Returns the
+// value to launch with, or sets the error.
+static bool rowscale_arg(const wfd_rowscale_t* rs, int n, int N, int K, int dtype, bool swiglu, const char* what,
+                         wfd_rowscale_t& out) {
+  out = wfd_rowscale_t{};
+  if (!rs) return true;
+  if (!rs->scale && !rs->part) {
+    set_error("%s: a row-scale argument needs scale or part", what);
+    return false;
+  }
+  if (rs->part) {
+    const int kc = dtype == kBF16 ? LinTraits<bf16_t>::KC : LinTraits<float>::KC;
+    const bool wide = wide_plan(n, N / 16, sub_chunks(K / kc), swiglu).wide;
+    if (!wide || rs->D <= 0 || rs->D % 8 || rs->D > kFoldMaxD || ((uintptr_t)rs->part & 7)) {
+      set_error("%s: group sums (rs->part) need a few-row launch (n=%d <= 16, K=%d) and 0 < D=%d <= %d, D %% 8 == 0",
+                what, n, K, rs->D, kFoldMaxD);
+      return false;
+    }
+  }
+  out = *rs;
+  return true;
 }
 
 }  // namespace wfd
@@ -1227,7 +1366,8 @@ int wfd_linear_pack(const void* W, void* W_packed, int N, int K, int dtype, int 
 }
 
 int wfd_linear(const void* x, const int32_t* x_rows, int64_t ldx, const void* W, void* y, int64_t ldy, int n, int N,
-               int K, int dtype, int out_dtype, int epilogue, int pair_off, hipStream_t stream) {
+               int K, int dtype, int out_dtype, int epilogue, int pair_off, const wfd_rowscale_t* rs,
+               hipStream_t stream) {
   using namespace wfd;
   if (n < 0 || N <= 0 || K <= 0 || ldx < K) {
     set_error("wfd_linear: bad shape n=%d N=%d K=%d ldx=%lld", n, N, K, (long long)ldx);
@@ -1266,19 +1406,22 @@ int wfd_linear(const void* x, const int32_t* x_rows, int64_t ldx, const void* W,
     set_error("wfd_linear: unknown epilogue %d", epilogue);
     return kUnsupported;
   }
+  wfd_rowscale_t rsv;
+  if (!rowscale_arg(rs, n, N, K, dtype, epilogue == kEpiSwiGLU, "wfd_linear", rsv)) return kBadArg;
   const RopeArgs ra{};
+  const TileArgmax am{nullptr, nullptr};
   if (dtype == kBF16 && out_dtype == kBF16) {
     if (epilogue == kEpiSwiGLU)
-      launch_linear<bf16_t, bf16_t, kEpiSwiGLU>(x, x_rows, ldx, W, y, ldy, n, N, K, pair_off, ra, stream);
+      launch_linear<bf16_t, bf16_t, kEpiSwiGLU>(x, x_rows, ldx, W, y, ldy, n, N, K, pair_off, ra, stream, am, rsv);
     else
-      launch_linear<bf16_t, bf16_t, kEpiPlain>(x, x_rows, ldx, W, y, ldy, n, N, K, 0, ra, stream);
+      launch_linear<bf16_t, bf16_t, kEpiPlain>(x, x_rows, ldx, W, y, ldy, n, N, K, 0, ra, stream, am, rsv);
   } else if (dtype == kBF16 && out_dtype == kF32 && epilogue == kEpiPlain) {
-    launch_linear<bf16_t, float, kEpiPlain>(x, x_rows, ldx, W, y, ldy, n, N, K, 0, ra, stream);
+    launch_linear<bf16_t, float, kEpiPlain>(x, x_rows, ldx, W, y, ldy, n, N, K, 0, ra, stream, am, rsv);
   } else if (dtype == kF32 && out_dtype == kF32) {
     if (epilogue == kEpiSwiGLU)
-      launch_linear<float, float, kEpiSwiGLU>(x, x_rows, ldx, W, y, ldy, n, N, K, pair_off, ra, stream);
+      launch_linear<float, float, kEpiSwiGLU>(x, x_rows, ldx, W, y, ldy, n, N, K, pair_off, ra, stream, am, rsv);
     else
-      launch_linear<float, float, kEpiPlain>(x, x_rows, ldx, W, y, ldy, n, N, K, 0, ra, stream);
+      launch_linear<float, float, kEpiPlain>(x, x_rows, ldx, W, y, ldy, n, N, K, 0, ra, stream, am, rsv);
   } else {
     set_error("wfd_linear: unsupported dtype=%d out_dtype=%d epilogue=%d", dtype, out_dtype, epilogue);
     return kUnsupported;
@@ -1293,7 +1436,8 @@ int wfd_linear_argmax_groups(int n, int N, int K, int dtype) {
 }
 
 int wfd_linear_argmax(const void* x, const int32_t* x_rows, int64_t ldx, const void* W, float* y, int64_t ldy, int n,
-                      int N, int K, int dtype, float* part_val, int32_t* part_idx, hipStream_t stream) {
+                      int N, int K, int dtype, float* part_val, int32_t* part_idx, const wfd_rowscale_t* rs,
+                      hipStream_t stream) {
   using namespace wfd;
   if (n <= 0 || N <= 0 || K <= 0 || ldx < K) {
     set_error("wfd_linear_argmax: bad shape n=%d N=%d K=%d ldx=%lld", n, N, K, (long long)ldx);
@@ -1321,16 +1465,19 @@ int wfd_linear_argmax(const void* x, const int32_t* x_rows, int64_t ldx, const v
     set_error("wfd_linear_argmax: ldy=%lld < N=%d", (long long)ldy, N);
     return kBadArg;
   }
+  wfd_rowscale_t rsv;
+  if (!rowscale_arg(rs, n, N, K, dtype, false, "wfd_linear_argmax", rsv)) return kBadArg;
   const RopeArgs ra{};
   launch_linear<bf16_t, float, kEpiPlain>(x, x_rows, ldx, W, y, ldy, n, N, K, 0, ra, stream,
-                                          TileArgmax{part_val, part_idx});
+                                          TileArgmax{part_val, part_idx}, rsv);
   return launch_status("wfd_linear_argmax");
 }
 
 int wfd_linear_qkv_rope_append(const void* x, const int32_t* x_rows, int64_t ldx, const void* Wqkv, int n, int K,
                                const int32_t* pos, const float* rope_cos, const float* rope_sin, int rope_rows,
                                const int64_t* flat_row, void* q_out, void* k_cache, void* v_cache,
-                               int64_t kv_block_rows, int H, int Hkv, int Dh, int dtype, hipStream_t stream) {
+                               int64_t kv_block_rows, int H, int Hkv, int Dh, int dtype, const wfd_rowscale_t* rs,
+                               hipStream_t stream) {
   using namespace wfd;
   if (n < 0 || K <= 0 || ldx < K || H <= 0 || Hkv <= 0 || H % Hkv != 0 || Dh <= 0 || Dh % 16 != 0 ||
       rope_rows <= 0 || kv_block_rows < 0) {
@@ -1358,16 +1505,56 @@ int wfd_linear_qkv_rope_append(const void* x, const int32_t* x_rows, int64_t ldx
     return kUnsupported;
   }
   const int N = (H + 2 * Hkv) * Dh;
+  wfd_rowscale_t rsv;
+  if (!rowscale_arg(rs, n, N, K, dtype, false, "wfd_linear_qkv_rope_append", rsv)) return kBadArg;
   const RopeArgs ra{pos, rope_cos, rope_sin, rope_rows, flat_row, q_out, k_cache, v_cache, kv_block_rows, H, Hkv, Dh};
+  const TileArgmax am{nullptr, nullptr};
   if (dtype == kBF16)
-    launch_linear<bf16_t, bf16_t, kEpiRope>(x, x_rows, ldx, Wqkv, nullptr, 0, n, N, K, 0, ra, stream);
+    launch_linear<bf16_t, bf16_t, kEpiRope>(x, x_rows, ldx, Wqkv, nullptr, 0, n, N, K, 0, ra, stream, am, rsv);
   else if (dtype == kF32)
-    launch_linear<float, float, kEpiRope>(x, x_rows, ldx, Wqkv, nullptr, 0, n, N, K, 0, ra, stream);
+    launch_linear<float, float, kEpiRope>(x, x_rows, ldx, Wqkv, nullptr, 0, n, N, K, 0, ra, stream, am, rsv);
   else {
     set_error("wfd_linear_qkv_rope_append: unsupported dtype=%d", dtype);
     return kUnsupported;
   }
   return launch_status("wfd_linear_qkv_rope_append");
+}
+
+int wfd_linear_prep(const void* x, const int32_t* x_rows, int64_t ldx, const void* W, int n, int N, int K, int dtype,
+                    const wfd_prep_t* pp, hipStream_t stream) {
+  using namespace wfd;
+  if (n < 0 || N <= 0 || N % 16 || K <= 0 || ldx < K || (dtype != kBF16 && dtype != kF32)) {
+    set_error("wfd_linear_prep: bad shape n=%d N=%d K=%d ldx=%lld dtype=%d", n, N, K, (long long)ldx, dtype);
+    return kBadArg;
+  }
+  if (n == 0) return kOk;
+  if (!x || !W || !pp || !pp->a_out || !pp->wb || !pp->part) {
+    set_error("wfd_linear_prep: null pointer argument (x, W, pp, a_out, wb and part are required)");
+    return kBadArg;
+  }
+  const int kc = wfd_linear_k_multiple(dtype);
+  if (K % kc || !wide_plan(n, N / 16, sub_chunks(K / kc), false).wide) {
+    set_error("wfd_linear_prep: n=%d K=%d is not a few-row launch (n <= 16, K a multiple of %d and at most 48 chunks)",
+              n, K, kc);
+    return kUnsupported;
+  }
+  const int64_t esz = dtype == kBF16 ? 2 : 4;
+  if (!x_rows && (int64_t)n * ldx * esz >= (int64_t)kBufInvalid) {
+    set_error("wfd_linear_prep: the x operand must span less than 2 GiB");
+    return kBadArg;
+  }
+  if ((((uintptr_t)x | (uintptr_t)W) & 15) || ((ldx * esz) & 15) || ((uintptr_t)pp->part & 7)) {
+    set_error("wfd_linear_prep: x rows and W must be 16-byte aligned, part 8-byte aligned");
+    return kBadArg;
+  }
+  const RopeArgs ra{};
+  const TileArgmax am{nullptr, nullptr};
+  const wfd_rowscale_t none{};
+  if (dtype == kBF16)
+    launch_linear<bf16_t, bf16_t, kEpiPrep>(x, x_rows, ldx, W, nullptr, 0, n, N, K, 0, ra, stream, am, none, *pp);
+  else
+    launch_linear<float, float, kEpiPrep>(x, x_rows, ldx, W, nullptr, 0, n, N, K, 0, ra, stream, am, none, *pp);
+  return launch_status("wfd_linear_prep");
 }
 
 }  // extern "C"

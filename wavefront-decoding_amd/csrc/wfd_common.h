@@ -196,6 +196,101 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// ---------------------------------------------------------------------------
+// Folded RMSNorm pairs (wfd_prep_t in wfd.h). Every product and sum below is
+// rounded on its own (contraction off), so the kernels that form these values
+// -- a linear's epilogue, the one-wave-per-row norm kernel -- agree bit for
+// bit whatever the compiler would fuse elsewhere.
+
+// One element of the residual stream and of the next linear's operand: y the
+// linear's fp32 output; with a residual, x = round((r_in * s_in) * w_in)
+// (s_in = w_in = 1 for a residual without a norm) and r = round(round(y) + x);
+// u = r * wa (wa = 1: norm a absent), A = round(u * wb). Also r^2 and u^2.
+struct PrepVal {
+  float r, A, sr, su;
+};
+template <typename T>
+__device__ __forceinline__ PrepVal prep_value(float y, bool res, float r_in, float s_in, float w_in, float wa,
+                                              float wb) {
+#pragma clang fp contract(off)
+  PrepVal o;
+  const float a = Elem<T>::round(y);
+  o.r = a;
+  if (res) {
+    const float x = Elem<T>::round((r_in * s_in) * w_in);
+    o.r = Elem<T>::round(a + x);
+  }
+  const float u = o.r * wa;
+  o.A = Elem<T>::round(u * wb);
+  o.sr = o.r * o.r;
+  o.su = u * u;
+  return o;
+}
+
+// The block's last norm of r: round((r * s) * w).
+template <typename T>
+__device__ __forceinline__ float norm_value(float r, float s, float w) {
+#pragma clang fp contract(off)
+  return Elem<T>::round((r * s) * w);
+}
+
+// ((v0+v1)+(v2+v3)): one half of an 8-column group's tree
+__device__ __forceinline__ float tree4(float v0, float v1, float v2, float v3) {
+#pragma clang fp contract(off)
+  return (v0 + v1) + (v2 + v3);
+}
+
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+
+// The two sums of one row from its group sums (one float2 per 8-column
+// group), by one wave: lane L holds groups L + 64 t (zeros past the last) and
+// adds them in t order from +0, then the lanes' butterfly (every lane ends
+// with the same bits: each step adds the same two values in either order).
+// Rows up to kFoldMaxD wide.
+constexpr int kFoldMaxD = 2048;
+constexpr int kFoldGroupsPerLane = kFoldMaxD / 8 / 64;
+
+__device__ __forceinline__ void fold_load(float2 (&gpv)[kFoldGroupsPerLane], const float2* gp, int G, int lane) {
+#pragma unroll
+  for (int t = 0; t < kFoldGroupsPerLane; ++t) {
+    const int gi = lane + 64 * t;
+    gpv[t] = gi < G ? gp[gi] : float2{0.f, 0.f};
+  }
+}
+
+__device__ __forceinline__ void fold_sums(const float2 (&gpv)[kFoldGroupsPerLane], float& sr, float& su) {
+#pragma clang fp contract(off)
+  sr = 0.f;
+  su = 0.f;
+#pragma unroll
+  for (int t = 0; t < kFoldGroupsPerLane; ++t) {
+    sr = sr + gpv[t].x;
+    su = su + gpv[t].y;
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    sr = sr + __shfl_xor(sr, m, 64);
+    su = su + __shfl_xor(su, m, 64);
+  }
+}
+
+// s_a and the linear's row scale s_a * s_b from the two sums.
+__device__ __forceinline__ void pair_scale(float sr, float su, int D, float eps, bool two, float& s_a,
+                                           float& scale) {
+#pragma clang fp contract(off)
+  s_a = two ? 1.0f / sqrtf(sr / (float)D + eps) : 1.0f;
+  const float s_b = 1.0f / sqrtf(((s_a * s_a) * su) / (float)D + eps);
+  scale = s_a * s_b;
+}
+
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+
 }  // namespace wfd
 
 // Host-side error reporting shared by every C-ABI entry point.

@@ -142,6 +142,19 @@ NO_EXPECT = -(1 << 62)
 _SPLIT_ROWS = (17, 512)
 
 
+# rows up to which a linear runs as the few-row kernel (one workgroup walks all of K)
+_FEW_ROWS = 16
+
+
+def _few_row_linear(n: int, K: int, dtype: torch.dtype) -> bool:
+    """Whether a linear over n rows and K inputs runs as the few-row kernel:
+    n <= 16 and at most 3 chunks per sub-slice of the arithmetic contract."""
+    kc = 128 if dtype == torch.bfloat16 else 64
+    P = K // kc
+    Q = (P + 3) // 4
+    return n <= _FEW_ROWS and (Q + 3) // 4 <= 3
+
+
 def _bucket(n: int) -> int:
     """Padded row count of a pass under graphs (one captured graph per
     count): powers of two up to 64, then multiples of 64, the many-row
@@ -211,6 +224,17 @@ class LoopedModel:
         # decode scratch: fixed capacity (captured graphs keep these addresses)
         self.max_rows = _bucket(max_rows or max_batch * self.R)
         self.sc = self._scratch(self.max_rows)
+        # folded norm pairs (decode): the residual stream after proj (r1) and
+        # after the MLP (r2), the next linear's operand A, the per-row scales
+        # s_a kept for the residual (s1, s2), the precomputed row scales of
+        # many-row launches, and the group sums a few-row producer leaves
+        cap = self.max_rows
+        self.sc["r1"] = torch.empty(cap, D, dtype=self.dtype, device=self.device)
+        self.sc["r2"] = torch.empty(cap, D, dtype=self.dtype, device=self.device)
+        self.sc["A"] = self._pitched(cap, D)
+        f32 = lambda k: torch.zeros(k, dtype=torch.float32, device=self.device)  # noqa: E731
+        self.sc["s1"], self.sc["s2"], self.sc["scale"] = f32(cap), f32(cap), f32(cap)
+        self.sc["gpart"] = f32(_FEW_ROWS * (D // 8) * 2)
         self.sc["logits"] = torch.empty(self.max_rows, cfg.vocab_size, dtype=torch.float32, device=self.device)
         self.sc["ids"] = torch.empty(self.max_rows, dtype=torch.int64, device=self.device)
         # column-group argmax bests of a few-row lm_head (at most 16 rows x N / 8 groups)
@@ -291,6 +315,7 @@ class LoopedModel:
         # fp32 slice sums of the split-K projections (at most 4 slices)
         sc["part"] = torch.empty(4 * min(cap, self.split_rows[1]) * c.d_model, dtype=torch.float32,
                                  device=self.device)
+
         if dense:  # the library GEMMs' unfused outputs: q|k|v rows, gate|up rows
             sc["qkv"] = mk((c.n_heads + 2 * c.n_kv_heads) * c.head_dim)
             sc["gu"] = mk(2 * c.ffn)
@@ -364,6 +389,74 @@ class LoopedModel:
             y = ops.linear(xin, Wp, n=n, x_rows=x_rows, out=keep if keep is not None else sc[tmp])
             ops.add_rmsnorm(y, w1, eps, n=n, **norm)
 
+    # -- one SandwichBlock over n decode rows, norms folded into the linears ---------
+    def _prep(self, xin: torch.Tensor, Wp, n: int, *, res, r_out: torch.Tensor, x_rows=None, wa=None, wb=None,
+              s_slot=None, final=None):
+        """A d_model-output linear (proj, the MLP down projection, the adapter)
+        and what follows it: r = round(y + x_res) into r_out (res = (r, s, w)
+        of the residual stream, or None), then either the next linear's operand
+        A = round((r * wa) * wb) in sc["A"] -- returning the RowScale that
+        linear reads (group sums for few rows, precomputed scales otherwise;
+        s_slot receives s_a) -- or, with final = (out, rows, w), the block's
+        last norm round((r * s) * w) into out[rows]. Few rows: the linear's
+        own epilogue (linear_prep); many rows: split-K slices reduced by the
+        row kernel (norm_prep), or the one-launch linear then norm_prep --
+        the same bits in every form."""
+        c, sc = self.cfg, self.sc
+        D, eps = c.d_model, c.norm_eps
+        r_in, s_in, w_in = res if res is not None else (None, None, None)
+        fin = final is not None
+        if fin:
+            h_out, h_rows, wf = final
+        if _few_row_linear(n, Wp.K, self.dtype):
+            ops.linear_prep(xin, Wp, n=n, x_rows=x_rows, r_in=r_in, s_in=s_in, w_in=w_in, r_out=r_out,
+                            a_out=sc["A"], wa=None if fin else wa, wb=wf if fin else wb, part=sc["gpart"])
+            if fin:
+                ops.norm_prep(n=n, D=D, dtype=self.dtype, eps=eps, a=r_out, wa=wf, h_out=h_out, h_rows=h_rows)
+                return None
+            return ops.RowScale(D=D, eps=eps, two=wa is not None, part=sc["gpart"], s_out=s_slot)
+        lo, hi = self.split_rows
+        src = {}
+        if lo <= n <= hi:
+            S = ops.linear_partials(xin, Wp, sc["part"], n=n, x_rows=x_rows)
+            src = dict(part=sc["part"], nslices=S)
+        else:
+            src = dict(a=ops.linear(xin, Wp, n=n, x_rows=x_rows, out=sc["a"]))
+        if fin:
+            ops.norm_prep(n=n, D=D, dtype=self.dtype, eps=eps, r_in=r_in, s_in=s_in, w_in=w_in, wa=wf,
+                          h_out=h_out, h_rows=h_rows, **src)
+            return None
+        ops.norm_prep(n=n, D=D, dtype=self.dtype, eps=eps, r_in=r_in, s_in=s_in, w_in=w_in, r_out=r_out,
+                      a_out=sc["A"], wa=wa, wb=wb, two=wa is not None, scale_out=sc["scale"], s_out=s_slot, **src)
+        return ops.RowScale(D=D, eps=eps, two=wa is not None, scale=sc["scale"])
+
+    def _dblock(self, prefix: str, n: int, pos_d, kvlen_d, rb_d, fr_d, kv_len_max: int, cache, inp, res, nxt,
+                final=None, group_first=None):
+        """One SandwichBlock over n decode rows (huginn_blocks.py:93-103 norms
+        and residuals) with its four RMSNorms folded into the linears:
+        `inp` is the RowScale of the operand in sc["A"] (None: the plain
+        normalized rows in sc["h"]), `res` the residual stream (r, s, w) the
+        block adds (s, w None: raw). Returns (inp, res) for the next block --
+        the pair (norm_4, nxt) -- or, with final = (out, rows), writes
+        norm_4's output there and returns (None, None)."""
+        c, W, sc = self.cfg, self.W, self.sc
+        xq = sc["h"] if inp is None else sc["A"]
+        q = ops.linear_qkv_rope_append(xq, W[prefix + "Wqkv"], pos_d, self.rope_cos, self.rope_sin, fr_d,
+                                       cache.flat_k, cache.flat_v, c.n_heads, c.n_kv_heads, c.head_dim, n=n,
+                                       q_out=sc["q"][:n], rowscale=inp)
+        o = ops.attn_decode(q, cache.flat_k, cache.flat_v, rb_d, kvlen_d, kv_len_max=kv_len_max, out=sc["o"][:n],
+                            workspace=self.attn_ws, group_first=group_first)
+        rs = self._prep(o.view(n, -1), W[prefix + "proj"], n, res=res, r_out=sc["r1"], wa=W[prefix + "norm_2"],
+                        wb=W[prefix + "norm_3"], s_slot=sc["s1"])
+        u = ops.linear(sc["A"], W[prefix + "fc"], n=n, out=sc["u"], swiglu=True, rowscale=rs)
+        mid = (sc["r1"], sc["s1"], W[prefix + "norm_2"])
+        if final is not None:
+            self._prep(u, W[prefix + "mlp_proj"], n, res=mid, r_out=sc["r2"], final=(*final, W[prefix + "norm_4"]))
+            return None, None
+        rs = self._prep(u, W[prefix + "mlp_proj"], n, res=mid, r_out=sc["r2"], wa=W[prefix + "norm_4"], wb=nxt,
+                        s_slot=sc["s2"])
+        return rs, (sc["r2"], sc["s2"], W[prefix + "norm_4"])
+
     # -- row tables ------------------------------------------------------------------
     def _layers(self, kind: str) -> int:
         c = self.cfg
@@ -380,42 +473,47 @@ class LoopedModel:
         off = nb if kind == "P" else 0
         rb = lambda l: t64[off + l * nb: off + (l + 1) * nb]  # noqa: E731
         fr = lambda l: t64[off + (L + l) * nb: off + (L + l + 1) * nb]  # noqa: E731
+        blk = lambda pre, l, inp, res, nxt, final=None: self._dblock(  # noqa: E731
+            pre, nb, pos_d, kvlen_d, rb(l), fr(l), kv_max, cache, inp, res, nxt, final=final, group_first=gf)
         if kind == "P":
-            # embed -> x, prelude.0.norm_1 -> h, and each token's initial loop
-            # state s0[pos] into its wave-state row (the prelude below writes
-            # only the row's static half)
+            # embed -> x (the first prelude block's raw residual), prelude.0.norm_1
+            # -> h, and each token's initial loop state s0[pos] into its
+            # wave-state row (the prelude below writes only the row's static half)
             ops.embed_rmsnorm(t64[:nb], W["wte"], c.emb_scale, W["prelude.0.norm_1"], c.norm_eps, h_out=sc["h"],
                               x_out=sc["x"], ring=self.tok_ring, n=nb,
                               copy=(self.s0, pos_d, self.pool, rows_d, c.d_model))
-            static_half = self.pool[:, c.d_model:]
+            inp, res = None, (sc["x"], None, None)
             for i in range(L):
-                nxt = W[f"prelude.{i + 1}.norm_1"] if i + 1 < L else None
-                self._block(f"prelude.{i}.", nb, sc, pos_d, kvlen_d, rb(i), fr(i), kv_max, ws, cache, nxt,
-                            final_out=static_half, final_rows=rows_d, group_first=gf)
+                last = i + 1 == L
+                inp, res = blk(f"prelude.{i}.", i, inp, res, None if last else W[f"prelude.{i + 1}.norm_1"],
+                               final=(self.pool[:, c.d_model:], rows_d) if last else None)
         elif kind == "R":
-            # adapter -> x (the first core block's residual), core.0.norm_1 -> h
-            self._linear_norm(self.pool, W["adapter"], nb, sc, "x", W["core.0.norm_1"], x_rows=rows_d,
-                              keep=sc["x"], x_out=sc["h"])
+            # adapter(cat[s, e]) -> the first core block's raw residual, with
+            # core.0.norm_1 folded into its Wqkv
+            inp = self._prep(self.pool, W["adapter"], nb, x_rows=rows_d, res=None, r_out=sc["r2"],
+                             wb=W["core.0.norm_1"])
+            res = (sc["r2"], None, None)
             for l in range(L):
-                nxt = W[f"core.{l + 1}.norm_1"] if l + 1 < L else None
-                self._block(f"core.{l}.", nb, sc, pos_d, kvlen_d, rb(l), fr(l), kv_max, ws, cache, nxt,
-                            final_out=self.pool, final_rows=rows_d, group_first=gf)
+                last = l + 1 == L
+                inp, res = blk(f"core.{l}.", l, inp, res, None if last else W[f"core.{l + 1}.norm_1"],
+                               final=(self.pool, rows_d) if last else None)
         else:
+            # ln_f -> x (the first coda block's raw residual), coda.0.norm_1 -> h
             ops.add_rmsnorm(self.pool, W["ln_f"], c.norm_eps, w2=W["coda.0.norm_1"], n=nb, a_rows=rows_d,
                             x_out=sc["x"], h_out=sc["h"])
+            inp, res = None, (sc["x"], None, None)
             for i in range(L):
-                nxt = W[f"coda.{i + 1}.norm_1"] if i + 1 < L else W["ln_f"]
-                self._block(f"coda.{i}.", nb, sc, pos_d, kvlen_d, rb(i), fr(i), kv_max, ws, cache, nxt,
-                            group_first=gf)
+                inp, res = blk(f"coda.{i}.", i, inp, res, W[f"coda.{i + 1}.norm_1"] if i + 1 < L else W["ln_f"])
+            # lm_head reads the last block's (norm_4, ln_f) pair
             am = dict(out=sc["ids"], ring=self.tok_ring, ring_rows=t32[3 * nb: 4 * nb],
                       expect=t64[2 * L * nb: 2 * L * nb + nb], accept_mapped=(self._flags_dev, self.max_rows))
             G = ops.linear_argmax_groups(nb, W["lm_head"]) if W["lm_head"].dtype == torch.bfloat16 else 0
             if G > 0:  # few rows: the argmax reads each 16-column group's best, not the whole vocabulary
-                ops.linear_argmax(sc["h"], W["lm_head"], n=nb, out=sc["logits"], part_val=sc["am_val"],
-                                  part_idx=sc["am_idx"])
+                ops.linear_argmax(sc["A"], W["lm_head"], n=nb, out=sc["logits"], part_val=sc["am_val"],
+                                  part_idx=sc["am_idx"], rowscale=inp)
                 ops.argmax_groups(sc["am_val"], sc["am_idx"], G, n=nb, **am)
             else:
-                ops.linear(sc["h"], W["lm_head"], n=nb, out=sc["logits"], out_dtype=torch.float32)
+                ops.linear(sc["A"], W["lm_head"], n=nb, out=sc["logits"], out_dtype=torch.float32, rowscale=inp)
                 ops.argmax(sc["logits"], n=nb, **am)
 
     # -- a tick: row tables, upload, launch -------------------------------------------

@@ -14,6 +14,7 @@ back, so the caller guarantees they index inside the buffers passed.
 """
 from __future__ import annotations
 
+import ctypes
 import math
 
 import torch
@@ -52,6 +53,63 @@ def _need(cond: bool, msg: str) -> None:
 def _rows(t: torch.Tensor | None, n: int, name: str) -> None:
     if t is not None:
         _need(t.dtype == torch.int32 and t.is_contiguous() and t.numel() >= n, f"{name}: int32 contiguous (>= {n})")
+
+
+class RowScale:
+    """Where a linear finds its rows' folded-norm scales (wfd_rowscale_t):
+    `scale` (n,) float32 precomputed by norm_prep, or `part` -- the group sums
+    linear_prep left, (n, D/8, 2) float32, few-row launches only -- with the
+    pair's form (`two`: norm a present) and eps; with `part`, `s_out` (n,)
+    float32 receives s_a."""
+
+    __slots__ = ("scale", "part", "D", "two", "eps", "s_out")
+
+    def __init__(self, *, D: int, eps: float, two: bool, scale: torch.Tensor | None = None,
+                 part: torch.Tensor | None = None, s_out: torch.Tensor | None = None):
+        _need((scale is None) != (part is None), "RowScale: exactly one of scale / part")
+        self.scale, self.part, self.D, self.two, self.eps, self.s_out = scale, part, D, two, eps, s_out
+
+    def check(self, n: int) -> None:
+        _need_cuda(self.scale, self.part, self.s_out)
+        for name, t, size in (("scale", self.scale, n), ("part", self.part, n * (self.D // 8) * 2),
+                              ("s_out", self.s_out, n)):
+            if t is not None:
+                _need(t.dtype == torch.float32 and t.is_contiguous() and t.numel() >= size,
+                      f"RowScale.{name}: float32 contiguous (>= {size})")
+
+    def args(self, n: int) -> _lib.RowScaleArgs:
+        self.check(n)
+        return _lib.RowScaleArgs(_p(self.scale), _p(self.part), self.D, int(bool(self.two)), float(self.eps),
+                                 _p(self.s_out))
+
+
+def _rs_ptr(rowscale: RowScale | None, n: int):
+    """(struct kept alive, its address or None) for a C call."""
+    if rowscale is None:
+        return None, None
+    st = rowscale.args(n)
+    return st, ctypes.addressof(st)
+
+
+def _prep_args(n: int, D: int, dtype, *, r_in=None, s_in=None, w_in=None, r_out=None, a_out=None, wa=None,
+               wb=None, part=None) -> _lib.PrepArgs:
+    """wfd_prep_t from torch tensors (rows (n, D) with a row pitch; weights (D,))."""
+    _need_cuda(r_in, s_in, w_in, r_out, a_out, wa, wb, part)
+    for name, t in (("r_in", r_in), ("r_out", r_out), ("a_out", a_out)):
+        if t is not None:
+            _need(t.dim() == 2 and t.stride(1) == 1 and t.shape[0] >= n and t.shape[1] >= D and t.dtype == dtype,
+                  f"{name}: ({n}+, {D}+) rows of {dtype}")
+    for name, t in (("w_in", w_in), ("wa", wa), ("wb", wb)):
+        if t is not None:
+            _need(t.is_contiguous() and t.numel() >= D and t.dtype == dtype, f"{name}: ({D},) {dtype}")
+    if s_in is not None:
+        _need(s_in.dtype == torch.float32 and s_in.is_contiguous() and s_in.numel() >= n, "s_in: float32 (n,)")
+    if part is not None:
+        _need(part.dtype == torch.float32 and part.is_contiguous() and part.numel() >= n * (D // 8) * 2,
+              "part: float32 (n, D/8, 2)")
+    ld = lambda t: t.stride(0) if t is not None else 0  # noqa: E731
+    return _lib.PrepArgs(_p(r_in), ld(r_in), _p(s_in), _p(w_in), _p(r_out), ld(r_out), _p(a_out), ld(a_out), _p(wa),
+                         _p(wb), _p(part))
 
 
 # ---------------------------------------------------------------------------
@@ -241,9 +299,11 @@ def qkv_rope_append(qkv: torch.Tensor, pos: torch.Tensor, rope_cos: torch.Tensor
 def linear_qkv_rope_append(x: torch.Tensor, Wqkv: torch.Tensor, pos: torch.Tensor, rope_cos: torch.Tensor,
                            rope_sin: torch.Tensor, flat_row: torch.Tensor, k_cache: torch.Tensor,
                            v_cache: torch.Tensor, H: int, Hkv: int, Dh: int, *, n: int | None = None,
-                           x_rows: torch.Tensor | None = None, q_out: torch.Tensor | None = None) -> torch.Tensor:
+                           x_rows: torch.Tensor | None = None, q_out: torch.Tensor | None = None,
+                           rowscale: RowScale | None = None) -> torch.Tensor:
     """q_out, plus k/v appended at flat_row: the Wqkv projection with RoPE and
-    the cache append as its epilogue (== linear() then qkv_rope_append())."""
+    the cache append as its epilogue (== linear() then qkv_rope_append()).
+    rowscale: x holds a folded norm pair's operand rows, scaled per row."""
     _need_cuda(x, pos, rope_cos, rope_sin, flat_row, k_cache, v_cache, x_rows, q_out)
     Wp = _packed(Wqkv, False)
     n = (x.shape[0] if x_rows is None else x_rows.numel()) if n is None else n
@@ -261,10 +321,11 @@ def linear_qkv_rope_append(x: torch.Tensor, Wqkv: torch.Tensor, pos: torch.Tenso
     if q_out is None:
         q_out = torch.empty(n, H, Dh, dtype=x.dtype, device=x.device)
     _need(q_out.is_contiguous() and q_out.numel() >= n * H * Dh and q_out.dtype == x.dtype, "q_out (n, H, Dh)")
+    keep, rsp = _rs_ptr(rowscale, n)
     rc = _lib.load().wfd_linear_qkv_rope_append(x.data_ptr(), _p(x_rows), x.stride(0), Wp.data.data_ptr(), n, K,
                                                 pos.data_ptr(), rope_cos.data_ptr(), rope_sin.data_ptr(),
                                                 rope_cos.shape[0], flat_row.data_ptr(), q_out.data_ptr(),
-                                                k_cache.data_ptr(), v_cache.data_ptr(), br, H, Hkv, Dh, _dt(x),
+                                                k_cache.data_ptr(), v_cache.data_ptr(), br, H, Hkv, Dh, _dt(x), rsp,
                                                 _stream())
     _lib.check(rc, "wfd_linear_qkv_rope_append")
     return q_out
@@ -322,9 +383,10 @@ def _packed(W, swiglu: bool) -> PackedWeight:
 
 def linear(x: torch.Tensor, W, *, n: int | None = None, x_rows: torch.Tensor | None = None,
            out: torch.Tensor | None = None, swiglu: bool = False, out_dtype: torch.dtype | None = None,
-           k: int | None = None) -> torch.Tensor:
+           k: int | None = None, rowscale: RowScale | None = None) -> torch.Tensor:
     """y = x[rows, :K] @ W^T (W: PackedWeight or plain (N, K)); swiglu: N = 2F,
-    y (n, F) = silu(g) * u."""
+    y (n, F) = silu(g) * u. rowscale: x holds a folded norm pair's operand
+    rows, and each output row is scaled (before the SwiGLU)."""
     _need_cuda(x, x_rows, out)
     Wp = _packed(W, swiglu)
     _need_cuda(Wp.data)
@@ -343,10 +405,67 @@ def linear(x: torch.Tensor, W, *, n: int | None = None, x_rows: torch.Tensor | N
     _need(out.dim() == 2 and out.stride(1) == 1 and out.shape[0] >= n and out.shape[1] >= width and out.dtype == od,
           "bad out")
     epi = _lib.EPI_SWIGLU if swiglu else _lib.EPI_PLAIN
+    keep, rsp = _rs_ptr(rowscale, n)
     rc = _lib.load().wfd_linear(x.data_ptr(), _p(x_rows), x.stride(0), Wp.data.data_ptr(), out.data_ptr(),
-                                out.stride(0), n, N, K, _dt(x), _DT[od], epi, N // 2 if swiglu else 0, _stream())
+                                out.stride(0), n, N, K, _dt(x), _DT[od], epi, N // 2 if swiglu else 0, rsp, _stream())
     _lib.check(rc, "wfd_linear")
     return out
+
+
+def linear_prep(x: torch.Tensor, W, *, n: int, a_out: torch.Tensor, wb: torch.Tensor, part: torch.Tensor,
+                x_rows: torch.Tensor | None = None, r_in: torch.Tensor | None = None,
+                s_in: torch.Tensor | None = None, w_in: torch.Tensor | None = None,
+                r_out: torch.Tensor | None = None, wa: torch.Tensor | None = None) -> None:
+    """A d_model-output linear (n <= 16) whose epilogue prepares a folded norm
+    pair (wfd_linear_prep): r = round(y + x_in) into r_out (x_in from r_in /
+    s_in / w_in, or none), A = round((r * wa) * wb) into a_out, and the
+    group sums into part."""
+    _need_cuda(x, x_rows)
+    Wp = _packed(W, False)
+    _need_cuda(Wp.data)
+    _need(x.dim() == 2 and x.stride(1) == 1 and x.dtype == Wp.dtype and x.shape[1] >= Wp.K, "x (rows, K+)")
+    _rows(x_rows, n, "x_rows")
+    _need(n >= 0 and (x_rows is not None or x.shape[0] >= n), f"x holds {x.shape[0]} rows < n={n}")
+    pp = _prep_args(n, Wp.N, x.dtype, r_in=r_in, s_in=s_in, w_in=w_in, r_out=r_out, a_out=a_out, wa=wa, wb=wb,
+                    part=part)
+    rc = _lib.load().wfd_linear_prep(x.data_ptr(), _p(x_rows), x.stride(0), Wp.data.data_ptr(), n, Wp.N, Wp.K,
+                                     _dt(x), ctypes.addressof(pp), _stream())
+    _lib.check(rc, "wfd_linear_prep")
+
+
+def norm_prep(*, n: int, D: int, dtype: torch.dtype, eps: float, a: torch.Tensor | None = None,
+              part: torch.Tensor | None = None, nslices: int = 0, r_in: torch.Tensor | None = None,
+              s_in: torch.Tensor | None = None, w_in: torch.Tensor | None = None,
+              r_out: torch.Tensor | None = None, a_out: torch.Tensor | None = None, wa: torch.Tensor | None = None,
+              wb: torch.Tensor | None = None, two: bool = True, scale_out: torch.Tensor | None = None,
+              s_out: torch.Tensor | None = None, h_out: torch.Tensor | None = None,
+              h_rows: torch.Tensor | None = None) -> None:
+    """The row form of a folded norm pair (wfd_norm_prep): y = a rows, or the
+    in-order slice sums of linear_partials (part, nslices); r, A, scale_out
+    (s_a * s_b) and s_out (s_a) -- or, with h_out, the block's last norm
+    round((r * s_a) * wa) into rows h_rows."""
+    _need_cuda(a, part, scale_out, s_out, h_out, h_rows)
+    _need((a is None) != (part is None), "norm_prep: exactly one of a / part")
+    if a is not None:
+        _need(a.dim() == 2 and a.stride(1) == 1 and a.dtype == dtype and a.shape[1] >= D
+              and a.shape[0] >= n, "a: (n, D) rows")
+    if part is not None:
+        _need(part.dtype == torch.float32 and part.is_contiguous() and part.numel() >= nslices * n * D,
+              "part: the slice sums of linear_partials")
+    for name, t in (("scale_out", scale_out), ("s_out", s_out)):
+        if t is not None:
+            _need(t.dtype == torch.float32 and t.is_contiguous() and t.numel() >= n, f"{name}: float32 (n,)")
+    if h_out is not None:
+        _need(h_out.dim() == 2 and h_out.stride(1) == 1 and h_out.dtype == dtype and h_out.shape[1] >= D, "h_out")
+        _rows(h_rows, n, "h_rows")
+        if h_rows is None:
+            _need(h_out.shape[0] >= n, "h_out rows < n")
+    pp = _prep_args(n, D, dtype, r_in=r_in, s_in=s_in, w_in=w_in, r_out=r_out, a_out=a_out, wa=wa, wb=wb)
+    rc = _lib.load().wfd_norm_prep(_p(a), a.stride(0) if a is not None else 0, _p(part), n * D, nslices,
+                                   ctypes.addressof(pp), int(bool(two)), float(eps), _p(scale_out), _p(s_out),
+                                   _p(h_out), _p(h_rows), h_out.stride(0) if h_out is not None else 0, n, D,
+                                   _DT[dtype], _stream())
+    _lib.check(rc, "wfd_norm_prep")
 
 
 def add_rmsnorm(a: torch.Tensor, w1: torch.Tensor, eps: float, *, res: torch.Tensor | None = None,
@@ -578,7 +697,7 @@ def linear_argmax_groups(n: int, W) -> int:
 
 def linear_argmax(x: torch.Tensor, W, *, n: int | None = None, x_rows: torch.Tensor | None = None,
                   out: torch.Tensor | None = None, part_val: torch.Tensor | None = None,
-                  part_idx: torch.Tensor | None = None):
+                  part_idx: torch.Tensor | None = None, rowscale: RowScale | None = None):
     """linear(x, W, out_dtype=float32) for bf16 x / W -- the same kernel, so
     the same bits -- that also leaves, per row and column group (G =
     linear_argmax_groups(n, W)), the first largest logit and its column in
@@ -607,8 +726,9 @@ def linear_argmax(x: torch.Tensor, W, *, n: int | None = None, x_rows: torch.Ten
           f"part_val: float32 (>= {n * G},)")
     _need(part_idx.dtype == torch.int32 and part_idx.is_contiguous() and part_idx.numel() >= n * G,
           f"part_idx: int32 (>= {n * G},)")
+    keep, rsp = _rs_ptr(rowscale, n)
     rc = _lib.load().wfd_linear_argmax(x.data_ptr(), _p(x_rows), x.stride(0), Wp.data.data_ptr(), out.data_ptr(),
-                                       out.stride(0), n, N, K, _dt(x), part_val.data_ptr(), part_idx.data_ptr(),
+                                       out.stride(0), n, N, K, _dt(x), part_val.data_ptr(), part_idx.data_ptr(), rsp,
                                        _stream())
     _lib.check(rc, "wfd_linear_argmax")
     return out, part_val, part_idx
