@@ -62,7 +62,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--quick", action="store_true", help="fewer extras (development)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--only", default="", help="comma list of sections: bs1,roofline,attn,linrows,bs32,prefill,c5,gqa,cpu (and the opt-in attnkeys)")
+    ap.add_argument("--only", default="", help="comma list of sections: bs1,roofline,attn,linrows,bs32,prefill,c5,gqa,cpu (and the opt-in attnkeys, foldlin, tick)")
     ap.add_argument("--eager", action="store_true", help="launch every pass eagerly (no hipGraph capture)")
     return ap.parse_args()
 
@@ -165,6 +165,163 @@ def linear_roofline(dev, cfg, n: int, iters: int = 24):
     del Ws
     torch.cuda.empty_cache()
     return res
+
+
+def foldlin_section(args, dev, res):
+    """Opt-in (`--only foldlin`): the few-row linears of one layer with and
+    without their folded norm work, at the bs=1 tick's 1 and 8 rows: Wqkv
+    (+RoPE, append) and gate|up + SwiGLU reading their row scales from group
+    sums, proj / mlp_proj with the residual-prep epilogue, against the plain
+    kernels and the separate residual norm they replace. Each form: average
+    launch duration from HIP events around graph replays of 24 launches over
+    rotating weight copies (> 512 MB)."""
+    import torch
+    from wavefront_decoding_amd import model as M
+    from wavefront_decoding_amd import ops
+
+    c = M.CONFIGS["looped-2048"]
+    D, F, H, Hkv, Dh = c.d_model, c.ffn, c.n_heads, c.n_kv_heads, c.head_dim
+    eps = c.norm_eps
+    iters = 24
+    shapes = {"Wqkv": (c.qkv_dim, D, False), "fc": (2 * F, D, True), "proj": (D, H * Dh, False),
+              "mlp_proj": (D, F, False)}
+    per = sum(N * K * 2 for N, K, _ in shapes.values())
+    copies = max(2, math.ceil(2 * MALL_BYTES / per) + 1)
+    g = torch.Generator(device=dev).manual_seed(3)
+    bf = torch.bfloat16
+    Ws = [{k: ops.pack_linear((0.02 * torch.randn(N, K, device=dev, generator=g)).to(bf), swiglu=sw)
+           for k, (N, K, sw) in shapes.items()} for _ in range(copies)]
+    wv = lambda: (1 + 0.1 * torch.randn(D, device=dev, generator=g)).to(bf)  # noqa: E731
+    w2, w3 = wv(), wv()
+    S = 1024
+    cos = torch.rand(S, Dh // 2, device=dev, generator=g)
+    sin = torch.rand(S, Dh // 2, device=dev, generator=g)
+    kc = torch.zeros(16, Hkv, Dh, dtype=bf, device=dev)
+    vc = torch.zeros_like(kc)
+    out = {}
+    for n in (1, 8):
+        x = torch.randn(n, max(D, F), device=dev, generator=g).to(bf)
+        r_in = torch.randn(n, D, device=dev, generator=g).to(bf)
+        s_in = torch.rand(n, device=dev, generator=g) + 0.5
+        r_out = torch.empty(n, D, dtype=bf, device=dev)
+        A = torch.empty(n, D, dtype=bf, device=dev)
+        gp = torch.empty(n * D // 4, dtype=torch.float32, device=dev)
+        s_out = torch.empty(n, dtype=torch.float32, device=dev)
+        y = torch.empty(n, 2 * F, dtype=bf, device=dev)
+        q = torch.empty(n, H, Dh, dtype=bf, device=dev)
+        pos = torch.arange(n, dtype=torch.int32, device=dev)
+        fr = torch.arange(n, dtype=torch.int64, device=dev)
+        ops.linear_prep(x, Ws[0]["proj"], n=n, r_in=r_in, s_in=s_in, w_in=w2, r_out=r_out, a_out=A, wa=w2, wb=w3,
+                        part=gp)
+        rs = ops.RowScale(D=D, eps=eps, two=True, part=gp, s_out=s_out)
+        forms = {
+            "Wqkv_plain": lambda W: ops.linear_qkv_rope_append(A, W["Wqkv"], pos, cos, sin, fr, kc, vc, H, Hkv, Dh,
+                                                               n=n, q_out=q),
+            "Wqkv_scaled": lambda W: ops.linear_qkv_rope_append(A, W["Wqkv"], pos, cos, sin, fr, kc, vc, H, Hkv, Dh,
+                                                                n=n, q_out=q, rowscale=rs),
+            "fc_plain": lambda W: ops.linear(A, W["fc"], n=n, out=y, swiglu=True),
+            "fc_scaled": lambda W: ops.linear(A, W["fc"], n=n, out=y, swiglu=True, rowscale=rs),
+            "proj_plain": lambda W: ops.linear(x, W["proj"], n=n, out=y, k=H * Dh),
+            "proj_prep": lambda W: ops.linear_prep(x, W["proj"], n=n, r_in=r_in, s_in=s_in, w_in=w2, r_out=r_out,
+                                                   a_out=A, wa=w2, wb=w3, part=gp),
+            "mlp_proj_plain": lambda W: ops.linear(x, W["mlp_proj"], n=n, out=y, k=F),
+            "mlp_proj_prep": lambda W: ops.linear_prep(x, W["mlp_proj"], n=n, r_in=r_in, s_in=s_in, w_in=w2,
+                                                       r_out=r_out, a_out=A, wa=w2, wb=w3, part=gp),
+            "residual_norm": lambda W: ops.add_rmsnorm(A, w2, eps, res=r_in, w2=w3, n=n, x_out=r_out, h_out=y[:, :D]),
+            "final_norm": lambda W: ops.norm_prep(n=n, D=D, dtype=bf, eps=eps, a=r_out, wa=w2, h_out=A),
+            # producer -> consumer chains, as a layer runs them
+            "chain_norm": lambda W: (ops.linear(x, W["mlp_proj"], n=n, out=y, k=F),
+                                     ops.add_rmsnorm(y[:, :D], w2, eps, res=r_in, w2=w3, n=n, x_out=r_out, h_out=A),
+                                     ops.linear_qkv_rope_append(A, W["Wqkv"], pos, cos, sin, fr, kc, vc, H, Hkv,
+                                                                Dh, n=n, q_out=q)),
+            "chain_fold": lambda W: (ops.linear_prep(x, W["mlp_proj"], n=n, r_in=r_in, s_in=s_in, w_in=w2,
+                                                     r_out=r_out, a_out=A, wa=w2, wb=w3, part=gp),
+                                     ops.linear_qkv_rope_append(A, W["Wqkv"], pos, cos, sin, fr, kc, vc, H, Hkv,
+                                                                Dh, n=n, q_out=q, rowscale=rs)),
+        }
+        row = {}
+        for name, fn in forms.items():
+            def loop(fn=fn):
+                for i in range(iters):
+                    fn(Ws[i % copies])
+            loop()
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                loop()
+            graph.replay()
+            row[name] = round(timed(lambda i: graph.replay(), 3) / iters * 1e3, 2)
+            del graph
+        out[f"n{n}"] = row
+        log(f"foldlin n={n}: {row}")
+    res["extra"]["fold_linears_us"] = out
+    del Ws
+    torch.cuda.empty_cache()
+
+
+def tick_section(args, dev, res):
+    """Opt-in (`--only tick`): where a bs=1 greedy tick's wall time goes. One
+    greedy WFD step of the headline is recorded pass for pass (the run_passes
+    calls the scheduler makes); the same passes are then replayed back to back
+    with no accept-flag read between them (the C passes' expected tokens
+    dropped), so the host stays ahead and HIP events measure the GPU's time
+    per tick. The difference to the real step is the host's share of the
+    critical path: reading the flags, routing, planning and launching the
+    next tick while the GPU waits."""
+    import torch
+    from wavefront_decoding_amd import model as M
+    from wavefront_decoding_amd.blocks import LoopedBlocksBatch
+    from wavefront_decoding_amd.engine import LoopedModel
+    from wavefront_decoding_amd.policy import SsdPolicy
+    from wavefront_decoding_amd.scheduler_batch import generate_wavefront_batch, prefill_once
+
+    cfg = M.CONFIGS["looped-2048"]
+    L, N = 512, 256
+    model = LoopedModel(cfg, M.init_weights(cfg, 0), dev, max_seq_len=L + N + 16, max_batch=1, use_graphs=True)
+    prompt = torch.randint(0, cfg.vocab_size, (1, L), generator=torch.Generator().manual_seed(0)).to(dev)
+    bb = LoopedBlocksBatch(model, batch_size=1)
+    pf = prefill_once(bb, prompt)
+    policy = SsdPolicy(cfg.T_total, 2)
+    generate_wavefront_batch(bb, prompt, N, policy, prefilled=pf)  # captures every pass shape
+    rec = []
+    inner = model.run_passes
+
+    def recording(cache, passes):
+        rec.append([(k, list(sq), list(ps), None if (k == "C" or ex is None) else list(ex))
+                    for k, sq, ps, ex in passes])
+        return inner(cache, passes)
+
+    model.run_passes = recording
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    generate_wavefront_batch(bb, prompt, N, policy, prefilled=pf)
+    torch.cuda.synchronize()
+    step_ms = (time.perf_counter() - t0) * 1e3
+    model.run_passes = inner
+    cache = pf.cache
+    for passes in rec[:64]:  # warm: any pass shape not captured yet
+        model.run_passes(cache, passes)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for passes in rec:
+        model.run_passes(cache, passes)
+    e1.record()
+    e1.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    gpu_ms = e0.elapsed_time(e1)
+    ticks = len(rec)
+    out = {"ticks": ticks, "step_us_per_tick": round(step_ms / ticks * 1e3, 1),
+           "replay_gpu_us_per_tick": round(gpu_ms / ticks * 1e3, 1),
+           "replay_wall_us_per_tick": round(wall_ms / ticks * 1e3, 1),
+           "passes_per_tick": round(sum(len(p) for p in rec) / ticks, 2),
+           "rows_per_tick": {k: round(sum(len(ps) for pp in rec for kk, _, ps, _ in pp if kk == k) / ticks, 2)
+                             for k in "PRC"}}
+    res["extra"]["bs1_tick_breakdown"] = out
+    log(f"tick: {out}")
+    del model, bb, pf
+    torch.cuda.empty_cache()
 
 
 # ---------------------------------------------------------------------------
@@ -801,6 +958,10 @@ def main():
         c5_section(args, dev, res)
     if want("gqa"):
         gqa_section(args, dev, res)
+    if "foldlin" in only:  # opt-in only: not part of the default run
+        foldlin_section(args, dev, res)
+    if "tick" in only:  # opt-in only: not part of the default run
+        tick_section(args, dev, res)
     if "attnkeys" in only:  # opt-in only: not part of the default run
         attnkeys_section(args, dev, res)
     if want("cpu") and not args.no_cpu:

@@ -63,8 +63,8 @@ int wfd_abi_version(void);
  * sits between the two linears. The sums are reduced in one fixed order
  * wherever they are formed: per 8-column group g (columns 8g..8g+7) the tree
  * ((c0+c1)+(c2+c3))+((c4+c5)+(c6+c7)) of the squares, then lane L of a wave
- * adds groups L, L+64, L+128, ... in order from +0 and the 64 lane sums meet
- * in a butterfly (xor 32, 16, ..., 1); every product and sum is rounded on
+ * adds groups 2L, 2L+1, 2L+128, 2L+129, ... in that order from +0 and the 64
+ * lane sums meet in a butterfly (xor 32, 16, ..., 1); every product and sum is rounded on
  * its own (no fused multiply-add). So a row's bits never depend on n or on
  * which kernels formed them.
  */
@@ -79,13 +79,14 @@ typedef struct wfd_prep {
   int64_t ld_a;
   const void* wa;     /* the next pair's weights (wa NULL: norm a absent) */
   const void* wb;
-  float* part;        /* wfd_linear_prep: the sums per 8-column group, part[(m * D / 8 + g) * 2 + {0, 1}] */
+  float* part;        /* wfd_linear_prep: the sums per 8-column group, part[(m * D / 8 + g) * 2 + {0, 1}]
+                         (16-byte aligned) */
 } wfd_prep_t;
 
 typedef struct wfd_rowscale {
   const float* scale; /* the per-row scale s_a * s_b (from wfd_norm_prep), or NULL and ... */
-  const float* part;  /* ... the group sums a wfd_linear_prep left (few-row launches only) */
-  int D;              /* row width of r (D / 8 groups) */
+  const float* part;  /* ... the group sums a wfd_linear_prep left (few-row launches only; 16-byte aligned) */
+  int D;              /* row width of r (D / 8 groups; D a multiple of 16) */
   int two;            /* 1: norm a present; 0: absent (s_a = 1) */
   float eps;
   float* s_out;       /* with part: s_a per row (NULL: not kept) */

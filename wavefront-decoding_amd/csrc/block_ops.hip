@@ -325,7 +325,7 @@ __global__ __launch_bounds__(256) void norm_prep_kernel(const T* __restrict__ a,
   constexpr int V = Chunk<T>::V;
   constexpr int KSTEP = Chunk<T>::KSTEP;
   constexpr int KC = Chunk<T>::KC;
-  __shared__ float2 gps[4][kFoldMaxD / 8];  // each row's group sums
+  __shared__ __align__(16) float2 gps[4][kFoldMaxD / 8];  // each row's group sums
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int i = blockIdx.x * (blockDim.x >> 6) + wv;
   const int lane = threadIdx.x & 63;
@@ -399,7 +399,7 @@ __global__ __launch_bounds__(256) void norm_prep_kernel(const T* __restrict__ a,
     }
   }
   asm volatile("" ::: "memory");  // the lanes' group sums are in LDS before any lane reads them (one wave)
-  float2 gpv[kFoldGroupsPerLane];
+  float4 gpv[kFoldLoadsPerLane];
   fold_load(gpv, gps[wv], G, lane);
   float srow, surow;
   fold_sums(gpv, srow, surow);

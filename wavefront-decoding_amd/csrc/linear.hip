@@ -469,24 +469,26 @@ __global__ __launch_bounds__(64 * WW) __attribute__((amdgpu_waves_per_eu(WW == 8
   // this epilogue thread's row scale (rs.scale), loaded before anything else
   const bool by_part = EPI != kEpiPrep && rs.part != nullptr;
   constexpr int RPW = kWideMaxRows / WW;  // rows whose sums a wave reduces: wave, wave + WW
-  // 16 waves: the group sums are loaded at launch and held through the main
-  // loop; 8 waves (three workgroups per CU by LDS, a register budget of 80)
-  // load them after it, one more round trip instead of a third of the residency
+  // 16 waves: the group sums are loaded at launch, ahead of the main loop's
+  // loads (behind them, the launch at 8 rows took 9.4 against 8.7 us), and
+  // held through its MFMAs; 8 waves (three workgroups per CU by LDS, a
+  // register budget of 80, which even one early row per wave would exceed)
+  // load them after the loop, one more round trip
   constexpr bool kEarlyGroups = WW == kWideWaves;
-  float2 gpv[RPW][kFoldGroupsPerLane];
+  float4 gpv[RPW][kFoldLoadsPerLane];
   float esc = 1.f;
-  auto load_groups = [&]() {
+  auto load_groups = [&](int q0, int q1) {
     const int G = rs.D >> 3;
     const int wv = threadIdx.x >> 6;
 #pragma unroll
-    for (int q = 0; q < RPW; ++q) {
+    for (int q = q0; q < q1; ++q) {
       const int rw = wv + WW * q;
       if (by_part && rw < n)  // uniform over the wave
         fold_load(gpv[q], reinterpret_cast<const float2*>(rs.part) + (int64_t)rw * G, G, threadIdx.x & 63);
     }
   };
   {
-    if constexpr (kEarlyGroups) load_groups();
+    if constexpr (kEarlyGroups) load_groups(0, RPW);
     if (EPI != kEpiPrep && rs.scale != nullptr && threadIdx.x < 256) {
       const int orow = 4 * ((threadIdx.x >> 2) >> 4) + (threadIdx.x & 3);
       esc = rs.scale[orow < n ? orow : 0];
@@ -583,7 +585,7 @@ __global__ __launch_bounds__(64 * WW) __attribute__((amdgpu_waves_per_eu(WW == 8
     }
     red[wave + WW * i][lane] = sub;
   }
-  if constexpr (!kEarlyGroups) load_groups();
+  if constexpr (!kEarlyGroups) load_groups(0, RPW);
 #pragma unroll
   for (int q = 0; q < RPW; ++q) {
     const int rw = wave + WW * q;
@@ -1268,9 +1270,9 @@ static bool rowscale_arg(const wfd_rowscale_t* rs, int n, int N, int K, int dtyp
   if (rs->part) {
     const int kc = dtype == kBF16 ? LinTraits<bf16_t>::KC : LinTraits<float>::KC;
     const bool wide = wide_plan(n, N / 16, sub_chunks(K / kc), swiglu).wide;
-    if (!wide || rs->D <= 0 || rs->D % 8 || rs->D > kFoldMaxD || ((uintptr_t)rs->part & 7)) {
-      set_error("%s: group sums (rs->part) need a few-row launch (n=%d <= 16, K=%d) and 0 < D=%d <= %d, D %% 8 == 0",
-                what, n, K, rs->D, kFoldMaxD);
+    if (!wide || rs->D <= 0 || rs->D % 16 || rs->D > kFoldMaxD || ((uintptr_t)rs->part & 15)) {
+      set_error("%s: group sums (rs->part, 16-byte aligned) need a few-row launch (n=%d <= 16, K=%d) and "
+                "0 < D=%d <= %d, D %% 16 == 0", what, n, K, rs->D, kFoldMaxD);
       return false;
     }
   }
@@ -1543,8 +1545,8 @@ int wfd_linear_prep(const void* x, const int32_t* x_rows, int64_t ldx, const voi
     set_error("wfd_linear_prep: the x operand must span less than 2 GiB");
     return kBadArg;
   }
-  if ((((uintptr_t)x | (uintptr_t)W) & 15) || ((ldx * esz) & 15) || ((uintptr_t)pp->part & 7)) {
-    set_error("wfd_linear_prep: x rows and W must be 16-byte aligned, part 8-byte aligned");
+  if ((((uintptr_t)x | (uintptr_t)W | (uintptr_t)pp->part) & 15) || ((ldx * esz) & 15)) {
+    set_error("wfd_linear_prep: x rows, W and part must be 16-byte aligned");
     return kBadArg;
   }
   const RopeArgs ra{};

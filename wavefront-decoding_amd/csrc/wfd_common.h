@@ -246,29 +246,33 @@ __device__ __forceinline__ float add_rn(float a, float b) {
 }
 
 // The two sums of one row from its group sums (one float2 per 8-column
-// group), by one wave: lane L holds groups L + 64 t (zeros past the last) and
-// adds them in t order from +0, then the lanes' butterfly (every lane ends
-// with the same bits: each step adds the same two values in either order).
-// Rows up to kFoldMaxD wide.
+// group), by one wave: lane L holds groups 2L + 128 t and 2L + 1 + 128 t
+// (16-byte loads; zeros past the last group) and adds them in that order,
+// t ascending, from +0; then the lanes' butterfly (every lane ends with the
+// same bits: each step adds the same two values in either order). Rows up to
+// kFoldMaxD wide.
 constexpr int kFoldMaxD = 2048;
-constexpr int kFoldGroupsPerLane = kFoldMaxD / 8 / 64;
+constexpr int kFoldLoadsPerLane = kFoldMaxD / 8 / 128;
 
-__device__ __forceinline__ void fold_load(float2 (&gpv)[kFoldGroupsPerLane], const float2* gp, int G, int lane) {
+__device__ __forceinline__ void fold_load(float4 (&gpv)[kFoldLoadsPerLane], const float2* gp, int G, int lane) {
+  const float4* g4 = reinterpret_cast<const float4*>(gp);
 #pragma unroll
-  for (int t = 0; t < kFoldGroupsPerLane; ++t) {
-    const int gi = lane + 64 * t;
-    gpv[t] = gi < G ? gp[gi] : float2{0.f, 0.f};
+  for (int t = 0; t < kFoldLoadsPerLane; ++t) {
+    const int gi = 2 * lane + 128 * t;  // G is even (D a multiple of 16)
+    gpv[t] = gi < G ? g4[gi >> 1] : float4{0.f, 0.f, 0.f, 0.f};
   }
 }
 
-__device__ __forceinline__ void fold_sums(const float2 (&gpv)[kFoldGroupsPerLane], float& sr, float& su) {
+__device__ __forceinline__ void fold_sums(const float4 (&gpv)[kFoldLoadsPerLane], float& sr, float& su) {
 #pragma clang fp contract(off)
   sr = 0.f;
   su = 0.f;
 #pragma unroll
-  for (int t = 0; t < kFoldGroupsPerLane; ++t) {
+  for (int t = 0; t < kFoldLoadsPerLane; ++t) {
     sr = sr + gpv[t].x;
     su = su + gpv[t].y;
+    sr = sr + gpv[t].z;
+    su = su + gpv[t].w;
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) {
