@@ -205,7 +205,7 @@ def foldlin_section(args, dev, res):
         s_in = torch.rand(n, device=dev, generator=g) + 0.5
         r_out = torch.empty(n, D, dtype=bf, device=dev)
         A = torch.empty(n, D, dtype=bf, device=dev)
-        gp = torch.empty(n * D // 4, dtype=torch.float32, device=dev)
+        gp = torch.empty(n * ops.FOLD_SLOTS * 2, dtype=torch.float32, device=dev)
         s_out = torch.empty(n, dtype=torch.float32, device=dev)
         y = torch.empty(n, 2 * F, dtype=bf, device=dev)
         q = torch.empty(n, H, Dh, dtype=bf, device=dev)

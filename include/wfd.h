@@ -62,11 +62,14 @@ int wfd_abi_version(void);
  * computes r = round(y + x), A and the sums in its epilogue, so no launch
  * sits between the two linears. The sums are reduced in one fixed order
  * wherever they are formed: per 8-column group g (columns 8g..8g+7) the tree
- * ((c0+c1)+(c2+c3))+((c4+c5)+(c6+c7)) of the squares, then lane L of a wave
- * adds groups 2L, 2L+1, 2L+128, 2L+129, ... in that order from +0 and the 64
- * lane sums meet in a butterfly (xor 32, 16, ..., 1); every product and sum is rounded on
- * its own (no fused multiply-add). So a row's bits never depend on n or on
- * which kernels formed them.
+ * ((c0+c1)+(c2+c3))+((c4+c5)+(c6+c7)) of the squares; the groups are dealt
+ * to the 64 lanes of a wave as wfd_linear's chunk layout deals a row's
+ * elements (lane c + 16 j takes, for s = 0..3, the group of elements
+ * 128 c + 32 s + 8 j for bf16, or 64 c + 16 s + 8 (j / 2) for fp32 from the
+ * even j), each lane adds its groups in s order from +0, and the 64 lane sums
+ * meet in a butterfly (xor 32, 16, ..., 1). Every product and sum is rounded
+ * on its own (no fused multiply-add). So a row's bits never depend on n or on
+ * which kernels formed them. Rows up to 2048 (bf16) / 1024 (fp32) wide.
  */
 typedef struct wfd_prep {
   const void* r_in;   /* residual stream to add (NULL: none) ... */
@@ -79,14 +82,15 @@ typedef struct wfd_prep {
   int64_t ld_a;
   const void* wa;     /* the next pair's weights (wa NULL: norm a absent) */
   const void* wb;
-  float* part;        /* wfd_linear_prep: the sums per 8-column group, part[(m * D / 8 + g) * 2 + {0, 1}]
-                         (16-byte aligned) */
+  float* part;        /* wfd_linear_prep: the two sums of each 8-column group, 256 float pairs per row
+                         (16-byte aligned), group g of row m at pair m * 256 + 4 (c + 16 j) + s for the
+                         lane (c, j) and step s that take it (above) */
 } wfd_prep_t;
 
 typedef struct wfd_rowscale {
   const float* scale; /* the per-row scale s_a * s_b (from wfd_norm_prep), or NULL and ... */
   const float* part;  /* ... the group sums a wfd_linear_prep left (few-row launches only; 16-byte aligned) */
-  int D;              /* row width of r (D / 8 groups; D a multiple of 16) */
+  int D;              /* row width of r (a multiple of 128 bf16 / 64 fp32 values) */
   int two;            /* 1: norm a present; 0: absent (s_a = 1) */
   float eps;
   float* s_out;       /* with part: s_a per row (NULL: not kept) */
@@ -278,12 +282,14 @@ int wfd_linear_prep(const void* x, const int32_t* x_rows, int64_t ldx, const voi
 /*
  * The row form of a folded norm pair, one wave per row: the row y is
  * a[i * lda] (part NULL) or the in-order slice sum of wfd_linear_partials'
- * part (rounded to dtype, wfd_linear's output bit for bit); r, A as
- * wfd_linear_prep computes them, and scale_out[i] = s_a * s_b, s_out[i] = s_a
- * (same sums, same order). With h_out instead (final form): h_out[h_rows ?
- * h_rows[i] : i] = round((r * s_a) * wa) with s_a from sum(r^2), the block's
- * last norm (pp->wb, a_out, scale_out unused). D a multiple of 128 (bf16) /
- * 64 (fp32), D <= 4096.
+ * part (rounded to dtype, wfd_linear's output bit for bit); r and A as
+ * wfd_linear_prep computes them (r into pp->r_out if given), scale_out[i] =
+ * s_a * s_b and s_out[i] = s_a (same sums, same order) when pp->a_out is
+ * given; and with h_out, h_out[h_rows ? h_rows[i] : i] = round((r * s_a) * wa),
+ * the output of norm a itself -- the normalized residual a many-row pass
+ * keeps instead of (r, s_a), or, without pp->a_out, the block's last norm.
+ * two = 1 exactly when pp->wa is given (norm a absent: s_a = 1, h = r).
+ * D a multiple of 128 (bf16) / 64 (fp32), at most 2048 (bf16) / 1024 (fp32).
  * Replaces: the residual norms after proj, the MLP down projection and the
  *   adapter (src/decoding/huginn_blocks.py:95,101-102,216;
  *   huginn_blocks_batch.py:159-161,299), for many-row unions and for the

@@ -54,7 +54,8 @@ def _reference(c, eps, res: bool, two: bool):
 
 
 def _row_forms(c, n, D, dtype, eps, res, two):
-    """The row kernel from the one-launch linear's rows and from split-K slices."""
+    """The row kernel from the one-launch linear's rows and from split-K slices,
+    each also writing norm a's output h (the many-row residual stream)."""
     out = []
     kw = dict(r_in=c["r_in"], s_in=c["s_in"], w_in=c["w_in"]) if res else {}
     for split in (False, True):
@@ -68,9 +69,10 @@ def _row_forms(c, n, D, dtype, eps, res, two):
             src = dict(part=part, nslices=S)
         else:
             src = dict(a=ops.linear(c["x"], c["W"], n=n))
+        h = torch.empty_like(r)
         ops.norm_prep(n=n, D=D, dtype=dtype, eps=eps, r_out=r, a_out=A, wa=c["wa"] if two else None, wb=c["wb"],
-                      two=two, scale_out=sc, s_out=sa, **kw, **src)
-        out.append((r, A, sc, sa))
+                      two=two, scale_out=sc, s_out=sa, h_out=h, **kw, **src)
+        out.append((r, A, sc, sa, h))
     return out
 
 
@@ -85,11 +87,13 @@ def test_prep_forms_same_bits_and_match_oracle(gpu, dtype, D, K, res, two):
         kw = dict(r_in=c["r_in"], s_in=c["s_in"], w_in=c["w_in"]) if res else {}
         r1 = torch.empty(n, D, dtype=dtype, device=gpu)
         A1 = torch.empty_like(r1)
-        gp = torch.full((n * (D // 8) * 2,), float("nan"), dtype=torch.float32, device=gpu)
+        gp = torch.full((n * ops.FOLD_SLOTS * 2,), float("nan"), dtype=torch.float32, device=gpu)
         ops.linear_prep(c["x"], c["W"], n=n, r_out=r1, a_out=A1, wa=c["wa"] if two else None, wb=c["wb"], part=gp,
                         **kw)
-        for r2, A2, sc2, sa2 in _row_forms(c, n, D, dtype, eps, res, two):
-            assert torch.equal(r1, r2) and torch.equal(A1, A2)
+        hf = torch.empty_like(r1)  # norm a alone, from r (the block's last-norm form)
+        ops.norm_prep(n=n, D=D, dtype=dtype, eps=eps, a=r1, wa=c["wa"] if two else None, h_out=hf, two=two)
+        for r2, A2, sc2, sa2, h2 in _row_forms(c, n, D, dtype, eps, res, two):
+            assert torch.equal(r1, r2) and torch.equal(A1, A2) and torch.equal(h2, hf)
         # consumers: group sums (few rows) against precomputed scales
         W2 = (0.02 * torch.randn(1024, D, generator=torch.Generator().manual_seed(7))).to(dtype).to(gpu)
         sa1 = torch.full((n,), -1.0, dtype=torch.float32, device=gpu)
@@ -100,6 +104,10 @@ def test_prep_forms_same_bits_and_match_oracle(gpu, dtype, D, K, res, two):
             assert torch.all(sa1 == 1.0)
         rr, h = _reference(c, eps, res, two)
         assert rel_err(_np(y1), h @ _np(W2).T) <= TOL[dtype]
+        if two:
+            assert rel_err(_np(hf), rr) <= TOL[dtype]
+        else:  # no norm a: s_a = 1 and h = r
+            assert torch.equal(hf, r1)
 
 
 @pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 2048), (torch.float32, 256)])
@@ -124,12 +132,12 @@ def test_consumers_same_bits_at_any_row_count(gpu, dtype, D):
         r = torch.empty(n, D, dtype=dtype, device=gpu)
         A = torch.empty_like(r)
         if n <= 16:
-            gp = torch.empty(n * (D // 8) * 2, dtype=torch.float32, device=gpu)
+            gp = torch.empty(n * ops.FOLD_SLOTS * 2, dtype=torch.float32, device=gpu)
             ops.linear_prep(cc["x"], cc["W"], n=n, r_in=cc["r_in"], s_in=cc["s_in"], w_in=cc["w_in"], r_out=r,
                             a_out=A, wa=cc["wa"], wb=cc["wb"], part=gp)
             rs = ops.RowScale(D=D, eps=eps, two=True, part=gp)
         else:
-            (r, A, sc, _), _ = _row_forms(cc, n, D, dtype, eps, True, True)
+            (r, A, sc, _, _), _ = _row_forms(cc, n, D, dtype, eps, True, True)
             rs = ops.RowScale(D=D, eps=eps, two=True, scale=sc)
         u = ops.linear(A, Wfc, n=n, swiglu=True, rowscale=rs)
         lg = ops.linear(A, Wlm, n=n, out_dtype=torch.float32, rowscale=rs)
@@ -173,9 +181,9 @@ def test_final_norm_and_qkv_consumer(gpu, n):
             if n <= 16:
                 ops.linear_prep(c["x"], c["W"], n=n, r_in=c["r_in"], s_in=c["s_in"], w_in=c["w_in"], r_out=r,
                                 a_out=torch.empty_like(r), wb=c["wa"],
-                                part=torch.empty(n * D // 4, dtype=torch.float32, device=gpu))
+                                part=torch.empty(n * ops.FOLD_SLOTS * 2, dtype=torch.float32, device=gpu))
             else:
-                (r, _, _, _), _ = _row_forms(c, n, D, dtype, eps, True, True)
+                (r, _, _, _, _), _ = _row_forms(c, n, D, dtype, eps, True, True)
             ops.norm_prep(n=n, D=D, dtype=dtype, eps=eps, a=r, wa=c["wa"], h_out=h, h_rows=rows)
         out.append(h)
     assert all(torch.equal(o, out[0]) for o in out)
@@ -191,12 +199,12 @@ def test_final_norm_and_qkv_consumer(gpu, n):
     r = torch.empty(n, D, dtype=dtype, device=gpu)
     A = torch.empty_like(r)
     if n <= 16:
-        gp = torch.empty(n * D // 4, dtype=torch.float32, device=gpu)
+        gp = torch.empty(n * ops.FOLD_SLOTS * 2, dtype=torch.float32, device=gpu)
         ops.linear_prep(c["x"], c["W"], n=n, r_in=c["r_in"], s_in=c["s_in"], w_in=c["w_in"], r_out=r, a_out=A,
                         wa=c["wa"], wb=c["wb"], part=gp)
         rs = ops.RowScale(D=D, eps=eps, two=True, part=gp)
     else:
-        (r, A, sc, _), _ = _row_forms(c, n, D, dtype, eps, True, True)
+        (r, A, sc, _, _), _ = _row_forms(c, n, D, dtype, eps, True, True)
         rs = ops.RowScale(D=D, eps=eps, two=True, scale=sc)
     kc = torch.zeros(n, Hkv, Dh, dtype=dtype, device=gpu)
     vc = torch.zeros_like(kc)

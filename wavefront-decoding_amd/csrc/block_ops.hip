@@ -304,18 +304,18 @@ static void launch_add_rmsnorm(int dtype, const void* a, const int32_t* a_rows, 
 }
 
 // Folded norm pairs, the row form (wfd_norm_prep; wfd_prep_t in wfd.h). One
-// wave per row, the lane layout of add_rmsnorm_kernel: lane (j, c) holds, per
-// round rr, chunk p = 16 rr + c, steps s, elements p KC + s KSTEP + j V ..
-// + V -- for bf16 one whole 8-column group per (rr, s), for fp32 half of one
-// (the other half in lane j ^ 1). Each element is wfd_linear_prep's epilogue
-// value (prep_value), the group sums are the same trees, gathered per row in
-// LDS and reduced in the one order (fold_load / fold_sums), so the scales
-// equal what a consumer computes from wfd_linear_prep's group sums, bit for
-// bit. SPLIT: y is the in-order slice sum of wfd_linear_partials (the
-// linear's output before its rounding); else y = a[i] (already rounded).
-// FINAL: h = round((r * s_a) * wa) for the rows h_rows, instead of A and the
-// scales.
-template <typename T, bool SPLIT, bool RES, bool FINAL, int MAXR>
+// wave per row, the lane layout of add_rmsnorm_kernel: lane L = c + 16 j
+// holds, at step s, the elements of chunk c at s KSTEP + j V -- for bf16 one
+// whole 8-column group, for fp32 half of one (the other half in lane L ^ 16).
+// Each element is wfd_linear_prep's epilogue value (prep_value), each group
+// sum the same tree, and the lane adds its groups in step order before the
+// butterfly -- the order a consumer adds the group sums wfd_linear_prep
+// stores (fold_slot), so the scales are equal bit for bit. SPLIT: y is the
+// in-order slice sum of wfd_linear_partials (the linear's output before its
+// rounding); else y = a[i] (already rounded). r (when kept) and A are stored
+// as soon as they are formed, the scales after the sums; XOUT keeps r for
+// h = round((r * s_a) * wa), the first norm's output, written to rows h_rows.
+template <typename T, bool SPLIT, bool RES, bool XOUT>
 __global__ __launch_bounds__(256) void norm_prep_kernel(const T* __restrict__ a, int64_t lda,
                                                         const float* __restrict__ part, int64_t slice_stride,
                                                         int nslices, const wfd_prep_t pp, int two, float eps,
@@ -325,133 +325,134 @@ __global__ __launch_bounds__(256) void norm_prep_kernel(const T* __restrict__ a,
   constexpr int V = Chunk<T>::V;
   constexpr int KSTEP = Chunk<T>::KSTEP;
   constexpr int KC = Chunk<T>::KC;
-  __shared__ __align__(16) float2 gps[4][kFoldMaxD / 8];  // each row's group sums
-  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int i = blockIdx.x * (blockDim.x >> 6) + wv;
+  const int i = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int c = lane & 15;
   const int j = lane >> 4;
   if (i >= n) return;  // no barriers below
   const int P = D / KC;
-  const int G = D / 8;
+  const int p = c < P ? c : P - 1;  // lanes past the last chunk re-read it (their values are never used)
+  const bool live = fold_lane_live<T>(lane, P);
   const T* wa_t = (const T*)pp.wa;
   const T* wb_t = (const T*)pp.wb;
-  float r[MAXR][kChunkSteps][V];
-  float A[MAXR][kChunkSteps][V];
+  const bool prep = pp.a_out != nullptr;  // uniform
+  [[maybe_unused]] float r[kChunkSteps][V];
+  float gr[kChunkSteps], gu[kChunkSteps];
   float s_in = 1.f;
   if constexpr (RES) {
     if (pp.s_in) s_in = pp.s_in[i];
   }
+  // every load of the row first, then the arithmetic and the stores: the
+  // stores cannot be shown not to alias the loads, so loads issued after one
+  // would wait for it, one HBM round trip per step
+  constexpr int YL = SPLIT ? kSplitMaxSlices * (V / 4) : 1;
+  const u32x4 one = Elem<T>::pack_ones();
+  u32x4 yraw[kChunkSteps][YL], rraw[kChunkSteps], wiraw[kChunkSteps], waraw[kChunkSteps], wbraw[kChunkSteps];
 #pragma unroll
-  for (int rr = 0; rr < MAXR; ++rr) {
-    const int p = rr * 16 + c < P ? rr * 16 + c : P - 1;  // lanes past the last chunk re-read it (never used)
+  for (int s = 0; s < kChunkSteps; ++s) {
+    const int64_t off = (int64_t)p * KC + s * KSTEP + j * V;
+    if constexpr (SPLIT) {
+#pragma unroll
+      for (int q = 0; q < kSplitMaxSlices; ++q) {
+        const float* src = part + q * slice_stride + (int64_t)i * D + off;
+#pragma unroll
+        for (int h = 0; h < V / 4; ++h) yraw[s][q * (V / 4) + h] = q < nslices ? ld16(src + 4 * h) : u32x4{0, 0, 0, 0};
+      }
+    } else {
+      yraw[s][0] = ld16(a + (int64_t)i * lda + off);
+    }
+    rraw[s] = wiraw[s] = one;
+    if constexpr (RES) {
+      rraw[s] = ld16((const T*)pp.r_in + (int64_t)i * pp.ld_in + off);
+      if (pp.w_in) wiraw[s] = ld16((const T*)pp.w_in + off);
+    }
+    waraw[s] = wa_t ? ld16(wa_t + off) : one;
+    wbraw[s] = prep ? ld16(wb_t + off) : one;
+  }
+#pragma unroll
+  for (int s = 0; s < kChunkSteps; ++s) {
+    const int64_t off = (int64_t)p * KC + s * KSTEP + j * V;
+    float y[V];
+    if constexpr (SPLIT) {
+      // slices in order from +0 (slices past nslices load as +0)
+#pragma unroll
+      for (int e = 0; e < V; ++e) y[e] = 0.f;
+#pragma unroll
+      for (int q = 0; q < kSplitMaxSlices; ++q) {
+#pragma unroll
+        for (int h = 0; h < V / 4; ++h) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[4 * h + e] += __uint_as_float(yraw[s][q * (V / 4) + h][e]);
+        }
+      }
+    } else {
+      Elem<T>::unpack(yraw[s][0], y);
+    }
+    float rin[V], win[V], wa[V], wb[V];
+    Elem<T>::unpack(rraw[s], rin);
+    Elem<T>::unpack(wiraw[s], win);
+    Elem<T>::unpack(waraw[s], wa);
+    Elem<T>::unpack(wbraw[s], wb);
+    float rv[V], Av[V], sr[V], su[V];
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const PrepVal pv = prep_value<T>(y[e], RES, rin[e], s_in, win[e], wa[e], wb[e]);
+      rv[e] = pv.r;
+      Av[e] = pv.A;
+      sr[e] = pv.sr;
+      su[e] = pv.su;
+    }
+    if constexpr (XOUT) {
+#pragma unroll
+      for (int e = 0; e < V; ++e) r[s][e] = rv[e];
+    }
+    if (c < P) {
+      if (pp.r_out) *reinterpret_cast<u32x4*>((T*)pp.r_out + (int64_t)i * pp.ld_out + off) = Elem<T>::pack(rv);
+      if (prep) *reinterpret_cast<u32x4*>((T*)pp.a_out + (int64_t)i * pp.ld_a + off) = Elem<T>::pack(Av);
+    }
+    // the group's tree: ((c0+c1)+(c2+c3))+((c4+c5)+(c6+c7))
+    float tr = tree4(sr[0], sr[1], sr[2], sr[3]);
+    float tu = tree4(su[0], su[1], su[2], su[3]);
+    if constexpr (V == 8) {
+      tr = add_rn(tr, tree4(sr[4], sr[5], sr[6], sr[7]));
+      tu = add_rn(tu, tree4(su[4], su[5], su[6], su[7]));
+    } else {  // the group's other half sits in lane L ^ 16
+      tr = add_rn(tr, __shfl_xor(tr, 16, 64));
+      tu = add_rn(tu, __shfl_xor(tu, 16, 64));
+    }
+    gr[s] = live ? tr : 0.f;
+    gu[s] = live ? tu : 0.f;
+  }
+  float srow, surow;
+  fold_sums(gr, gu, srow, surow);
+  float s_a, scale;
+  pair_scale(srow, surow, D, eps, two != 0, s_a, scale);
+  if (prep && lane == 0) {
+    scale_out[i] = scale;
+    if (s_out) s_out[i] = s_a;
+  }
+  if constexpr (XOUT) {
+    const int64_t orow = h_rows ? h_rows[i] : i;
 #pragma unroll
     for (int s = 0; s < kChunkSteps; ++s) {
       const int64_t off = (int64_t)p * KC + s * KSTEP + j * V;
-      float y[V];
-      if constexpr (SPLIT) {
-        // slices in order from +0 (a slice past nslices re-reads slice 0 and adds +0)
+      float wa[V], h[V];
+      Elem<T>::unpack(waraw[s], wa);
 #pragma unroll
-        for (int e = 0; e < V; ++e) y[e] = 0.f;
-#pragma unroll
-        for (int q = 0; q < kSplitMaxSlices; ++q) {
-          const bool live = q < nslices;
-          const float* src = part + (live ? q : 0) * slice_stride + (int64_t)i * D + off;
-#pragma unroll
-          for (int h = 0; h < V / 4; ++h) {
-            const u32x4 w = ld16(src + 4 * h);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) y[4 * h + e] += live ? __uint_as_float(w[e]) : 0.f;
-          }
-        }
-      } else {
-        Elem<T>::unpack(ld16(a + (int64_t)i * lda + off), y);
-      }
-      float rin[V], win[V], wa[V], wb[V];
-#pragma unroll
-      for (int e = 0; e < V; ++e) rin[e] = win[e] = wa[e] = wb[e] = 1.f;
-      if constexpr (RES) {
-        Elem<T>::unpack(ld16((const T*)pp.r_in + (int64_t)i * pp.ld_in + off), rin);
-        if (pp.w_in) Elem<T>::unpack(ld16((const T*)pp.w_in + off), win);
-      }
-      if (wa_t) Elem<T>::unpack(ld16(wa_t + off), wa);
-      if constexpr (!FINAL) Elem<T>::unpack(ld16(wb_t + off), wb);
-      float sr[V], su[V];
-#pragma unroll
-      for (int e = 0; e < V; ++e) {
-        const PrepVal pv = prep_value<T>(y[e], RES, rin[e], s_in, win[e], wa[e], wb[e]);
-        r[rr][s][e] = pv.r;
-        A[rr][s][e] = pv.A;
-        sr[e] = pv.sr;
-        su[e] = pv.su;
-      }
-      // the group's tree: ((c0+c1)+(c2+c3))+((c4+c5)+(c6+c7))
-      float gr = tree4(sr[0], sr[1], sr[2], sr[3]);
-      float gu = tree4(su[0], su[1], su[2], su[3]);
-      if constexpr (V == 8) {
-        gr = add_rn(gr, tree4(sr[4], sr[5], sr[6], sr[7]));
-        gu = add_rn(gu, tree4(su[4], su[5], su[6], su[7]));
-      } else {  // the other half of the group sits in lane j ^ 1
-        gr = add_rn(gr, __shfl_xor(gr, 16, 64));
-        gu = add_rn(gu, __shfl_xor(gu, 16, 64));
-      }
-      if (rr * 16 + c < P && (V == 8 || (j & 1) == 0)) gps[wv][off >> 3] = float2{gr, gu};
-    }
-  }
-  asm volatile("" ::: "memory");  // the lanes' group sums are in LDS before any lane reads them (one wave)
-  float4 gpv[kFoldLoadsPerLane];
-  fold_load(gpv, gps[wv], G, lane);
-  float srow, surow;
-  fold_sums(gpv, srow, surow);
-  float s_a, scale;
-  pair_scale(srow, surow, D, eps, two != 0, s_a, scale);
-  if constexpr (FINAL) {
-    const int64_t orow = h_rows ? h_rows[i] : i;
-#pragma unroll
-    for (int rr = 0; rr < MAXR; ++rr)
-#pragma unroll
-      for (int s = 0; s < kChunkSteps; ++s) {
-        const int p = rr * 16 + c;
-        float wa[V], h[V];
-#pragma unroll
-        for (int e = 0; e < V; ++e) wa[e] = 1.f;
-        if (wa_t) Elem<T>::unpack(ld16(wa_t + (int64_t)(p < P ? p : P - 1) * KC + s * KSTEP + j * V), wa);
-#pragma unroll
-        for (int e = 0; e < V; ++e) h[e] = norm_value<T>(r[rr][s][e], s_a, wa[e]);
-        if (p < P)
-          *reinterpret_cast<u32x4*>(h_out + orow * ldh + (int64_t)p * KC + s * KSTEP + j * V) = Elem<T>::pack(h);
-      }
-  } else {
-#pragma unroll
-    for (int rr = 0; rr < MAXR; ++rr)
-#pragma unroll
-      for (int s = 0; s < kChunkSteps; ++s) {
-        const int p = rr * 16 + c;
-        if (p >= P) continue;
-        const int64_t off = (int64_t)p * KC + s * KSTEP + j * V;
-        if (pp.r_out) *reinterpret_cast<u32x4*>((T*)pp.r_out + (int64_t)i * pp.ld_out + off) = Elem<T>::pack(r[rr][s]);
-        *reinterpret_cast<u32x4*>((T*)pp.a_out + (int64_t)i * pp.ld_a + off) = Elem<T>::pack(A[rr][s]);
-      }
-    if (lane == 0) {
-      scale_out[i] = scale;
-      if (s_out) s_out[i] = s_a;
+      for (int e = 0; e < V; ++e) h[e] = norm_value<T>(r[s][e], s_a, wa[e]);
+      if (c < P) *reinterpret_cast<u32x4*>(h_out + orow * ldh + off) = Elem<T>::pack(h);
     }
   }
 }
 
-template <typename T, bool SPLIT, bool RES, bool FINAL>
+template <typename T, bool SPLIT, bool RES, bool XOUT>
 static void launch_norm_prep_t(const void* a, int64_t lda, const float* part, int64_t slice_stride, int nslices,
                                const wfd_prep_t& pp, int two, float eps, float* scale_out, float* s_out, void* h_out,
                                const int32_t* h_rows, int64_t ldh, int n, int D, hipStream_t stream) {
   const int rpw = n >= kNormRowsPerCuLaunch ? 4 : 1;  // as add_rmsnorm: rows spread one per CU below 1024
   const dim3 grid((n + rpw - 1) / rpw), block(64 * rpw);
-  if (D <= 16 * Chunk<T>::KC)
-    hipLaunchKernelGGL((norm_prep_kernel<T, SPLIT, RES, FINAL, 1>), grid, block, 0, stream, (const T*)a, lda, part,
-                       slice_stride, nslices, pp, two, eps, scale_out, s_out, (T*)h_out, h_rows, ldh, n, D);
-  else
-    hipLaunchKernelGGL((norm_prep_kernel<T, SPLIT, RES, FINAL, kFoldMaxD / (16 * Chunk<T>::KC)>), grid, block, 0,
-                       stream, (const T*)a, lda, part, slice_stride, nslices, pp, two, eps, scale_out, s_out,
-                       (T*)h_out, h_rows, ldh, n, D);
+  hipLaunchKernelGGL((norm_prep_kernel<T, SPLIT, RES, XOUT>), grid, block, 0, stream, (const T*)a, lda, part,
+                     slice_stride, nslices, pp, two, eps, scale_out, s_out, (T*)h_out, h_rows, ldh, n, D);
 }
 
 template <typename T>
@@ -789,17 +790,21 @@ int wfd_norm_prep(const void* a, int64_t lda, const float* part, int64_t slice_s
     return kUnsupported;
   }
   const int kc = dtype == kBF16 ? Chunk<bf16_t>::KC : Chunk<float>::KC;
-  if (n < 0 || D <= 0 || D > kFoldMaxD || D % kc != 0 ||
+  const int dmax = dtype == kBF16 ? fold_max_d<bf16_t>() : fold_max_d<float>();
+  if (n < 0 || D <= 0 || D > dmax || D % kc != 0 ||
       (part && (nslices < 1 || nslices > kSplitMaxSlices || slice_stride < (int64_t)n * D))) {
-    set_error("wfd_norm_prep: bad shape n=%d D=%d (a multiple of %d, at most %d) nslices=%d", n, D, kc, kFoldMaxD,
+    set_error("wfd_norm_prep: bad shape n=%d D=%d (a multiple of %d, at most %d) nslices=%d", n, D, kc, dmax,
               nslices);
     return kBadArg;
   }
   if (n == 0) return kOk;
-  const bool fin = h_out != nullptr;
-  if (!pp || (!part && !a) || (fin && (!pp->wa || !two)) || (!fin && (!pp->a_out || !pp->wb || !scale_out))) {
-    set_error("wfd_norm_prep: null pointer argument (the final form needs h_out, pp->wa and two; the prep form "
-              "pp->a_out, pp->wb and scale_out)");
+  if (!pp || (!part && !a) || (!h_out && !pp->a_out) || (pp->a_out && (!pp->wb || !scale_out))) {
+    set_error("wfd_norm_prep: null pointer argument (a or part; h_out or pp->a_out; the prep form needs pp->wb "
+              "and scale_out)");
+    return kBadArg;
+  }
+  if ((pp->wa != nullptr) != (two != 0)) {
+    set_error("wfd_norm_prep: two must be set exactly when norm a's weight pp->wa is given");
     return kBadArg;
   }
   const int esz = dtype == kBF16 ? 2 : 4;

@@ -475,16 +475,17 @@ __global__ __launch_bounds__(64 * WW) __attribute__((amdgpu_waves_per_eu(WW == 8
   // register budget of 80, which even one early row per wave would exceed)
   // load them after the loop, one more round trip
   constexpr bool kEarlyGroups = WW == kWideWaves;
-  float4 gpv[RPW][kFoldLoadsPerLane];
+  float4 gpv[RPW][2];
   float esc = 1.f;
   auto load_groups = [&](int q0, int q1) {
-    const int G = rs.D >> 3;
     const int wv = threadIdx.x >> 6;
+    const int PD = rs.D / LinTraits<T>::KC;  // chunks of a row of r
 #pragma unroll
     for (int q = q0; q < q1; ++q) {
       const int rw = wv + WW * q;
       if (by_part && rw < n)  // uniform over the wave
-        fold_load(gpv[q], reinterpret_cast<const float2*>(rs.part) + (int64_t)rw * G, G, threadIdx.x & 63);
+        fold_load<T>(gpv[q], reinterpret_cast<const float2*>(rs.part) + (int64_t)rw * kFoldSlots,
+                     threadIdx.x & 63, PD);
     }
   };
   {
@@ -591,7 +592,7 @@ __global__ __launch_bounds__(64 * WW) __attribute__((amdgpu_waves_per_eu(WW == 8
     const int rw = wave + WW * q;
     if (by_part && rw < n) {  // row rw's scale from its group sums (uniform over the wave)
       float sr, su;
-      fold_sums(gpv[q], sr, su);
+      fold_sums4(gpv[q], sr, su);
       float s_a, scale;
       pair_scale(sr, su, rs.D, rs.eps, rs.two != 0, s_a, scale);
       if (lane == 0) {
@@ -637,10 +638,8 @@ __global__ __launch_bounds__(64 * WW) __attribute__((amdgpu_waves_per_eu(WW == 8
         const int k = 16 * g + (ln & 15);
         if (pp.r_out) Elem<T>::store((T*)pp.r_out + (int64_t)row * pp.ld_out + k, pv.r);
         if (pp.a_out) Elem<T>::store((T*)pp.a_out + (int64_t)row * pp.ld_a + k, pv.A);
-        if ((k & 7) == 0 && pp.part) {
-          float2* gp = reinterpret_cast<float2*>(pp.part) + (int64_t)row * (16 * gridDim.x / (HALF ? 2 : 1) / 8);
-          gp[k >> 3] = float2{tr, tu};
-        }
+        if ((k & 7) == 0 && pp.part)
+          reinterpret_cast<float2*>(pp.part)[(int64_t)row * kFoldSlots + fold_slot<T>(k >> 3)] = float2{tr, tu};
       }
       return;
     }
@@ -1270,9 +1269,10 @@ static bool rowscale_arg(const wfd_rowscale_t* rs, int n, int N, int K, int dtyp
   if (rs->part) {
     const int kc = dtype == kBF16 ? LinTraits<bf16_t>::KC : LinTraits<float>::KC;
     const bool wide = wide_plan(n, N / 16, sub_chunks(K / kc), swiglu).wide;
-    if (!wide || rs->D <= 0 || rs->D % 16 || rs->D > kFoldMaxD || ((uintptr_t)rs->part & 15)) {
+    const int dmax = dtype == kBF16 ? fold_max_d<bf16_t>() : fold_max_d<float>();
+    if (!wide || rs->D <= 0 || rs->D % kc || rs->D > dmax || ((uintptr_t)rs->part & 15)) {
       set_error("%s: group sums (rs->part, 16-byte aligned) need a few-row launch (n=%d <= 16, K=%d) and "
-                "0 < D=%d <= %d, D %% 16 == 0", what, n, K, rs->D, kFoldMaxD);
+                "0 < D=%d <= %d, a multiple of %d", what, n, K, rs->D, dmax, kc);
       return false;
     }
   }
@@ -1535,6 +1535,11 @@ int wfd_linear_prep(const void* x, const int32_t* x_rows, int64_t ldx, const voi
     return kBadArg;
   }
   const int kc = wfd_linear_k_multiple(dtype);
+  const int dmax = dtype == kBF16 ? fold_max_d<bf16_t>() : fold_max_d<float>();
+  if (N > dmax || N % kc) {
+    set_error("wfd_linear_prep: N=%d must be a multiple of %d, at most %d", N, kc, dmax);
+    return kUnsupported;
+  }
   if (K % kc || !wide_plan(n, N / 16, sub_chunks(K / kc), false).wide) {
     set_error("wfd_linear_prep: n=%d K=%d is not a few-row launch (n <= 16, K a multiple of %d and at most 48 chunks)",
               n, K, kc);

@@ -73,6 +73,7 @@ struct Elem<float> {
     u32x4 w = {__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]), __float_as_uint(o[3])};
     return w;
   }
+  __device__ __forceinline__ static u32x4 pack_ones() { return u32x4{0x3f800000u, 0x3f800000u, 0x3f800000u, 0x3f800000u}; }
 };
 
 template <>
@@ -95,6 +96,7 @@ struct Elem<bf16_t> {
     for (int e = 0; e < 4; ++e) w[e] = f32x2_to_bf16x2_bits(o[2 * e], o[2 * e + 1]);
     return w;
   }
+  __device__ __forceinline__ static u32x4 pack_ones() { return u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u}; }
 };
 
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
@@ -245,40 +247,68 @@ __device__ __forceinline__ float add_rn(float a, float b) {
   return a + b;
 }
 
-// The two sums of one row from its group sums (one float2 per 8-column
-// group), by one wave: lane L holds groups 2L + 128 t and 2L + 1 + 128 t
-// (16-byte loads; zeros past the last group) and adds them in that order,
-// t ascending, from +0; then the lanes' butterfly (every lane ends with the
-// same bits: each step adds the same two values in either order). Rows up to
-// kFoldMaxD wide.
-constexpr int kFoldMaxD = 2048;
-constexpr int kFoldLoadsPerLane = kFoldMaxD / 8 / 128;
+// Where a row's group sums sit, and the order they are added in. A row (at
+// most one round of 16 chunks: 2048 bf16 / 1024 fp32 values) held by one
+// wave in the chunk layout gives lane L = c + 16 j, at step s, the elements
+// of chunk c at s KSTEP + j V: bf16, all of group 16 c + 4 s + j; fp32, half
+// of group 8 c + 2 s + j / 2 (the other half in lane L ^ 16). The sums of
+// that group are stored at slot 4 (c + 16 j) + s of the row's 256 slots (for
+// fp32 from the even j), so lane L finds its four groups, in step order, at
+// slots 4 L .. 4 L + 3. The row's sums: each lane adds its groups in step
+// order from +0 (lanes with no group, past the row or fp32's odd j, add
+// nothing), then the lanes' butterfly (xor 32, 16, ..., 1: every lane ends
+// with the same bits, each step adding the same two values in either order).
+constexpr int kFoldSlots = 256;  // per row
 
-__device__ __forceinline__ void fold_load(float4 (&gpv)[kFoldLoadsPerLane], const float2* gp, int G, int lane) {
-  const float4* g4 = reinterpret_cast<const float4*>(gp);
-#pragma unroll
-  for (int t = 0; t < kFoldLoadsPerLane; ++t) {
-    const int gi = 2 * lane + 128 * t;  // G is even (D a multiple of 16)
-    gpv[t] = gi < G ? g4[gi >> 1] : float4{0.f, 0.f, 0.f, 0.f};
-  }
+template <typename T>
+__host__ __device__ constexpr int fold_max_d() {
+  return 16 * Chunk<T>::KC;
 }
 
-__device__ __forceinline__ void fold_sums(const float4 (&gpv)[kFoldLoadsPerLane], float& sr, float& su) {
+// slot of 8-column group g
+template <typename T>
+__device__ __forceinline__ int fold_slot(int g) {
+  if constexpr (Chunk<T>::V == 8) return 4 * ((g >> 4) + 16 * (g & 3)) + ((g >> 2) & 3);
+  return 4 * ((g >> 3) + 32 * (g & 1)) + ((g >> 1) & 3);
+}
+
+// lane `lane` of a wave holds groups of this row (P chunks)?
+template <typename T>
+__device__ __forceinline__ bool fold_lane_live(int lane, int P) {
+  return (lane & 15) < P && (Chunk<T>::V == 8 || ((lane >> 4) & 1) == 0);
+}
+
+__device__ __forceinline__ void fold_sums(const float (&gr)[kChunkSteps], const float (&gu)[kChunkSteps], float& sr,
+                                          float& su) {
 #pragma clang fp contract(off)
   sr = 0.f;
   su = 0.f;
 #pragma unroll
-  for (int t = 0; t < kFoldLoadsPerLane; ++t) {
-    sr = sr + gpv[t].x;
-    su = su + gpv[t].y;
-    sr = sr + gpv[t].z;
-    su = su + gpv[t].w;
+  for (int t = 0; t < kChunkSteps; ++t) {
+    sr = sr + gr[t];
+    su = su + gu[t];
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) {
     sr = sr + __shfl_xor(sr, m, 64);
     su = su + __shfl_xor(su, m, 64);
   }
+}
+
+// A consumer's copy of lane `lane`'s four groups of a row (zeros where the
+// lane holds none): two 16-byte loads of slots 4 lane .. 4 lane + 3.
+template <typename T>
+__device__ __forceinline__ void fold_load(float4 (&gpv)[2], const float2* row_slots, int lane, int P) {
+  const float4* g4 = reinterpret_cast<const float4*>(row_slots) + 2 * lane;
+  const bool live = fold_lane_live<T>(lane, P);
+  gpv[0] = live ? g4[0] : float4{0.f, 0.f, 0.f, 0.f};
+  gpv[1] = live ? g4[1] : float4{0.f, 0.f, 0.f, 0.f};
+}
+
+__device__ __forceinline__ void fold_sums4(const float4 (&gpv)[2], float& sr, float& su) {
+  const float gr[kChunkSteps] = {gpv[0].x, gpv[0].z, gpv[1].x, gpv[1].z};
+  const float gu[kChunkSteps] = {gpv[0].y, gpv[0].w, gpv[1].y, gpv[1].w};
+  fold_sums(gr, gu, sr, su);
 }
 
 // s_a and the linear's row scale s_a * s_b from the two sums.

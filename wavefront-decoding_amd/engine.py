@@ -234,7 +234,7 @@ class LoopedModel:
         self.sc["A"] = self._pitched(cap, D)
         f32 = lambda k: torch.zeros(k, dtype=torch.float32, device=self.device)  # noqa: E731
         self.sc["s1"], self.sc["s2"], self.sc["scale"] = f32(cap), f32(cap), f32(cap)
-        self.sc["gpart"] = f32(_FEW_ROWS * (D // 8) * 2)
+        self.sc["gpart"] = f32(_FEW_ROWS * ops.FOLD_SLOTS * 2)
         self.sc["logits"] = torch.empty(self.max_rows, cfg.vocab_size, dtype=torch.float32, device=self.device)
         self.sc["ids"] = torch.empty(self.max_rows, dtype=torch.int64, device=self.device)
         # column-group argmax bests of a few-row lm_head (at most 16 rows x N / 8 groups)
@@ -393,15 +393,17 @@ class LoopedModel:
     def _prep(self, xin: torch.Tensor, Wp, n: int, *, res, r_out: torch.Tensor, x_rows=None, wa=None, wb=None,
               s_slot=None, final=None):
         """A d_model-output linear (proj, the MLP down projection, the adapter)
-        and what follows it: r = round(y + x_res) into r_out (res = (r, s, w)
-        of the residual stream, or None), then either the next linear's operand
-        A = round((r * wa) * wb) in sc["A"] -- returning the RowScale that
-        linear reads (group sums for few rows, precomputed scales otherwise;
-        s_slot receives s_a) -- or, with final = (out, rows, w), the block's
-        last norm round((r * s) * w) into out[rows]. Few rows: the linear's
-        own epilogue (linear_prep); many rows: split-K slices reduced by the
-        row kernel (norm_prep), or the one-launch linear then norm_prep --
-        the same bits in every form."""
+        and what follows it: r = round(y + x_res) (res = (r, s, w) of the
+        residual stream, or None), then either the next linear's operand
+        A = round((r * wa) * wb) in sc["A"] -- returning (RowScale that
+        linear reads, the residual stream the block adds next) -- or, with
+        final = (out, rows, w), the block's last norm round((r * s) * w) into
+        out[rows]. Few rows: the linear's own epilogue (linear_prep), r into
+        r_out and the group sums (the next residual is (r_out, s_slot, wa),
+        s_slot filled by the consumer). Many rows: split-K slices reduced by
+        the row kernel (norm_prep), or the one-launch linear then norm_prep,
+        which has s_a in hand and writes the normalized residual
+        round((r * s_a) * wa) into r_out itself. The same bits in every form."""
         c, sc = self.cfg, self.sc
         D, eps = c.d_model, c.norm_eps
         r_in, s_in, w_in = res if res is not None else (None, None, None)
@@ -414,7 +416,8 @@ class LoopedModel:
             if fin:
                 ops.norm_prep(n=n, D=D, dtype=self.dtype, eps=eps, a=r_out, wa=wf, h_out=h_out, h_rows=h_rows)
                 return None
-            return ops.RowScale(D=D, eps=eps, two=wa is not None, part=sc["gpart"], s_out=s_slot)
+            return (ops.RowScale(D=D, eps=eps, two=wa is not None, part=sc["gpart"], s_out=s_slot),
+                    (r_out, s_slot if wa is not None else None, wa))
         lo, hi = self.split_rows
         src = {}
         if lo <= n <= hi:
@@ -426,9 +429,9 @@ class LoopedModel:
             ops.norm_prep(n=n, D=D, dtype=self.dtype, eps=eps, r_in=r_in, s_in=s_in, w_in=w_in, wa=wf,
                           h_out=h_out, h_rows=h_rows, **src)
             return None
-        ops.norm_prep(n=n, D=D, dtype=self.dtype, eps=eps, r_in=r_in, s_in=s_in, w_in=w_in, r_out=r_out,
-                      a_out=sc["A"], wa=wa, wb=wb, two=wa is not None, scale_out=sc["scale"], s_out=s_slot, **src)
-        return ops.RowScale(D=D, eps=eps, two=wa is not None, scale=sc["scale"])
+        ops.norm_prep(n=n, D=D, dtype=self.dtype, eps=eps, r_in=r_in, s_in=s_in, w_in=w_in, a_out=sc["A"],
+                      wa=wa, wb=wb, two=wa is not None, scale_out=sc["scale"], h_out=r_out, **src)
+        return ops.RowScale(D=D, eps=eps, two=wa is not None, scale=sc["scale"]), (r_out, None, None)
 
     def _dblock(self, prefix: str, n: int, pos_d, kvlen_d, rb_d, fr_d, kv_len_max: int, cache, inp, res, nxt,
                 final=None, group_first=None):
@@ -446,16 +449,14 @@ class LoopedModel:
                                        q_out=sc["q"][:n], rowscale=inp)
         o = ops.attn_decode(q, cache.flat_k, cache.flat_v, rb_d, kvlen_d, kv_len_max=kv_len_max, out=sc["o"][:n],
                             workspace=self.attn_ws, group_first=group_first)
-        rs = self._prep(o.view(n, -1), W[prefix + "proj"], n, res=res, r_out=sc["r1"], wa=W[prefix + "norm_2"],
-                        wb=W[prefix + "norm_3"], s_slot=sc["s1"])
+        rs, mid = self._prep(o.view(n, -1), W[prefix + "proj"], n, res=res, r_out=sc["r1"],
+                             wa=W[prefix + "norm_2"], wb=W[prefix + "norm_3"], s_slot=sc["s1"])
         u = ops.linear(sc["A"], W[prefix + "fc"], n=n, out=sc["u"], swiglu=True, rowscale=rs)
-        mid = (sc["r1"], sc["s1"], W[prefix + "norm_2"])
         if final is not None:
             self._prep(u, W[prefix + "mlp_proj"], n, res=mid, r_out=sc["r2"], final=(*final, W[prefix + "norm_4"]))
             return None, None
-        rs = self._prep(u, W[prefix + "mlp_proj"], n, res=mid, r_out=sc["r2"], wa=W[prefix + "norm_4"], wb=nxt,
-                        s_slot=sc["s2"])
-        return rs, (sc["r2"], sc["s2"], W[prefix + "norm_4"])
+        return self._prep(u, W[prefix + "mlp_proj"], n, res=mid, r_out=sc["r2"], wa=W[prefix + "norm_4"], wb=nxt,
+                          s_slot=sc["s2"])
 
     # -- row tables ------------------------------------------------------------------
     def _layers(self, kind: str) -> int:
@@ -490,9 +491,8 @@ class LoopedModel:
         elif kind == "R":
             # adapter(cat[s, e]) -> the first core block's raw residual, with
             # core.0.norm_1 folded into its Wqkv
-            inp = self._prep(self.pool, W["adapter"], nb, x_rows=rows_d, res=None, r_out=sc["r2"],
-                             wb=W["core.0.norm_1"])
-            res = (sc["r2"], None, None)
+            inp, res = self._prep(self.pool, W["adapter"], nb, x_rows=rows_d, res=None, r_out=sc["r2"],
+                                  wb=W["core.0.norm_1"])
             for l in range(L):
                 last = l + 1 == L
                 inp, res = blk(f"core.{l}.", l, inp, res, None if last else W[f"core.{l + 1}.norm_1"],

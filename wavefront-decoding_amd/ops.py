@@ -55,12 +55,16 @@ def _rows(t: torch.Tensor | None, n: int, name: str) -> None:
         _need(t.dtype == torch.int32 and t.is_contiguous() and t.numel() >= n, f"{name}: int32 contiguous (>= {n})")
 
 
+# group-sum pairs per row of a few-row producer (wfd_prep_t.part)
+FOLD_SLOTS = 256
+
+
 class RowScale:
     """Where a linear finds its rows' folded-norm scales (wfd_rowscale_t):
     `scale` (n,) float32 precomputed by norm_prep, or `part` -- the group sums
-    linear_prep left, (n, D/8, 2) float32, few-row launches only -- with the
-    pair's form (`two`: norm a present) and eps; with `part`, `s_out` (n,)
-    float32 receives s_a."""
+    linear_prep left, FOLD_SLOTS float pairs per row, few-row launches only --
+    with the pair's form (`two`: norm a present) and eps; with `part`,
+    `s_out` (n,) float32 receives s_a."""
 
     __slots__ = ("scale", "part", "D", "two", "eps", "s_out")
 
@@ -71,7 +75,7 @@ class RowScale:
 
     def check(self, n: int) -> None:
         _need_cuda(self.scale, self.part, self.s_out)
-        for name, t, size in (("scale", self.scale, n), ("part", self.part, n * (self.D // 8) * 2),
+        for name, t, size in (("scale", self.scale, n), ("part", self.part, n * FOLD_SLOTS * 2),
                               ("s_out", self.s_out, n)):
             if t is not None:
                 _need(t.dtype == torch.float32 and t.is_contiguous() and t.numel() >= size,
@@ -105,8 +109,8 @@ def _prep_args(n: int, D: int, dtype, *, r_in=None, s_in=None, w_in=None, r_out=
     if s_in is not None:
         _need(s_in.dtype == torch.float32 and s_in.is_contiguous() and s_in.numel() >= n, "s_in: float32 (n,)")
     if part is not None:
-        _need(part.dtype == torch.float32 and part.is_contiguous() and part.numel() >= n * (D // 8) * 2,
-              "part: float32 (n, D/8, 2)")
+        _need(part.dtype == torch.float32 and part.is_contiguous() and part.numel() >= n * FOLD_SLOTS * 2,
+              f"part: float32 (n, {FOLD_SLOTS}, 2)")
     ld = lambda t: t.stride(0) if t is not None else 0  # noqa: E731
     return _lib.PrepArgs(_p(r_in), ld(r_in), _p(s_in), _p(w_in), _p(r_out), ld(r_out), _p(a_out), ld(a_out), _p(wa),
                          _p(wb), _p(part))
@@ -441,9 +445,10 @@ def norm_prep(*, n: int, D: int, dtype: torch.dtype, eps: float, a: torch.Tensor
               s_out: torch.Tensor | None = None, h_out: torch.Tensor | None = None,
               h_rows: torch.Tensor | None = None) -> None:
     """The row form of a folded norm pair (wfd_norm_prep): y = a rows, or the
-    in-order slice sums of linear_partials (part, nslices); r, A, scale_out
-    (s_a * s_b) and s_out (s_a) -- or, with h_out, the block's last norm
-    round((r * s_a) * wa) into rows h_rows."""
+    in-order slice sums of linear_partials (part, nslices); with a_out: A,
+    scale_out (s_a * s_b), s_out (s_a) and r into r_out if given; with
+    h_out: norm a's output round((r * s_a) * wa) into rows h_rows (without
+    a_out: the block's last norm)."""
     _need_cuda(a, part, scale_out, s_out, h_out, h_rows)
     _need((a is None) != (part is None), "norm_prep: exactly one of a / part")
     if a is not None:
