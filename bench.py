@@ -463,10 +463,13 @@ def bs1_section(args, dev, res):
 
 def linrows_section(args, dev, res):
     """The decode linears of the 2048-d model at the row counts of bs=32
-    passes (17-256 rows): per shape, the launch the engine uses (the split-K
-    slice launch plus its split residual norm for the 2048-column
-    projections; one launch for gate|up + SwiGLU and Wqkv), timed like the
-    n=8 shapes (HIP events around graph replays over rotating weight copies)."""
+    passes (17-256 rows): per shape, the launches the engine uses -- for the
+    2048-column projections the split-K slice launch plus the row kernel of
+    the folded norm pair after it (residual add, both norms' scales, the next
+    linear's operand and norm a's output); gate|up + SwiGLU and Wqkv as one
+    launch that scales its rows by the pair's precomputed scale -- timed like
+    the n=8 shapes (HIP events around graph replays over rotating weight
+    copies)."""
     import torch
     from wavefront_decoding_amd import model as M
     from wavefront_decoding_amd import ops
@@ -490,18 +493,20 @@ def linrows_section(args, dev, res):
             x = torch.randn(n, K + 32, device=dev, generator=g).to(torch.bfloat16)[:, :K]
             res_ = torch.randn(n, D, device=dev, generator=g).to(torch.bfloat16)
             y = torch.empty(n, N // 2 if sw else N, device=dev, dtype=torch.bfloat16)
-            xo, ho = torch.empty(n, D, device=dev, dtype=torch.bfloat16), torch.empty(n, D, device=dev,
+            Ao, ho = torch.empty(n, D, device=dev, dtype=torch.bfloat16), torch.empty(n, D, device=dev,
                                                                                       dtype=torch.bfloat16)
+            scale = torch.rand(n, device=dev, generator=g) + 0.5
+            rs = ops.RowScale(D=D, eps=1e-6, two=True, scale=scale)
             split = N == D
 
-            def loop(Ws=Ws, x=x, y=y, n=n, sw=sw, split=split, res_=res_, xo=xo, ho=ho):
+            def loop(Ws=Ws, x=x, y=y, n=n, sw=sw, split=split, res_=res_, Ao=Ao, ho=ho, scale=scale, rs=rs):
                 for i in range(iters):
                     if split:
                         S = ops.linear_partials(x, Ws[i % copies], part, n=n)
-                        ops.add_rmsnorm_split(part, S, n, w1, 1e-6, dtype=torch.bfloat16, res=res_, w2=w2,
-                                              x_out=xo, h_out=ho)
+                        ops.norm_prep(n=n, D=D, dtype=torch.bfloat16, eps=1e-6, part=part, nslices=S, r_in=res_,
+                                      a_out=Ao, wa=w1, wb=w2, two=True, scale_out=scale, h_out=ho)
                     else:
-                        ops.linear(x, Ws[i % copies], n=n, out=y, swiglu=sw)
+                        ops.linear(x, Ws[i % copies], n=n, out=y, swiglu=sw, rowscale=rs)
 
             loop()
             torch.cuda.synchronize()
@@ -514,7 +519,8 @@ def linrows_section(args, dev, res):
             wb = N * K * 2
             out[f"{name}_n{n}"] = {"us": round(us, 2), "weight_MB": round(wb / 1e6, 2),
                                    "GBs": round(wb / (us * 1e-6) / 1e9, 1),
-                                   "form": "split-K slices + split residual norm" if split else "one launch"}
+                                   "form": "split-K slices + folded norm pair's row kernel" if split
+                                   else "one launch, row-scaled"}
         del Ws
     torch.cuda.empty_cache()
     res["extra"]["linears_bs32_rows"] = out
