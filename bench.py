@@ -62,7 +62,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--quick", action="store_true", help="fewer extras (development)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--only", default="", help="comma list of sections: bs1,roofline,attn,linrows,bs32,prefill,c5,gqa,cpu (and the opt-in attnkeys, foldlin, tick)")
+    ap.add_argument("--only", default="", help="comma list of sections: bs1,roofline,attn,linrows,bs32,prefill,c5,gqa,cpu (and the opt-in attnkeys, attnoverlap, foldlin, tick)")
     ap.add_argument("--eager", action="store_true", help="launch every pass eagerly (no hipGraph capture)")
     return ap.parse_args()
 
@@ -626,6 +626,102 @@ def attnkeys_section(args, dev, res):
     log(f"attnkeys: {out}")
 
 
+def attnoverlap_section(args, dev, res):
+    """Opt-in (`--only attnoverlap`): how much of one bs=1 layer's Wqkv +
+    attention pair a form that overlaps them could hide, at the headline's
+    layer tick (8 rows; Wqkv 6144 x 2048 with the folded norm pair's row scale
+    from group sums, RoPE and the slot append; attention over 512..778-key
+    prefixes, 16 heads x 128). Per iteration of a captured graph, timed with
+    HIP events: the Wqkv launch alone, the attention launch alone, the two in
+    order on one stream (the dependent pair the decode runs), the attention
+    alone on a side branch (the fork / join's own cost), and the two on
+    parallel branches of the graph (the attention reads q and a KV set that
+    the concurrent Wqkv does not write). Weight copies and KV sets rotate over
+    > 512 MB. The parallel figure bounds any overlapped form from below: such
+    a form must still wait for its rows' q before the first QK^T."""
+    import torch
+    from wavefront_decoding_amd import model as M
+    from wavefront_decoding_amd import ops
+
+    c = M.CONFIGS["looped-2048"]
+    n, H, Hkv, Dh, D = 8, c.n_heads, c.n_kv_heads, c.head_dim, c.d_model
+    lens = [512 + 38 * i for i in range(n)]
+    S = max(lens) + 1
+    g = torch.Generator(device=dev).manual_seed(3)
+    per = (H + 2 * Hkv) * Dh * D * 2 + n * S * Hkv * Dh * 2 * 2
+    ns = max(3, math.ceil(2 * MALL_BYTES / per) + 1)
+    Ws = [ops.pack_linear((0.02 * torch.randn((H + 2 * Hkv) * Dh, D, device=dev, generator=g)).to(torch.bfloat16))
+          for _ in range(ns)]
+    kv = [(torch.randn(n, Hkv, S, Dh, device=dev, generator=g).to(torch.bfloat16),
+           torch.randn(n, Hkv, S, Dh, device=dev, generator=g).to(torch.bfloat16)) for _ in range(ns)]
+    x = torch.randn(n, D + 32, device=dev, generator=g).to(torch.bfloat16)[:, :D]
+    part = torch.rand(n * ops.FOLD_SLOTS * 2, device=dev, generator=g) + 0.5
+    rs = ops.RowScale(D=D, eps=c.norm_eps, two=True, part=part)
+    pos = torch.tensor([L - 1 for L in lens], dtype=torch.int32, device=dev)
+    kl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    rb = torch.tensor([i * S for i in range(n)], dtype=torch.int64, device=dev)
+    fr = rb + pos.to(torch.int64)
+    ang = torch.rand(S, Dh // 2, device=dev, generator=g) * 6.28
+    cos_t, sin_t = torch.cos(ang).contiguous(), torch.sin(ang).contiguous()
+    q = torch.empty(n, H, Dh, device=dev, dtype=torch.bfloat16)
+    q_prev = torch.randn(n, H, Dh, device=dev, generator=g).to(torch.bfloat16)
+    o = torch.empty_like(q)
+    ws = ops.attn_workspace(n, H, Dh, max(lens), dev)
+    iters = 24
+
+    def wqkv(i):
+        kc, vc = kv[(i + 1) % ns]
+        ops.linear_qkv_rope_append(x, Ws[i % ns], pos, cos_t, sin_t, fr, kc, vc, H, Hkv, Dh, n=n, q_out=q,
+                                   rowscale=rs)
+
+    def attn(i, qq):
+        kc, vc = kv[i % ns]
+        ops.attn_decode(qq, kc, vc, rb, kl, kv_len_max=max(lens), out=o, workspace=ws)
+
+    side = torch.cuda.Stream()
+
+    def run(mode):
+        cur = torch.cuda.current_stream()
+        for i in range(iters):
+            if mode == "wqkv":
+                wqkv(i)
+            elif mode == "attn":
+                attn(i, q_prev)
+            elif mode == "serial":
+                wqkv(i)
+                attn(i, q)
+            elif mode == "fork_attn":  # the attention alone on the side branch: the fork / join's own cost
+                side.wait_stream(cur)
+                with torch.cuda.stream(side):
+                    attn(i, q_prev)
+                cur.wait_stream(side)
+            else:  # two branches of the graph, joined at the end of every iteration
+                side.wait_stream(cur)
+                with torch.cuda.stream(side):
+                    attn(i, q_prev)
+                wqkv(i)
+                cur.wait_stream(side)
+
+    out = {}
+    for mode in ("wqkv", "attn", "serial", "fork_attn", "parallel"):
+        run(mode)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            run(mode)
+        graph.replay()
+        out[f"{mode}_us"] = round(timed(lambda i: graph.replay(), 3) / iters * 1e3, 2)
+        del graph
+    out["overlap_bound_us"] = round(out["serial_us"] - out["parallel_us"], 2)
+    # the same bound with the fork / join's own cost taken out of the parallel pair
+    out["overlap_bound_net_us"] = round(out["serial_us"] - (out["parallel_us"] - (out["fork_attn_us"] - out["attn_us"])),
+                                        2)
+    res["extra"]["attention_overlap"] = out
+    log(f"attnoverlap: {out}")
+    del Ws, kv
+    torch.cuda.empty_cache()
+
+
 def gqa_section(args, dev, res):
     """Long-context GQA decode: one R tick for 4 sequences x W=16 rows over a
     32k random-filled prompt cache (prefill of 4 x 32k prompts is out of scope)."""
@@ -968,6 +1064,8 @@ def main():
         foldlin_section(args, dev, res)
     if "tick" in only:  # opt-in only: not part of the default run
         tick_section(args, dev, res)
+    if "attnoverlap" in only:  # opt-in only: not part of the default run
+        attnoverlap_section(args, dev, res)
     if "attnkeys" in only:  # opt-in only: not part of the default run
         attnkeys_section(args, dev, res)
     if want("cpu") and not args.no_cpu:
