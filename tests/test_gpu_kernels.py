@@ -113,11 +113,14 @@ def test_attn_decode_row_invariant(gpu, dtype, H, Hkv, Dh):
     (16, 4, 128, [(0, 64), (0, 65), (37, 100)]),        # GQA, tile edges, a segment after a cached prefix
     (4, 4, 64, [(0, 1), (5, 3), (0, 130), (120, 70)]),  # tiny heads, 1-row and ragged segments
     (16, 16, 64, [(0, 257), (300, 1)]),                 # a lone query over a 300-key prefix
+    (16, 16, 128, [(0, 1000), (0, 63), (64, 64)]),      # many tiles per key stream, odd and even tile counts
+    (16, 16, 64, [(0, 2100), (10, 300)]),               # one key stream (> 2048 rows at 16 heads) beside two
 ])
 def test_attn_prefill_matches_oracle(gpu, H, Hkv, Dh, segs, blocks):
     """MFMA causal prefill: segment (pos0, len) on its own slot, each row
     attending keys [0, its position]; against the oracle, and both cache
-    layouts give the same bits."""
+    layouts give the same bits. A segment takes one or two key streams by its
+    own length, so each segment's rows equal its rows launched alone."""
     dtype = torch.bfloat16
     g = torch.Generator().manual_seed(len(segs) * 31 + Dh)
     S = max(p0 + n for p0, n in segs) + 5
@@ -142,6 +145,12 @@ def test_attn_prefill_matches_oracle(gpu, H, Hkv, Dh, segs, blocks):
     ref = ok.attention_rows(_np(q), _np(K), _np(V), rb.numpy(), kl.numpy())
     assert rel_err(_np(out), ref) <= 2e-2
     assert torch.equal(out, other)
+    if len(segs) > 1:  # each segment alone: the same bits
+        for i, (pp, ln) in enumerate(segs):
+            alone = ops.attn_prefill(q[qs[i]:qs[i + 1]].to(gpu), Kd.to(gpu), Vd.to(gpu), seg_rb[i:i + 1].to(gpu),
+                                     torch.tensor([0, ln], dtype=torch.int32, device=gpu), p0[i:i + 1].to(gpu),
+                                     max_seg_len=ln)
+            assert torch.equal(alone, out[qs[i]:qs[i + 1]]), i
     # per-row agreement with the decode kernel on the same rows (different arithmetic, same math)
     dec = ops.attn_decode(q.to(gpu), K.to(gpu), V.to(gpu), rb.to(gpu), kl.to(gpu), kv_len_max=int(kl.max()))
     assert rel_err(_np(out), _np(dec)) <= 2e-2
