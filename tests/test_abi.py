@@ -9,7 +9,7 @@ import subprocess
 import pytest
 import torch
 
-from wavefront_decoding_amd import _lib
+from wavefront_decoding_amd import _lib, ops
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -108,3 +108,18 @@ def test_alignment_and_grid_checks_reject_before_launch():
     # one grid row per 128-query tile: at most 65535 of them
     rc = lib.wfd_attn_prefill(4096, 4096, 4096, 0, 16, 16, 16, 4096, 1, 65535 * 128 + 1, 16, 16, 64, 1, 0.1, None)
     assert rc < 0 and b"beyond the grid" in lib.wfd_last_error()
+
+
+def test_engine_rejects_rows_wider_than_the_folded_norms_take():
+    """The decode step folds each RMSNorm pair into the linears, one wave per
+    row: d_model up to 16 K chunks (2048 bf16, 1024 fp32). A wider model is
+    refused when the engine is built, before anything is allocated."""
+    import dataclasses
+
+    from wavefront_decoding_amd import model as M
+    from wavefront_decoding_amd.engine import LoopedModel
+
+    assert ops.fold_max_d(torch.bfloat16) == 2048 and ops.fold_max_d(torch.float32) == 1024
+    wide = dataclasses.replace(M.CONFIGS["looped-2048"], d_model=4096)
+    with pytest.raises(ValueError, match="folded norm pairs"):
+        LoopedModel(wide, {}, "cpu", max_seq_len=16)

@@ -114,3 +114,4 @@ def test_add_rmsnorm_split_rejects_short_buffers():
         ops.add_rmsnorm_split(part, 4, n, w, 1e-6, x_out=_m(n - 1, D), **kw)
     with pytest.raises(_lib.WfdError, match="h_out"):
         ops.add_rmsnorm_split(part, 4, n, w, 1e-6, w2=w, x_out=_m(n, D), h_out=_m(n - 1, D), **kw)
+

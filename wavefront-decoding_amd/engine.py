@@ -9,9 +9,13 @@ of rows -- any mix of sequences, positions and loop depths -- through:
   coda_union     ln_f(pool[row][:D]) -> coda blocks -> ln_f -> lm_head -> argmax
   prefill_seq    the same blocks over a whole prompt, every slot filled
 
-and every block is: linear(Wqkv) with RoPE + cache append fused -> attn_decode ->
-linear(proj) -> add_rmsnorm(norm_2, norm_3) -> linear(fc, swiglu) ->
-linear(mlp_proj) -> add_rmsnorm(norm_4, next norm_1).
+and every decode block is: linear(Wqkv) with RoPE + cache append fused ->
+attn_decode -> linear(proj) -> linear(fc, swiglu) -> linear(mlp_proj), each
+residual add and the RMSNorm pair after it -- (norm_2, norm_3), then (norm_4,
+the next norm_1) -- folded into the linears around it: the producing linear
+(or, above 16 rows, the row kernel norm_prep) writes the residual stream and
+the next linear's operand, and the consuming linear scales its rows (see
+_prep). The prompt pass (prefill_seq) keeps separate add_rmsnorm launches.
 
 Row tables (positions, slot row bases, append rows, pool rows) are built on
 the host per call and read by the kernels as device data. Each row's
@@ -179,6 +183,9 @@ class LoopedModel:
         self.cfg = cfg
         self.device = torch.device(device)
         self.dtype = cfg.torch_dtype
+        if cfg.d_model > ops.fold_max_d(self.dtype):
+            raise ValueError(f"{cfg.name}: d_model={cfg.d_model} is wider than the decode step's folded norm pairs "
+                             f"take ({ops.fold_max_d(self.dtype)} for {self.dtype}: one wave holds a row)")
         self.max_seq_len = max_seq_len
         self.max_batch = max_batch
         self.state_init = state_init

@@ -342,6 +342,13 @@ def linear_k_multiple(dtype: torch.dtype) -> int:
     return int(_lib.load().wfd_linear_k_multiple(_DT[dtype]))
 
 
+def fold_max_d(dtype: torch.dtype) -> int:
+    """Widest row (d_model) a folded norm pair takes: one wave holds a whole
+    row as 16 chunks of the linears' K granularity (wfd_linear_prep,
+    wfd_norm_prep): 2048 bf16, 1024 fp32."""
+    return 16 * linear_k_multiple(dtype)
+
+
 class PackedWeight:
     """A linear weight in the kernels' packed layout (wfd_linear_pack): same
     bytes as the (N, K) nn.Linear weight, in MFMA fragment order. `swiglu`
