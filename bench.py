@@ -62,7 +62,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--quick", action="store_true", help="fewer extras (development)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--only", default="", help="comma list of sections: bs1,roofline,attn,linrows,bs32,prefill,c5,gqa,cpu (and the opt-in attnkeys, attnoverlap, foldlin, tick)")
+    ap.add_argument("--only", default="", help="comma list of sections: bs1,roofline,attn,linrows,bs32,prefill,c5,gqa,cpu (and the opt-in attnkeys, attnoverlap, foldlin, linsweep, tick)")
     ap.add_argument("--eager", action="store_true", help="launch every pass eagerly (no hipGraph capture)")
     return ap.parse_args()
 
@@ -267,7 +267,9 @@ def tick_section(args, dev, res):
     dropped), so the host stays ahead and HIP events measure the GPU's time
     per tick. The difference to the real step is the host's share of the
     critical path: reading the flags, routing, planning and launching the
-    next tick while the GPU waits."""
+    next tick while the GPU waits. A further step with host timestamps gives
+    the mean host time of a launch call and of the routing between a verify
+    tick's flags and the next launch call."""
     import torch
     from wavefront_decoding_amd import model as M
     from wavefront_decoding_amd.blocks import LoopedBlocksBatch
@@ -297,7 +299,30 @@ def tick_section(args, dev, res):
     generate_wavefront_batch(bb, prompt, N, policy, prefilled=pf)
     torch.cuda.synchronize()
     step_ms = (time.perf_counter() - t0) * 1e3
-    model.run_passes = inner
+    # the host's own share: a second step with host timestamps around every
+    # launch call and every accept-flag read (the scheduler's routing sits
+    # between a verify tick's flags and the next launch call)
+    flags_in, stamps = model.accept_flags, []
+
+    def stamped_launch(cache, passes):
+        a = time.perf_counter()
+        r = inner(cache, passes)
+        stamps.append(("launch", a, time.perf_counter()))
+        return r
+
+    def stamped_flags(timeout_s=30.0):
+        a = time.perf_counter()
+        r = flags_in(timeout_s)
+        stamps.append(("flags", a, time.perf_counter()))
+        return r
+
+    model.run_passes, model.accept_flags = stamped_launch, stamped_flags
+    generate_wavefront_batch(bb, prompt, N, policy, prefilled=pf)
+    torch.cuda.synchronize()
+    model.run_passes, model.accept_flags = inner, flags_in
+    launch_us = [1e6 * (b - a) for k, a, b in stamps if k == "launch"]
+    route_us = [1e6 * (nxt[1] - cur[2]) for cur, nxt in zip(stamps, stamps[1:])
+                if cur[0] == "flags" and nxt[0] == "launch"]
     cache = pf.cache
     for passes in rec[:64]:  # warm: any pass shape not captured yet
         model.run_passes(cache, passes)
@@ -316,6 +341,8 @@ def tick_section(args, dev, res):
            "replay_gpu_us_per_tick": round(gpu_ms / ticks * 1e3, 1),
            "replay_wall_us_per_tick": round(wall_ms / ticks * 1e3, 1),
            "passes_per_tick": round(sum(len(p) for p in rec) / ticks, 2),
+           "host_launch_call_us": round(sum(launch_us) / max(len(launch_us), 1), 1),
+           "host_route_after_flags_us": round(sum(route_us) / max(len(route_us), 1), 1),
            "rows_per_tick": {k: round(sum(len(ps) for pp in rec for kk, _, ps, _ in pp if kk == k) / ticks, 2)
                              for k in "PRC"}}
     res["extra"]["bs1_tick_breakdown"] = out
@@ -624,6 +651,52 @@ def attnkeys_section(args, dev, res):
         out[f"row1_L{L}"] = {"us": round(us, 2), "GBs": round(by / us / 1e3, 1)}
     res["extra"]["attention_key_sweep"] = out
     log(f"attnkeys: {out}")
+
+
+def linsweep_section(args, dev, res):
+    """Opt-in (`--only linsweep`): the few-row linear's time against its
+    weight bytes -- a plain 2048-input bf16 linear over 4096..8192 output
+    columns at 1 and 8 rows, each timed like the n=8 shapes (HIP events
+    around graph replays of 24 launches over rotating weight copies). The
+    fit time = fixed part + bytes / rate separates the per-launch fixed part
+    from the streaming rate."""
+    import torch
+    from wavefront_decoding_amd import ops
+
+    g = torch.Generator(device=dev).manual_seed(2)
+    K, iters = 2048, 24
+    out, pts = {}, {1: [], 8: []}
+    for N in (4096, 5120, 6144, 7168, 8192):
+        copies = max(2, math.ceil(2 * MALL_BYTES / (N * K * 2)) + 1)
+        Ws = [ops.pack_linear((0.02 * torch.randn(N, K, device=dev, generator=g)).to(torch.bfloat16))
+              for _ in range(copies)]
+        for n in (1, 8):
+            x = torch.randn(n, K + 32, device=dev, generator=g).to(torch.bfloat16)[:, :K]
+            y = torch.empty(n, N, device=dev, dtype=torch.bfloat16)
+
+            def loop(Ws=Ws, x=x, y=y, n=n):
+                for i in range(iters):
+                    ops.linear(x, Ws[i % len(Ws)], n=n, out=y)
+
+            loop()
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                loop()
+            graph.replay()
+            us = timed(lambda i: graph.replay(), 3) / iters * 1e3
+            del graph
+            out[f"N{N}_n{n}"] = round(us, 2)
+            pts[n].append((N * K * 2, us))
+        del Ws
+    for n, p in pts.items():  # least-squares line us = a + bytes / rate
+        xs, ys = [b for b, _ in p], [u for _, u in p]
+        mx, my = sum(xs) / len(xs), sum(ys) / len(ys)
+        slope = sum((a - mx) * (b - my) for a, b in zip(xs, ys)) / sum((a - mx) ** 2 for a in xs)
+        out[f"fit_n{n}"] = {"fixed_us": round(my - slope * mx, 2), "rate_GBs": round(1e-3 / slope, 1)}
+    res["extra"]["linear_bytes_sweep"] = out
+    log(f"linsweep: {out}")
+    torch.cuda.empty_cache()
 
 
 def attnoverlap_section(args, dev, res):
@@ -1064,6 +1137,8 @@ def main():
         foldlin_section(args, dev, res)
     if "tick" in only:  # opt-in only: not part of the default run
         tick_section(args, dev, res)
+    if "linsweep" in only:  # opt-in only: not part of the default run
+        linsweep_section(args, dev, res)
     if "attnoverlap" in only:  # opt-in only: not part of the default run
         attnoverlap_section(args, dev, res)
     if "attnkeys" in only:  # opt-in only: not part of the default run
