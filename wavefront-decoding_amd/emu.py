@@ -9,7 +9,7 @@ import random
 class EmulatedAcceptance:
     def __init__(self, rate: float, seed: int = 0):
         if not 0.0 <= rate <= 1.0:
-            raise AssertionError(f"acceptance rate must be in [0,1], got {rate}")
+            raise AssertionError(f"EmulatedAcceptance: rate {rate} is not a probability (0 <= rate <= 1)")
         self.rate = float(rate)
         self.seed = seed
         self.rng = random.Random(seed)

@@ -18,13 +18,13 @@ class SsdPolicy:
 
     def __post_init__(self) -> None:
         if self.T_draft < 1 or self.T_total < self.T_draft:
-            raise ValueError(f"Invalid policy: T_total={self.T_total}, T_draft={self.T_draft}. "
-                             "Require 1 <= T_draft <= T_total.")
+            raise ValueError(f"SsdPolicy: the draft depth must lie in [1, T_total] "
+                             f"(T_total={self.T_total}, T_draft={self.T_draft})")
         if self.mode != "greedy":
             raise ValueError(f"Unsupported sampling mode {self.mode!r}: this build decodes greedily (lossless).")
         if self.T_total % self.T_draft:
-            warnings.warn(f"T_total ({self.T_total}) is not a multiple of T_draft ({self.T_draft}); "
-                          "the wave size will fluctuate.", stacklevel=2)
+            warnings.warn(f"SsdPolicy: T_draft={self.T_draft} does not divide T_total={self.T_total}, so the "
+                          "number of tokens in flight varies from tick to tick", stacklevel=2)
 
     @property
     def steady_state_active_size(self) -> int:
