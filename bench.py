@@ -32,6 +32,12 @@ layer tick of the 2048-d model at bs=1: 8 rows x 16 heads x Dh 128 over
 gate|up projection with the SwiGLU epilogue at 8 rows. Both take `achieved`
 from HIP events around graph replays on the launch stream and `traffic` from
 the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes.
+
+Opt-in sections (`--only`, never part of the default run): attnkeys (the
+bs=1 attention launch against its key count), attnoverlap (Wqkv and the
+attention in sequence and side by side), foldlin (the folded norm pairs'
+linears and chains against separate norms), linsweep (a few-row linear's time
+against its weight bytes) and tick (a bs=1 tick's GPU and host time).
 """
 from __future__ import annotations
 
