@@ -133,9 +133,9 @@ class BatchStaticKVCache:
 
     def drop_positions_at_and_after(self, b: int, position: int) -> None:
         """Per-sequence rollback: truncate sequence b's logical lengths only."""
-        for sl in range(self.n_slots):
-            if self.seqlen[sl][b] > position:
-                self.seqlen[sl][b] = position
+        for row in self.seqlen:  # on the host's path from a reject to the next launch
+            if row[b] > position:
+                row[b] = position
 
     def reset_lengths(self) -> None:
         """Forget every sequence (buffers are reused as they are; reads are

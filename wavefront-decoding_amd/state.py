@@ -14,7 +14,7 @@ from typing import Literal, Optional
 Role = Literal["verify", "draft"]
 
 
-@dataclass
+@dataclass(slots=True)
 class ActiveToken:
     """One token progressing through the recurrent core.
 
