@@ -77,6 +77,7 @@ def _row_forms(c, n, D, dtype, eps, res, two):
 
 
 @pytest.mark.parametrize("dtype,D,K", [(torch.bfloat16, 2048, 2048), (torch.bfloat16, 2048, 5632),
+                                       (torch.bfloat16, 512, 1024), (torch.bfloat16, 128, 256),
                                        (torch.float32, 256, 1024)])
 @pytest.mark.parametrize("res,two", [(True, True), (False, False), (True, False)])
 def test_prep_forms_same_bits_and_match_oracle(gpu, dtype, D, K, res, two):
@@ -110,7 +111,7 @@ def test_prep_forms_same_bits_and_match_oracle(gpu, dtype, D, K, res, two):
             assert torch.equal(hf, r1)
 
 
-@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 2048), (torch.float32, 256)])
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 2048), (torch.bfloat16, 512), (torch.float32, 256)])
 def test_consumers_same_bits_at_any_row_count(gpu, dtype, D):
     """A row's outputs do not depend on n: rows prepared and consumed at 1-16
     rows (group sums, few-row kernels -- SwiGLU at 704 tiles takes the 8-wave
