@@ -175,7 +175,10 @@ int wfd_attn_varlen_rows(const int32_t* cu_q, const int32_t* cu_k, int nseg, int
  * start at seg_row_base[s]; query row j attends that slot's keys [0, its
  * position] (bottom-right causal), which must already be appended. out: (n, H,
  * Dh). max_seg_len >= every segment length sizes the grid. Tables are device
- * data. q, the caches and out are 16-byte aligned.
+ * data. q, the caches and out are 16-byte aligned. A segment of at most
+ * (256 / H) * 128 rows is computed with two key streams per workgroup, a
+ * longer one with one; the choice depends only on the segment's length and H,
+ * so a segment's output bits do not depend on the other segments of the call.
  * Replaces: attn_dense(q, k, v, causal=True) (src/decoding/fa4_attention.py:189-215)
  *   from _block_dense (src/decoding/huginn_blocks_batch.py:163-170), and the
  *   grouped causal segments of _core_attn_varlen (src/decoding/parcae_blocks.py:435-456).
