@@ -105,6 +105,14 @@ def test_alignment_and_grid_checks_reject_before_launch():
     assert rc == -1 and b"16-byte aligned" in lib.wfd_last_error()
     rc = lib.wfd_attn_prefill(4096, 4096, 4096, 0, 16, 16, 16, 4096 + 2, 1, 10, 16, 16, 64, 1, 0.1, None)
     assert rc == -1 and b"16-byte aligned" in lib.wfd_last_error()
+    # row pitches below the row width of the folded norm pairs' rows
+    pp_short = _lib.PrepArgs(None, 0, None, None, None, 0, 4096, 1024, None, 8192, 12288)  # ld_a 1024 < N 2048
+    rc = lib.wfd_linear_prep(4096, None, 2048, 8192, 8, 2048, 2048, 1, ctypes.addressof(pp_short), None)
+    assert rc == -1 and b"row pitch" in lib.wfd_last_error()
+    pp_norm = _lib.PrepArgs(None, 0, None, None, None, 0, 4096, 2048, None, 8192, None)
+    rc = lib.wfd_norm_prep(4096, 1024, None, 0, 0, ctypes.addressof(pp_norm), 0, 1e-6, 4096, None, None, None, 0, 4,
+                           2048, 1, None)  # lda 1024 < D 2048
+    assert rc == -1 and b"row pitch" in lib.wfd_last_error()
     # one grid row per 128-query tile: at most 65535 of them
     rc = lib.wfd_attn_prefill(4096, 4096, 4096, 0, 16, 16, 16, 4096, 1, 65535 * 128 + 1, 16, 16, 64, 1, 0.1, None)
     assert rc < 0 and b"beyond the grid" in lib.wfd_last_error()

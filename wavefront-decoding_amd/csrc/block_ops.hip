@@ -807,6 +807,11 @@ int wfd_norm_prep(const void* a, int64_t lda, const float* part, int64_t slice_s
     set_error("wfd_norm_prep: two must be set exactly when norm a's weight pp->wa is given");
     return kBadArg;
   }
+  if ((a && lda < D) || (pp->r_in && pp->ld_in < D) || (pp->r_out && pp->ld_out < D) || (pp->a_out && pp->ld_a < D) ||
+      (h_out && ldh < D)) {
+    set_error("wfd_norm_prep: a row pitch is below D=%d", D);
+    return kBadArg;
+  }
   const int esz = dtype == kBF16 ? 2 : 4;
   if ((((uintptr_t)a | (uintptr_t)part | (uintptr_t)pp->r_in | (uintptr_t)pp->w_in | (uintptr_t)pp->r_out |
         (uintptr_t)pp->a_out | (uintptr_t)pp->wa | (uintptr_t)pp->wb | (uintptr_t)h_out) & 15) ||

@@ -1545,6 +1545,10 @@ int wfd_linear_prep(const void* x, const int32_t* x_rows, int64_t ldx, const voi
               n, K, kc);
     return kUnsupported;
   }
+  if ((pp->r_in && pp->ld_in < N) || (pp->r_out && pp->ld_out < N) || pp->ld_a < N) {
+    set_error("wfd_linear_prep: a row pitch of r_in / r_out / a_out is below N=%d", N);
+    return kBadArg;
+  }
   const int64_t esz = dtype == kBF16 ? 2 : 4;
   if (!x_rows && (int64_t)n * ldx * esz >= (int64_t)kBufInvalid) {
     set_error("wfd_linear_prep: the x operand must span less than 2 GiB");
